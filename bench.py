@@ -1,0 +1,183 @@
+#!/usr/bin/env python3
+"""Decode benchmark: batch-1 greedy decode tok/s of the 28-layer q4 Qwen3-VL-2B-shaped text
+decoder at 4k context, on one MI355X.
+
+Workload (vision-shaped context): random-init q4 group-64 weights, 4096-token prefill = 16 text
+tokens, 1024 synthetic fp16 N(0,1) visual embeddings on a 32x32 merged grid (3D M-RoPE,
+interleaved sections 24/20/20) with three DeepStack feature sets injected after layers 0-2, then
+3056 random text tokens; then greedy decode.  A step is one decode token.  `value` is decode
+tokens/s over exactly --steps timed steps, inputs resident in HBM, after --warmup untimed steps.
+
+Also reported: prefill tok/s, the HBM-roofline fraction of decode (weight + KV bytes per token /
+8 TB/s), the isolated GEMV roofline of the dominant kernel shape, and the oracle's CPU decode
+rate on the host (bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from instantcua_amd import engine as eng  # noqa: E402
+from instantcua_amd import synth  # noqa: E402
+from instantcua_amd.modelfile import Dims, WeightFormat  # noqa: E402
+
+HBM_PEAK = 8.0e12  # B/s, MI355X
+LAYERS = 28
+VIS_OFFSET, LLM_H, LLM_W = 16, 32, 32
+PREFILL = 4096
+
+
+def weight_bytes_per_token(fmt=WeightFormat.Q4) -> int:
+    """Algorithmic weight bytes one decode token streams: four matrices per layer, norms, lm_head."""
+    def mat(rows, K):
+        if fmt == WeightFormat.Q4:
+            return rows * K // 2 + rows * (K // 64) * 4
+        return rows * K + rows * (K // 32) * 2
+    H, FF = Dims.hidden, Dims.ff
+    layer = mat(Dims.qkv_rows, H) + mat(H, H) + mat(Dims.gu_rows, H) + mat(H, FF)
+    norms = LAYERS * (2 * H * 4 + 2 * Dims.head_dim * 4) + H * 4
+    return LAYERS * layer + norms + mat(Dims.vocab, H)
+
+
+def kv_bytes_per_token(ctx: int) -> int:
+    return LAYERS * 2 * Dims.kv_heads * Dims.head_dim * 2 * ctx
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_roofline(iters=200):
+    """Isolated q4 dequant-GEMV at the gate+up shape (the largest per-layer matrix), rotating
+    distinct weight copies (> 256 MB) so the Infinity Cache cannot serve repeats."""
+    K, N = Dims.hidden, Dims.gu_rows
+    m = synth.make_matrix(WeightFormat.Q4, N, K, tag="bench-gemv")
+    per = m.codes.nbytes + m.sb.nbytes
+    copies = max(2, int(np.ceil(300e6 / per)))
+    codes = [eng.DeviceBuffer.from_array(m.codes) for _ in range(copies)]
+    sbs = [eng.DeviceBuffer.from_array(m.sb) for _ in range(copies)]
+    x = eng.DeviceBuffer.from_array(synth.fp16_normal((1, K), "bench-gemv-x"))
+    y = eng.DeviceBuffer(N * 4)
+    us = eng.gemv_bench(WeightFormat.Q4, codes, sbs, N, K, x, y, iters)
+    traffic = per + K * 2 + N * 4
+    for b in codes + sbs + [x, y]:
+        b.free()
+    return {"kernel": f"q4 GEMV {K}x{N}", "us": us, "bytes": traffic, "copies": copies}
+
+
+def cpu_baseline(img, ctx, seconds=10.0):
+    """Oracle decode steps at the same context on the host cores (KV filled with fp16 N(0,1))."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    oracle.build()
+    max_steps = 40
+    om = oracle.OracleModel(img, ctx + max_steps + 2)
+    for l in range(om.layers):
+        for kind in (0, 1):
+            om.kv(l, kind)[:, :ctx] = synth.fp16_normal((Dims.kv_heads, ctx, Dims.head_dim), f"cpu-kv{kind}", l)
+    tok = np.array([1], dtype=np.int32)
+    om.run_pass(tok, ctx)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        om.run_pass(tok, ctx + 1 + n)
+        n += 1
+        if time.perf_counter() - t0 > seconds or n >= max_steps:
+            break
+    dt = time.perf_counter() - t0
+    threads = oracle.get_threads()
+    om.close()
+    return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps of the 28-layer q4 decoder at {ctx}-token context (oracle, fp64 accumulation)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU decode is a design note only",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    K, W = args.steps, args.warmup
+    t0 = time.time()
+    img = synth.build_model_image(WeightFormat.Q4, n_layers=LAYERS, tag="bench-q4")
+    vp = synth.visual_prompt(PREFILL, VIS_OFFSET, LLM_H, LLM_W, tag="bench-vis")
+    log(f"model image {img.nbytes / 1e6:.0f} MB built in {time.time() - t0:.1f}s")
+
+    maxctx = PREFILL + W + K + 8
+    e = eng.Engine(image=img, max_context=maxctx, max_steps=W + K + 2)
+    e.eos = (-1, -1)
+    e.prepare_mrope(VIS_OFFSET, LLM_H, LLM_W)
+    e.set_visual(vp.pooler.astype(np.float32), [d.astype(np.float32) for d in vp.deepstack])
+
+    t1 = time.perf_counter()
+    e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=W + K + 1)
+    prefill_wall = time.perf_counter() - t1
+    prefill_ms = e.last_timing["prefill_ms"]
+    log(f"prefill {PREFILL} tokens: {prefill_ms:.1f} ms (GPU events), {prefill_wall * 1e3:.1f} ms wall")
+
+    if W:
+        e.decode_steps(W)
+    eng.lib().icua_device_sync()
+    t2 = time.perf_counter()
+    e.decode_steps(K)
+    eng.lib().icua_device_sync()
+    wall = time.perf_counter() - t2
+    dec_ms = e.last_timing["decode_ms"]
+    st = e.state()
+    assert st["step"] == 1 + W + K and not st["done"] or st["step"] == 1 + W + K, st
+    ms_per_step = dec_ms / K
+    value = K / (dec_ms / 1e3)
+    ctx_mid = PREFILL + W + K // 2
+    bytes_tok = weight_bytes_per_token() + kv_bytes_per_token(ctx_mid)
+    log(f"decode: {ms_per_step * 1e3:.1f} us/token ({value:.0f} tok/s); wall {wall * 1e3:.1f} ms")
+
+    g = gemv_roofline()
+    achieved = g["bytes"] / (g["us"] * 1e-6)
+    e.close()
+
+    cpu = None if args.no_cpu else cpu_baseline(img, PREFILL)
+
+    out = {
+        "metric": "decode tok/s @bs1 (q4 2B VL decoder, 4k ctx)",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4 weights, int codes x fp activations, fp32 accumulate, fp16 KV",
+        "data": "synthetic (seeded random-init weights and inputs of the Qwen3-VL-2B text-decoder shape)",
+        "config": {"workload": "28-layer q4 g64 decoder, 4096-token vision-context prefill "
+                               "(16 text + 32x32 visual + 3056 text, DeepStack), greedy decode",
+                   "prefill_tokens": PREFILL, "context_at_timing": [PREFILL + W, PREFILL + W + K],
+                   "batch": 1},
+        "decode_roofline_frac": round(bytes_tok / (ms_per_step * 1e-3) / HBM_PEAK, 4),
+        "decode_bytes_per_token": bytes_tok,
+        "prefill_tok_s": round(PREFILL / (prefill_ms / 1e3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "kernel": g["kernel"], "kernel_us": round(g["us"], 3), "bytes_per_launch": g["bytes"]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

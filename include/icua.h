@@ -1,0 +1,151 @@
+/* icua.h -- C ABI of the MI355X (gfx950) Qwen3-VL text-decoder engine.
+ *
+ * Drop-in boundary for instantcua's `Engine` (Sources/Engine/Engine.swift:5-827).  The Swift
+ * class keeps its API and forwards to these functions, in the style of the reference's C target
+ * Sources/CShim (Package.swift:14; Sources/CShim/include/cshim.h:1-4).  Plain pointers and
+ * sizes only.  Every function returns 0 on success and a negative code on failure; the message
+ * is available from icua_last_error() (thread-local), which the Swift wrapper maps to
+ * `EngineError` (Sources/Engine/ModelFile.swift:158-161).
+ *
+ * Threading and ownership follow the reference: one engine is bound to one HIP stream and is
+ * not thread-safe; calls are synchronous (they return after the GPU work completes, as
+ * `waitUntilCompleted` does in Engine.swift:786-791); the engine owns all device memory; input
+ * arrays are borrowed and copied in.
+ */
+#ifndef ICUA_H
+#define ICUA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct icua_engine icua_engine;
+
+/* Weight formats of the .icua file (ModelFile.swift:6-9). */
+enum { ICUA_FMT_F16 = 0, ICUA_FMT_Q8 = 1, ICUA_FMT_Q4 = 2 };
+
+/* Engine flags (icua_engine_create / icua_set_flags). */
+enum {
+    ICUA_FLAG_GRAMMAR_PAIRS = 1, /* forced syntax pairs + ')' stop of k_commit (Shaders.swift:1543-1560) */
+    ICUA_FLAG_PREFIX_CACHE = 2,  /* reuse the KV of an identical pre-image prefix (Engine.swift:719-735) */
+};
+
+/* Decode control block, first twelve fields as `State` (Shaders.swift:41-54). */
+typedef struct {
+    int32_t pos, n, step, done, maxctx, maxsteps, eos0, eos1, vis_offset, n_vis, rope_delta, npatches;
+    int32_t flags, logits_rows;
+} icua_state_t;
+
+/* Engine.Timing (Engine.swift:44-52). */
+typedef struct {
+    double vision_ms, prefill_ms, decode_ms, total_ms;
+    int64_t prefill_tokens, generated_tokens;
+} icua_timing_t;
+
+typedef struct {
+    int32_t format, layers, max_context, max_pass, max_steps;
+    int64_t weight_bytes, kv_bytes;
+} icua_info_t;
+
+/* Last error message of the calling thread ("" if none). */
+const char* icua_last_error(void);
+
+/* Engine.init(modelPath:maxContext:maxPass:maxSteps:copyWeights:pinMemory:) (Engine.swift:54-185).
+ * Loads the .icua file (ModelFile.init, ModelFile.swift:124-149) and copies the decoder tensors
+ * to device memory.  max_ctx <= 16384. */
+int icua_engine_create(const char* path, int max_ctx, int max_pass, int max_steps, uint32_t flags,
+                       icua_engine** out);
+/* Same, from an in-memory .icua image (len bytes) that the caller keeps alive during the call. */
+int icua_engine_create_from_memory(const void* image, size_t len, int max_ctx, int max_pass, int max_steps,
+                                   uint32_t flags, icua_engine** out);
+void icua_engine_destroy(icua_engine* e);
+int icua_engine_info(icua_engine* e, icua_info_t* out);
+
+/* Engine.eos (Engine.swift:12). */
+int icua_set_eos(icua_engine* e, int32_t eos0, int32_t eos1);
+/* Engine.usePrefixCache and the grammar option. */
+int icua_set_flags(icua_engine* e, uint32_t flags);
+
+/* Engine.prepareMRoPE(visOffset:llmH:llmW:) (Engine.swift:254-298); vis_offset < 0: text only. */
+int icua_prepare_mrope(icua_engine* e, int vis_offset, int llm_h, int llm_w);
+
+/* Replaces Engine.poolerBuf / deepstackBufs (Engine.swift:20-21): visual embeddings
+ * pooler[n_vis][2048] and three DeepStack sets deepstack[i][n_vis][2048], fp32 host arrays.
+ * deepstack may be NULL (no DeepStack injection). */
+int icua_set_visual(icua_engine* e, const float* pooler, const float* const* deepstack, int n_vis);
+
+/* Engine.encodePrefill (Engine.swift:658-673) run to completion: embeds tokens[0..n) at cache
+ * slots start_pos.., runs every decoder layer (DeepStack after layers 0-2 at the visual rows),
+ * then lm_head + greedy commit of the first generated token.  Resets step/done.
+ * vis_offset is the row of the first image-pad token in `tokens` (-1: none).
+ * write_logits: keep the first-token logits for icua_logits(). */
+int icua_prefill(icua_engine* e, const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new,
+                 int write_logits);
+
+/* k x Engine.encodeDecodeStep (Engine.swift:675-681), GPU-resident (one captured HIP graph per
+ * step, token feedback on the device); returns after completion.  Steps after a stop are no-ops. */
+int icua_decode_steps(icua_engine* e, int k);
+
+/* Engine.generateVision (Engine.swift:696-827) minus the vision encoder: prefill + greedy decode
+ * of up to max_new tokens; out_tokens receives them up to (excluding) EOS; *n_out their count.
+ * vis_offset: first image-pad row or -1; with ICUA_FLAG_PREFIX_CACHE the KV of an identical
+ * prefix tokens[0..vis_offset) is reused. */
+int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, int max_new,
+                  int32_t* out_tokens, int* n_out);
+
+/* Speculative verify: m <= 8 draft tokens at the current position in one pass with a causal
+ * tail; out_argmax[m] gets each row's greedy token; out_logits ([m][151936]) may be NULL.
+ * The cache keeps the drafts' K/V; the position is left unchanged (the caller accepts a prefix
+ * and calls icua_set_position).  No reference counterpart: the reference's n = 2 grammar pass
+ * (Shaders.swift:735-788) is the closest multi-token decode. */
+int icua_verify(icua_engine* e, const int32_t* draft, int m, int32_t* out_argmax, float* out_logits);
+
+/* Rewinds / advances the cache position and re-arms decoding with `next_token` as the input of
+ * the next step (done = 0). */
+int icua_set_position(icua_engine* e, int pos, int32_t next_token, int step, int max_steps);
+
+/* Reads the control block / the committed tokens / the last written logits (rows x 151936). */
+int icua_read_state(icua_engine* e, icua_state_t* out);
+int icua_read_tokens(icua_engine* e, int32_t* dst, int n);
+int icua_logits(icua_engine* e, float* dst, int rows);
+
+/* Engine.lastTiming (Engine.swift:52, 818-825). */
+int icua_timing(icua_engine* e, icua_timing_t* out);
+
+/* Engine.encodeLLMLayer (Engine.swift:476-629) on explicit rows: runs decoder layer `layer` on
+ * x_in[n][2048] (fp32) for cache slots pos..pos+n-1 (n <= 8), writes their K/V, x_out[n][2048]. */
+int icua_layer_step(icua_engine* e, int layer, const float* x_in, int n, int pos, float* x_out);
+
+/* KV cache access (kc/vc, Engine.swift:110-112): kind 0 = K, 1 = V; data [8][nslots][128] fp16. */
+int icua_read_kv(icua_engine* e, int layer, int kind, int slot0, int nslots, uint16_t* dst);
+int icua_write_kv(icua_engine* e, int layer, int kind, int slot0, int nslots, const uint16_t* src);
+
+/* Pass activations of the last layer run (Engine.swift:24 x, qkvBuf, attnh, hbuf): for tests.
+ * ICUA_BUF_X fp32 [8][2048]; ICUA_BUF_QKV fp32 [8][4096] raw fused QKV rows; ICUA_BUF_ATTN fp16
+ * [8][2048] attention output; ICUA_BUF_MLP fp16 [8][6144] SwiGLU output. */
+enum { ICUA_BUF_X = 0, ICUA_BUF_QKV = 1, ICUA_BUF_ATTN = 2, ICUA_BUF_MLP = 3 };
+int icua_read_buffer(icua_engine* e, int which, void* dst, size_t bytes);
+
+/* ---- standalone kernels on device buffers (isolated dequant-GEMV sweep, codec checks) ---- */
+int icua_dev_alloc(size_t bytes, void** ptr);
+int icua_dev_free(void* ptr);
+int icua_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int icua_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int icua_device_sync(void);
+
+/* y[m][N] = W[N][K] . x[m][K]: W in the .icua codec (codes + scales), x fp16, y fp32;
+ * K in {2048, 6144}, N % 8 == 0, m <= 8.  The dot64_row family of Shaders.swift:480-595. */
+int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const void* d_x, int m, float* d_y);
+/* Times `iters` launches of icua_gemv cycling over `ncopies` weight copies; *avg_us per launch. */
+int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb, int ncopies, int N, int K,
+                    const void* d_x, float* d_y, int iters, double* avg_us);
+/* Bit-exact dequantisation of rows [row0, row0 + rows) to fp32 (Shaders.swift:464-476). */
+int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,860 @@
+// Host engine behind include/icua.h: model load, device buffers, pass orchestration and the
+// GPU-resident greedy decode loop.  Mirrors Sources/Engine/Engine.swift (init 54-185,
+// prepareMRoPE 254-298, encodeLLMLayer 476-629, encodeLMHead 631-644, encodeCommit 646-656,
+// encodePrefill 658-673, encodeDecodeStep 675-681, generateVision 696-827).
+//
+// Differences by design: one HIP stream instead of Metal command buffers; one decode step is a
+// captured HIP graph replayed per token (the reference encodes 8 steps per command buffer);
+// prefill runs in passes of up to MAXM rows through the same kernels as decode.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/icua.h"
+#include "icua_kernels.h"
+
+using namespace icua;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const std::string& msg) {
+    g_err = msg;
+    return -1;
+}
+
+#define HIPCK(call)                                                                             \
+    do {                                                                                        \
+        hipError_t _e = (call);                                                                 \
+        if (_e != hipSuccess) return fail(std::string(#call) + ": " + hipGetErrorString(_e));   \
+    } while (0)
+
+// Tensor ids (Sources/Engine/ModelFile.swift:62-111).
+constexpr int T_EMBED = 315, T_EMBED_SB = 316, T_FINAL_NORM = 317, T_LAYER_BASE = 318, T_PER_LAYER = 14;
+constexpr int T_COUNT = 710;
+constexpr uint32_t MAGIC = 0x31554349u;  // "ICU1"
+
+size_t code_bytes(int fmt, size_t rows, size_t K) { return fmt == 2 ? rows * K / 2 : fmt == 1 ? rows * K : rows * K * 2; }
+size_t sb_bytes(int fmt, size_t rows, size_t K) { return fmt == 2 ? rows * (K / 64) * 4 : fmt == 1 ? rows * (K / 32) * 2 : 0; }
+
+struct LayerW {
+    const float *attn_norm, *q_norm, *k_norm, *mlp_norm;
+    const uint8_t *wqkv, *wqkv_sb, *wo, *wo_sb, *wgu, *wgu_sb, *wd, *wd_sb;
+};
+
+// M-RoPE table (Engine.swift:121-125, 254-298): inv-freq in double, angle = double(float(p) *
+// float(invf)), cos/sin in double rounded to float.
+void mrope_table(int maxctx, int vis_offset, int llm_h, int llm_w, std::vector<float>& out) {
+    double invf[64];
+    for (int i = 0; i < 64; ++i) invf[i] = 1.0 / std::pow(5000000.0, (double)(2 * i) / 128.0);
+    const int n_vis = llm_h * llm_w;
+    const int delta = std::max(llm_h, llm_w) - n_vis;
+    out.resize((size_t)maxctx * 128);
+    for (int slot = 0; slot < maxctx; ++slot) {
+        int pt, ph, pw;
+        if (vis_offset < 0 || slot < vis_offset) {
+            pt = ph = pw = slot;
+        } else if (slot < vis_offset + n_vis) {
+            const int v = slot - vis_offset;
+            pt = vis_offset;
+            ph = vis_offset + v / llm_w;
+            pw = vis_offset + v % llm_w;
+        } else {
+            pt = ph = pw = slot + delta;
+        }
+        for (int i = 0; i < 64; ++i) {
+            // mrope_section [24, 20, 20] interleaved: H at 1:60:3, W at 2:60:3, else T.
+            const int p = (i < 60 && i % 3 == 1) ? ph : (i < 60 && i % 3 == 2) ? pw : pt;
+            const double ang = (double)((float)p * (float)invf[i]);
+            out[(size_t)slot * 128 + 2 * i] = (float)std::cos(ang);
+            out[(size_t)slot * 128 + 2 * i + 1] = (float)std::sin(ang);
+        }
+    }
+}
+
+struct NullState {
+    State* d = nullptr;
+};
+NullState g_null_state;  // control block for standalone kernels (done = 0)
+
+int null_state(State** out, int n) {
+    if (!g_null_state.d) HIPCK(hipMalloc(&g_null_state.d, sizeof(State)));
+    State s{};
+    s.n = n;
+    s.maxctx = 1;
+    HIPCK(hipMemcpy(g_null_state.d, &s, sizeof s, hipMemcpyHostToDevice));
+    *out = g_null_state.d;
+    return 0;
+}
+
+}  // namespace
+
+struct icua_engine {
+    int fmt = 0, layers = 0, maxctx = 0, maxpass = 0, maxsteps = 0;
+    uint32_t flags = 0;
+    int eos0 = 151645, eos1 = 151643;  // Engine.swift:12
+    hipStream_t stream = nullptr;
+    uint8_t* d_weights = nullptr;
+    size_t weight_bytes = 0;
+    const uint8_t *E = nullptr, *Esb = nullptr;
+    const float* final_norm = nullptr;
+    LayerW L[MAX_LAYERS];
+    float *x = nullptr, *qkv = nullptr, *rope = nullptr, *part = nullptr, *pval = nullptr, *logits = nullptr;
+    uint16_t *attn = nullptr, *h = nullptr, *kv = nullptr;
+    int *counters = nullptr, *pidx = nullptr, *out_tokens = nullptr, *prompt = nullptr, *argmax_rows = nullptr;
+    State* st = nullptr;
+    float* pooler = nullptr;
+    float* ds[3] = {nullptr, nullptr, nullptr};
+    bool has_ds = false;
+    int n_vis = 0;
+    hipGraphExec_t graph[2] = {nullptr, nullptr};
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    icua_timing_t timing{};
+    std::vector<int32_t> cached_prefix;
+    int mrope_key[3] = {-999, 0, 0};
+    int last_logits_rows = 0;
+
+    uint16_t* kv_ptr(int l, int kind) const { return kv + ((size_t)l * 2 + kind) * NKV * (size_t)maxctx * HD; }
+
+    int read_state(State& s) {
+        HIPCK(hipMemcpyAsync(&s, st, sizeof s, hipMemcpyDeviceToHost, stream));
+        HIPCK(hipStreamSynchronize(stream));
+        return 0;
+    }
+    int write_state(const State& s) {
+        HIPCK(hipMemcpyAsync(st, &s, sizeof s, hipMemcpyHostToDevice, stream));
+        HIPCK(hipStreamSynchronize(stream));
+        return 0;
+    }
+
+    // encodeLLMLayer for the rows of the current pass (pos / n from the control block).
+    int enqueue_layer(int l, int mt, int row0) {
+        const LayerW& w = L[l];
+        GemvArgs a{};
+        a.st = st;
+        a.m_fixed = 0;
+        // 1. RMSNorm + fused QKV.
+        a.w = w.wqkv;
+        a.sb = w.wqkv_sb;
+        a.N = QKV;
+        a.x = x;
+        a.norm_w = w.attn_norm;
+        a.y = qkv;
+        HIPCK(launch_gemv(fmt, GEMV_QKV, a, mt, stream));
+        // 2. q/k norm + M-RoPE + KV write + causal GQA attention.
+        AttnArgs t{};
+        t.qkv = qkv;
+        t.q_norm = w.q_norm;
+        t.k_norm = w.k_norm;
+        t.rope = rope;
+        t.kc = kv_ptr(l, 0);
+        t.vc = kv_ptr(l, 1);
+        t.part = part;
+        t.counters = counters;
+        t.out = attn;
+        t.st = st;
+        HIPCK(launch_attention(t, mt, stream));
+        // 3. O projection + residual.
+        a.w = w.wo;
+        a.sb = w.wo_sb;
+        a.N = H;
+        a.x = attn;
+        a.norm_w = nullptr;
+        a.y = x;
+        HIPCK(launch_gemv(fmt, GEMV_O, a, mt, stream));
+        // 4. RMSNorm + gate|up + SwiGLU.
+        a.w = w.wgu;
+        a.sb = w.wgu_sb;
+        a.N = GU;
+        a.x = x;
+        a.norm_w = w.mlp_norm;
+        a.h = h;
+        HIPCK(launch_gemv(fmt, GEMV_GU, a, mt, stream));
+        // 5. Down projection + residual (+ DeepStack after layers 0-2 at visual rows).
+        a.w = w.wd;
+        a.sb = w.wd_sb;
+        a.N = H;
+        a.x = h;
+        a.norm_w = nullptr;
+        a.y = x;
+        a.ds = (has_ds && l < 3) ? ds[l] : nullptr;
+        a.ds_row0 = row0;
+        HIPCK(launch_gemv(fmt, GEMV_DOWN, a, mt, stream));
+        return 0;
+    }
+
+    int enqueue_head(int mt, int verify_only) {
+        GemvArgs a{};
+        a.st = st;
+        a.w = E;
+        a.sb = Esb;
+        a.N = VOCAB;
+        a.x = x;
+        a.norm_w = final_norm;
+        a.pval = pval;
+        a.pidx = pidx;
+        a.logits = logits;
+        HIPCK(launch_gemv(fmt, GEMV_LMHEAD, a, mt, stream));
+        CommitArgs c{};
+        c.pval = pval;
+        c.pidx = pidx;
+        c.st = st;
+        c.out_tokens = out_tokens;
+        c.E = E;
+        c.Esb = Esb;
+        c.fmt = fmt;
+        c.x = x;
+        c.argmax_rows = argmax_rows;
+        c.verify_only = verify_only;
+        HIPCK(launch_commit(c, stream));
+        return 0;
+    }
+
+    int enqueue_step(int mt) {
+        for (int l = 0; l < layers; ++l)
+            if (enqueue_layer(l, mt, 0)) return -1;
+        return enqueue_head(mt, 0);
+    }
+
+    int decode_mt() const { return (flags & ICUA_FLAG_GRAMMAR_PAIRS) ? MAXM : 1; }
+
+    int ensure_graph(int mt) {
+        const int gi = mt == 1 ? 0 : 1;
+        if (graph[gi]) return 0;
+        // Eager dry run with done = 1 so every kernel and attribute is set up before capture.
+        State s;
+        if (read_state(s)) return -1;
+        State dry = s;
+        dry.done = 1;
+        if (write_state(dry) || enqueue_step(mt)) return -1;
+        HIPCK(hipStreamSynchronize(stream));
+        if (write_state(s)) return -1;
+        hipGraph_t g;
+        HIPCK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_step(mt);
+        hipError_t e2 = hipStreamEndCapture(stream, &g);
+        if (rc) return rc;
+        HIPCK(e2);
+        HIPCK(hipGraphInstantiate(&graph[gi], g, nullptr, nullptr, 0));
+        HIPCK(hipGraphDestroy(g));
+        return 0;
+    }
+
+    int init_device(const uint8_t* img, size_t len, int max_ctx, int max_pass, int max_steps, uint32_t fl) {
+        if (len < 16384 || len % 16384) return fail("bad model size " + std::to_string(len));
+        const uint32_t* hdr = (const uint32_t*)img;
+        if (hdr[0] != MAGIC) return fail("not an instantcua model");
+        if (hdr[1] != 1) return fail("unsupported version");
+        if (hdr[2] > 2) return fail("unknown weight format");
+        if (hdr[3] != (uint32_t)T_COUNT) return fail("tensor table mismatch");
+        if (max_ctx < 1 || max_ctx > 16384) return fail("max_ctx must be in 1..16384");
+        fmt = (int)hdr[2];
+        maxctx = max_ctx;
+        maxpass = max_pass;
+        maxsteps = max_steps;
+        flags = fl;
+        const uint64_t* tab = (const uint64_t*)(img + 16);
+        // Expected sizes of every decoder tensor; the layer stack ends at the first empty QKV.
+        struct Want {
+            int id;
+            size_t bytes;
+        };
+        std::vector<Want> want = {{T_EMBED, code_bytes(fmt, VOCAB, H)},
+                                  {T_EMBED_SB, sb_bytes(fmt, VOCAB, H)},
+                                  {T_FINAL_NORM, (size_t)H * 4}};
+        layers = 0;
+        while (layers < MAX_LAYERS && tab[2 * (T_LAYER_BASE + layers * T_PER_LAYER + 1) + 1] != 0) layers++;
+        if (layers == 0) return fail("model has no decoder layers");
+        for (int l = 0; l < layers; ++l) {
+            const int b = T_LAYER_BASE + l * T_PER_LAYER;
+            want.push_back({b + 0, (size_t)H * 4});
+            want.push_back({b + 1, code_bytes(fmt, QKV, H)});
+            want.push_back({b + 2, sb_bytes(fmt, QKV, H)});
+            want.push_back({b + 3, (size_t)HD * 4});
+            want.push_back({b + 4, (size_t)HD * 4});
+            want.push_back({b + 5, code_bytes(fmt, H, H)});
+            want.push_back({b + 6, sb_bytes(fmt, H, H)});
+            want.push_back({b + 7, (size_t)H * 4});
+            want.push_back({b + 8, code_bytes(fmt, GU, H)});
+            want.push_back({b + 9, sb_bytes(fmt, GU, H)});
+            want.push_back({b + 10, code_bytes(fmt, H, FF)});
+            want.push_back({b + 11, sb_bytes(fmt, H, FF)});
+        }
+        std::vector<size_t> dev_off(T_COUNT, 0);
+        size_t total = 0;
+        for (const Want& w : want) {
+            const uint64_t off = tab[2 * w.id], sz = tab[2 * w.id + 1];
+            if (sz != w.bytes || off + sz > len)
+                return fail("tensor " + std::to_string(w.id) + ": size " + std::to_string(sz) + ", want " +
+                            std::to_string(w.bytes));
+            total = (total + 255) & ~(size_t)255;
+            dev_off[w.id] = total;
+            total += w.bytes;
+        }
+        weight_bytes = total;
+        HIPCK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+        HIPCK(hipEventCreate(&ev0));
+        HIPCK(hipEventCreate(&ev1));
+        HIPCK(hipMalloc(&d_weights, total));
+        for (const Want& w : want)
+            if (w.bytes) HIPCK(hipMemcpy(d_weights + dev_off[w.id], img + tab[2 * w.id], w.bytes, hipMemcpyHostToDevice));
+        auto P = [&](int id) { return d_weights + dev_off[id]; };
+        E = P(T_EMBED);
+        Esb = P(T_EMBED_SB);
+        final_norm = (const float*)P(T_FINAL_NORM);
+        for (int l = 0; l < layers; ++l) {
+            const int b = T_LAYER_BASE + l * T_PER_LAYER;
+            LayerW& w = L[l];
+            w.attn_norm = (const float*)P(b + 0);
+            w.wqkv = P(b + 1);
+            w.wqkv_sb = P(b + 2);
+            w.q_norm = (const float*)P(b + 3);
+            w.k_norm = (const float*)P(b + 4);
+            w.wo = P(b + 5);
+            w.wo_sb = P(b + 6);
+            w.mlp_norm = (const float*)P(b + 7);
+            w.wgu = P(b + 8);
+            w.wgu_sb = P(b + 9);
+            w.wd = P(b + 10);
+            w.wd_sb = P(b + 11);
+        }
+        HIPCK(hipMalloc(&x, sizeof(float) * MAXM * H));
+        HIPCK(hipMalloc(&qkv, sizeof(float) * MAXM * QKV));
+        HIPCK(hipMalloc(&attn, sizeof(uint16_t) * MAXM * H));
+        HIPCK(hipMalloc(&h, sizeof(uint16_t) * MAXM * FF));
+        const size_t kvn = (size_t)layers * 2 * NKV * maxctx * HD;
+        HIPCK(hipMalloc(&kv, kvn * 2));
+        HIPCK(hipMemset(kv, 0, kvn * 2));
+        HIPCK(hipMalloc(&rope, sizeof(float) * (size_t)maxctx * 128));
+        HIPCK(hipMalloc(&part, sizeof(float) * (size_t)NKV * ATTN_SPLITS * MAXM * 2 * (HD + 2)));
+        HIPCK(hipMalloc(&counters, sizeof(int) * NKV));
+        HIPCK(hipMemset(counters, 0, sizeof(int) * NKV));
+        HIPCK(hipMalloc(&pval, sizeof(float) * MAXM * LMH_WAVES));
+        HIPCK(hipMalloc(&pidx, sizeof(int) * MAXM * LMH_WAVES));
+        HIPCK(hipMalloc(&logits, sizeof(float) * (size_t)MAXM * VOCAB));
+        HIPCK(hipMalloc(&out_tokens, sizeof(int) * (maxsteps + 4)));
+        HIPCK(hipMemset(out_tokens, 0, sizeof(int) * (maxsteps + 4)));
+        HIPCK(hipMalloc(&prompt, sizeof(int) * (size_t)std::max(maxctx, MAXM)));
+        HIPCK(hipMalloc(&argmax_rows, sizeof(int) * MAXM));
+        HIPCK(hipMalloc(&st, sizeof(State)));
+        State s{};
+        s.done = 1;
+        s.n = 1;
+        s.maxctx = maxctx;
+        s.maxsteps = maxsteps;
+        s.eos0 = eos0;
+        s.eos1 = eos1;
+        s.vis_offset = -1;
+        if (write_state(s)) return -1;
+        return prepare_mrope(-1, 1, 1);
+    }
+
+    int prepare_mrope(int vis_offset, int llm_h, int llm_w) {
+        if (vis_offset >= 0 && (llm_h <= 0 || llm_w <= 0)) return fail("bad visual grid");
+        if (mrope_key[0] == vis_offset && mrope_key[1] == llm_h && mrope_key[2] == llm_w) return 0;
+        std::vector<float> tab;
+        mrope_table(maxctx, vis_offset, llm_h, llm_w, tab);
+        HIPCK(hipMemcpy(rope, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
+        mrope_key[0] = vis_offset;
+        mrope_key[1] = llm_h;
+        mrope_key[2] = llm_w;
+        return 0;
+    }
+
+    int prefill(const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new, int write_logits) {
+        if (n <= 0) return fail("empty prompt");
+        if (max_new < 1) max_new = 1;
+        if (start_pos < 0 || start_pos + n + max_new - 1 > maxctx) return fail("prompt exceeds max context");
+        for (int i = 0; i < n; ++i)
+            if (tokens[i] < 0 || tokens[i] >= VOCAB) return fail("token id out of range");
+        if (vis_offset >= n) return fail("vis_offset beyond the prompt");
+        if (vis_offset >= 0 && n_vis <= 0) return fail("visual rows requested but no visual embeddings set");
+        HIPCK(hipMemcpyAsync(prompt, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, stream));
+        State s{};
+        s.pos = start_pos;
+        s.n = std::min(n, MAXM);
+        s.step = 0;
+        s.done = 0;
+        s.maxctx = maxctx;
+        s.maxsteps = std::max(1, std::min(max_new, maxsteps));
+        s.eos0 = eos0;
+        s.eos1 = eos1;
+        s.vis_offset = vis_offset;
+        s.n_vis = vis_offset >= 0 ? n_vis : 0;
+        s.rope_delta = 0;
+        s.flags = (flags & ICUA_FLAG_GRAMMAR_PAIRS) ? STATE_FLAG_GRAMMAR : 0;
+        s.logits_rows = 0;
+        if (write_state(s)) return -1;
+        HIPCK(hipEventRecord(ev0, stream));
+        for (int r0 = 0; r0 < n; r0 += MAXM) {
+            const int m = std::min(MAXM, n - r0);
+            const bool last = (r0 + m == n);
+            HIPCK(launch_set_pass(st, start_pos + r0, m, last && write_logits ? 1 : 0, stream));
+            EmbedArgs ea{};
+            ea.toks = prompt;
+            ea.E = E;
+            ea.Esb = Esb;
+            ea.fmt = fmt;
+            ea.pooler = vis_offset >= 0 ? pooler : nullptr;
+            ea.row0 = r0;
+            ea.x = x;
+            ea.st = st;
+            ea.n = m;
+            HIPCK(launch_embed(ea, stream));
+            for (int l = 0; l < layers; ++l)
+                if (enqueue_layer(l, MAXM, r0)) return -1;
+        }
+        if (enqueue_head(MAXM, 0)) return -1;
+        HIPCK(hipEventRecord(ev1, stream));
+        HIPCK(hipEventSynchronize(ev1));
+        float ms = 0;
+        HIPCK(hipEventElapsedTime(&ms, ev0, ev1));
+        timing.prefill_ms = ms;
+        timing.prefill_tokens = n;
+        last_logits_rows = write_logits ? 1 : 0;
+        return 0;
+    }
+
+    int decode_steps(int k, double* ms_out) {
+        const int mt = decode_mt();
+        if (ensure_graph(mt)) return -1;
+        HIPCK(hipEventRecord(ev0, stream));
+        for (int i = 0; i < k; ++i) HIPCK(hipGraphLaunch(graph[mt == 1 ? 0 : 1], stream));
+        HIPCK(hipEventRecord(ev1, stream));
+        HIPCK(hipEventSynchronize(ev1));
+        float ms = 0;
+        HIPCK(hipEventElapsedTime(&ms, ev0, ev1));
+        if (ms_out) *ms_out = ms;
+        last_logits_rows = 0;
+        return 0;
+    }
+};
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+
+extern "C" {
+
+const char* icua_last_error(void) { return g_err.c_str(); }
+
+int icua_engine_create_from_memory(const void* image, size_t len, int max_ctx, int max_pass, int max_steps,
+                                   uint32_t flags, icua_engine** out) {
+    if (!image || !out) return fail("null argument");
+    icua_engine* e = new icua_engine();
+    if (e->init_device((const uint8_t*)image, len, max_ctx, max_pass, max_steps, flags)) {
+        std::string msg = g_err;
+        icua_engine_destroy(e);
+        g_err = msg;
+        return -1;
+    }
+    *out = e;
+    return 0;
+}
+
+int icua_engine_create(const char* path, int max_ctx, int max_pass, int max_steps, uint32_t flags,
+                       icua_engine** out) {
+    if (!path || !out) return fail("null argument");
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) return fail(std::string("cannot open ") + path);
+    struct stat sb;
+    if (fstat(fd, &sb) != 0) {
+        close(fd);
+        return fail(std::string("cannot stat ") + path);
+    }
+    const size_t size = (size_t)sb.st_size;
+    void* p = mmap(nullptr, size, PROT_READ, MAP_SHARED, fd, 0);
+    close(fd);
+    if (p == MAP_FAILED) return fail(std::string("mmap failed for ") + path);
+    int rc = icua_engine_create_from_memory(p, size, max_ctx, max_pass, max_steps, flags, out);
+    munmap(p, size);
+    return rc;
+}
+
+void icua_engine_destroy(icua_engine* e) {
+    if (!e) return;
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    for (auto& g : e->graph)
+        if (g) (void)hipGraphExecDestroy(g);
+    void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->pval,
+                    e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
+                    e->ds[0], e->ds[1], e->ds[2]};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    if (e->ev0) (void)hipEventDestroy(e->ev0);
+    if (e->ev1) (void)hipEventDestroy(e->ev1);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+}
+
+int icua_engine_info(icua_engine* e, icua_info_t* out) {
+    if (!e || !out) return fail("null argument");
+    out->format = e->fmt;
+    out->layers = e->layers;
+    out->max_context = e->maxctx;
+    out->max_pass = e->maxpass;
+    out->max_steps = e->maxsteps;
+    out->weight_bytes = (int64_t)e->weight_bytes;
+    out->kv_bytes = (int64_t)e->layers * 2 * NKV * e->maxctx * HD * 2;
+    return 0;
+}
+
+int icua_set_eos(icua_engine* e, int32_t eos0, int32_t eos1) {
+    if (!e) return fail("null engine");
+    e->eos0 = eos0;
+    e->eos1 = eos1;
+    return 0;
+}
+
+int icua_set_flags(icua_engine* e, uint32_t flags) {
+    if (!e) return fail("null engine");
+    e->flags = flags;
+    return 0;
+}
+
+int icua_prepare_mrope(icua_engine* e, int vis_offset, int llm_h, int llm_w) {
+    if (!e) return fail("null engine");
+    return e->prepare_mrope(vis_offset, llm_h, llm_w);
+}
+
+int icua_set_visual(icua_engine* e, const float* pooler, const float* const* deepstack, int n_vis) {
+    if (!e || !pooler || n_vis <= 0) return fail("bad visual inputs");
+    if (n_vis > e->maxctx) return fail("too many visual rows");
+    if (n_vis > e->n_vis) {
+        if (e->pooler) (void)hipFree(e->pooler);
+        for (auto& d : e->ds)
+            if (d) {
+                (void)hipFree(d);
+                d = nullptr;
+            }
+        e->pooler = nullptr;
+        HIPCK(hipMalloc(&e->pooler, sizeof(float) * (size_t)n_vis * H));
+        for (auto& d : e->ds) HIPCK(hipMalloc(&d, sizeof(float) * (size_t)n_vis * H));
+    }
+    HIPCK(hipMemcpy(e->pooler, pooler, sizeof(float) * (size_t)n_vis * H, hipMemcpyHostToDevice));
+    e->has_ds = deepstack != nullptr;
+    if (deepstack)
+        for (int i = 0; i < 3; ++i)
+            HIPCK(hipMemcpy(e->ds[i], deepstack[i], sizeof(float) * (size_t)n_vis * H, hipMemcpyHostToDevice));
+    e->n_vis = n_vis;
+    return 0;
+}
+
+int icua_prefill(icua_engine* e, const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new,
+                 int write_logits) {
+    if (!e || !tokens) return fail("null argument");
+    return e->prefill(tokens, n, start_pos, vis_offset, max_new, write_logits);
+}
+
+int icua_decode_steps(icua_engine* e, int k) {
+    if (!e) return fail("null engine");
+    double ms = 0;
+    if (e->decode_steps(k, &ms)) return -1;
+    e->timing.decode_ms = ms;
+    return 0;
+}
+
+int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, int max_new, int32_t* out_tokens,
+                  int* n_out) {
+    if (!e || !tokens || !out_tokens || !n_out) return fail("null argument");
+    const auto t0 = std::chrono::steady_clock::now();
+    // System-prompt KV prefix cache (Engine.swift:719-735).
+    bool hit = false;
+    if ((e->flags & ICUA_FLAG_PREFIX_CACHE) && vis_offset > 0) {
+        std::vector<int32_t> prefix(tokens, tokens + vis_offset);
+        hit = (prefix == e->cached_prefix);
+        e->cached_prefix = prefix;
+    }
+    const int start = hit ? vis_offset : 0;
+    const int active = n - start;
+    const int active_vis = vis_offset >= 0 ? vis_offset - start : -1;
+    max_new = std::max(1, std::min(max_new, e->maxsteps));
+    if (e->prefill(tokens + start, active, start, active_vis, max_new, 0)) return -1;
+    double dec_ms = 0;
+    int submitted = 1;
+    while (submitted < max_new) {  // batches of 8 steps (Engine.swift:771-792)
+        const int count = std::min(8, max_new - submitted);
+        double ms = 0;
+        if (e->decode_steps(count, &ms)) return -1;
+        dec_ms += ms;
+        submitted += count;
+        State s;
+        if (e->read_state(s)) return -1;
+        if (s.done) break;
+    }
+    State s;
+    if (e->read_state(s)) return -1;
+    std::vector<int32_t> toks(std::max(s.step, 1));
+    HIPCK(hipMemcpy(toks.data(), e->out_tokens, sizeof(int32_t) * s.step, hipMemcpyDeviceToHost));
+    int cnt = 0;
+    for (int i = 0; i < s.step; ++i) {
+        if (toks[i] == e->eos0 || toks[i] == e->eos1) break;
+        out_tokens[cnt++] = toks[i];
+    }
+    *n_out = cnt;
+    const auto t1 = std::chrono::steady_clock::now();
+    e->timing.decode_ms = dec_ms;
+    e->timing.total_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    e->timing.generated_tokens = cnt;
+    e->timing.vision_ms = 0;
+    return 0;
+}
+
+int icua_verify(icua_engine* e, const int32_t* draft, int m, int32_t* out_argmax, float* out_logits) {
+    if (!e || !draft || !out_argmax) return fail("null argument");
+    if (m < 1 || m > MAXM) return fail("verify takes 1..8 draft tokens");
+    State s;
+    if (e->read_state(s)) return -1;
+    if (s.pos + m > e->maxctx) return fail("verify exceeds max context");
+    for (int i = 0; i < m; ++i)
+        if (draft[i] < 0 || draft[i] >= VOCAB) return fail("token id out of range");
+    HIPCK(hipMemcpyAsync(e->prompt, draft, sizeof(int32_t) * m, hipMemcpyHostToDevice, e->stream));
+    State v = s;
+    v.n = m;
+    v.done = 0;
+    v.vis_offset = -1;
+    v.logits_rows = m;
+    if (e->write_state(v)) return -1;
+    EmbedArgs ea{};
+    ea.toks = e->prompt;
+    ea.E = e->E;
+    ea.Esb = e->Esb;
+    ea.fmt = e->fmt;
+    ea.row0 = 0;
+    ea.x = e->x;
+    ea.st = e->st;
+    ea.n = m;
+    HIPCK(launch_embed(ea, e->stream));
+    for (int l = 0; l < e->layers; ++l)
+        if (e->enqueue_layer(l, MAXM, 0)) return -1;
+    if (e->enqueue_head(MAXM, 1)) return -1;
+    HIPCK(hipStreamSynchronize(e->stream));
+    HIPCK(hipMemcpy(out_argmax, e->argmax_rows, sizeof(int32_t) * m, hipMemcpyDeviceToHost));
+    if (out_logits)
+        HIPCK(hipMemcpy(out_logits, e->logits, sizeof(float) * (size_t)m * VOCAB, hipMemcpyDeviceToHost));
+    e->last_logits_rows = m;
+    return e->write_state(s);
+}
+
+int icua_set_position(icua_engine* e, int pos, int32_t next_token, int step, int max_steps) {
+    if (!e) return fail("null engine");
+    if (pos < 0 || pos >= e->maxctx) return fail("position out of range");
+    if (next_token < 0 || next_token >= VOCAB) return fail("token out of range");
+    if (step < 0 || step >= std::max(1, std::min(max_steps, e->maxsteps))) return fail("step out of range");
+    State s;
+    if (e->read_state(s)) return -1;
+    s.pos = pos;
+    s.n = 1;
+    s.done = 0;
+    s.step = step;
+    s.maxsteps = std::max(1, std::min(max_steps, e->maxsteps));
+    s.vis_offset = -1;
+    s.logits_rows = 0;
+    s.flags = (e->flags & ICUA_FLAG_GRAMMAR_PAIRS) ? STATE_FLAG_GRAMMAR : 0;
+    if (e->write_state(s)) return -1;
+    HIPCK(hipMemcpy(e->prompt, &next_token, sizeof(int32_t), hipMemcpyHostToDevice));
+    EmbedArgs ea{};
+    ea.toks = e->prompt;
+    ea.E = e->E;
+    ea.Esb = e->Esb;
+    ea.fmt = e->fmt;
+    ea.row0 = 0;
+    ea.x = e->x;
+    ea.st = e->st;
+    ea.n = 1;
+    HIPCK(launch_embed(ea, e->stream));
+    HIPCK(hipStreamSynchronize(e->stream));
+    return 0;
+}
+
+int icua_read_state(icua_engine* e, icua_state_t* out) {
+    if (!e || !out) return fail("null argument");
+    State s;
+    if (e->read_state(s)) return -1;
+    static_assert(sizeof(icua_state_t) <= sizeof(State), "state layout");
+    std::memcpy(out, &s, sizeof(icua_state_t));
+    return 0;
+}
+
+int icua_read_tokens(icua_engine* e, int32_t* dst, int n) {
+    if (!e || !dst) return fail("null argument");
+    if (n < 0 || n > e->maxsteps + 4) return fail("token count out of range");
+    HIPCK(hipMemcpy(dst, e->out_tokens, sizeof(int32_t) * n, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int icua_logits(icua_engine* e, float* dst, int rows) {
+    if (!e || !dst) return fail("null argument");
+    if (rows < 1 || rows > MAXM) return fail("rows out of range");
+    HIPCK(hipMemcpy(dst, e->logits, sizeof(float) * (size_t)rows * VOCAB, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int icua_timing(icua_engine* e, icua_timing_t* out) {
+    if (!e || !out) return fail("null argument");
+    *out = e->timing;
+    return 0;
+}
+
+int icua_layer_step(icua_engine* e, int layer, const float* x_in, int n, int pos, float* x_out) {
+    if (!e || !x_in || !x_out) return fail("null argument");
+    if (layer < 0 || layer >= e->layers) return fail("layer out of range");
+    if (n < 1 || n > MAXM) return fail("layer_step takes 1..8 rows");
+    if (pos < 0 || pos + n > e->maxctx) return fail("slots out of range");
+    State s;
+    if (e->read_state(s)) return -1;
+    State v = s;
+    v.pos = pos;
+    v.n = n;
+    v.done = 0;
+    v.vis_offset = -1;
+    if (e->write_state(v)) return -1;
+    HIPCK(hipMemcpy(e->x, x_in, sizeof(float) * (size_t)n * H, hipMemcpyHostToDevice));
+    if (e->enqueue_layer(layer, n == 1 ? 1 : MAXM, 0)) return -1;
+    HIPCK(hipStreamSynchronize(e->stream));
+    HIPCK(hipMemcpy(x_out, e->x, sizeof(float) * (size_t)n * H, hipMemcpyDeviceToHost));
+    return e->write_state(s);
+}
+
+static int kv_copy(icua_engine* e, int layer, int kind, int slot0, int nslots, void* host, bool to_dev) {
+    if (!e || !host) return fail("null argument");
+    if (layer < 0 || layer >= e->layers || kind < 0 || kind > 1) return fail("bad layer/kind");
+    if (slot0 < 0 || nslots < 0 || slot0 + nslots > e->maxctx) return fail("slots out of range");
+    for (int g = 0; g < NKV; ++g) {
+        uint16_t* dev = e->kv_ptr(layer, kind) + ((size_t)g * e->maxctx + slot0) * HD;
+        uint16_t* hp = (uint16_t*)host + (size_t)g * nslots * HD;
+        const size_t bytes = (size_t)nslots * HD * 2;
+        if (to_dev)
+            HIPCK(hipMemcpy(dev, hp, bytes, hipMemcpyHostToDevice));
+        else
+            HIPCK(hipMemcpy(hp, dev, bytes, hipMemcpyDeviceToHost));
+    }
+    return 0;
+}
+
+int icua_read_kv(icua_engine* e, int layer, int kind, int slot0, int nslots, uint16_t* dst) {
+    return kv_copy(e, layer, kind, slot0, nslots, dst, false);
+}
+
+int icua_write_kv(icua_engine* e, int layer, int kind, int slot0, int nslots, const uint16_t* src) {
+    return kv_copy(e, layer, kind, slot0, nslots, (void*)src, true);
+}
+
+int icua_read_buffer(icua_engine* e, int which, void* dst, size_t bytes) {
+    if (!e || !dst) return fail("null argument");
+    const void* src = nullptr;
+    size_t cap = 0;
+    switch (which) {
+        case ICUA_BUF_X: src = e->x; cap = sizeof(float) * MAXM * H; break;
+        case ICUA_BUF_QKV: src = e->qkv; cap = sizeof(float) * MAXM * QKV; break;
+        case ICUA_BUF_ATTN: src = e->attn; cap = sizeof(uint16_t) * MAXM * H; break;
+        case ICUA_BUF_MLP: src = e->h; cap = sizeof(uint16_t) * MAXM * FF; break;
+        default: return fail("unknown buffer");
+    }
+    if (bytes > cap) return fail("read past the buffer");
+    HIPCK(hipStreamSynchronize(e->stream));
+    HIPCK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int icua_dev_alloc(size_t bytes, void** ptr) {
+    if (!ptr) return fail("null argument");
+    HIPCK(hipMalloc(ptr, bytes));
+    return 0;
+}
+int icua_dev_free(void* ptr) {
+    HIPCK(hipFree(ptr));
+    return 0;
+}
+int icua_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    HIPCK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return 0;
+}
+int icua_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    HIPCK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return 0;
+}
+int icua_device_sync(void) {
+    HIPCK(hipDeviceSynchronize());
+    return 0;
+}
+
+static int gemv_setup(int fmt, int N, int K, int m, GemvArgs& a, GemvOp& op) {
+    if (fmt < 0 || fmt > 2) return fail("bad format");
+    if (K != H && K != FF) return fail("K must be 2048 or 6144");
+    if (N <= 0 || N % 8) return fail("N must be a positive multiple of 8");
+    if (m < 1 || m > MAXM) return fail("m must be 1..8");
+    State* st;
+    if (null_state(&st, m)) return -1;
+    a = GemvArgs{};
+    a.st = st;
+    a.m_fixed = m;
+    a.N = N;
+    op = (K == H) ? GEMV_PLAIN_F16IN : GEMV_PLAIN_F16IN_K6144;
+    const int R = (K == H) ? 8 : 4;
+    const int nblocks = N / R;
+    a.blocks = std::max(1, std::min((nblocks + 3) / 4, 2048));
+    return 0;
+}
+
+int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const void* d_x, int m, float* d_y) {
+    GemvArgs a;
+    GemvOp op;
+    if (gemv_setup(fmt, N, K, m, a, op)) return -1;
+    a.w = (const uint8_t*)d_codes;
+    a.sb = (const uint8_t*)d_sb;
+    a.x = d_x;
+    a.y = d_y;
+    HIPCK(launch_gemv(fmt, op, a, m == 1 ? 1 : MAXM, nullptr));
+    HIPCK(hipDeviceSynchronize());
+    return 0;
+}
+
+int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb, int ncopies, int N, int K,
+                    const void* d_x, float* d_y, int iters, double* avg_us) {
+    if (!d_codes || !d_sb || ncopies < 1 || iters < 1 || !avg_us) return fail("bad arguments");
+    GemvArgs a;
+    GemvOp op;
+    if (gemv_setup(fmt, N, K, 1, a, op)) return -1;
+    a.x = d_x;
+    a.y = d_y;
+    hipEvent_t e0, e1;
+    HIPCK(hipEventCreate(&e0));
+    HIPCK(hipEventCreate(&e1));
+    // warm-up
+    a.w = (const uint8_t*)d_codes[0];
+    a.sb = (const uint8_t*)d_sb[0];
+    HIPCK(launch_gemv(fmt, op, a, 1, nullptr));
+    HIPCK(hipEventRecord(e0, nullptr));
+    for (int i = 0; i < iters; ++i) {
+        a.w = (const uint8_t*)d_codes[i % ncopies];
+        a.sb = (const uint8_t*)d_sb[i % ncopies];
+        HIPCK(launch_gemv(fmt, op, a, 1, nullptr));
+    }
+    HIPCK(hipEventRecord(e1, nullptr));
+    HIPCK(hipEventSynchronize(e1));
+    float ms = 0;
+    HIPCK(hipEventElapsedTime(&ms, e0, e1));
+    *avg_us = (double)ms * 1000.0 / iters;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return 0;
+}
+
+int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out) {
+    if (fmt < 0 || fmt > 2) return fail("bad format");
+    if (K <= 0 || K % 64 || rows < 0 || row0 < 0) return fail("bad shape");
+    HIPCK(launch_dequant(fmt, (const uint8_t*)d_codes, (const uint8_t*)d_sb, K, row0, rows, d_out, nullptr));
+    HIPCK(hipDeviceSynchronize());
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,118 @@
+/* CPU oracle for the Qwen3-VL text-decoder token loop -- TEST INFRASTRUCTURE ONLY.
+ *
+ * This library is the parity checker.  Only tests, the smoke check and the CPU-baseline
+ * leg of the benchmark may load it; the product library never links or calls it.
+ *
+ * It restates the reference decoder math (tools/reference/qwen3vl_ref.py:142-155,
+ * 243-336) over weights dequantised bit-exactly from the reference codecs
+ * (Sources/Engine/Convert.swift:215-270; Shaders.swift:464-476), with the reference
+ * engine's storage rounding points (fp16 GEMV inputs: Shaders.swift:634-669; fp16 KV
+ * cache: Shaders.swift:776-787, 914-921) and the engine's M-RoPE table
+ * (Sources/Engine/Engine.swift:121-125, 254-298).
+ *
+ * Arithmetic contract: every operation is evaluated in double precision and each
+ * intermediate tensor is stored as float32 (round-to-nearest-even), exactly where the
+ * reference engine keeps an fp32 buffer.  fp16 rounding is applied to those float32
+ * values where the engine stores halves.  Dot products accumulate in double and are
+ * therefore exact up to 2^-53 relative: products of an fp32 weight and an fp16
+ * activation are exact in double.
+ *
+ * Results do not depend on the OpenMP thread count: every dot product and every
+ * reduction is computed by one thread in a fixed order.
+ */
+#ifndef ICUA_ORACLE_H
+#define ICUA_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Fixed decoder dimensions (Sources/Engine/ModelFile.swift:47-59). */
+#define OR_H 2048
+#define OR_FF 6144
+#define OR_NH 16
+#define OR_NKV 8
+#define OR_HD 128
+#define OR_QKV 4096
+#define OR_GU 12288
+#define OR_VOCAB 151936
+#define OR_MAXLAYERS 28
+#define OR_IMAGE_PAD 151655
+
+/* fp16 <-> fp32 (IEEE binary16, round to nearest even). */
+float or_h2f(uint16_t h);
+uint16_t or_f2h(float f);
+
+/* Dequantise `rows` rows of a [rows][K] matrix to fp32 (fmt 0 f16, 1 q8, 2 q4).
+ * q4: w = fl32(s * q + b) (Convert.swift:245-262; Shaders.swift:470-475);
+ * q8: w = s * q (Convert.swift:214-233; Shaders.swift:466-468); f16: w = half value. */
+void or_dequant(int fmt, const uint8_t* codes, const uint8_t* sb, int rows, int K, float* out);
+
+/* y[t][r] = sum_k W[r][k] * x[t][k] for t < n tokens; x are fp16 bit patterns [n][K];
+ * double accumulation, float32 result. */
+void or_gemv(int fmt, const uint8_t* codes, const uint8_t* sb, int N, int K,
+             const uint16_t* x, int n, float* y);
+
+/* Engine M-RoPE table rope[slot][64] = (cos, sin) float pairs (Engine.swift:254-298). */
+void or_mrope_table(int maxctx, int vis_offset, int llm_h, int llm_w, float* out);
+
+/* Whole-decoder state over an in-memory .icua image. */
+typedef struct or_model or_model;
+
+or_model* or_model_new(const uint8_t* img, size_t len, int maxctx);
+void or_model_free(or_model* m);
+int or_model_layers(const or_model* m);
+int or_model_format(const or_model* m);
+const char* or_last_error(void);
+
+/* prepareMRoPE (Engine.swift:254-298); vis_offset < 0 means text-only. */
+void or_prepare_mrope(or_model* m, int vis_offset, int llm_h, int llm_w);
+
+/* KV cache of layer l: kind 0 = K, 1 = V; layout [NKV][maxctx][HD] fp16. */
+uint16_t* or_kv(or_model* m, int layer, int kind);
+
+/* Runs decoder layer `l` on n rows of the fp32 residual x[n][H] in place, for tokens at
+ * cache slots pos .. pos+n-1 (causal).  Writes their K/V into the cache. */
+void or_layer(or_model* m, int l, float* x, int n, int pos);
+
+/* Test taps: when set (non-NULL), or_layer copies its raw QKV rows [n][4096], attention output
+ * [n][2048] and SwiGLU output [n][6144] (fp32, before fp16 rounding) into these buffers. */
+void or_debug_taps(float* qkv, float* att, float* act);
+
+/* Token embedding row (Shaders.swift:676-692 text branch) into x[H]. */
+void or_embed(const or_model* m, int tok, float* x);
+
+/* Final RMSNorm + tied lm_head of one residual row: logits[VOCAB]. */
+void or_lm_head(const or_model* m, const float* x, float* logits);
+
+/* One pass of n tokens at slots pos..pos+n-1 (prefill, decode step or verify):
+ *  - token rows are embedded from E; if vis_offset >= 0, rows vis_offset..vis_offset+n_vis-1
+ *    holding IMAGE_PAD take pooler rows (fp32 [n_vis][H]) instead (Shaders.swift:676-692);
+ *  - after layers 0..2 the deepstack[i] rows (fp32 [n_vis][H]) are added to those rows
+ *    (qwen3vl_ref.py:279-283; Shaders.swift:696-707), when deepstack is not NULL;
+ *  - logits_rows = 0: none; 1: last row only; n: every row.  logits: [logits_rows][VOCAB].
+ * Returns 0 on success. */
+int or_pass(or_model* m, const int32_t* toks, int n, int pos, const float* pooler, int vis_offset,
+            int n_vis, const float* const* deepstack, int logits_rows, float* logits);
+
+/* Lowest index of the maximum (np.argmax semantics; Shaders.swift:1476-1488, 1509-1530). */
+int or_argmax(const float* v, int n);
+
+/* Greedy generation: prefill `toks` (n) at slot 0 with the visual inputs as in or_pass,
+ * then decode until `steps` tokens are produced (the first from the prefill).  No EOS
+ * stop.  out_tokens[steps]; margins[steps] (top-1 minus top-2 logit, may be NULL);
+ * out_first_logits[VOCAB] (may be NULL).  Returns 0 on success. */
+int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, int vis_offset,
+                int n_vis, const float* const* deepstack, int steps, int32_t* out_tokens,
+                float* margins, float* out_first_logits);
+
+/* Threads used by the OpenMP regions (0 = library default). */
+void or_set_threads(int n);
+int or_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

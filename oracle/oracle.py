@@ -1,0 +1,210 @@
+"""ctypes bindings of the CPU oracle (oracle/liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests, the smoke check and the CPU-baseline leg of the benchmark import this
+module; the product package never does.  The arithmetic contract is in oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+H, FF, NH, NKV, HD, QKV, GU, VOCAB = 2048, 6144, 16, 8, 128, 4096, 12288, 151936
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the Makefile next to this file."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-B" if force else "all", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.or_h2f.argtypes = [C.c_uint16]
+        L.or_h2f.restype = C.c_float
+        L.or_f2h.argtypes = [C.c_float]
+        L.or_f2h.restype = C.c_uint16
+        L.or_dequant.argtypes = [C.c_int, _u8p, C.c_void_p, C.c_int, C.c_int, _f32p]
+        L.or_gemv.argtypes = [C.c_int, _u8p, C.c_void_p, C.c_int, C.c_int, _u16p, C.c_int, _f32p]
+        L.or_mrope_table.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, _f32p]
+        L.or_model_new.argtypes = [C.c_void_p, C.c_size_t, C.c_int]
+        L.or_model_new.restype = C.c_void_p
+        L.or_model_free.argtypes = [C.c_void_p]
+        L.or_model_layers.argtypes = [C.c_void_p]
+        L.or_model_format.argtypes = [C.c_void_p]
+        L.or_last_error.restype = C.c_char_p
+        L.or_prepare_mrope.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int]
+        L.or_kv.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        L.or_kv.restype = C.POINTER(C.c_uint16)
+        L.or_layer.argtypes = [C.c_void_p, C.c_int, _f32p, C.c_int, C.c_int]
+        L.or_debug_taps.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+        L.or_embed.argtypes = [C.c_void_p, C.c_int, _f32p]
+        L.or_lm_head.argtypes = [C.c_void_p, _f32p, _f32p]
+        L.or_pass.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                              C.c_int, C.c_void_p]
+        L.or_argmax.argtypes = [_f32p, C.c_int]
+        L.or_generate.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
+                                  _i32p, C.c_void_p, C.c_void_p]
+        L.or_set_threads.argtypes = [C.c_int]
+        L.or_get_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def set_threads(n: int) -> None:
+    lib().or_set_threads(n)
+
+
+def get_threads() -> int:
+    return lib().or_get_threads()
+
+
+def h2f(h: int) -> float:
+    return lib().or_h2f(h)
+
+
+def f2h(f: float) -> int:
+    return lib().or_f2h(f)
+
+
+def dequant(fmt: int, codes: np.ndarray, sb: np.ndarray, rows: int, K: int) -> np.ndarray:
+    out = np.empty((rows, K), dtype=np.float32)
+    sb = np.ascontiguousarray(sb, dtype=np.uint8)
+    lib().or_dequant(fmt, np.ascontiguousarray(codes, dtype=np.uint8), _ptr(sb), rows, K, out)
+    return out
+
+
+def gemv(fmt: int, codes: np.ndarray, sb: np.ndarray, N: int, K: int, x_f16: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x_f16, dtype=np.float16).reshape(-1, K)
+    n = x.shape[0]
+    y = np.empty((n, N), dtype=np.float32)
+    sb = np.ascontiguousarray(sb, dtype=np.uint8)
+    lib().or_gemv(fmt, np.ascontiguousarray(codes, dtype=np.uint8), _ptr(sb), N, K, x.view(np.uint16), n, y)
+    return y
+
+
+def mrope_table(maxctx: int, vis_offset: int, llm_h: int, llm_w: int) -> np.ndarray:
+    out = np.empty((maxctx, 64, 2), dtype=np.float32)
+    lib().or_mrope_table(maxctx, vis_offset, llm_h, llm_w, out)
+    return out
+
+
+class OracleModel:
+    """The whole-decoder oracle over an in-memory ``.icua`` image."""
+
+    def __init__(self, image: np.ndarray, maxctx: int):
+        self.image = np.ascontiguousarray(image, dtype=np.uint8)
+        self.maxctx = maxctx
+        h = lib().or_model_new(_ptr(self.image), self.image.nbytes, maxctx)
+        if not h:
+            raise RuntimeError("oracle: " + lib().or_last_error().decode())
+        self.h = h
+        self.layers = lib().or_model_layers(h)
+        self.fmt = lib().or_model_format(h)
+
+    def close(self):
+        if self.h:
+            lib().or_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def prepare_mrope(self, vis_offset: int, llm_h: int, llm_w: int) -> None:
+        lib().or_prepare_mrope(self.h, vis_offset, llm_h, llm_w)
+
+    def kv(self, layer: int, kind: int) -> np.ndarray:
+        """Writable view of the fp16 cache of one layer: [NKV][maxctx][HD] (kind 0 K, 1 V)."""
+        p = lib().or_kv(self.h, layer, kind)
+        arr = np.ctypeslib.as_array(p, shape=(NKV * self.maxctx * HD,))
+        return arr.view(np.float16).reshape(NKV, self.maxctx, HD)
+
+    def layer(self, l: int, x: np.ndarray, pos: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, H).copy()
+        lib().or_layer(self.h, l, x, x.shape[0], pos)
+        return x
+
+    def layer_taps(self, l: int, x: np.ndarray, pos: int):
+        """or_layer with the intermediate taps: (x_out, qkv_raw, attn_out, act)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, H).copy()
+        n = x.shape[0]
+        qkv = np.empty((n, QKV), np.float32)
+        att = np.empty((n, H), np.float32)
+        act = np.empty((n, FF), np.float32)
+        lib().or_debug_taps(qkv.ctypes.data, att.ctypes.data, act.ctypes.data)
+        try:
+            lib().or_layer(self.h, l, x, n, pos)
+        finally:
+            lib().or_debug_taps(None, None, None)
+        return x, qkv, att, act
+
+    def embed(self, tok: int) -> np.ndarray:
+        x = np.empty(H, dtype=np.float32)
+        lib().or_embed(self.h, tok, x)
+        return x
+
+    def lm_head(self, x: np.ndarray) -> np.ndarray:
+        out = np.empty(VOCAB, dtype=np.float32)
+        lib().or_lm_head(self.h, np.ascontiguousarray(x, dtype=np.float32), out)
+        return out
+
+    @staticmethod
+    def _visual(pooler, deepstack):
+        pool = None if pooler is None else np.ascontiguousarray(pooler, dtype=np.float32)
+        ds_keep = None
+        ds_ptr = None
+        if deepstack is not None:
+            ds_keep = [np.ascontiguousarray(d, dtype=np.float32) for d in deepstack]
+            arr = (C.c_void_p * 3)(*[d.ctypes.data for d in ds_keep])
+            ds_ptr = C.cast(arr, C.c_void_p)
+            ds_keep.append(arr)
+        return pool, ds_keep, ds_ptr
+
+    def run_pass(self, toks, pos: int, pooler=None, vis_offset: int = -1, deepstack=None,
+                 logits_rows: int = 1) -> np.ndarray:
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        n = toks.size
+        pool, keep, ds_ptr = self._visual(pooler, deepstack)
+        n_vis = 0 if pool is None else pool.shape[0]
+        out = np.empty((max(logits_rows, 1), VOCAB), dtype=np.float32)
+        rc = lib().or_pass(self.h, toks, n, pos, _ptr(pool), vis_offset, n_vis, ds_ptr, logits_rows,
+                           _ptr(out) if logits_rows else None)
+        if rc:
+            raise RuntimeError("oracle: " + lib().or_last_error().decode())
+        return out[:logits_rows]
+
+    def generate(self, toks, steps: int, pooler=None, vis_offset: int = -1, deepstack=None):
+        """Greedy tokens, top-2 margins and first logits (prefill at slot 0, no EOS stop)."""
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        pool, keep, ds_ptr = self._visual(pooler, deepstack)
+        n_vis = 0 if pool is None else pool.shape[0]
+        out = np.empty(steps, dtype=np.int32)
+        margins = np.empty(steps, dtype=np.float32)
+        first = np.empty(VOCAB, dtype=np.float32)
+        rc = lib().or_generate(self.h, toks, toks.size, _ptr(pool), vis_offset, n_vis, ds_ptr, steps, out,
+                               _ptr(margins), _ptr(first))
+        if rc:
+            raise RuntimeError("oracle: " + lib().or_last_error().decode())
+        return out, margins, first

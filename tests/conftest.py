@@ -1,0 +1,52 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+    config.addinivalue_line("markers", "slow: long-running full-size check")
+
+
+@pytest.fixture(scope="session")
+def oracle_mod():
+    import oracle
+
+    oracle.build()
+    return oracle
+
+
+def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    """max |got - ref| / max |ref| (the logits tolerance metric)."""
+    ref = np.asarray(ref, dtype=np.float64)
+    got = np.asarray(got, dtype=np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def near_tie(logits_margin: float, top1: float) -> bool:
+    """A greedy divergence is a reported near-tie when the oracle's top-1/top-2 margin is
+    below 1e-3 of the top logit."""
+    return logits_margin < 1e-3 * max(abs(top1), 1.0)
+
+
+def compare_greedy(gpu_tokens, ref_tokens, ref_margins, ref_top=None):
+    """Returns (n_identical_prefix, note).  Raises AssertionError on a divergence that is not a
+    near-tie of the oracle."""
+    gpu_tokens = list(gpu_tokens)
+    ref_tokens = list(ref_tokens)
+    n = min(len(gpu_tokens), len(ref_tokens))
+    for i in range(n):
+        if gpu_tokens[i] != ref_tokens[i]:
+            top = 10.0 if ref_top is None else ref_top[i]
+            if near_tie(float(ref_margins[i]), top):
+                return i, f"near-tie at step {i}: oracle margin {ref_margins[i]:.3g}"
+            raise AssertionError(
+                f"greedy divergence at step {i}: gpu {gpu_tokens[i]} oracle {ref_tokens[i]} "
+                f"(oracle top-2 margin {ref_margins[i]:.4g})")
+    return n, "identical"

@@ -1,0 +1,201 @@
+"""GPU parity of the decoder path (layer step, prefill, greedy decode, verify) against the
+oracle on seeded synthetic models, through the C ABI."""
+import numpy as np
+import pytest
+
+from conftest import compare_greedy, rel_err
+from instantcua_amd import synth
+from instantcua_amd.engine import Engine
+from instantcua_amd.modelfile import Dims, WeightFormat
+
+pytestmark = pytest.mark.gpu
+
+NKV, HD = Dims.kv_heads, Dims.head_dim
+
+
+@pytest.fixture(scope="module")
+def q4_small():
+    return synth.build_model_image(WeightFormat.Q4, n_layers=2, tag="q4-small")
+
+
+@pytest.fixture(scope="module")
+def q8_small():
+    return synth.build_model_image(WeightFormat.Q8, n_layers=2, tag="q8-small")
+
+
+def _fp16_close(got, ref):
+    """fp16 cache rows: equal except rare one-ulp rounding-boundary cases."""
+    g = got.astype(np.float16).view(np.int16).astype(np.int32)
+    r = ref.astype(np.float16).view(np.int16).astype(np.int32)
+    d = np.abs(g - r)
+    assert d.max() <= 1, f"max ulp diff {d.max()}"
+    assert (d > 0).mean() < 1e-3, f"ulp-mismatch fraction {(d > 0).mean():.3g}"
+
+
+def test_single_layer_q8_step(oracle_mod):
+    """One q8 decoder layer at cache slot 511 over 511 prior fp16 N(0,1) rows."""
+    img = synth.build_model_image(WeightFormat.Q8, n_layers=1, tag="cfg1")
+    pos = 511
+    kc = synth.fp16_normal((NKV, pos, HD), "cfg1-k")
+    vc = synth.fp16_normal((NKV, pos, HD), "cfg1-v")
+    x = synth.fp16_normal((1, Dims.hidden), "cfg1-x").astype(np.float32)
+
+    om = oracle_mod.OracleModel(img, 1024)
+    om.kv(0, 0)[:, :pos] = kc
+    om.kv(0, 1)[:, :pos] = vc
+    ref = om.layer(0, x, pos)
+    ref_k = om.kv(0, 0)[:, pos].copy()
+    ref_v = om.kv(0, 1)[:, pos].copy()
+
+    with Engine(image=img, max_context=1024) as e:
+        e.write_kv(0, 0, 0, kc)
+        e.write_kv(0, 1, 0, vc)
+        got = e.layer_step(0, x, pos)
+        got_k = e.read_kv(0, 0, pos, 1)[:, 0]
+        got_v = e.read_kv(0, 1, pos, 1)[:, 0]
+        # prior slots untouched
+        assert np.array_equal(e.read_kv(0, 0, 0, pos).view(np.uint16), kc.view(np.uint16))
+    assert rel_err(got, ref) < 1e-4, rel_err(got, ref)
+    _fp16_close(got_k, ref_k)
+    _fp16_close(got_v, ref_v)
+
+
+@pytest.mark.parametrize("n", [1, 5, 8])
+def test_multi_row_layer_q4(oracle_mod, q4_small, n):
+    """A pass of n rows through layer 1 with a causal tail over 37 prior rows."""
+    pos = 37
+    kc = synth.fp16_normal((NKV, pos, HD), "mr-k", n)
+    vc = synth.fp16_normal((NKV, pos, HD), "mr-v", n)
+    x = synth.fp16_normal((n, Dims.hidden), "mr-x", n).astype(np.float32)
+    om = oracle_mod.OracleModel(q4_small, 256)
+    om.kv(1, 0)[:, :pos] = kc
+    om.kv(1, 1)[:, :pos] = vc
+    ref = om.layer(1, x, pos)
+    with Engine(image=q4_small, max_context=256) as e:
+        e.write_kv(1, 0, 0, kc)
+        e.write_kv(1, 1, 0, vc)
+        got = e.layer_step(1, x, pos)
+        gk = e.read_kv(1, 0, pos, n)
+    assert rel_err(got, ref) < 1e-4, rel_err(got, ref)
+    _fp16_close(gk, om.kv(1, 0)[:, pos:pos + n])
+
+
+@pytest.mark.parametrize("fmt_name", ["q4", "q8"])
+def test_greedy_decode_small(oracle_mod, q4_small, q8_small, fmt_name):
+    img = q4_small if fmt_name == "q4" else q8_small
+    toks = synth.random_tokens(21, "greedy-" + fmt_name)
+    steps = 32
+    om = oracle_mod.OracleModel(img, 256)
+    ref_toks, margins, ref_first = om.generate(toks, steps)
+    with Engine(image=img, max_context=256, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        first = e.prefill(toks, max_new=steps, write_logits=True)
+        lg = e.logits(1)[0]
+        e.decode_steps(steps - 1)
+        st = e.state()
+        got = e.tokens(st["step"])
+    assert rel_err(lg, ref_first) < 1e-2
+    assert rel_err(lg, ref_first) < 1e-4, f"first-logit rel err {rel_err(lg, ref_first):.3g}"
+    assert first == ref_toks[0]
+    assert st["step"] == steps and st["done"] == 1
+    n, note = compare_greedy(got, ref_toks, margins, ref_first.max() * np.ones(steps))
+    print(f"{fmt_name}: {n}/{steps} identical ({note})")
+
+
+def test_generate_api_matches_oracle(oracle_mod, q4_small):
+    toks = synth.random_tokens(13, "gen-api")
+    om = oracle_mod.OracleModel(q4_small, 128)
+    ref, margins, first = om.generate(toks, 16)
+    with Engine(image=q4_small, max_context=128, max_steps=64) as e:
+        e.eos = (-1, -1)
+        out = e.generate(toks, max_new_tokens=16)
+        t = e.last_timing
+    assert len(out) == 16
+    compare_greedy(out, ref, margins, first.max() * np.ones(16))
+    assert t["prefill_tokens"] == 13 and t["generated_tokens"] == 16
+
+
+def test_eos_stops_generation(q4_small):
+    toks = synth.random_tokens(9, "eos")
+    with Engine(image=q4_small, max_context=128, max_steps=64) as e:
+        e.eos = (-1, -1)
+        free = e.generate(toks, max_new_tokens=12)
+        stop_tok = free[3]
+        e.eos = (stop_tok, -1)
+        out = e.generate(toks, max_new_tokens=12)
+    k = free.index(stop_tok)
+    assert out == free[:k]
+
+
+def test_visual_prefill_deepstack(oracle_mod, q4_small):
+    """Image-pad rows take visual embeddings, 3D M-RoPE positions, DeepStack after layers 0-2."""
+    vp = synth.visual_prompt(40, vis_offset=5, llm_h=4, llm_w=6, tag="vis")
+    pooler = vp.pooler.astype(np.float32)
+    ds = [d.astype(np.float32) for d in vp.deepstack]
+    steps = 8
+    om = oracle_mod.OracleModel(q4_small, 128)
+    om.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
+    ref, margins, first = om.generate(vp.tokens, steps, pooler=pooler, vis_offset=vp.vis_offset, deepstack=ds)
+    with Engine(image=q4_small, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
+        e.set_visual(pooler, ds)
+        e.prefill(vp.tokens, vis_offset=vp.vis_offset, max_new=steps, write_logits=True)
+        lg = e.logits(1)[0]
+        e.decode_steps(steps - 1)
+        got = e.tokens(steps)
+    assert rel_err(lg, first) < 1e-4, rel_err(lg, first)
+    compare_greedy(got, ref, margins, first.max() * np.ones(steps))
+
+
+def test_verify_eight_drafts(oracle_mod, q4_small):
+    toks = synth.random_tokens(19, "verify")
+    draft = synth.random_tokens(8, "verify-draft")
+    om = oracle_mod.OracleModel(q4_small, 128)
+    om.run_pass(toks, 0, logits_rows=1)
+    ref_lg = om.run_pass(draft, len(toks), logits_rows=8)
+    with Engine(image=q4_small, max_context=128, max_steps=16) as e:
+        e.prefill(toks, max_new=4)
+        st0 = e.state()
+        am, lg = e.verify(draft, want_logits=True)
+        st1 = e.state()
+    assert st0["pos"] == st1["pos"] == len(toks)
+    assert rel_err(lg, ref_lg) < 1e-4, rel_err(lg, ref_lg)
+    ref_am = ref_lg.argmax(axis=1)
+    for i in range(8):
+        if am[i] != ref_am[i]:
+            srt = np.sort(ref_lg[i])
+            assert srt[-1] - srt[-2] < 1e-3 * abs(srt[-1]), f"row {i}: {am[i]} vs {ref_am[i]}"
+
+
+@pytest.mark.parametrize("fmt", [WeightFormat.Q4, WeightFormat.Q8])
+def test_layer_stages(oracle_mod, fmt):
+    """Stage-by-stage parity of one layer pass (3 rows over 29 prior slots): raw QKV rows,
+    attention output, SwiGLU output and the residual."""
+    img = synth.build_model_image(fmt, n_layers=1, tag=f"stages{fmt}")
+    pos, n = 29, 3
+    kc = synth.fp16_normal((NKV, pos, HD), "st-k")
+    vc = synth.fp16_normal((NKV, pos, HD), "st-v")
+    x = synth.fp16_normal((n, Dims.hidden), "st-x").astype(np.float32)
+    om = oracle_mod.OracleModel(img, 64)
+    om.kv(0, 0)[:, :pos] = kc
+    om.kv(0, 1)[:, :pos] = vc
+    ref_x, ref_qkv, ref_att, ref_act = om.layer_taps(0, x, pos)
+    with Engine(image=img, max_context=64) as e:
+        e.write_kv(0, 0, 0, kc)
+        e.write_kv(0, 1, 0, vc)
+        got_x = e.layer_step(0, x, pos)
+        qkv = e.read_buffer("qkv", n)
+        att = e.read_buffer("attn", n).astype(np.float32)
+        act = e.read_buffer("mlp", n).astype(np.float32)
+    errs = {
+        "qkv": rel_err(qkv, ref_qkv),
+        "attn": rel_err(att, ref_att.astype(np.float16).astype(np.float32)),
+        "mlp": rel_err(act, ref_act.astype(np.float16).astype(np.float32)),
+        "x": rel_err(got_x, ref_x),
+    }
+    print(fmt, {k: f"{v:.3g}" for k, v in errs.items()})
+    assert errs["qkv"] < 2e-5
+    assert errs["attn"] < 2e-3  # fp16 outputs: at most ~1 ulp apart
+    assert errs["mlp"] < 2e-3
+    assert errs["x"] < 1e-4
