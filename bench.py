@@ -62,13 +62,14 @@ def gemv_roofline(iters=200):
     m = synth.make_matrix(WeightFormat.Q4, N, K, tag="bench-gemv")
     per = m.codes.nbytes + m.sb.nbytes
     copies = max(2, int(np.ceil(300e6 / per)))
-    codes = [eng.DeviceBuffer.from_array(m.codes) for _ in range(copies)]
-    sbs = [eng.DeviceBuffer.from_array(m.sb) for _ in range(copies)]
-    x = eng.DeviceBuffer.from_array(synth.fp16_normal((1, K), "bench-gemv-x"))
+    src_c = eng.DeviceBuffer.from_array(m.codes)
+    src_s = eng.DeviceBuffer.from_array(m.sb)
+    tiles = [eng.repack(WeightFormat.Q4, src_c, src_s, N, K) for _ in range(copies)]
+    x = eng.DeviceBuffer.from_array(synth.fp16_normal((1, K), "bench-gemv-x").astype(np.float32))
     y = eng.DeviceBuffer(N * 4)
-    us = eng.gemv_bench(WeightFormat.Q4, codes, sbs, N, K, x, y, iters)
-    traffic = per + K * 2 + N * 4
-    for b in codes + sbs + [x, y]:
+    us = eng.gemv_bench(WeightFormat.Q4, [t[0] for t in tiles], [t[1] for t in tiles], N, K, x, y, iters)
+    traffic = per + K * 4 + N * 4
+    for b in [src_c, src_s, x, y] + [b for t in tiles for b in t]:
         b.free()
     return {"kernel": f"q4 GEMV {K}x{N}", "us": us, "bytes": traffic, "copies": copies}
 

@@ -123,9 +123,9 @@ int icua_layer_step(icua_engine* e, int layer, const float* x_in, int n, int pos
 int icua_read_kv(icua_engine* e, int layer, int kind, int slot0, int nslots, uint16_t* dst);
 int icua_write_kv(icua_engine* e, int layer, int kind, int slot0, int nslots, const uint16_t* src);
 
-/* Pass activations of the last layer run (Engine.swift:24 x, qkvBuf, attnh, hbuf): for tests.
- * ICUA_BUF_X fp32 [8][2048]; ICUA_BUF_QKV fp32 [8][4096] raw fused QKV rows; ICUA_BUF_ATTN fp16
- * [8][2048] attention output; ICUA_BUF_MLP fp16 [8][6144] SwiGLU output. */
+/* Pass activations of the last layer run (Engine.swift:24 x, qkvBuf, attn, hbuf): for tests.
+ * ICUA_BUF_X fp32 [8][2048]; ICUA_BUF_QKV fp32 [8][4096] raw fused QKV rows; ICUA_BUF_ATTN fp32
+ * [8][2048] attention output; ICUA_BUF_MLP fp32 [8][6144] SwiGLU output. */
 enum { ICUA_BUF_X = 0, ICUA_BUF_QKV = 1, ICUA_BUF_ATTN = 2, ICUA_BUF_MLP = 3 };
 int icua_read_buffer(icua_engine* e, int which, void* dst, size_t bytes);
 
@@ -136,14 +136,20 @@ int icua_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int icua_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int icua_device_sync(void);
 
-/* y[m][N] = W[N][K] . x[m][K]: W in the .icua codec (codes + scales), x fp16, y fp32;
- * K in {2048, 6144}, N % 8 == 0, m <= 8.  The dot64_row family of Shaders.swift:480-595. */
-int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const void* d_x, int m, float* d_y);
-/* Times `iters` launches of icua_gemv cycling over `ncopies` weight copies; *avg_us per launch. */
+/* Repacks a row-major .icua matrix [N][K] (codes + scales, Convert.swift:157-171) into the
+ * engine's device layout: 16-row matrix-core tiles, same byte count; scales keep their layout.
+ * K in {2048, 6144}, N % 16 == 0. */
+int icua_repack(int fmt, const void* d_codes, const void* d_sb, int N, int K, void* d_tiled_codes, void* d_tiled_sb);
+/* y[m][N] = W[N][K] . x[m][K]: W repacked by icua_repack, x fp32, y fp32; K in {2048, 6144},
+ * N % 16 == 0, m <= 8.  The dot64_row GEMV family of Shaders.swift:480-595. */
+int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const float* d_x, int m, float* d_y);
+/* Times `iters` launches of icua_gemv (m = 1) cycling over `ncopies` weight copies; *avg_us per
+ * launch (HIP events on the launch stream). */
 int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb, int ncopies, int N, int K,
-                    const void* d_x, float* d_y, int iters, double* avg_us);
-/* Bit-exact dequantisation of rows [row0, row0 + rows) to fp32 (Shaders.swift:464-476). */
-int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out);
+                    const float* d_x, float* d_y, int iters, double* avg_us);
+/* Bit-exact dequantisation of rows [row0, row0 + rows) to fp32 (Shaders.swift:464-476), from
+ * the row-major .icua layout (tiled = 0) or the repacked layout (tiled = 1). */
+int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out, int tiled);
 
 #ifdef __cplusplus
 }

@@ -109,7 +109,9 @@ struct icua_engine {
     const float* final_norm = nullptr;
     LayerW L[MAX_LAYERS];
     float *x = nullptr, *qkv = nullptr, *rope = nullptr, *part = nullptr, *pval = nullptr, *logits = nullptr;
-    uint16_t *attn = nullptr, *h = nullptr, *kv = nullptr;
+    float *attn = nullptr, *h = nullptr;
+    uint16_t* kv = nullptr;
+    int splits = 0;
     int *counters = nullptr, *pidx = nullptr, *out_tokens = nullptr, *prompt = nullptr, *argmax_rows = nullptr;
     State* st = nullptr;
     float* pooler = nullptr;
@@ -159,10 +161,9 @@ struct icua_engine {
         t.kc = kv_ptr(l, 0);
         t.vc = kv_ptr(l, 1);
         t.part = part;
-        t.counters = counters;
         t.out = attn;
         t.st = st;
-        HIPCK(launch_attention(t, mt, stream));
+        HIPCK(launch_attention(t, mt, splits, stream));
         // 3. O projection + residual.
         a.w = w.wo;
         a.sb = w.wo_sb;
@@ -305,8 +306,40 @@ struct icua_engine {
         HIPCK(hipEventCreate(&ev0));
         HIPCK(hipEventCreate(&ev1));
         HIPCK(hipMalloc(&d_weights, total));
+        // Matrices are repacked into the GEMV tile layout through a staging buffer; norm vectors
+        // are copied as they are.
+        struct Mat {
+            int codes, sb, rows, K, gu;
+        };
+        std::vector<Mat> mats = {{T_EMBED, T_EMBED_SB, VOCAB, H, 0}};
+        for (int l = 0; l < layers; ++l) {
+            const int b = T_LAYER_BASE + l * T_PER_LAYER;
+            mats.push_back({b + 1, b + 2, QKV, H, 0});
+            mats.push_back({b + 5, b + 6, H, H, 0});
+            mats.push_back({b + 8, b + 9, GU, H, 1});
+            mats.push_back({b + 10, b + 11, H, FF, 0});
+        }
+        std::vector<bool> is_mat(T_COUNT, false);
+        size_t stage_bytes = 0;
+        for (const Mat& m : mats) {
+            is_mat[m.codes] = is_mat[m.sb] = true;
+            stage_bytes = std::max(stage_bytes, code_bytes(fmt, m.rows, m.K) + sb_bytes(fmt, m.rows, m.K) + 256);
+        }
         for (const Want& w : want)
-            if (w.bytes) HIPCK(hipMemcpy(d_weights + dev_off[w.id], img + tab[2 * w.id], w.bytes, hipMemcpyHostToDevice));
+            if (!is_mat[w.id] && w.bytes)
+                HIPCK(hipMemcpy(d_weights + dev_off[w.id], img + tab[2 * w.id], w.bytes, hipMemcpyHostToDevice));
+        uint8_t* staging = nullptr;
+        HIPCK(hipMalloc(&staging, stage_bytes));
+        for (const Mat& m : mats) {
+            const size_t cb = code_bytes(fmt, m.rows, m.K), sbb = sb_bytes(fmt, m.rows, m.K);
+            const size_t sb_off = (cb + 255) & ~(size_t)255;
+            HIPCK(hipMemcpy(staging, img + tab[2 * m.codes], cb, hipMemcpyHostToDevice));
+            if (sbb) HIPCK(hipMemcpy(staging + sb_off, img + tab[2 * m.sb], sbb, hipMemcpyHostToDevice));
+            HIPCK(launch_repack(fmt, staging, staging + sb_off, d_weights + dev_off[m.codes], d_weights + dev_off[m.sb],
+                                m.rows, m.K, m.gu, nullptr));
+            HIPCK(hipDeviceSynchronize());
+        }
+        HIPCK(hipFree(staging));
         auto P = [&](int id) { return d_weights + dev_off[id]; };
         E = P(T_EMBED);
         Esb = P(T_EMBED_SB);
@@ -329,13 +362,14 @@ struct icua_engine {
         }
         HIPCK(hipMalloc(&x, sizeof(float) * MAXM * H));
         HIPCK(hipMalloc(&qkv, sizeof(float) * MAXM * QKV));
-        HIPCK(hipMalloc(&attn, sizeof(uint16_t) * MAXM * H));
-        HIPCK(hipMalloc(&h, sizeof(uint16_t) * MAXM * FF));
+        HIPCK(hipMalloc(&attn, sizeof(float) * MAXM * H));
+        HIPCK(hipMalloc(&h, sizeof(float) * MAXM * FF));
         const size_t kvn = (size_t)layers * 2 * NKV * maxctx * HD;
         HIPCK(hipMalloc(&kv, kvn * 2));
         HIPCK(hipMemset(kv, 0, kvn * 2));
         HIPCK(hipMalloc(&rope, sizeof(float) * (size_t)maxctx * 128));
-        HIPCK(hipMalloc(&part, sizeof(float) * (size_t)NKV * ATTN_SPLITS * MAXM * 2 * (HD + 2)));
+        splits = attention_splits(maxctx);
+        HIPCK(hipMalloc(&part, sizeof(float) * (size_t)NKV * splits * MAXM * 2 * (HD + 2)));
         HIPCK(hipMalloc(&counters, sizeof(int) * NKV));
         HIPCK(hipMemset(counters, 0, sizeof(int) * NKV));
         HIPCK(hipMalloc(&pval, sizeof(float) * MAXM * LMH_WAVES));
@@ -755,8 +789,8 @@ int icua_read_buffer(icua_engine* e, int which, void* dst, size_t bytes) {
     switch (which) {
         case ICUA_BUF_X: src = e->x; cap = sizeof(float) * MAXM * H; break;
         case ICUA_BUF_QKV: src = e->qkv; cap = sizeof(float) * MAXM * QKV; break;
-        case ICUA_BUF_ATTN: src = e->attn; cap = sizeof(uint16_t) * MAXM * H; break;
-        case ICUA_BUF_MLP: src = e->h; cap = sizeof(uint16_t) * MAXM * FF; break;
+        case ICUA_BUF_ATTN: src = e->attn; cap = sizeof(float) * MAXM * H; break;
+        case ICUA_BUF_MLP: src = e->h; cap = sizeof(float) * MAXM * FF; break;
         default: return fail("unknown buffer");
     }
     if (bytes > cap) return fail("read past the buffer");
@@ -790,7 +824,7 @@ int icua_device_sync(void) {
 static int gemv_setup(int fmt, int N, int K, int m, GemvArgs& a, GemvOp& op) {
     if (fmt < 0 || fmt > 2) return fail("bad format");
     if (K != H && K != FF) return fail("K must be 2048 or 6144");
-    if (N <= 0 || N % 8) return fail("N must be a positive multiple of 8");
+    if (N <= 0 || N % 16) return fail("N must be a positive multiple of 16");
     if (m < 1 || m > MAXM) return fail("m must be 1..8");
     State* st;
     if (null_state(&st, m)) return -1;
@@ -798,14 +832,22 @@ static int gemv_setup(int fmt, int N, int K, int m, GemvArgs& a, GemvOp& op) {
     a.st = st;
     a.m_fixed = m;
     a.N = N;
-    op = (K == H) ? GEMV_PLAIN_F16IN : GEMV_PLAIN_F16IN_K6144;
-    const int R = (K == H) ? 8 : 4;
-    const int nblocks = N / R;
-    a.blocks = std::max(1, std::min((nblocks + 3) / 4, 2048));
+    op = (K == H) ? GEMV_PLAIN : GEMV_PLAIN_K6144;
+    a.blocks = std::max(1, std::min(N / 16, 4096));
     return 0;
 }
 
-int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const void* d_x, int m, float* d_y) {
+int icua_repack(int fmt, const void* d_codes, const void* d_sb, int N, int K, void* d_tiled_codes, void* d_tiled_sb) {
+    if (fmt < 0 || fmt > 2) return fail("bad format");
+    if (K != H && K != FF) return fail("K must be 2048 or 6144");
+    if (N <= 0 || N % 16) return fail("N must be a positive multiple of 16");
+    HIPCK(launch_repack(fmt, (const uint8_t*)d_codes, (const uint8_t*)d_sb, (uint8_t*)d_tiled_codes,
+                        (uint8_t*)d_tiled_sb, N, K, 0, nullptr));
+    HIPCK(hipDeviceSynchronize());
+    return 0;
+}
+
+int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const float* d_x, int m, float* d_y) {
     GemvArgs a;
     GemvOp op;
     if (gemv_setup(fmt, N, K, m, a, op)) return -1;
@@ -819,7 +861,7 @@ int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, cons
 }
 
 int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb, int ncopies, int N, int K,
-                    const void* d_x, float* d_y, int iters, double* avg_us) {
+                    const float* d_x, float* d_y, int iters, double* avg_us) {
     if (!d_codes || !d_sb || ncopies < 1 || iters < 1 || !avg_us) return fail("bad arguments");
     GemvArgs a;
     GemvOp op;
@@ -849,10 +891,11 @@ int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb
     return 0;
 }
 
-int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out) {
+int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out, int tiled) {
     if (fmt < 0 || fmt > 2) return fail("bad format");
     if (K <= 0 || K % 64 || rows < 0 || row0 < 0) return fail("bad shape");
-    HIPCK(launch_dequant(fmt, (const uint8_t*)d_codes, (const uint8_t*)d_sb, K, row0, rows, d_out, nullptr));
+    if (tiled && (K % 2048 || (row0 + rows) % 16 != 0)) return fail("tiled dequant takes whole 16-row blocks of K % 2048 == 0");
+    HIPCK(launch_dequant(fmt, (const uint8_t*)d_codes, (const uint8_t*)d_sb, K, row0, rows, d_out, tiled, nullptr));
     HIPCK(hipDeviceSynchronize());
     return 0;
 }

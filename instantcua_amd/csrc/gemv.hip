@@ -1,163 +1,202 @@
-// Group-wise dequant-GEMV for batch-1 decode (and passes of up to MAXM tokens), gfx950.
+// Group-wise dequant-GEMV on the matrix cores, for passes of 1..8 tokens, gfx950.
 //
 // Replaces the reference's dot64_row / reduce8 GEMV family (Shaders.swift:480-631) and the
 // GEMV parts of k_attn_in, k_o_proj, k_mlp_in, k_mlp_out and k_lm_head (Shaders.swift:714-834,
-// 1293-1495).
+// 1293-1495); math per tools/reference/qwen3vl_ref.py (fp32 activations).
 //
-// Mapping.  A weight row is streamed in 1 KiB chunks: lane l of a wave loads bytes
-// [1024 c + 16 l, +16) of chunk c with one 128-bit load, so one wave instruction reads 1 KiB
-// of one row, fully coalesced.  For both q4 (group 64 = 32 bytes) and q8 (group 32 = 32 bytes)
-// that slice lies in group 32 c + l / 2.  A wave keeps R rows in flight, accumulates per-lane
-// partials in fp32 with v_dot2c_f32_f16 on exactly unpacked codes, applies the group scale
-// per lane, and reduces the R rows together with permlane swaps and DPP (reduce_rows).
+// Arithmetic.  y[r] = sum_g sum_{k in g} (s_rg q_rk + b_rg) x_k.  For each group g and token,
+// the fp32 activations are written exactly-rounded as 22-bit integers X_k = rint(x_k 2^(21-e_g))
+// (e_g = exponent of the group's largest |x|) split into three signed bytes (hi, mid, lo).
+// The integer codes q times those bytes go through v_mfma_i32_16x16x64_i8 (q4, group 64) or
+// v_mfma_i32_16x16x32_i8 (q8, group 32): the integer partial sums are exact.  Per group:
+//   S = 65536 C_hi + 256 C_mid + C_lo,  y += (s 2^(e_g-21)) S + b (2^(e_g-21) sum X_k).
+// The only roundings are the 22-bit activation quantisation (<= 2^-22 of the group max) and the
+// fp32 group scaling, i.e. fp32-level accuracy with no fp16 activation rounding.  f16 weights
+// use v_mfma_f32_16x16x32_f16 with the activation split into fp16 hi + lo parts.
 //
-// Activations: the workgroup stages the fp16 GEMV input of every token of the pass in LDS,
-// in a per-format pair order so that a 128-bit LDS read yields the f16x2 operands that match
-// the unpacked code pairs.  The prologue optionally applies RMSNorm (Shaders.swift:634-657):
-// x * rsqrt(mean(x^2) + eps) * w rounded to fp16, exactly the reference rounding point.
+// Operand roles.  A (16 "rows") holds activations: row m = 4 t + slice (t = token of the
+// pass, slice 3 zero); B (16 "columns") holds 16 weight rows.  Lane l of both operands holds
+// row/column l % 16 and K-slot group l / 16; the accumulator lane l holds C[4 (l/16) + i][l % 16],
+// so every lane ends with the three slices of one (token, weight row) pair: no cross-lane
+// reduction is needed.  A pass covers 4 tokens (int8) or 8 tokens (f16, rows hi/lo).
+//
+// Layout (repacked once at load, see repack_*): 16-row blocks; each 1 KiB chunk of a block
+// holds, for lane l, the 16 bytes it feeds to the matrix core (q4: groups 2c and 2c+1, eight
+// bytes each with nibbles ordered so that (v & 0x0F0F0F0F) and (v >> 4 & 0x0F0F0F0F) give the
+// bytes in K order).  One wave load is 1 KiB contiguous.  Scales stay row-major [row][K/G].
+//
+// Work split.  A workgroup owns one 16-row block at a time; its KS waves split the block's
+// chunks and reduce their partial sums through LDS in a fixed order (deterministic).  K is
+// processed in 2048-wide segments so the activation operands of a segment fit in 32 KiB of LDS.
+// Weight loads of a segment are issued before its activation staging, overlapping the
+// RMSNorm / slicing prologue with the HBM latency.
 #include "icua_device.h"
 #include "icua_kernels.h"
 
 namespace icua {
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+constexpr int SEG = 2048;
+
 template <int FMT>
-struct FmtT;
+struct TileT;
 template <>
-struct FmtT<FMT_Q4> {
-    static constexpr int E = 32;    // elements per lane per chunk
-    static constexpr int BLK = 8;   // pair-permutation block
-    static constexpr int XP = 16;   // f16x2 operands per lane per chunk
-    static constexpr int row_bytes(int K) { return K / 2; }
+struct TileT<FMT_Q4> {
+    static constexpr int CHK = 128;  // K per 1 KiB chunk
+    static constexpr int G = 64;     // group size
+    static constexpr int TOK = 4;    // tokens per pass
 };
 template <>
-struct FmtT<FMT_Q8> {
-    static constexpr int E = 16;
-    static constexpr int BLK = 4;
-    static constexpr int XP = 8;
-    static constexpr int row_bytes(int K) { return K; }
+struct TileT<FMT_Q8> {
+    static constexpr int CHK = 64;
+    static constexpr int G = 32;
+    static constexpr int TOK = 4;
 };
 template <>
-struct FmtT<FMT_F16> {
-    static constexpr int E = 8;
-    static constexpr int BLK = 2;
-    static constexpr int XP = 4;
-    static constexpr int row_bytes(int K) { return 2 * K; }
+struct TileT<FMT_F16> {
+    static constexpr int CHK = 32;
+    static constexpr int G = 32;  // K of one MFMA (no scales)
+    static constexpr int TOK = 8;
 };
 
-// Position inside a permutation block where element i of the block is stored.
+// LDS: activation operands of one segment and pass (32 KiB int8 / 64 KiB f16), per-(token,
+// group) factors, per-token RMSNorm scales and the cross-wave partial sums.
 template <int FMT>
-__device__ __forceinline__ int perm_pos(int i) {
-    if constexpr (FMT == FMT_Q4) {
-        // block [x0..x7] stored as [x0 x4 x1 x5 x2 x6 x3 x7]
-        return (i & 3) * 2 + (i >> 2);
-    } else if constexpr (FMT == FMT_Q8) {
-        // block [x0..x3] stored as [x0 x2 x1 x3]
-        return (i & 1) * 2 + (i >> 1);
-    } else {
-        return i;
-    }
-}
+struct Smem {
+    static constexpr int A_BYTES = (FMT == FMT_F16) ? 65536 : 32768;
+    static constexpr int NG = SEG / TileT<FMT>::G;
+    static constexpr int TOK = TileT<FMT>::TOK;
+    static constexpr int bytes(int ks) { return A_BYTES + TOK * NG * 8 + MAXM * 4 + ks * 64 * 2 * 4 + 64; }
+};
 
-// Stage the fp16 GEMV inputs of M rows into LDS (pair order) and the per-lane-slice sums.
+// Stages the activation operands of segment `seg`, tokens [t0, t0 + TOK) of the pass.
 template <int FMT, int K, int PRO>
-__device__ __forceinline__ void stage_inputs(const GemvArgs& a, int M, int row0, uint16_t* xs, float* xsum,
-                                             float* red) {
-    constexpr int E = FmtT<FMT>::E, BLK = FmtT<FMT>::BLK;
-    const int tid = threadIdx.x;
-    const int nthr = blockDim.x;
-    const int wave = tid / WAVE, lane = tid % WAVE;
-    for (int t = 0; t < M; ++t) {
-        float scale = 1.f;
-        const int r = row0 + t;
-        if constexpr (PRO == PRO_NORM) {
-            const float* xr = (const float*)a.x + (size_t)r * K;
-            float ss = 0.f;
-            for (int k = tid; k < K; k += nthr) {
-                float v = xr[k];
-                ss += v * v;
-            }
-            ss = wave_sum(ss);
-            if (lane == 0) red[wave] = ss;
-            __syncthreads();
-            float tot = 0.f;
-            for (int w = 0; w < nthr / WAVE; ++w) tot += red[w];
-            scale = 1.0f / sqrtf(tot / (float)K + EPS);
-            __syncthreads();
-        }
-        for (int k = tid; k < K; k += nthr) {
-            uint16_t hv;
+__device__ __forceinline__ void stage(const GemvArgs& a, int seg, int t0, int M, int row0, uint8_t* Alds, float* fx,
+                                      const float* nscale) {
+    constexpr int TOK = TileT<FMT>::TOK;
+    constexpr int G = TileT<FMT>::G;
+    constexpr int NG = SEG / G;
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    // One unit = 8 consecutive activations of one token; the units of a group sit in adjacent
+    // lanes (G / 8 of them), so the group reductions are DPP steps.
+    for (int u = tid; u < TOK * (SEG / 8); u += nthr) {
+        const int tl = u / (SEG / 8);
+        const int k0 = (u % (SEG / 8)) * 8;  // within the segment
+        const int t = t0 + tl;
+        float v[8];
+        if (t < M) {
+            const float* xr = a.x + (size_t)(row0 + t) * K + seg * SEG + k0;
+            const float4 p0 = ((const float4*)xr)[0], p1 = ((const float4*)xr)[1];
+            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+            v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
             if constexpr (PRO == PRO_NORM) {
-                const float* xr = (const float*)a.x + (size_t)r * K;
-                hv = f2h(xr[k] * scale * a.norm_w[k]);
-            } else if constexpr (PRO == PRO_F32) {
-                hv = f2h(((const float*)a.x)[(size_t)r * K + k]);
-            } else {
-                hv = ((const uint16_t*)a.x)[(size_t)r * K + k];
+                const float sc = nscale[t];
+                const float* w = a.norm_w + seg * SEG + k0;
+                const float4 w0 = ((const float4*)w)[0], w1 = ((const float4*)w)[1];
+                v[0] = v[0] * sc * w0.x; v[1] = v[1] * sc * w0.y; v[2] = v[2] * sc * w0.z; v[3] = v[3] * sc * w0.w;
+                v[4] = v[4] * sc * w1.x; v[5] = v[5] * sc * w1.y; v[6] = v[6] * sc * w1.z; v[7] = v[7] * sc * w1.w;
             }
-            const int blk = k / BLK, i = k % BLK;
-            xs[t * K + blk * BLK + perm_pos<FMT>(i)] = hv;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.f;
+        }
+        if constexpr (FMT == FMT_F16) {
+            // rows m = 2 tl + {hi, lo}; chunk c = k0 / 32, K-slot q = (k0 % 32) / 8.
+            uint32_t hi[8], lo[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const f16 h = (f16)v[i];
+                hi[i] = __builtin_bit_cast(uint16_t, h);
+                lo[i] = __builtin_bit_cast(uint16_t, (f16)(v[i] - (float)h));
+            }
+            const int c = k0 / 32, q = (k0 % 32) / 8;
+            uint4 Hv, Lv;
+            Hv.x = hi[0] | hi[1] << 16; Hv.y = hi[2] | hi[3] << 16; Hv.z = hi[4] | hi[5] << 16; Hv.w = hi[6] | hi[7] << 16;
+            Lv.x = lo[0] | lo[1] << 16; Lv.y = lo[2] | lo[3] << 16; Lv.z = lo[4] | lo[5] << 16; Lv.w = lo[6] | lo[7] << 16;
+            uint4* A = (uint4*)Alds + c * 64;
+            A[(2 * tl) + 16 * q] = Hv;
+            A[(2 * tl + 1) + 16 * q] = Lv;
+        } else {
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+            int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
+            bits = max(bits, dpp_i<DPP_XOR1>(bits));
+            bits = max(bits, dpp_i<DPP_XOR2>(bits));
+            if constexpr (G == 64) bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
+            int e = ((bits >> 23) & 0xFF) - 127;
+            if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
+            const int sh = 21 - e;
+            int X[8];
+            int xs = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                X[i] = (int)rintf(ldexpf(v[i], sh));
+                xs += X[i];
+            }
+            xs += dpp_i<DPP_XOR1>(xs);
+            xs += dpp_i<DPP_XOR2>(xs);
+            if constexpr (G == 64) xs += dpp_i<DPP_HALF_MIRROR>(xs);
+            // Balanced byte slices: X = 65536 hi + 256 mid + lo, each in [-128, 127].
+            uint32_t sl[3][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int x = X[4 * h + i];
+                    const int lo = (int)(int8_t)(x & 0xFF);
+                    const int r1 = (x - lo) >> 8;
+                    const int mid = (int)(int8_t)(r1 & 0xFF);
+                    const int hi = (r1 - mid) >> 8;
+                    p0 |= (uint32_t)(lo & 0xFF) << (8 * i);
+                    p1 |= (uint32_t)(mid & 0xFF) << (8 * i);
+                    p2 |= (uint32_t)(hi & 0xFF) << (8 * i);
+                }
+                sl[0][h] = p0;
+                sl[1][h] = p1;
+                sl[2][h] = p2;
+            }
+            const int gl = k0 / G, kk = k0 % G;
+            if constexpr (FMT == FMT_Q4) {
+                const int q = kk / 16, j0 = kk % 16;  // K-slot (16 K) and byte offset 0 / 8
+                uint8_t* A = Alds + gl * 1024;
+                // rows m = 4 tl + {0 hi, 1 mid, 2 lo, 3 zero}
+                *(uint2*)(A + ((4 * tl + 0) + 16 * q) * 16 + j0) = make_uint2(sl[2][0], sl[2][1]);
+                *(uint2*)(A + ((4 * tl + 1) + 16 * q) * 16 + j0) = make_uint2(sl[1][0], sl[1][1]);
+                *(uint2*)(A + ((4 * tl + 2) + 16 * q) * 16 + j0) = make_uint2(sl[0][0], sl[0][1]);
+                *(uint2*)(A + ((4 * tl + 3) + 16 * q) * 16 + j0) = make_uint2(0u, 0u);
+            } else {
+                const int q = kk / 8;  // K-slot of 8 K
+                uint8_t* A = Alds + gl * 512;
+                *(uint2*)(A + ((4 * tl + 0) + 16 * q) * 8) = make_uint2(sl[2][0], sl[2][1]);
+                *(uint2*)(A + ((4 * tl + 1) + 16 * q) * 8) = make_uint2(sl[1][0], sl[1][1]);
+                *(uint2*)(A + ((4 * tl + 2) + 16 * q) * 8) = make_uint2(sl[0][0], sl[0][1]);
+                *(uint2*)(A + ((4 * tl + 3) + 16 * q) * 8) = make_uint2(0u, 0u);
+            }
+            if (kk == 0) {
+                const float f = ldexpf(1.0f, -sh);
+                fx[(tl * NG + gl) * 2 + 0] = f;
+                fx[(tl * NG + gl) * 2 + 1] = (float)xs * f;
+            }
         }
     }
-    __syncthreads();
-    // Per-lane-slice sums X (slices of E elements).
-    constexpr int NS = K / E;
-    for (int idx = tid; idx < M * NS; idx += nthr) {
-        const int t = idx / NS, s = idx % NS;
-        const uint16_t* p = xs + t * K + s * E;
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < E; ++i) acc += h2f(p[i]);
-        xsum[idx] = acc;
-    }
-    __syncthreads();
 }
 
-// Per-lane partial of one row chunk for one token.
-template <int FMT>
-__device__ __forceinline__ float chunk_partial(const uint4& w, uint32_t sbv, const f16x2* x, float X) {
-    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-    if constexpr (FMT == FMT_Q4) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f16x2 p[4];
-            q4_unpack(d[j], p);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc = dot2(p[i], x[4 * j + i], acc);
-        }
-        const f16x2 sb2 = as_h2(sbv);
-        const float s = (float)sb2.x, b = (float)sb2.y;
-        return (16.f * s) * (acc - X) + b * X;
-    } else if constexpr (FMT == FMT_Q8) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f16x2 p[2];
-            q8_unpack(d[j], p);
-            acc = dot2(p[0], x[2 * j], acc);
-            acc = dot2(p[1], x[2 * j + 1], acc);
-        }
-        const float s = h2f((uint16_t)sbv);
-        return s * (acc - 1152.f * X);
-    } else {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc = dot2(as_h2(d[j]), x[j], acc);
-        return acc;
-    }
-}
-
-template <int FMT, int K, int R, int MT, int PRO, int EPI>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+template <int FMT, int K, int KS, int MT, int PRO, int EPI>
+__global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
     const State* st = a.st;
     if (st->done) return;
-    constexpr int E = FmtT<FMT>::E, XP = FmtT<FMT>::XP;
-    constexpr int RB = FmtT<FMT>::row_bytes(K);
-    constexpr int NCH = RB / 1024;
-    static_assert(RB % 1024 == 0, "row must be a whole number of 1 KiB chunks");
-    constexpr int NS = K / E;
+    using T = TileT<FMT>;
+    constexpr int NSEG = K / SEG;
+    constexpr int CPS = SEG / T::CHK;  // chunks per segment
+    constexpr int CPW = CPS / KS;      // chunks per wave per segment
+    static_assert(CPS % KS == 0, "chunks per segment must split evenly over the waves");
+    constexpr int NG = SEG / T::G;
+    constexpr int NC = K / T::CHK;  // chunks per row block
 
-    // Rows of the input to use: a contiguous run [row0, row0 + M).
     int M, row0;
     if (a.m_fixed > 0) {
         M = a.m_fixed;
@@ -173,38 +212,43 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         }
     }
     if (M > MT) M = MT;
+    const int npass = (M + T::TOK - 1) / T::TOK;
 
     extern __shared__ __align__(16) uint8_t smem[];
-    uint16_t* xs = (uint16_t*)smem;                       // [MT][K] fp16, pair order
-    float* xsum = (float*)(smem + MT * K * 2);            // [MT][NS]
-    float* red = xsum + MT * NS;                          // [8]
-    stage_inputs<FMT, K, PRO>(a, M, row0, xs, xsum, red);
+    uint8_t* Alds = smem;
+    float* fx = (float*)(smem + Smem<FMT>::A_BYTES);
+    float* nscale = fx + T::TOK * NG * 2;
+    float* part = nscale + MAXM;      // [KS][2][64]
+    float* red = part + KS * 2 * 64;  // [16]
 
-    const int lane = threadIdx.x % WAVE;
-    const int wave = threadIdx.x / WAVE;
-    const int waves_per_blk = blockDim.x / WAVE;
-    const int gw = blockIdx.x * waves_per_blk + wave;
-    const int nw = gridDim.x * waves_per_blk;
-    const int nblocks = (EPI == EPI_SWIGLU) ? (FF / (R / 2)) : (a.N / R);
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
 
-    // Single-token fast path keeps its operands in registers for the whole kernel.
-    f16x2 xr[MT == 1 ? NCH * XP : 1];
-    float Xr[MT == 1 ? NCH : 1];
-    if constexpr (MT == 1) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int s = c * WAVE + lane;
-            const uint4* src = (const uint4*)(xs + s * E);
-#pragma unroll
-            for (int q = 0; q < XP / 4; ++q) {
-                uint4 v = src[q];
-                xr[c * XP + 4 * q + 0] = as_h2(v.x);
-                xr[c * XP + 4 * q + 1] = as_h2(v.y);
-                xr[c * XP + 4 * q + 2] = as_h2(v.z);
-                xr[c * XP + 4 * q + 3] = as_h2(v.w);
+    // RMSNorm scale of every token over the full K, once per workgroup.
+    if constexpr (PRO == PRO_NORM) {
+        for (int t = 0; t < M; ++t) {
+            const float* xr = a.x + (size_t)(row0 + t) * K;
+            float ss = 0.f;
+            for (int k = tid; k < K; k += KS * 64) {
+                const float v = xr[k];
+                ss += v * v;
             }
-            Xr[c] = xsum[s];
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave] = ss;
+            __syncthreads();
+            if (tid == 0) {
+                float tot = 0.f;
+                for (int w = 0; w < KS; ++w) tot += red[w];
+                nscale[t] = 1.0f / sqrtf(tot / (float)K + EPS);
+            }
+            __syncthreads();
         }
+    }
+
+    const int nrb = (EPI == EPI_SWIGLU) ? (FF / 8) : (a.N / 16);
+    const bool stage_once = (NSEG == 1) && (npass == 1);
+    if (stage_once) {
+        stage<FMT, K, PRO>(a, 0, 0, M, row0, Alds, fx, nscale);
+        __syncthreads();
     }
 
     float best_v[MT];
@@ -215,123 +259,174 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         best_i[t] = 0x7fffffff;
     }
 
-    for (int blk = gw; blk < nblocks; blk += nw) {
-        int rows[R];
+    const int r16 = lane % 16, lg = lane / 16;
+    for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
+        const int row = rb * 16 + r16;  // tiled row of this lane
+        const uint8_t* wblk = a.w + (size_t)rb * NC * 1024;
+        float acc[2] = {0.f, 0.f};
+        for (int seg = 0; seg < NSEG; ++seg) {
+            // Weights of this wave's chunks, issued before the activation staging.
+            uint4 wv[CPW];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if constexpr (EPI == EPI_SWIGLU)
-                rows[r] = (r < R / 2) ? blk * (R / 2) + r : FF + blk * (R / 2) + (r - R / 2);
-            else
-                rows[r] = blk * R + r;
-        }
-        uint4 w[R][NCH];
-        uint32_t sbv[R][NCH];
+            for (int i = 0; i < CPW; ++i) {
+                const int c = seg * CPS + wave * CPW + i;
+                wv[i] = ((const uint4*)(wblk + (size_t)c * 1024))[lane];
+            }
+            uint2 sbv[CPW];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t* rowp = a.w + (size_t)rows[r] * RB;
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                w[r][c] = ((const uint4*)(rowp + c * 1024))[lane];
+            for (int i = 0; i < CPW; ++i) {
+                const int c = seg * CPS + wave * CPW + i;
                 if constexpr (FMT == FMT_Q4)
-                    sbv[r][c] = ((const uint32_t*)a.sb)[(size_t)rows[r] * (K / 64) + 32 * c + lane / 2];
+                    sbv[i] = *(const uint2*)(a.sb + ((size_t)row * (K / 64) + 2 * c) * 4);
                 else if constexpr (FMT == FMT_Q8)
-                    sbv[r][c] = ((const uint16_t*)a.sb)[(size_t)rows[r] * (K / 32) + 32 * c + lane / 2];
+                    sbv[i] = make_uint2(*(const uint32_t*)(a.sb + ((size_t)row * (K / 32) + 2 * c) * 2), 0u);
                 else
-                    sbv[r][c] = 0;
+                    sbv[i] = make_uint2(0u, 0u);
+            }
+            for (int p = 0; p < npass; ++p) {
+                if (!stage_once) {
+                    __syncthreads();
+                    stage<FMT, K, PRO>(a, seg, p * T::TOK, M, row0, Alds, fx, nscale);
+                    __syncthreads();
+                }
+                float pacc = 0.f, pacc2 = 0.f;
+#pragma unroll
+                for (int i = 0; i < CPW; ++i) {
+                    const int cs = wave * CPW + i;  // chunk within the segment
+                    if constexpr (FMT == FMT_Q4) {
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const uint32_t d0 = hh ? wv[i].z : wv[i].x;
+                            const uint32_t d1 = hh ? wv[i].w : wv[i].y;
+                            v4i B;
+                            B[0] = (int)(d0 & 0x0F0F0F0Fu);
+                            B[1] = (int)((d0 >> 4) & 0x0F0F0F0Fu);
+                            B[2] = (int)(d1 & 0x0F0F0F0Fu);
+                            B[3] = (int)((d1 >> 4) & 0x0F0F0F0Fu);
+                            const int gl = 2 * cs + hh;
+                            const v4i A = *(const v4i*)(Alds + gl * 1024 + lane * 16);
+                            const v4i zero = {0, 0, 0, 0};
+                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero, 0, 0, 0);
+                            const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
+                            const f16x2 sb2 = as_h2(hh ? sbv[i].y : sbv[i].x);
+                            const float f = fx[(lg * NG + gl) * 2], X = fx[(lg * NG + gl) * 2 + 1];
+                            pacc = fmaf((float)sb2.x * f, S, fmaf((float)sb2.y, X, pacc));
+                        }
+                    } else if constexpr (FMT == FMT_Q8) {
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const long B = (long)(hh ? ((uint64_t)wv[i].w << 32 | wv[i].z)
+                                                     : ((uint64_t)wv[i].y << 32 | wv[i].x));
+                            const int gl = 2 * cs + hh;
+                            const long A = *(const long*)(Alds + gl * 512 + lane * 8);
+                            const v4i zero = {0, 0, 0, 0};
+                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+                            const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
+                            const f16x2 s2 = as_h2(sbv[i].x);
+                            const float s = hh ? (float)s2.y : (float)s2.x;
+                            pacc = fmaf(s * fx[(lg * NG + gl) * 2], S, pacc);
+                        }
+                    } else {
+                        const v8h B = __builtin_bit_cast(v8h, wv[i]);
+                        const v8h A = *(const v8h*)(Alds + cs * 1024 + lane * 16);
+                        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                        const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, zero, 0, 0, 0);
+                        pacc += C[0] + C[1];
+                        pacc2 += C[2] + C[3];
+                    }
+                }
+                if constexpr (FMT == FMT_F16) {
+                    acc[0] += pacc;
+                    acc[1] += pacc2;
+                } else {
+                    acc[p] += pacc;  // pass p covers tokens 4 p .. 4 p + 3
+                }
             }
         }
+        // Cross-wave reduction in a fixed order.
+        if constexpr (KS > 1) {
+            part[(wave * 2 + 0) * 64 + lane] = acc[0];
+            part[(wave * 2 + 1) * 64 + lane] = acc[1];
+            __syncthreads();
+            if (wave == 0) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            if (t >= M) break;
-            float part[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) part[r] = 0.f;
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const f16x2* xp;
-                float X;
-                f16x2 xl[MT == 1 ? 1 : XP];
-                if constexpr (MT == 1) {
-                    xp = xr + c * XP;
-                    X = Xr[c];
-                } else {
-                    const int s = c * WAVE + lane;
-                    const uint4* src = (const uint4*)(xs + t * K + s * E);
-#pragma unroll
-                    for (int q = 0; q < XP / 4; ++q) {
-                        uint4 v = src[q];
-                        xl[4 * q + 0] = as_h2(v.x);
-                        xl[4 * q + 1] = as_h2(v.y);
-                        xl[4 * q + 2] = as_h2(v.z);
-                        xl[4 * q + 3] = as_h2(v.w);
-                    }
-                    xp = xl;
-                    X = xsum[t * NS + s];
+                for (int j = 0; j < 2; ++j) {
+                    float s = part[j * 64 + lane];
+                    for (int w = 1; w < KS; ++w) s += part[(w * 2 + j) * 64 + lane];
+                    acc[j] = s;
                 }
-#pragma unroll
-                for (int r = 0; r < R; ++r) part[r] += chunk_partial<FMT>(w[r][c], sbv[r][c], xp, X);
             }
-            const float y = reduce_rows<R>(part, lane);
-            const int r = lane / (WAVE / R);
-            const bool writer = (lane % (WAVE / R)) == 0;
-            const int tok = row0 + t;
-            if constexpr (EPI == EPI_STORE) {
-                if (writer) a.y[(size_t)tok * a.N + rows[r]] = y;
-            } else if constexpr (EPI == EPI_RESID) {
-                if (writer) {
-                    float* xo = a.y + (size_t)tok * a.N + rows[r];
-                    float v = *xo + y;
-                    if (a.ds) {  // DeepStack residual of a visual row (Shaders.swift:696-707)
-                        const int vrow = a.ds_row0 + tok - st->vis_offset;
-                        if (st->vis_offset >= 0 && vrow >= 0 && vrow < st->n_vis)
-                            v = v + a.ds[(size_t)vrow * H + rows[r]];
+            __syncthreads();
+        }
+        if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                // int8 formats: acc[j] is token 4 j + lg; f16: token 2 lg + j.
+                const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
+                const bool valid = t < M;
+                const float y = acc[j];
+                if constexpr (EPI == EPI_STORE) {
+                    if (valid) a.y[(size_t)(row0 + t) * a.N + row] = y;
+                } else if constexpr (EPI == EPI_RESID) {
+                    if (valid) {
+                        float* xo = a.y + (size_t)(row0 + t) * a.N + row;
+                        float v = *xo + y;
+                        if (a.ds) {  // DeepStack residual of a visual row (Shaders.swift:696-707)
+                            const int vrow = a.ds_row0 + t - st->vis_offset;
+                            if (st->vis_offset >= 0 && vrow >= 0 && vrow < st->n_vis)
+                                v = v + a.ds[(size_t)vrow * H + row];
+                        }
+                        *xo = v;
                     }
-                    *xo = v;
+                } else if constexpr (EPI == EPI_SWIGLU) {
+                    // Block rb: gate units 8 rb .. 8 rb + 7 in columns 0-7, matching up rows in 8-15.
+                    const float up = __shfl_xor(y, 8);
+                    if (valid && r16 < 8) {
+                        const float g = y;
+                        a.h[(size_t)(row0 + t) * FF + rb * 8 + r16] = (g / (1.f + expf(-g))) * up;
+                    }
+                } else {  // EPI_ARGMAX: tiled rows are the vocabulary ids
+                    if (valid) {
+                        if (a.logits && st->logits_rows > 0) a.logits[(size_t)t * VOCAB + row] = y;
+#pragma unroll
+                        for (int tt = 0; tt < MT; ++tt)
+                            if (tt == t) argmax_merge(best_v[tt], best_i[tt], y, row);
+                    }
                 }
-            } else if constexpr (EPI == EPI_SWIGLU) {
-                const float up = __shfl_xor(y, 32);  // row r + R/2 sits 32 lanes up
-                if (writer && r < R / 2) {
-                    const float g = y;
-                    const float act = (g / (1.f + expf(-g))) * up;
-                    a.h[(size_t)tok * FF + rows[r]] = f2h(act);
-                }
-            } else {  // EPI_ARGMAX
-                if (writer && a.logits && st->logits_rows > 0)  // single-row mode writes logits row 0
-                    a.logits[(size_t)(tok - row0) * VOCAB + rows[r]] = y;
-                argmax_merge(best_v[t], best_i[t], y, rows[r]);
             }
         }
     }
     if constexpr (EPI == EPI_ARGMAX) {
+        if (wave == 0) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            if (t >= M) break;
-            float v = best_v[t];
-            int i = best_i[t];
-            wave_argmax(v, i);
-            if (lane == 0) {
-                a.pval[(size_t)(row0 + t) * LMH_WAVES + gw] = v;
-                a.pidx[(size_t)(row0 + t) * LMH_WAVES + gw] = i;
+            for (int t = 0; t < MT; ++t) {
+                if (t >= M) break;
+                float v = best_v[t];
+                int i = best_i[t];
+                wave_argmax(v, i);
+                if (lane == 0) {
+                    a.pval[(size_t)(row0 + t) * LMH_WAVES + blockIdx.x] = v;
+                    a.pidx[(size_t)(row0 + t) * LMH_WAVES + blockIdx.x] = i;
+                }
             }
         }
     }
 }
 
-template <int FMT, int K, int R, int MT, int PRO, int EPI>
+template <int FMT, int K, int KS, int MT, int PRO, int EPI>
 static hipError_t launch_one(const GemvArgs& a, int blocks, hipStream_t s) {
-    constexpr int E = FmtT<FMT>::E;
-    size_t lds = (size_t)MT * K * 2 + (size_t)MT * (K / E) * 4 + 64;
-    auto kern = gemv_kernel<FMT, K, R, MT, PRO, EPI>;
+    const size_t lds = Smem<FMT>::bytes(KS);
+    auto kern = gemv_kernel<FMT, K, KS, MT, PRO, EPI>;
     static bool attr_set = false;
     if (!attr_set) {
-        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(KS * 64), lds, s, a);
     return hipGetLastError();
 }
 
-// Dispatch on (format, op).  `mt` selects the single-token (1) or multi-token (MAXM) kernel.
 template <int FMT>
 static hipError_t gemv_fmt(GemvOp op, const GemvArgs& a, int mt, hipStream_t s) {
     const bool one = (mt == 1);
@@ -339,24 +434,24 @@ static hipError_t gemv_fmt(GemvOp op, const GemvArgs& a, int mt, hipStream_t s) 
         case GEMV_QKV:  // RMSNorm -> fused QKV rows, fp32 out
             return one ? launch_one<FMT, H, 4, 1, PRO_NORM, EPI_STORE>(a, QKV / 16, s)
                        : launch_one<FMT, H, 4, MAXM, PRO_NORM, EPI_STORE>(a, QKV / 16, s);
-        case GEMV_O:  // fp16 attention output -> O rows, residual add
-            return one ? launch_one<FMT, H, 4, 1, PRO_F16, EPI_RESID>(a, H / 16, s)
-                       : launch_one<FMT, H, 4, MAXM, PRO_F16, EPI_RESID>(a, H / 16, s);
-        case GEMV_GU:  // RMSNorm -> gate|up pairs -> SwiGLU, fp16 out
-            return one ? launch_one<FMT, H, 8, 1, PRO_NORM, EPI_SWIGLU>(a, FF / 16, s)
-                       : launch_one<FMT, H, 8, MAXM, PRO_NORM, EPI_SWIGLU>(a, FF / 16, s);
-        case GEMV_DOWN:  // fp16 SwiGLU output -> down rows, residual add
-            return one ? launch_one<FMT, FF, 4, 1, PRO_F16, EPI_RESID>(a, H / 16, s)
-                       : launch_one<FMT, FF, 4, MAXM, PRO_F16, EPI_RESID>(a, H / 16, s);
+        case GEMV_O:  // attention output -> O rows, residual add
+            return one ? launch_one<FMT, H, 4, 1, PRO_F32, EPI_RESID>(a, H / 16, s)
+                       : launch_one<FMT, H, 4, MAXM, PRO_F32, EPI_RESID>(a, H / 16, s);
+        case GEMV_GU:  // RMSNorm -> gate|up pairs -> SwiGLU
+            return one ? launch_one<FMT, H, 4, 1, PRO_NORM, EPI_SWIGLU>(a, FF / 8, s)
+                       : launch_one<FMT, H, 4, MAXM, PRO_NORM, EPI_SWIGLU>(a, FF / 8, s);
+        case GEMV_DOWN:  // SwiGLU output -> down rows, residual add
+            return one ? launch_one<FMT, FF, 4, 1, PRO_F32, EPI_RESID>(a, H / 16, s)
+                       : launch_one<FMT, FF, 4, MAXM, PRO_F32, EPI_RESID>(a, H / 16, s);
         case GEMV_LMHEAD:  // final RMSNorm -> tied embedding rows -> argmax partials
-            return one ? launch_one<FMT, H, 8, 1, PRO_NORM, EPI_ARGMAX>(a, LMH_WAVES / 4, s)
-                       : launch_one<FMT, H, 8, MAXM, PRO_NORM, EPI_ARGMAX>(a, LMH_WAVES / 4, s);
-        case GEMV_PLAIN_F16IN:  // isolated GEMV: fp16 x in, fp32 y out
-            return one ? launch_one<FMT, H, 8, 1, PRO_F16, EPI_STORE>(a, a.blocks, s)
-                       : launch_one<FMT, H, 8, MAXM, PRO_F16, EPI_STORE>(a, a.blocks, s);
-        case GEMV_PLAIN_F16IN_K6144:
-            return one ? launch_one<FMT, FF, 4, 1, PRO_F16, EPI_STORE>(a, a.blocks, s)
-                       : launch_one<FMT, FF, 4, MAXM, PRO_F16, EPI_STORE>(a, a.blocks, s);
+            return one ? launch_one<FMT, H, 4, 1, PRO_NORM, EPI_ARGMAX>(a, LMH_WAVES, s)
+                       : launch_one<FMT, H, 4, MAXM, PRO_NORM, EPI_ARGMAX>(a, LMH_WAVES, s);
+        case GEMV_PLAIN:  // isolated GEMV, K = 2048
+            return one ? launch_one<FMT, H, 4, 1, PRO_F32, EPI_STORE>(a, a.blocks, s)
+                       : launch_one<FMT, H, 4, MAXM, PRO_F32, EPI_STORE>(a, a.blocks, s);
+        case GEMV_PLAIN_K6144:
+            return one ? launch_one<FMT, FF, 4, 1, PRO_F32, EPI_STORE>(a, a.blocks, s)
+                       : launch_one<FMT, FF, 4, MAXM, PRO_F32, EPI_STORE>(a, a.blocks, s);
     }
     return hipErrorInvalidValue;
 }
@@ -371,6 +466,86 @@ hipError_t launch_gemv(int fmt, GemvOp op, const GemvArgs& a, int mt, hipStream_
             return gemv_fmt<FMT_F16>(op, a, mt, s);
     }
     return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------------------------------
+// Repacking from the .icua row-major layout (Convert.swift:157-171) into 16-row MFMA tiles.
+
+// Source row of a tiled row: identity, or for the fused gate|up matrix the interleave that puts
+// gate units 8 rb .. 8 rb + 7 and their up rows into tiled block rb.
+__device__ __forceinline__ int src_row(int trow, int gu_interleave) {
+    if (!gu_interleave) return trow;
+    const int rb = trow / 16, r = trow % 16;
+    return r < 8 ? rb * 8 + r : FF + rb * 8 + (r - 8);
+}
+
+__global__ void repack_codes_kernel(int fmt, const uint8_t* src, uint8_t* dst, int N, int K, int gu) {
+    const int chk = fmt == FMT_Q4 ? 128 : fmt == FMT_Q8 ? 64 : 32;
+    const int nc = K / chk;
+    const size_t total = (size_t)(N / 16) * nc * 64;  // one thread per 16-byte lane slice
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int l = (int)(idx % 64);
+        const size_t bc = idx / 64;
+        const int c = (int)(bc % nc);
+        const int rb = (int)(bc / nc);
+        const int r = l % 16, q = l / 16;
+        const int srow = src_row(rb * 16 + r, gu);
+        uint8_t out[16];
+        if (fmt == FMT_Q4) {
+            const uint8_t* rowp = src + (size_t)srow * (K / 2);
+            for (int hh = 0; hh < 2; ++hh) {
+                const int kbase = (2 * c + hh) * 64 + 16 * q;  // the 16 K of this slot
+                for (int d = 0; d < 2; ++d)
+                    for (int b = 0; b < 4; ++b) {
+                        const int klo = kbase + 8 * d + b, khi = klo + 4;
+                        const uint8_t vlo = (rowp[klo / 2] >> (4 * (klo & 1))) & 15;
+                        const uint8_t vhi = (rowp[khi / 2] >> (4 * (khi & 1))) & 15;
+                        out[8 * hh + 4 * d + b] = (uint8_t)(vlo | (vhi << 4));
+                    }
+            }
+        } else if (fmt == FMT_Q8) {
+            const uint8_t* rowp = src + (size_t)srow * K;
+            for (int hh = 0; hh < 2; ++hh)
+                for (int j = 0; j < 8; ++j) out[8 * hh + j] = rowp[(2 * c + hh) * 32 + 8 * q + j];
+        } else {
+            const uint16_t* rowp = (const uint16_t*)src + (size_t)srow * K;
+            for (int j = 0; j < 8; ++j) {
+                const uint16_t v = rowp[c * 32 + 8 * q + j];
+                out[2 * j] = (uint8_t)(v & 0xFF);
+                out[2 * j + 1] = (uint8_t)(v >> 8);
+            }
+        }
+        uint4 o;
+        o.x = out[0] | out[1] << 8 | out[2] << 16 | (uint32_t)out[3] << 24;
+        o.y = out[4] | out[5] << 8 | out[6] << 16 | (uint32_t)out[7] << 24;
+        o.z = out[8] | out[9] << 8 | out[10] << 16 | (uint32_t)out[11] << 24;
+        o.w = out[12] | out[13] << 8 | out[14] << 16 | (uint32_t)out[15] << 24;
+        ((uint4*)dst)[idx] = o;
+    }
+}
+
+__global__ void repack_rows_kernel(const uint8_t* src, uint8_t* dst, int N, int row_bytes, int gu) {
+    const size_t total = (size_t)N * row_bytes;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int trow = (int)(i / row_bytes);
+        const int b = (int)(i % row_bytes);
+        dst[i] = src[(size_t)src_row(trow, gu) * row_bytes + b];
+    }
+}
+
+hipError_t launch_repack(int fmt, const uint8_t* codes, const uint8_t* sb, uint8_t* dcodes, uint8_t* dsb, int N, int K,
+                         int gu_interleave, hipStream_t s) {
+    if (N % 16 || K % SEG || (gu_interleave && N != GU)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(repack_codes_kernel, dim3(2048), dim3(256), 0, s, fmt, codes, dcodes, N, K, gu_interleave);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (fmt != FMT_F16) {
+        const int rbytes = fmt == FMT_Q4 ? (K / 64) * 4 : (K / 32) * 2;
+        hipLaunchKernelGGL(repack_rows_kernel, dim3(2048), dim3(256), 0, s, sb, dsb, N, rbytes, gu_interleave);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 }  // namespace icua

@@ -15,18 +15,18 @@ enum GemvOp {
     GEMV_GU = 2,
     GEMV_DOWN = 3,
     GEMV_LMHEAD = 4,
-    GEMV_PLAIN_F16IN = 5,        // K = 2048, fp16 x -> fp32 y
-    GEMV_PLAIN_F16IN_K6144 = 6,  // K = 6144, fp16 x -> fp32 y
+    GEMV_PLAIN = 5,        // K = 2048, fp32 x -> fp32 y
+    GEMV_PLAIN_K6144 = 6,  // K = 6144, fp32 x -> fp32 y
 };
 
 struct GemvArgs {
-    const uint8_t* w;       // codes [N][row bytes]
-    const uint8_t* sb;      // q4: half2 (scale, bias) [N][K/64]; q8: half [N][K/32]
+    const uint8_t* w;       // codes in 16-row MFMA tiles (launch_repack)
+    const uint8_t* sb;      // q4: half2 (scale, bias) [N][K/64]; q8: half [N][K/32] (tiled row order)
     int N;                  // output rows
-    const void* x;          // PRO_NORM/PRO_F32: fp32 [M][K]; PRO_F16: fp16 [M][K]
+    const float* x;         // fp32 activations [M][K]
     const float* norm_w;    // PRO_NORM weights [K]
     float* y;               // EPI_STORE: y [M][N]; EPI_RESID: residual x [M][N] (+=)
-    uint16_t* h;            // EPI_SWIGLU: fp16 [M][FF]
+    float* h;               // EPI_SWIGLU: [M][FF]
     const float* ds;        // EPI_RESID: DeepStack rows [n_vis][H] or null
     int ds_row0;            // prompt row of pass row 0 (DeepStack visual-row lookup)
     float* pval;            // EPI_ARGMAX partials [MAXM][LMH_WAVES]
@@ -39,6 +39,12 @@ struct GemvArgs {
 
 hipError_t launch_gemv(int fmt, GemvOp op, const GemvArgs& a, int mt, hipStream_t s);
 
+// Repacks a row-major .icua matrix (codes + scales) into the GEMV tile layout.  gu_interleave
+// reorders the fused gate|up rows so that tiled block b holds gate units 8b..8b+7 and then the
+// matching up rows.  N % 16 == 0, K % 2048 == 0.
+hipError_t launch_repack(int fmt, const uint8_t* codes, const uint8_t* sb, uint8_t* dcodes, uint8_t* dsb, int N, int K,
+                         int gu_interleave, hipStream_t s);
+
 struct AttnArgs {
     const float* qkv;       // raw fused QKV rows [M][QKV] fp32
     const float* q_norm;    // [HD]
@@ -46,20 +52,21 @@ struct AttnArgs {
     const float* rope;      // [maxctx][64] (cos, sin)
     uint16_t* kc;           // this layer's K cache [NKV][maxctx][HD] fp16
     uint16_t* vc;           // this layer's V cache
-    float* part;            // split partials [NKV][ATTN_SPLITS][MAXM][2][HD + 2]
-    int* counters;          // [NKV] arrival counters, zero between launches
-    uint16_t* out;          // attention output fp16 [M][H]
+    float* part;            // split partials [NKV][splits][MAXM][2][HD + 2]
+    float* out;             // attention output fp32 [M][H]
     const State* st;
     int m_fixed;
 };
-hipError_t launch_attention(const AttnArgs& a, int mt, hipStream_t s);
+// Grid width for a cache of maxctx slots (64-slot splits + the tail split).
+int attention_splits(int maxctx);
+hipError_t launch_attention(const AttnArgs& a, int mt, int splits, hipStream_t s);
 
 struct CommitArgs {
     const float* pval;
     const int* pidx;
     State* st;
     int* out_tokens;
-    const uint8_t* E;       // embedding codes
+    const uint8_t* E;       // embedding codes (tiled layout)
     const uint8_t* Esb;
     int fmt;
     float* x;               // residual rows to receive the next token embedding(s)
@@ -84,8 +91,9 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 // Sets pos / n / logits_rows of the control block on the stream.
 hipError_t launch_set_pass(State* st, int pos, int n, int logits_rows, hipStream_t s);
 
-// Bit-exact dequantisation of rows [row0, row0 + rows) to fp32 (w = s*q + b / s*q / half).
+// Bit-exact dequantisation of rows [row0, row0 + rows) to fp32 (w = s*q + b / s*q / half),
+// from the row-major .icua layout (tiled = 0) or the GEMV tile layout (tiled = 1).
 hipError_t launch_dequant(int fmt, const uint8_t* w, const uint8_t* sb, int K, int row0, int rows, float* out,
-                          hipStream_t s);
+                          int tiled, hipStream_t s);
 
 }  // namespace icua

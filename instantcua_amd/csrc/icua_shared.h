@@ -19,10 +19,8 @@ constexpr float EPS = 1e-6f;          // Shaders.swift:36
 
 // Tokens one pass of the GEMV path carries (decode n = 1, grammar pairs n = 2, verify n <= 8).
 constexpr int MAXM = 8;
-// Key splits per KV group in decode attention (flash-decoding partials).
-constexpr int ATTN_SPLITS = 64;
-// Waves that produce lm_head argmax partials.
-constexpr int LMH_WAVES = 2048;
+// Workgroups that produce lm_head argmax partials.
+constexpr int LMH_WAVES = 1024;
 
 enum WeightFormat { FMT_F16 = 0, FMT_Q8 = 1, FMT_Q4 = 2 };
 

@@ -4,8 +4,10 @@
 
 namespace icua {
 
-// One embedding element (Shaders.swift:464-476 embed_at): q4 s*q + b, q8 s*q, f16 half.
-__device__ __forceinline__ float embed_at(int fmt, const uint8_t* E, const uint8_t* Esb, size_t row, int i, int K) {
+// One dequantised element (Shaders.swift:464-476 embed_at): q4 s*q + b, q8 s*q, f16 half;
+// row-major .icua layout.
+__device__ __forceinline__ float dequant_rowmajor(int fmt, const uint8_t* E, const uint8_t* Esb, size_t row, int i,
+                                                  int K) {
     if (fmt == FMT_Q4) {
         const uint8_t b = E[row * (K / 2) + (i >> 1)];
         const float q = (float)((i & 1) ? (b >> 4) : (b & 15));
@@ -16,6 +18,27 @@ __device__ __forceinline__ float embed_at(int fmt, const uint8_t* E, const uint8
         return s * (float)(int8_t)E[row * K + i];
     }
     return h2f(((const uint16_t*)E)[row * K + i]);
+}
+
+// The same element read from the GEMV tile layout (gemv.hip repack_codes_kernel): lane
+// l = r + 16 q of chunk c holds 16 bytes; scales stay row-major.
+__device__ __forceinline__ float dequant_tiled(int fmt, const uint8_t* E, const uint8_t* Esb, size_t row, int k, int K) {
+    const size_t rb = row / 16;
+    const int r = (int)(row % 16);
+    if (fmt == FMT_Q4) {
+        const int nc = K / 128, c = k / 128, h = (k % 128) / 64, kk = k % 64, q = kk / 16, j = kk % 16;
+        const int d = j / 8, jj = j % 8;
+        const uint8_t b = E[((rb * nc + c) * 64 + r + 16 * q) * 16 + 8 * h + 4 * d + (jj % 4)];
+        const float qv = (float)((jj / 4) ? (b >> 4) : (b & 15));
+        const f16x2 sb = as_h2(((const uint32_t*)Esb)[row * (K / 64) + k / 64]);
+        return (float)sb.x * qv + (float)sb.y;
+    } else if (fmt == FMT_Q8) {
+        const int nc = K / 64, c = k / 64, h = (k % 64) / 32, q = (k % 32) / 8, j = k % 8;
+        const float s = h2f(((const uint16_t*)Esb)[row * (K / 32) + k / 32]);
+        return s * (float)(int8_t)E[((rb * nc + c) * 64 + r + 16 * q) * 16 + 8 * h + j];
+    }
+    const int nc = K / 32, c = k / 32, q = (k % 32) / 8, j = k % 8;
+    return h2f(((const uint16_t*)E)[((rb * nc + c) * 64 + r + 16 * q) * 8 + j]);
 }
 
 // Greedy commit (Shaders.swift:1501-1571): global argmax of the lm_head partials (ties to the
@@ -95,9 +118,9 @@ __global__ __launch_bounds__(1024) void commit_kernel(CommitArgs a) {
     __syncthreads();
     const int t0 = tok_s[0], t1 = tok_s[1];
     if (t0 < 0) return;
-    for (int i = tid; i < H; i += 1024) a.x[i] = embed_at(a.fmt, a.E, a.Esb, (size_t)t0, i, H);
+    for (int i = tid; i < H; i += 1024) a.x[i] = dequant_tiled(a.fmt, a.E, a.Esb, (size_t)t0, i, H);
     if (t1 >= 0)
-        for (int i = tid; i < H; i += 1024) a.x[H + i] = embed_at(a.fmt, a.E, a.Esb, (size_t)t1, i, H);
+        for (int i = tid; i < H; i += 1024) a.x[H + i] = dequant_tiled(a.fmt, a.E, a.Esb, (size_t)t1, i, H);
 }
 
 hipError_t launch_commit(const CommitArgs& a, hipStream_t s) {
@@ -120,7 +143,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     if (a.pooler && tok == IMAGE_PAD_ID && st->vis_offset >= 0 && v >= 0 && v < st->n_vis) {
         for (int i = threadIdx.x; i < H; i += 256) xr[i] = a.pooler[(size_t)v * H + i];
     } else {
-        for (int i = threadIdx.x; i < H; i += 256) xr[i] = embed_at(a.fmt, a.E, a.Esb, (size_t)tok, i, H);
+        for (int i = threadIdx.x; i < H; i += 256) xr[i] = dequant_tiled(a.fmt, a.E, a.Esb, (size_t)tok, i, H);
     }
 }
 
@@ -130,21 +153,22 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t s) {
 }
 
 __global__ __launch_bounds__(256) void dequant_kernel(int fmt, const uint8_t* w, const uint8_t* sb, int K, int row0,
-                                                       int rows, float* out) {
+                                                       int rows, float* out, int tiled) {
     const size_t total = (size_t)rows * K;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
         const size_t r = i / K;
         const int k = (int)(i % K);
-        out[i] = embed_at(fmt, w, sb, (size_t)row0 + r, k, K);
+        out[i] = tiled ? dequant_tiled(fmt, w, sb, (size_t)row0 + r, k, K)
+                       : dequant_rowmajor(fmt, w, sb, (size_t)row0 + r, k, K);
     }
 }
 
 hipError_t launch_dequant(int fmt, const uint8_t* w, const uint8_t* sb, int K, int row0, int rows, float* out,
-                          hipStream_t s) {
+                          int tiled, hipStream_t s) {
     size_t total = (size_t)rows * K;
     int blocks = (int)((total + 255) / 256);
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(dequant_kernel, dim3(blocks), dim3(256), 0, s, fmt, w, sb, K, row0, rows, out);
+    hipLaunchKernelGGL(dequant_kernel, dim3(blocks), dim3(256), 0, s, fmt, w, sb, K, row0, rows, out, tiled);
     return hipGetLastError();
 }
 

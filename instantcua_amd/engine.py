@@ -33,7 +33,7 @@ EXPORTS = [
     "icua_prefill", "icua_decode_steps", "icua_generate", "icua_verify", "icua_set_position",
     "icua_read_state", "icua_read_tokens", "icua_logits", "icua_timing", "icua_layer_step",
     "icua_read_kv", "icua_write_kv", "icua_read_buffer", "icua_dev_alloc", "icua_dev_free", "icua_memcpy_h2d",
-    "icua_memcpy_d2h", "icua_device_sync", "icua_gemv", "icua_gemv_bench", "icua_dequant",
+    "icua_memcpy_d2h", "icua_device_sync", "icua_repack", "icua_gemv", "icua_gemv_bench", "icua_dequant",
 ]
 
 
@@ -98,7 +98,8 @@ def lib() -> C.CDLL:
         L.icua_memcpy_d2h.argtypes = [vp, vp, sz]
         L.icua_gemv.argtypes = [i32, vp, vp, i32, i32, vp, i32, vp]
         L.icua_gemv_bench.argtypes = [i32, vp, vp, i32, i32, i32, vp, vp, i32, C.POINTER(C.c_double)]
-        L.icua_dequant.argtypes = [i32, vp, vp, i32, i32, i32, vp]
+        L.icua_dequant.argtypes = [i32, vp, vp, i32, i32, i32, vp, i32]
+        L.icua_repack.argtypes = [i32, vp, vp, i32, i32, vp, vp]
         _lib = L
     return _lib
 
@@ -164,8 +165,16 @@ def gemv_bench(fmt: int, codes: Sequence[DeviceBuffer], sbs: Sequence[DeviceBuff
 
 
 def dequant(fmt: int, codes: DeviceBuffer, sb: DeviceBuffer, K: int, row0: int, rows: int,
-            out: DeviceBuffer) -> None:
-    _check(lib().icua_dequant(fmt, codes.ptr, sb.ptr, K, row0, rows, out.ptr))
+            out: DeviceBuffer, tiled: bool = False) -> None:
+    _check(lib().icua_dequant(fmt, codes.ptr, sb.ptr, K, row0, rows, out.ptr, int(tiled)))
+
+
+def repack(fmt: int, codes: DeviceBuffer, sb: DeviceBuffer, N: int, K: int):
+    """Row-major .icua matrix -> (tiled codes, scales) device buffers of the GEMV layout."""
+    tc = DeviceBuffer(codes.nbytes)
+    ts = DeviceBuffer(sb.nbytes)
+    _check(lib().icua_repack(fmt, codes.ptr, sb.ptr, N, K, tc.ptr, ts.ptr))
+    return tc, ts
 
 
 # ---------------------------------------------------------------------------------------------
@@ -315,8 +324,8 @@ class Engine:
 
     def read_buffer(self, which: str, rows: int = MAXM) -> np.ndarray:
         """Pass activations of the last layer run: 'x', 'qkv', 'attn' or 'mlp'."""
-        spec = {"x": (0, np.float32, H), "qkv": (1, np.float32, 4096), "attn": (2, np.float16, H),
-                "mlp": (3, np.float16, FF)}[which]
+        spec = {"x": (0, np.float32, H), "qkv": (1, np.float32, 4096), "attn": (2, np.float32, H),
+                "mlp": (3, np.float32, FF)}[which]
         out = np.empty((rows, spec[2]), dtype=spec[1])
         _check(lib().icua_read_buffer(self._h, spec[0], _p(out), out.nbytes))
         return out

@@ -178,4 +178,6 @@ class ModelFile:
         return n
 
     def close(self) -> None:
+        """Unmaps the file; arrays returned by ``array`` must be released first."""
+        self._table = None
         self._mm.close()

@@ -156,9 +156,9 @@ static void gemv_d(int fmt, const uint8_t* codes, const uint8_t* sb, int N, int 
     }
 }
 
-void or_gemv(int fmt, const uint8_t* codes, const uint8_t* sb, int N, int K, const uint16_t* x, int n, float* y) {
+void or_gemv(int fmt, const uint8_t* codes, const uint8_t* sb, int N, int K, const float* x, int n, float* y) {
     double* xd = (double*)aligned_alloc(64, sizeof(double) * (size_t)n * K);
-    for (size_t i = 0; i < (size_t)n * K; ++i) xd[i] = or_h2f(x[i]);
+    for (size_t i = 0; i < (size_t)n * K; ++i) xd[i] = x[i];
     gemv_d(fmt, codes, sb, N, K, xd, n, y);
     free(xd);
 }
@@ -318,13 +318,13 @@ uint16_t* or_kv(or_model* m, int layer, int kind) {
     return m->kv + ((size_t)layer * 2 + kind) * OR_NKV * m->maxctx * OR_HD;
 }
 
-/* RMSNorm(H) -> fp16 GEMV input, kept as double for the dot products (Shaders.swift:634-657;
- * qwen3vl_ref.py:148-150). */
-static void rmsnorm_to_h(const float* x, const float* w, int n, double* out) {
+/* RMSNorm(H) -> fp32 GEMV input, kept as double for the dot products (qwen3vl_ref.py:148-150;
+ * Shaders.swift:634-657 computes the same expression). */
+static void rmsnorm_in(const float* x, const float* w, int n, double* out) {
     double ss = 0;
     for (int i = 0; i < n; ++i) ss += (double)x[i] * x[i];
     double scale = 1.0 / sqrt(ss / n + OR_EPS);
-    for (int i = 0; i < n; ++i) out[i] = or_h2f(or_f2h((float)((double)x[i] * scale * (double)w[i])));
+    for (int i = 0; i < n; ++i) out[i] = (float)((double)x[i] * scale * (double)w[i]);
 }
 
 /* Per-head RMSNorm(128) in place, fp32 result (Shaders.swift:764-769; qwen3vl_ref.py:254-255). */
@@ -374,7 +374,7 @@ void or_layer(or_model* m, int l, float* x, int n, int pos) {
     const size_t mc = (size_t)m->maxctx;
 
     /* 1. RMSNorm -> fused QKV GEMV (Convert.swift:185-188 row order q|k|v). */
-    for (int t = 0; t < n; ++t) rmsnorm_to_h(x + (size_t)t * H, L->attn_norm, H, xd + (size_t)t * H);
+    for (int t = 0; t < n; ++t) rmsnorm_in(x + (size_t)t * H, L->attn_norm, H, xd + (size_t)t * H);
     gemv_d(m->fmt, L->wqkv, L->wqkv_sb, OR_QKV, H, xd, n, qkv);
     if (g_dbg_qkv) memcpy(g_dbg_qkv, qkv, sizeof(float) * (size_t)n * OR_QKV);
 
@@ -450,20 +450,20 @@ void or_layer(or_model* m, int l, float* x, int n, int pos) {
     free(vf);
 
     if (g_dbg_att) memcpy(g_dbg_att, att, sizeof(float) * (size_t)n * H);
-    /* 4. O projection on the fp16 attention output, residual add in fp32. */
-    for (size_t i = 0; i < (size_t)n * H; ++i) xd[i] = or_h2f(or_f2h(att[i]));
+    /* 4. O projection of the fp32 attention output, residual add in fp32. */
+    for (size_t i = 0; i < (size_t)n * H; ++i) xd[i] = att[i];
     gemv_d(m->fmt, L->wo, L->wo_sb, H, H, xd, n, y);
     for (size_t i = 0; i < (size_t)n * H; ++i) x[i] = x[i] + y[i];
 
-    /* 5. RMSNorm -> gate|up GEMV (Convert.swift:193-194) -> SwiGLU -> fp16 -> down GEMV. */
-    for (int t = 0; t < n; ++t) rmsnorm_to_h(x + (size_t)t * H, L->mlp_norm, H, xd + (size_t)t * H);
+    /* 5. RMSNorm -> gate|up GEMV (Convert.swift:193-194) -> SwiGLU (fp32) -> down GEMV. */
+    for (int t = 0; t < n; ++t) rmsnorm_in(x + (size_t)t * H, L->mlp_norm, H, xd + (size_t)t * H);
     gemv_d(m->fmt, L->wgu, L->wgu_sb, OR_GU, H, xd, n, gu);
     for (int t = 0; t < n; ++t) {
         for (int i = 0; i < FF; ++i) {
             double g = gu[(size_t)t * OR_GU + i], u = gu[(size_t)t * OR_GU + FF + i];
             float a = (float)(g / (1.0 + exp(-g)) * u);
             if (g_dbg_act) g_dbg_act[(size_t)t * FF + i] = a;
-            xd[(size_t)t * FF + i] = or_h2f(or_f2h(a));
+            xd[(size_t)t * FF + i] = a;
         }
     }
     gemv_d(m->fmt, L->wd, L->wd_sb, H, FF, xd, n, y);
@@ -478,7 +478,7 @@ void or_layer(or_model* m, int l, float* x, int n, int pos) {
 
 void or_lm_head(const or_model* m, const float* x, float* logits) {
     double* h = (double*)aligned_alloc(64, sizeof(double) * OR_H);
-    rmsnorm_to_h(x, m->final_norm, OR_H, h);
+    rmsnorm_in(x, m->final_norm, OR_H, h);
     gemv_d(m->fmt, m->embed, m->embed_sb, OR_VOCAB, OR_H, h, 1, logits);
     free(h);
 }

@@ -4,18 +4,18 @@
  * leg of the benchmark may load it; the product library never links or calls it.
  *
  * It restates the reference decoder math (tools/reference/qwen3vl_ref.py:142-155,
- * 243-336) over weights dequantised bit-exactly from the reference codecs
- * (Sources/Engine/Convert.swift:215-270; Shaders.swift:464-476), with the reference
- * engine's storage rounding points (fp16 GEMV inputs: Shaders.swift:634-669; fp16 KV
- * cache: Shaders.swift:776-787, 914-921) and the engine's M-RoPE table
- * (Sources/Engine/Engine.swift:121-125, 254-298).
+ * 243-336), which is fp32 throughout, over weights dequantised bit-exactly from the
+ * reference codecs (Sources/Engine/Convert.swift:215-270; Shaders.swift:464-476), with an
+ * fp16 KV cache (the reference engine's cache format, Shaders.swift:776-787, 914-921; the
+ * workloads specify it) and the engine's M-RoPE table (Sources/Engine/Engine.swift:121-125,
+ * 254-298).
  *
  * Arithmetic contract: every operation is evaluated in double precision and each
- * intermediate tensor is stored as float32 (round-to-nearest-even), exactly where the
- * reference engine keeps an fp32 buffer.  fp16 rounding is applied to those float32
- * values where the engine stores halves.  Dot products accumulate in double and are
- * therefore exact up to 2^-53 relative: products of an fp32 weight and an fp16
- * activation are exact in double.
+ * intermediate tensor is stored as float32 (round-to-nearest-even).  GEMV inputs are those
+ * float32 values (the reference engine's extra fp16 rounding of GEMV inputs,
+ * Shaders.swift:634-669, is not applied).  K/V rows are rounded to fp16 when written to
+ * the cache.  Dot products accumulate in double: products of an fp32 weight and an fp32
+ * activation are exact in double, so a dot product carries one double rounding per term.
  *
  * Results do not depend on the OpenMP thread count: every dot product and every
  * reduction is computed by one thread in a fixed order.
@@ -50,10 +50,10 @@ uint16_t or_f2h(float f);
  * q8: w = s * q (Convert.swift:214-233; Shaders.swift:466-468); f16: w = half value. */
 void or_dequant(int fmt, const uint8_t* codes, const uint8_t* sb, int rows, int K, float* out);
 
-/* y[t][r] = sum_k W[r][k] * x[t][k] for t < n tokens; x are fp16 bit patterns [n][K];
+/* y[t][r] = sum_k W[r][k] * x[t][k] for t < n tokens; x fp32 [n][K];
  * double accumulation, float32 result. */
 void or_gemv(int fmt, const uint8_t* codes, const uint8_t* sb, int N, int K,
-             const uint16_t* x, int n, float* y);
+             const float* x, int n, float* y);
 
 /* Engine M-RoPE table rope[slot][64] = (cos, sin) float pairs (Engine.swift:254-298). */
 void or_mrope_table(int maxctx, int vis_offset, int llm_h, int llm_w, float* out);
@@ -78,7 +78,7 @@ uint16_t* or_kv(or_model* m, int layer, int kind);
 void or_layer(or_model* m, int l, float* x, int n, int pos);
 
 /* Test taps: when set (non-NULL), or_layer copies its raw QKV rows [n][4096], attention output
- * [n][2048] and SwiGLU output [n][6144] (fp32, before fp16 rounding) into these buffers. */
+ * [n][2048] and SwiGLU output [n][6144] (fp32) into these buffers. */
 void or_debug_taps(float* qkv, float* att, float* act);
 
 /* Token embedding row (Shaders.swift:676-692 text branch) into x[H]. */

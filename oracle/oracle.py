@@ -43,7 +43,7 @@ def lib():
         L.or_f2h.argtypes = [C.c_float]
         L.or_f2h.restype = C.c_uint16
         L.or_dequant.argtypes = [C.c_int, _u8p, C.c_void_p, C.c_int, C.c_int, _f32p]
-        L.or_gemv.argtypes = [C.c_int, _u8p, C.c_void_p, C.c_int, C.c_int, _u16p, C.c_int, _f32p]
+        L.or_gemv.argtypes = [C.c_int, _u8p, C.c_void_p, C.c_int, C.c_int, _f32p, C.c_int, _f32p]
         L.or_mrope_table.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, _f32p]
         L.or_model_new.argtypes = [C.c_void_p, C.c_size_t, C.c_int]
         L.or_model_new.restype = C.c_void_p
@@ -96,12 +96,12 @@ def dequant(fmt: int, codes: np.ndarray, sb: np.ndarray, rows: int, K: int) -> n
     return out
 
 
-def gemv(fmt: int, codes: np.ndarray, sb: np.ndarray, N: int, K: int, x_f16: np.ndarray) -> np.ndarray:
-    x = np.ascontiguousarray(x_f16, dtype=np.float16).reshape(-1, K)
+def gemv(fmt: int, codes: np.ndarray, sb: np.ndarray, N: int, K: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
     n = x.shape[0]
     y = np.empty((n, N), dtype=np.float32)
     sb = np.ascontiguousarray(sb, dtype=np.uint8)
-    lib().or_gemv(fmt, np.ascontiguousarray(codes, dtype=np.uint8), _ptr(sb), N, K, x.view(np.uint16), n, y)
+    lib().or_gemv(fmt, np.ascontiguousarray(codes, dtype=np.uint8), _ptr(sb), N, K, x, n, y)
     return y
 
 

@@ -24,12 +24,16 @@ def q8_small():
 
 
 def _fp16_close(got, ref):
-    """fp16 cache rows: equal except rare one-ulp rounding-boundary cases."""
-    g = got.astype(np.float16).view(np.int16).astype(np.int32)
-    r = ref.astype(np.float16).view(np.int16).astype(np.int32)
-    d = np.abs(g - r)
-    assert d.max() <= 1, f"max ulp diff {d.max()}"
-    assert (d > 0).mean() < 1e-3, f"ulp-mismatch fraction {(d > 0).mean():.3g}"
+    """fp16 cache rows: equal up to one fp16 ulp of the value (rounding-boundary cases of
+    fp32-level differences), plus 1e-6 of the row scale for values near zero (RoPE
+    cancellation)."""
+    g = got.astype(np.float32)
+    r = ref.astype(np.float32)
+    ulp = np.spacing(np.abs(r).astype(np.float16)).astype(np.float32)
+    tol = ulp + 1e-6 * np.abs(r).max()
+    bad = np.abs(g - r) > tol
+    assert not bad.any(), f"{bad.sum()} cache values beyond one ulp"
+    assert (g != r).mean() < 2e-2, f"mismatch fraction {(g != r).mean():.3g}"
 
 
 def test_single_layer_q8_step(oracle_mod):
@@ -55,7 +59,7 @@ def test_single_layer_q8_step(oracle_mod):
         got_v = e.read_kv(0, 1, pos, 1)[:, 0]
         # prior slots untouched
         assert np.array_equal(e.read_kv(0, 0, 0, pos).view(np.uint16), kc.view(np.uint16))
-    assert rel_err(got, ref) < 1e-4, rel_err(got, ref)
+    assert rel_err(got, ref) < 2e-5, rel_err(got, ref)
     _fp16_close(got_k, ref_k)
     _fp16_close(got_v, ref_v)
 
@@ -76,7 +80,7 @@ def test_multi_row_layer_q4(oracle_mod, q4_small, n):
         e.write_kv(1, 1, 0, vc)
         got = e.layer_step(1, x, pos)
         gk = e.read_kv(1, 0, pos, n)
-    assert rel_err(got, ref) < 1e-4, rel_err(got, ref)
+    assert rel_err(got, ref) < 2e-5, rel_err(got, ref)
     _fp16_close(gk, om.kv(1, 0)[:, pos:pos + n])
 
 
@@ -94,7 +98,7 @@ def test_greedy_decode_small(oracle_mod, q4_small, q8_small, fmt_name):
         e.decode_steps(steps - 1)
         st = e.state()
         got = e.tokens(st["step"])
-    assert rel_err(lg, ref_first) < 1e-2
+    assert rel_err(lg, ref_first) < 1e-2  # the stated logits tolerance
     assert rel_err(lg, ref_first) < 1e-4, f"first-logit rel err {rel_err(lg, ref_first):.3g}"
     assert first == ref_toks[0]
     assert st["step"] == steps and st["done"] == 1
@@ -186,16 +190,16 @@ def test_layer_stages(oracle_mod, fmt):
         e.write_kv(0, 1, 0, vc)
         got_x = e.layer_step(0, x, pos)
         qkv = e.read_buffer("qkv", n)
-        att = e.read_buffer("attn", n).astype(np.float32)
-        act = e.read_buffer("mlp", n).astype(np.float32)
+        att = e.read_buffer("attn", n)
+        act = e.read_buffer("mlp", n)
     errs = {
         "qkv": rel_err(qkv, ref_qkv),
-        "attn": rel_err(att, ref_att.astype(np.float16).astype(np.float32)),
-        "mlp": rel_err(act, ref_act.astype(np.float16).astype(np.float32)),
+        "attn": rel_err(att, ref_att),
+        "mlp": rel_err(act, ref_act),
         "x": rel_err(got_x, ref_x),
     }
     print(fmt, {k: f"{v:.3g}" for k, v in errs.items()})
-    assert errs["qkv"] < 2e-5
-    assert errs["attn"] < 2e-3  # fp16 outputs: at most ~1 ulp apart
-    assert errs["mlp"] < 2e-3
-    assert errs["x"] < 1e-4
+    assert errs["qkv"] < 2e-6
+    assert errs["attn"] < 1e-5
+    assert errs["mlp"] < 1e-5
+    assert errs["x"] < 1e-5
