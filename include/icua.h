@@ -31,6 +31,7 @@ enum { ICUA_FMT_F16 = 0, ICUA_FMT_Q8 = 1, ICUA_FMT_Q4 = 2 };
 enum {
     ICUA_FLAG_GRAMMAR_PAIRS = 1, /* forced syntax pairs + ')' stop of k_commit (Shaders.swift:1543-1560) */
     ICUA_FLAG_PREFIX_CACHE = 2,  /* reuse the KV of an identical pre-image prefix (Engine.swift:719-735) */
+    ICUA_FLAG_GRAPH_DECODE = 4,  /* decode through the per-kernel HIP graph instead of the persistent kernel */
 };
 
 /* Decode control block, first twelve fields as `State` (Shaders.swift:41-54). */
@@ -48,6 +49,8 @@ typedef struct {
 typedef struct {
     int32_t format, layers, max_context, max_pass, max_steps;
     int64_t weight_bytes, kv_bytes;
+    int32_t persistent_decode; /* 1 if icua_decode_steps can use the persistent kernel on this device */
+    int32_t reserved;
 } icua_info_t;
 
 /* Last error message of the calling thread ("" if none). */
@@ -85,8 +88,11 @@ int icua_set_visual(icua_engine* e, const float* pooler, const float* const* dee
 int icua_prefill(icua_engine* e, const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new,
                  int write_logits);
 
-/* k x Engine.encodeDecodeStep (Engine.swift:675-681), GPU-resident (one captured HIP graph per
- * step, token feedback on the device); returns after completion.  Steps after a stop are no-ops. */
+/* k x Engine.encodeDecodeStep (Engine.swift:675-681), GPU-resident with token feedback on the
+ * device; returns after completion.  Steps after a stop are no-ops.  q4 / q8 models without
+ * grammar pairs run all k steps in one persistent cooperative kernel (one workgroup per CU);
+ * otherwise, or with ICUA_FLAG_GRAPH_DECODE, each step replays a captured HIP graph of the
+ * per-stage kernels.  Both paths compute the same arithmetic. */
 int icua_decode_steps(icua_engine* e, int k);
 
 /* Engine.generateVision (Engine.swift:696-827) minus the vision encoder: prefill + greedy decode

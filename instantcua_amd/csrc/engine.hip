@@ -20,6 +20,7 @@
 
 #include "../../include/icua.h"
 #include "icua_kernels.h"
+#include "icua_persist.h"
 
 using namespace icua;
 
@@ -124,6 +125,10 @@ struct icua_engine {
     std::vector<int32_t> cached_prefix;
     int mrope_key[3] = {-999, 0, 0};
     int last_logits_rows = 0;
+    // Persistent decode kernel: counter block, device copy of the layer table, availability.
+    unsigned* psync = nullptr;
+    LayerPtrs* d_layers = nullptr;
+    bool persist_ok = false;
 
     uint16_t* kv_ptr(int l, int kind) const { return kv + ((size_t)l * 2 + kind) * NKV * (size_t)maxctx * HD; }
 
@@ -369,7 +374,10 @@ struct icua_engine {
         HIPCK(hipMemset(kv, 0, kvn * 2));
         HIPCK(hipMalloc(&rope, sizeof(float) * (size_t)maxctx * 128));
         splits = attention_splits(maxctx);
-        HIPCK(hipMalloc(&part, sizeof(float) * (size_t)NKV * splits * MAXM * 2 * (HD + 2)));
+        // Split partials of the graph path, or of the persistent kernel's 32 splits per group.
+        const size_t part_floats =
+            std::max((size_t)NKV * splits * MAXM * 2 * (HD + 2), (size_t)PERSIST_WGS * 2 * (HD + 2));
+        HIPCK(hipMalloc(&part, sizeof(float) * part_floats));
         HIPCK(hipMalloc(&counters, sizeof(int) * NKV));
         HIPCK(hipMemset(counters, 0, sizeof(int) * NKV));
         HIPCK(hipMalloc(&pval, sizeof(float) * MAXM * LMH_WAVES));
@@ -389,7 +397,66 @@ struct icua_engine {
         s.eos1 = eos1;
         s.vis_offset = -1;
         if (write_state(s)) return -1;
+        if (init_persistent()) return -1;
         return prepare_mrope(-1, 1, 1);
+    }
+
+    // The persistent kernel needs all PERSIST_WGS workgroups (one per CU) resident at once.
+    int init_persistent() {
+        persist_ok = false;
+        if (fmt != 2 && fmt != 1) return 0;
+        int dev = 0, coop = 0, cus = 0;
+        HIPCK(hipGetDevice(&dev));
+        HIPCK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+        HIPCK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        if (!coop || cus < PERSIST_WGS) return 0;
+        HIPCK(hipMalloc(&psync, persistent_sync_bytes()));
+        std::vector<LayerPtrs> lp(layers);
+        for (int l = 0; l < layers; ++l) {
+            const LayerW& w = L[l];
+            lp[l] = LayerPtrs{w.attn_norm, w.q_norm, w.k_norm, w.mlp_norm, w.wqkv, w.wqkv_sb,
+                              w.wo,        w.wo_sb,  w.wgu,    w.wgu_sb,   w.wd,   w.wd_sb};
+        }
+        HIPCK(hipMalloc(&d_layers, sizeof(LayerPtrs) * layers));
+        HIPCK(hipMemcpy(d_layers, lp.data(), sizeof(LayerPtrs) * layers, hipMemcpyHostToDevice));
+        persist_ok = true;
+        return 0;
+    }
+
+    bool use_persistent() const { return persist_ok && !(flags & (ICUA_FLAG_GRAMMAR_PAIRS | ICUA_FLAG_GRAPH_DECODE)); }
+
+    int enqueue_persistent(int k) {
+        PersistArgs a{};
+        a.layers = d_layers;
+        a.nlayers = layers;
+        a.nsteps = k;
+        a.maxctx = maxctx;
+        a.E = E;
+        a.Esb = Esb;
+        a.final_norm = final_norm;
+        a.rope = rope;
+        a.kv = kv;
+        a.x = x;
+        a.qkv = qkv;
+        a.attn = attn;
+        a.h = h;
+        a.part = part;
+        a.pval = pval;
+        a.pidx = pidx;
+        a.st = st;
+        a.out_tokens = out_tokens;
+        a.sync = psync;
+        HIPCK(hipMemsetAsync(psync, 0, persistent_sync_bytes(), stream));
+        HIPCK(launch_persistent(fmt, a, stream));
+        return 0;
+    }
+
+    // Error flag of the last persistent launch (a bounded wait timed out).
+    int check_persistent() {
+        unsigned err = 0;
+        HIPCK(hipMemcpy(&err, psync + persistent_error_slot(), sizeof err, hipMemcpyDeviceToHost));
+        if (err) return fail("persistent decode kernel: a synchronisation wait timed out");
+        return 0;
     }
 
     int prepare_mrope(int vis_offset, int llm_h, int llm_w) {
@@ -459,12 +526,24 @@ struct icua_engine {
     }
 
     int decode_steps(int k, double* ms_out) {
+        if (k < 0) return fail("negative step count");
+        bool persistent = use_persistent();
+        if (persistent) {  // single-row passes only (a grammar pair pass takes the graph path)
+            State s;
+            if (read_state(s)) return -1;
+            if (s.n != 1 || (s.flags & STATE_FLAG_GRAMMAR)) persistent = false;
+        }
         const int mt = decode_mt();
-        if (ensure_graph(mt)) return -1;
+        if (!persistent && ensure_graph(mt)) return -1;
         HIPCK(hipEventRecord(ev0, stream));
-        for (int i = 0; i < k; ++i) HIPCK(hipGraphLaunch(graph[mt == 1 ? 0 : 1], stream));
+        if (persistent) {
+            if (k > 0 && enqueue_persistent(k)) return -1;
+        } else {
+            for (int i = 0; i < k; ++i) HIPCK(hipGraphLaunch(graph[mt == 1 ? 0 : 1], stream));
+        }
         HIPCK(hipEventRecord(ev1, stream));
         HIPCK(hipEventSynchronize(ev1));
+        if (persistent && k > 0 && check_persistent()) return -1;
         float ms = 0;
         HIPCK(hipEventElapsedTime(&ms, ev0, ev1));
         if (ms_out) *ms_out = ms;
@@ -520,7 +599,7 @@ void icua_engine_destroy(icua_engine* e) {
         if (g) (void)hipGraphExecDestroy(g);
     void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->pval,
                     e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
-                    e->ds[0], e->ds[1], e->ds[2]};
+                    e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_layers};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (e->ev0) (void)hipEventDestroy(e->ev0);
@@ -538,6 +617,8 @@ int icua_engine_info(icua_engine* e, icua_info_t* out) {
     out->max_steps = e->maxsteps;
     out->weight_bytes = (int64_t)e->weight_bytes;
     out->kv_bytes = (int64_t)e->layers * 2 * NKV * e->maxctx * HD * 2;
+    out->persistent_decode = e->persist_ok ? 1 : 0;
+    out->reserved = 0;
     return 0;
 }
 
@@ -615,7 +696,8 @@ int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, 
     double dec_ms = 0;
     int submitted = 1;
     while (submitted < max_new) {  // batches of 8 steps (Engine.swift:771-792)
-        const int count = std::min(8, max_new - submitted);
+        // The persistent kernel stops on the device at EOS: no host round trip per batch.
+        const int count = e->use_persistent() ? max_new - submitted : std::min(8, max_new - submitted);
         double ms = 0;
         if (e->decode_steps(count, &ms)) return -1;
         dec_ms += ms;

@@ -1,0 +1,48 @@
+// Launch interface of the persistent decode kernel (persist.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "icua_shared.h"
+
+namespace icua {
+
+// Workgroups of the persistent kernel: one per CU of an MI355X.  The static work split
+// (16-row blocks of QKV / O / gate|up / down, 32 attention splits per KV group) is built for
+// exactly this many.
+constexpr int PERSIST_WGS = 256;
+
+struct LayerPtrs {
+    const float *attn_norm, *q_norm, *k_norm, *mlp_norm;
+    const uint8_t *wqkv, *wqkv_sb, *wo, *wo_sb, *wgu, *wgu_sb, *wd, *wd_sb;
+};
+
+struct PersistArgs {
+    const LayerPtrs* layers;  // device array [nlayers]
+    int nlayers;
+    int nsteps;             // decode steps to run (stops early when the control block says done)
+    int maxctx;
+    const uint8_t* E;       // tied embedding / lm_head codes (tiled) and scales
+    const uint8_t* Esb;
+    const float* final_norm;
+    const float* rope;      // [maxctx][64] (cos, sin)
+    uint16_t* kv;           // [layers][2][NKV][maxctx][HD] fp16
+    float* x;               // residual [H]
+    float* qkv;             // [QKV]
+    float* attn;            // [H]
+    float* h;               // [FF]
+    float* part;            // [NKV][32][2][HD + 2]
+    float* pval;            // [PERSIST_WGS]
+    int* pidx;
+    State* st;
+    int* out_tokens;
+    unsigned* sync;         // persistent_sync_bytes() of zeroed counters
+};
+
+hipError_t launch_persistent(int fmt, const PersistArgs& a, hipStream_t s);
+// Size of the counter block the kernel synchronises through (zeroed before every launch), and
+// the index (in unsigned words) of its error flag: non-zero after a launch means a wait timed out.
+size_t persistent_sync_bytes();
+int persistent_error_slot();
+
+}  // namespace icua

@@ -4,43 +4,6 @@
 
 namespace icua {
 
-// One dequantised element (Shaders.swift:464-476 embed_at): q4 s*q + b, q8 s*q, f16 half;
-// row-major .icua layout.
-__device__ __forceinline__ float dequant_rowmajor(int fmt, const uint8_t* E, const uint8_t* Esb, size_t row, int i,
-                                                  int K) {
-    if (fmt == FMT_Q4) {
-        const uint8_t b = E[row * (K / 2) + (i >> 1)];
-        const float q = (float)((i & 1) ? (b >> 4) : (b & 15));
-        const f16x2 sb = as_h2(((const uint32_t*)Esb)[row * (K / 64) + (i >> 6)]);
-        return (float)sb.x * q + (float)sb.y;
-    } else if (fmt == FMT_Q8) {
-        const float s = h2f(((const uint16_t*)Esb)[row * (K / 32) + (i >> 5)]);
-        return s * (float)(int8_t)E[row * K + i];
-    }
-    return h2f(((const uint16_t*)E)[row * K + i]);
-}
-
-// The same element read from the GEMV tile layout (gemv.hip repack_codes_kernel): lane
-// l = r + 16 q of chunk c holds 16 bytes; scales stay row-major.
-__device__ __forceinline__ float dequant_tiled(int fmt, const uint8_t* E, const uint8_t* Esb, size_t row, int k, int K) {
-    const size_t rb = row / 16;
-    const int r = (int)(row % 16);
-    if (fmt == FMT_Q4) {
-        const int nc = K / 128, c = k / 128, h = (k % 128) / 64, kk = k % 64, q = kk / 16, j = kk % 16;
-        const int d = j / 8, jj = j % 8;
-        const uint8_t b = E[((rb * nc + c) * 64 + r + 16 * q) * 16 + 8 * h + 4 * d + (jj % 4)];
-        const float qv = (float)((jj / 4) ? (b >> 4) : (b & 15));
-        const f16x2 sb = as_h2(((const uint32_t*)Esb)[row * (K / 64) + k / 64]);
-        return (float)sb.x * qv + (float)sb.y;
-    } else if (fmt == FMT_Q8) {
-        const int nc = K / 64, c = k / 64, h = (k % 64) / 32, q = (k % 32) / 8, j = k % 8;
-        const float s = h2f(((const uint16_t*)Esb)[row * (K / 32) + k / 32]);
-        return s * (float)(int8_t)E[((rb * nc + c) * 64 + r + 16 * q) * 16 + 8 * h + j];
-    }
-    const int nc = K / 32, c = k / 32, q = (k % 32) / 8, j = k % 8;
-    return h2f(((const uint16_t*)E)[((rb * nc + c) * 64 + r + 16 * q) * 8 + j]);
-}
-
 // Greedy commit (Shaders.swift:1501-1571): global argmax of the lm_head partials (ties to the
 // lowest id), state update, stop test, optional grammar pairs, and the embedding of the next
 // token(s) into the residual rows.  One workgroup of 1024 threads.
@@ -86,13 +49,15 @@ __global__ __launch_bounds__(1024) void commit_kernel(CommitArgs a) {
     __syncthreads();
     if (halt) return;
     if (tid == 0) {
-        const int tok = tok_last;
+        int tok = tok_last;
+        const bool bad = tok < 0 || tok >= VOCAB;  // no finite logit (NaN model): stop on token 0
+        if (bad) tok = 0;
         st->pos += n;
         st->vis_offset = -1;
         a.out_tokens[st->step] = tok;
         st->step += 1;
         const bool grammar = st->flags & STATE_FLAG_GRAMMAR;
-        const bool stop = tok == st->eos0 || tok == st->eos1 || (grammar && tok == 8) || st->step >= st->maxsteps ||
+        const bool stop = bad || tok == st->eos0 || tok == st->eos1 || (grammar && tok == 8) || st->step >= st->maxsteps ||
                           st->pos + 2 > st->maxctx;  // no cache room for the next pass
         if (stop) {
             st->done = 1;

@@ -26,6 +26,7 @@ MAXM = 8
 
 FLAG_GRAMMAR_PAIRS = 1
 FLAG_PREFIX_CACHE = 2
+FLAG_GRAPH_DECODE = 4
 
 EXPORTS = [
     "icua_last_error", "icua_engine_create", "icua_engine_create_from_memory", "icua_engine_destroy",
@@ -55,7 +56,7 @@ class _Timing(C.Structure):
 class _Info(C.Structure):
     _fields_ = [("format", C.c_int32), ("layers", C.c_int32), ("max_context", C.c_int32),
                 ("max_pass", C.c_int32), ("max_steps", C.c_int32), ("weight_bytes", C.c_int64),
-                ("kv_bytes", C.c_int64)]
+                ("kv_bytes", C.c_int64), ("persistent_decode", C.c_int32), ("reserved", C.c_int32)]
 
 
 _lib = None
@@ -206,6 +207,7 @@ class Engine:
         self.max_steps = info.max_steps
         self.weight_bytes = info.weight_bytes
         self.kv_bytes = info.kv_bytes
+        self.persistent_decode = bool(info.persistent_decode)
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -246,6 +248,15 @@ class Engine:
     @grammar_pairs.setter
     def grammar_pairs(self, v: bool):
         self.set_flags((self._flags | FLAG_GRAMMAR_PAIRS) if v else (self._flags & ~FLAG_GRAMMAR_PAIRS))
+
+    @property
+    def graph_decode(self) -> bool:
+        """Decode through the per-kernel HIP graph instead of the persistent kernel."""
+        return bool(self._flags & FLAG_GRAPH_DECODE)
+
+    @graph_decode.setter
+    def graph_decode(self, v: bool):
+        self.set_flags((self._flags | FLAG_GRAPH_DECODE) if v else (self._flags & ~FLAG_GRAPH_DECODE))
 
     def set_flags(self, flags: int) -> None:
         _check(lib().icua_set_flags(self._h, flags))
