@@ -374,10 +374,7 @@ struct icua_engine {
         HIPCK(hipMemset(kv, 0, kvn * 2));
         HIPCK(hipMalloc(&rope, sizeof(float) * (size_t)maxctx * 128));
         splits = attention_splits(maxctx);
-        // Split partials of the graph path, or of the persistent kernel's 32 splits per group.
-        const size_t part_floats =
-            std::max((size_t)NKV * splits * MAXM * 2 * (HD + 2), (size_t)PERSIST_WGS * 2 * (HD + 2));
-        HIPCK(hipMalloc(&part, sizeof(float) * part_floats));
+        HIPCK(hipMalloc(&part, sizeof(float) * (size_t)NKV * splits * MAXM * 2 * (HD + 2)));
         HIPCK(hipMalloc(&counters, sizeof(int) * NKV));
         HIPCK(hipMemset(counters, 0, sizeof(int) * NKV));
         HIPCK(hipMalloc(&pval, sizeof(float) * MAXM * LMH_WAVES));
@@ -437,15 +434,9 @@ struct icua_engine {
         a.rope = rope;
         a.kv = kv;
         a.x = x;
-        a.qkv = qkv;
-        a.attn = attn;
-        a.h = h;
-        a.part = part;
-        a.pval = pval;
-        a.pidx = pidx;
         a.st = st;
         a.out_tokens = out_tokens;
-        a.sync = psync;
+        a.ll = (uint64_t*)psync;
         HIPCK(hipMemsetAsync(psync, 0, persistent_sync_bytes(), stream));
         HIPCK(launch_persistent(fmt, a, stream));
         return 0;

@@ -20,28 +20,22 @@ struct LayerPtrs {
 struct PersistArgs {
     const LayerPtrs* layers;  // device array [nlayers]
     int nlayers;
-    int nsteps;             // decode steps to run (stops early when the control block says done)
-    int maxctx;
-    const uint8_t* E;       // tied embedding / lm_head codes (tiled) and scales
+    int nsteps;               // decode steps to run (stops early at a stop condition)
+    int maxctx;               // cache capacity (row stride of the K/V cache)
+    const uint8_t* E;         // tied embedding / lm_head codes (tiled) and scales
     const uint8_t* Esb;
     const float* final_norm;
-    const float* rope;      // [maxctx][64] (cos, sin)
-    uint16_t* kv;           // [layers][2][NKV][maxctx][HD] fp16
-    float* x;               // residual [H]
-    float* qkv;             // [QKV]
-    float* attn;            // [H]
-    float* h;               // [FF]
-    float* part;            // [NKV][32][2][HD + 2]
-    float* pval;            // [PERSIST_WGS]
-    int* pidx;
+    const float* rope;        // [maxctx][64] (cos, sin)
+    uint16_t* kv;             // [layers][2][NKV][maxctx][HD] fp16
+    float* x;                 // residual row [H]: the next token's embedding, in and out
     State* st;
     int* out_tokens;
-    unsigned* sync;         // persistent_sync_bytes() of zeroed counters
+    uint64_t* ll;             // packet area of persistent_sync_bytes(), zeroed before the launch
 };
 
 hipError_t launch_persistent(int fmt, const PersistArgs& a, hipStream_t s);
-// Size of the counter block the kernel synchronises through (zeroed before every launch), and
-// the index (in unsigned words) of its error flag: non-zero after a launch means a wait timed out.
+// Size of the packet area the workgroups exchange data through (zeroed before every launch), and
+// the index (in 32-bit words) of its error flag: non-zero after a launch means a wait timed out.
 size_t persistent_sync_bytes();
 int persistent_error_slot();
 

@@ -1,31 +1,38 @@
 // Persistent decode kernel: whole greedy decode steps (28 layers + lm_head + commit) in one
-// cooperative launch, gfx950.  Same math and tile layout as gemv.hip / attention.hip; the
-// difference is the schedule.
+// cooperative launch, gfx950.  Same arithmetic and weight tiles as gemv.hip / attention.hip /
+// misc.hip; the difference is the schedule.
 //
 // Why.  As separate kernels a decode step is ~170 dependent launches whose fixed latency
-// (launch, cold weight fetch, prologue, drain: 5-10 us each) dominates the 180 us the step's
-// bytes need at 8 TB/s.  Here every workgroup stays resident and, before waiting for a stage's
-// inputs, already issues the loads of its slice of that stage's weights (and K/V rows), so the
-// HBM latency overlaps the synchronisation.
+// (launch, cold weight fetch, prologue, drain: 5-10 us each) dominates the ~180 us the step's
+// bytes need at 8 TB/s.  Here every workgroup stays resident and, before it waits for a stage's
+// inputs, already has the loads of its slice of that stage's weights (and K/V rows) in flight.
 //
 // Grid.  One 512-thread workgroup per CU (256).  Static work split per layer:
-//   QKV   256 row blocks, block w                  (fused q|k|v rows, Convert.swift:185-188)
-//   attn  KV group g = w / 32, slot range s = w % 32 of [0, pos); split 31 also owns the new row
-//   merge the last split to arrive for a group merges the group's 32 partials
+//   QKV   256 row blocks of the fused q|k|v rows (Convert.swift:185-188), block w
+//   attn  KV group g = w % 8, split s = w / 8: the pos + 1 cache rows of the group (rows < pos and
+//         the new row) are spread evenly over the 32 splits; the split holding row pos writes it
+//   merge split 31 of group g (workgroup 248 + g, which has no O / down work) merges the 32
+//         partials of the group
 //   O     128 row blocks, workgroups 0..127
 //   GU    768 row blocks (8 gate + 8 up rows each), blocks 3w .. 3w + 2
 //   down  128 row blocks (K = 6144), workgroups 0..127
-// then lm_head over 9496 row blocks (w, w + 256, ...) with per-workgroup argmax partials, and the
-// commit (Shaders.swift:1501-1571) by the last workgroup to finish lm_head.
+// then lm_head over 9496 row blocks (w, w + 256, ...) with a per-workgroup argmax, and the greedy
+// commit (Shaders.swift:1501-1571), which every workgroup evaluates redundantly from the 256
+// argmax partials; workgroup 0 alone writes the control block and the token list.
 //
-// Synchronisation.  Monotonic arrival counters in device memory (zeroed before the launch);
-// a stage waits until the counter of its inputs reaches the count for (step, layer).  Large
-// fan-ins arrive on 16 counters in separate 256-byte lines and are polled by one wave (one
-// lane per counter).  Activations crossing workgroups are written and read with device-scope
-// relaxed atomics (global_store/load ... sc1: coherent across the XCDs' L2s, no cache
-// flushes); each arrival follows an s_waitcnt vmcnt(0) (the workgroup barrier before it), so
-// a counter value implies the data it covers is visible.  Every spin is bounded: a timeout
-// raises an error flag that makes all workgroups leave, and the host reports it.
+// Data exchange.  Every value that crosses workgroups travels as a 64-bit packet (fp32 value,
+// 32-bit round tag) written with one device-scope store and read with device-scope loads
+// (global_store/load_dwordx2 ... sc1: coherent across the XCDs' L2s without cache flushes).  A
+// consumer polls the packets it needs until each carries the tag of the round it expects, so the
+// data is its own flag: no fences, counters or store acknowledgements on the critical path.
+// A buffer is rewritten only after every consumer of its previous round has read it: each
+// producer first consumes outputs that, through the stage chain, every such consumer produced
+// after its read.  The packet area is zeroed before each launch and tags start at 1, so a tag
+// never matches stale data.  The one value read with plain loads across workgroups is the new
+// K/V cache row: it is stored device-scope, acknowledged before the writer's next packet, first
+// read a step later, and rows >= pos are never loaded early (a line cached early would go
+// stale).  Every poll is bounded: a timeout raises an error flag that makes all workgroups
+// leave, and the host reports it.
 #include "icua_device.h"
 #include "icua_kernels.h"
 #include "icua_persist.h"
@@ -36,27 +43,24 @@ namespace pk {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int THREADS = 512, WAVES = 8;
-constexpr int NWG = PERSIST_WGS;   // 256
-constexpr int ATT_SPLITS = NWG / NKV;  // 32
-constexpr int SPIN_LIMIT = 4000000;
-constexpr int PART = HD + 2;
-constexpr int ATT_SPQ = 8;                 // cache slots per quarter-wave per block
-constexpr int ATT_BLOCK = 32 * ATT_SPQ;     // 256 slots per block
+constexpr int NWG = PERSIST_WGS;         // 256
+constexpr int ATT_SPLITS = NWG / NKV;    // 32
+constexpr int SPIN_LIMIT = 2000000;      // polls (>= ~1 us each) before a wait gives up
+constexpr int PART = HD + 2;             // partial of one head: o[128], m, l
+constexpr int ATT_SPQ = 8;               // cache slots per quarter-wave per block
+constexpr int ATT_BLOCK = 32 * ATT_SPQ;  // 256 slots per block
+constexpr int MERGER0 = NWG - NKV;       // workgroup 248 + g merges group g (its split 31)
 
-// Counter slots (each in its own 256-byte line).
-enum {
-    C_COMMIT = 0,
-    C_QKV = 1,      // + g
-    C_ATT = 9,      // + g
-    C_MERGED = 17,
-    C_ERR = 18,
-    C_O = 32,       // 16 sub-counters each
-    C_GU = 48,
-    C_DOWN = 64,
-    C_LM = 80,
-    C_SLOTS = 96,
-};
-__device__ __forceinline__ unsigned* slot(unsigned* s, int i) { return s + i * 64; }
+// Packet area (64-bit packets), zeroed before every launch.
+constexpr int XP = 0;                 // residual x [H]
+constexpr int QKVP = XP + H;          // fused q|k|v [QKV]
+constexpr int ATTNP = QKVP + QKV;     // merged attention [H]
+constexpr int HP = ATTNP + H;         // SwiGLU activations [FF]
+constexpr int LMP = HP + FF;          // argmax partials [NWG][2] (value, index)
+constexpr int PARTP = LMP + 2 * NWG;  // attention partials [NKV][32][2][PART]
+constexpr int PACKETS = PARTP + NKV * ATT_SPLITS * 2 * PART;
+constexpr int ERRW = PACKETS * 2;     // error flag (32-bit word index)
+static_assert(MERGER0 % NKV == 0, "merger of group g must be split 31 of group g");
 
 // threadIdx.x behind an empty asm: per-lane address math derived from it is recomputed where it
 // is used instead of being hoisted out of the step / layer loops and held live (which spills).
@@ -66,128 +70,130 @@ __device__ __forceinline__ int my_tid() {
     return t;
 }
 
-__device__ __forceinline__ unsigned ldc(const unsigned* p) {
+__device__ __forceinline__ uint64_t ld64(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ unsigned addc(unsigned* p, unsigned v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ldf(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void stf(float* p, float v) {
+__device__ __forceinline__ void st64(uint64_t* p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int ldi(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void sti(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ float2 ldf2(const float* p) {
-    const uint64_t v = __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float2(__builtin_bit_cast(float, (uint32_t)v), __builtin_bit_cast(float, (uint32_t)(v >> 32)));
+__device__ __forceinline__ uint64_t pack(float v, unsigned tag) { return (uint64_t)as_u32(v) | ((uint64_t)tag << 32); }
+__device__ __forceinline__ uint64_t pack_i(int v, unsigned tag) { return (uint64_t)(uint32_t)v | ((uint64_t)tag << 32); }
+__device__ __forceinline__ unsigned tag_of(uint64_t p) { return (unsigned)(p >> 32); }
+__device__ __forceinline__ float val_of(uint64_t p) { return as_f32((uint32_t)p); }
+
+__device__ __forceinline__ unsigned load_err(const unsigned* e) {
+    return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void stf2(float* p, float a, float b) {
-    const uint64_t v = (uint64_t)__builtin_bit_cast(uint32_t, a) | ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
-    __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void raise_err(unsigned* e) {
+    __hip_atomic_store(e, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-struct Shared {
-    uint8_t A[96 * 1024];      // activation operands (q4: 1 KiB per 64-K group, up to K = 6144)
-    float fx[192 * 2];         // per-group (2^(e-21), sum X * 2^(e-21))
-    float red[THREADS / 64 * 64];
-    float qs[2][HD];           // attention: two query heads
-    float ktail[HD], vtail[HD];
-    float sc[2][256];          // attention scores of one block
-    float ored[WAVES][2][HD];
-    float misc[64];
-    int flag;
-};
-
-// ------------------------------------------------------------------------------------------
-// Waits.  Wave 0 polls; the whole workgroup learns the outcome through LDS.
-
-__device__ bool wait_single(Shared& S, unsigned* sync, int idx, unsigned target) {
-    __syncthreads();
-    if (my_tid() < 64) {
-        int ok = 1, it = 0;
-        if (my_tid() == 0) {
-            while (ldc(slot(sync, idx)) < target) {
-                if ((++it & 255) == 0 && ldc(slot(sync, C_ERR)) != 0) { ok = 0; break; }
-                if (it > SPIN_LIMIT) {
-                    __hip_atomic_store(slot(sync, C_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    ok = 0;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            S.flag = ok;
-        }
+// Polls packets p[i] = src[off(i)] (i < N; off(i) < 0: unused) until each carries `tag`.  Returns
+// false on timeout (after raising the error flag) or when another workgroup raised it.
+template <int N, typename Off>
+__device__ __forceinline__ bool poll(const uint64_t* src, Off off, unsigned tag, uint64_t (&p)[N], unsigned* err) {
+    const uint64_t filler = (uint64_t)tag << 32;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int o = off(i);
+        p[i] = o >= 0 ? ld64(src + o) : filler;
     }
-    __syncthreads();
-    return S.flag != 0;
+    for (int it = 0;; ++it) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) ok &= tag_of(p[i]) == tag;
+        if (ok) return true;
+        if (it >= SPIN_LIMIT) {
+            raise_err(err);
+            return false;
+        }
+        if ((it & 63) == 63 && load_err(err)) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if (tag_of(p[i]) != tag) p[i] = ld64(src + off(i));
+    }
 }
 
-// Fan-in over 16 sub-counters at idx..idx+15; `per_sub` arrivals per sub-counter per round.
-__device__ bool wait_fan(Shared& S, unsigned* sync, int idx, unsigned per_sub_target) {
-    __syncthreads();
-    if (my_tid() < 64) {
-        const int lane = my_tid();
-        int ok = 1, it = 0;
-        while (true) {
-            const bool mine = (lane >= 16) || ldc(slot(sync, idx + lane)) >= per_sub_target;
-            if (__all(mine)) break;
-            if ((++it & 255) == 0 && ldc(slot(sync, C_ERR)) != 0) { ok = 0; break; }
-            if (it > SPIN_LIMIT) {
-                if (lane == 0) __hip_atomic_store(slot(sync, C_ERR), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
+// Waits until sentinel packet src[sent(t)] carries `tag` for every thread t < nsent (one packet
+// per producer store instruction), so that the bulk of a vector is read once instead of being
+// polled: polling whole vectors from every workgroup floods the fabric.  Whole-workgroup call.
+template <typename Sent>
+__device__ __forceinline__ bool wait_sentinels(const uint64_t* src, int nsent, Sent sent, unsigned tag,
+                                               unsigned* err) {
+    const int tid = my_tid();
+    bool ok = true;
+    if (tid < nsent) {
+        const uint64_t* q = src + sent(tid);
+        uint64_t p = ld64(q);
+        for (int it = 0; tag_of(p) != tag; ++it) {
+            if (it >= SPIN_LIMIT) {
+                raise_err(err);
+                ok = false;
+                break;
+            }
+            if ((it & 63) == 63 && load_err(err)) {
+                ok = false;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
+            p = ld64(q);
         }
-        if (lane == 0) S.flag = ok;
     }
-    __syncthreads();
-    return S.flag != 0;
+    return !__syncthreads_or(!ok);
 }
 
-// Arrival after this workgroup's coherent stores.  Every wave first waits until its own stores
-// are acknowledged (s_waitcnt vmcnt(0): a device-scope store is then visible to every CU); the
-// workgroup barrier alone does not wait for global stores on gfx950.
-__device__ __forceinline__ unsigned arrive(unsigned* sync, int idx) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    unsigned old = 0;
-    if (my_tid() == 0) old = addc(slot(sync, idx), 1u);
-    return old;
+// Producers of the packet vectors and their sentinels.  A sentinel only decides when to read
+// the vector; the tag check of every packet read afterwards is what guarantees the data.
+enum Src { SRC_X = 0, SRC_ATTN = 1, SRC_H = 2 };
+// x: workgroup p < 128 stores packets 16p .. 16p + 15 with one instruction.
+// attn: merger g stores head (2g + hh) elements d with waves 0-3 (64 elements each).
+// h: workgroup p < 256 stores 8 packets per block 3p + j, j = 0, 1, 2; its last block is polled.
+template <int SRC>
+__device__ __forceinline__ int sentinel_count() {
+    return SRC == SRC_X ? H / 16 : SRC == SRC_ATTN ? 4 * NKV : NWG;
 }
+template <int SRC>
+__device__ __forceinline__ int sentinel_of(int t) {
+    if constexpr (SRC == SRC_X) return 16 * t;
+    else if constexpr (SRC == SRC_ATTN) return (t / 4) * 2 * HD + (t % 4) * 64;
+    else return 8 * (3 * t + 2);
+}
+
+struct Shared {
+    uint8_t A[96 * 1024];  // activation operands (1 KiB per q4 group / 512 B per q8 group, K <= 6144)
+    float fx[192 * 2];     // per-group (2^(e-21), sum X * 2^(e-21))
+    float red[WAVES * 64];
+    float emb[H];          // embedding of the token being decoded
+    float xown[16];        // residual rows of this workgroup's O / down block (workgroups < 128)
+    float qs[2][HD];       // attention: two query heads
+    float ktail[HD], vtail[HD];
+    float sc[2][ATT_BLOCK];
+    float ored[WAVES][2][HD];
+    float misc[64];
+    int imisc[64];
+    uint64_t tmark[2];  // profiling builds: sentinel / packet times of the last vector staging
+};
 
 // ------------------------------------------------------------------------------------------
-// Activation staging for one token: fp32 vector (coherent loads) -> 22-bit slices -> A operands.
-// Rows 0, 1, 2 of each group tile hold the hi, mid, lo slices; rows 3..15 stay zero (zeroed at
-// kernel start).
+// Activation staging for one token: 8 consecutive activations per unit, units u = tid and
+// tid + 512 (K / 8 units) -> optional RMSNorm -> 22-bit slices -> A operands.  Rows 0, 1, 2 of each
+// group tile hold the hi, mid, lo slices; rows 3..15 stay zero (zeroed at kernel start).
 
 template <int FMT>
-__device__ void stage_vec(Shared& S, const float* src, int K, const float* norm_w) {
+__device__ __forceinline__ void stage_vals(Shared& S, float (&v)[2][8], int K, const float* norm_w) {
     constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
     constexpr int TILE = (FMT == FMT_Q4) ? 1024 : 512;
     const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
     const int nunits = K / 8;
-    float v[2][8];
-    float ss = 0.f;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int u = tid + it * THREADS;
-        if (u < nunits) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float2 p = ldf2(src + u * 8 + 2 * i);
-                v[it][2 * i] = p.x;
-                v[it][2 * i + 1] = p.y;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) ss += v[it][i] * v[it][i];
-        }
-    }
     float scale = 1.f;
     if (norm_w) {
+        float ss = 0.f;
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+            if (tid + it * THREADS < nunits)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss += v[it][i] * v[it][i];
         ss = wave_sum(ss);
         if (lane == 0) S.red[wave] = ss;
         __syncthreads();
@@ -215,12 +221,12 @@ __device__ void stage_vec(Shared& S, const float* src, int K, const float* norm_
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
-        int bits = (int)as_u32(amax);
+        int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
         bits = max(bits, dpp_i<DPP_XOR1>(bits));
         bits = max(bits, dpp_i<DPP_XOR2>(bits));
         if constexpr (G == 64) bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
         int e = ((bits >> 23) & 0xFF) - 127;
-        if (bits == 0) e = -100;
+        if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
         const int sh = 21 - e;
         int X[8], xs = 0;
 #pragma unroll
@@ -273,8 +279,50 @@ __device__ void stage_vec(Shared& S, const float* src, int K, const float* norm_
     __syncthreads();
 }
 
+// Stages a packet vector of K values (round `tag`).  false (for the whole workgroup) on error.
+template <int FMT, int SRC>
+__device__ __forceinline__ bool stage_packets(Shared& S, const uint64_t* src, unsigned tag, int K, const float* norm_w,
+                              unsigned* err) {
+    if (!wait_sentinels(src, sentinel_count<SRC>(), [](int t) { return sentinel_of<SRC>(t); }, tag, err)) return false;
+#ifdef ICUA_PERSIST_TRACE
+    if (my_tid() == 0) S.tmark[0] = wall_clock64();
+#endif
+    const int tid = my_tid();
+    const int nunits = K / 8;
+    uint64_t p[16];
+    const bool ok = poll<16>(
+        src,
+        [&](int i) {
+            const int u = tid + (i / 8) * THREADS;
+            return u < nunits ? u * 8 + i % 8 : -1;
+        },
+        tag, p, err);
+    if (__syncthreads_or(!ok)) return false;
+#ifdef ICUA_PERSIST_TRACE
+    if (my_tid() == 0) S.tmark[1] = wall_clock64();
+#endif
+    float v[2][8];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i / 8][i % 8] = val_of(p[i]);
+    stage_vals<FMT>(S, v, K, norm_w);
+    return true;
+}
+
+// Stages the embedding held in LDS (K = H).
+template <int FMT>
+__device__ __forceinline__ void stage_emb(Shared& S, const float* norm_w) {
+    const int tid = my_tid();
+    float v[2][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        v[0][i] = tid < H / 8 ? S.emb[tid * 8 + i] : 0.f;
+        v[1][i] = 0.f;
+    }
+    stage_vals<FMT>(S, v, H, norm_w);
+}
+
 // One 1 KiB chunk of a 16-row block against the staged operands; returns the lane's partial
-// (lanes 0-15 hold rows 0-15 of the block for the token).
+// (lanes 0-15 hold rows 0-15 of the block).
 template <int FMT>
 __device__ __forceinline__ float chunk_mac(const Shared& S, uint4 wv, uint2 sbv, int c, int lane) {
     float acc = 0.f;
@@ -311,13 +359,38 @@ __device__ __forceinline__ float chunk_mac(const Shared& S, uint4 wv, uint2 sbv,
     return acc;
 }
 
-// Chunk geometry: q4 chunk = 128 K (two 64-K groups), q8 chunk = 64 K (two 32-K groups).
+// Scales of chunk c of tiled row `row`: q4 chunk = 128 K (two half2 (scale, bias) of 64-K
+// groups), q8 chunk = 64 K (two half scales of 32-K groups).
 template <int FMT>
 __device__ __forceinline__ uint2 load_sb(const uint8_t* sb, int row, int K, int c) {
     if constexpr (FMT == FMT_Q4)
         return *(const uint2*)(sb + ((size_t)row * (K / 64) + 2 * c) * 4);
     else
         return make_uint2(*(const uint32_t*)(sb + ((size_t)row * (K / 32) + 2 * c) * 2), 0u);
+}
+
+// The CW chunks of wave `wave` of 16-row block rb (chunks wave * CW .. wave * CW + CW - 1).
+template <int FMT, int CW>
+__device__ __forceinline__ void load_block(const uint8_t* w, const uint8_t* sb, int rb, int K, int wave, int lane,
+                                           uint4 (&wv)[CW], uint2 (&sbv)[CW]) {
+    constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
+    const int cpb = K / CHK;
+    const uint8_t* blk = w + (size_t)rb * cpb * 1024;
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+        const int c = wave * CW + i;
+        wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
+        sbv[i] = load_sb<FMT>(sb, rb * 16 + lane % 16, K, c);
+    }
+}
+
+template <int FMT, int CW>
+__device__ __forceinline__ float block_mac(const Shared& S, const uint4 (&wv)[CW], const uint2 (&sbv)[CW], int wave,
+                                           int lane) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < CW; ++i) acc += chunk_mac<FMT>(S, wv[i], sbv[i], wave * CW + i, lane);
+    return acc;
 }
 
 // Cross-wave sum of per-lane partials; returns the total in wave 0 (lanes 0-15 meaningful).
@@ -344,75 +417,75 @@ __device__ __forceinline__ void norm_rope(float& a, float& b, const float* w, co
 }
 
 // ------------------------------------------------------------------------------------------
+// Stage timeline of the last step of a launch (per workgroup, per layer, 32 event slots; steady
+// clock), compiled only with -DICUA_PERSIST_TRACE for profiling builds.  Slots 16 + 2k and
+// 17 + 2k: sentinels seen and packets read by the k-th vector staging of the layer.
+#ifdef ICUA_PERSIST_TRACE
+__device__ uint64_t g_trace[NWG][MAX_LAYERS + 1][32];
+#define PK_TRACE(layer, ev)                                                                  \
+    do {                                                                                     \
+        if (step == a.nsteps - 1 && my_tid() == 0) g_trace[w][layer][ev] = wall_clock64(); \
+    } while (0)
+#define PK_TRACE_MARKS(layer, k)                                           \
+    do {                                                                   \
+        if (step == a.nsteps - 1 && my_tid() == 0) {                       \
+            g_trace[w][layer][16 + 2 * (k)] = S.tmark[0];                  \
+            g_trace[w][layer][17 + 2 * (k)] = S.tmark[1];                  \
+        }                                                                  \
+    } while (0)
+#else
+#define PK_TRACE(layer, ev) \
+    do {                    \
+    } while (0)
+#define PK_TRACE_MARKS(layer, k) \
+    do {                         \
+    } while (0)
+#endif
 
 template <int FMT>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
-    constexpr int CPB2 = (FMT == FMT_Q4) ? H / 128 : H / 64;    // chunks per block, K = 2048
-    constexpr int CPB6 = (FMT == FMT_Q4) ? FF / 128 : FF / 64;  // K = 6144
-    constexpr int CW2 = CPB2 / WAVES, CW6 = CPB6 / WAVES;       // chunks per wave
+    constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
+    constexpr int CW2 = H / CHK / WAVES;   // chunks per wave, K = 2048
+    constexpr int CW6 = FF / CHK / WAVES;  // K = 6144
+    constexpr int NRB = VOCAB / 16;        // lm_head row blocks
     __shared__ Shared S;
     const int w = blockIdx.x;
-    unsigned* sync = a.sync;
+    uint64_t* ll = a.ll;
+    unsigned* err = (unsigned*)a.ll + ERRW;
     for (int i = my_tid(); i < (int)sizeof(S.A) / 4; i += THREADS) ((uint32_t*)S.A)[i] = 0u;
+
+    // Control block and the embedding of the first token (written before this launch).
+    State* st = a.st;
+    if (st->done || st->n != 1) return;  // single-row passes only (checked by the host too)
+    int pos = st->pos, stp = st->step;
+    const int maxsteps = st->maxsteps, eos0 = st->eos0, eos1 = st->eos1, maxctx = st->maxctx;
+    for (int i = my_tid(); i < H; i += THREADS) S.emb[i] = a.x[i];
+    if (my_tid() < 16 && w < H / 16) S.xown[my_tid()] = a.x[w * 16 + my_tid()];
     __syncthreads();
 
     const int L = a.nlayers;
     for (int step = 0; step < a.nsteps; ++step) {
-        if (!wait_single(S, sync, C_COMMIT, (unsigned)step)) return;
-        const int done = ldi(&a.st->done);
-        const int pos = ldi(&a.st->pos);
-        if (done) break;
-        if (pos + 1 > a.maxctx || ldi(&a.st->n) != 1) break;  // host-checked; single-row passes only
+        if (pos + 1 > maxctx) break;  // the commit stops earlier; guards the cache row
         for (int l = 0; l < L; ++l) {
             const LayerPtrs& P = a.layers[l];
-            const unsigned round = (unsigned)(step * L + l);  // completed layers before this one
+            const unsigned r = (unsigned)(step * L + l);  // round of this layer
 
-            // ---------------- QKV: row block w -------------------------------------------
+            // Attention geometry of this workgroup (KV group g, split s) and its first block of
+            // K/V rows, issued before the QKV stage so that they stream in behind it.  The pos + 1
+            // rows of the group (rows < pos and the new row) are spread evenly over the 32 splits;
+            // the split holding row pos writes it.  Only rows < pos are loaded from the cache.
+            const int g = w % NKV, s = w / NKV;
+            const int tot = pos + 1;
+            const int chunk = (tot + ATT_SPLITS - 1) / ATT_SPLITS;
+            const int j0 = min(s * chunk, tot), j1 = min(j0 + chunk, tot);
+            const bool tail = (j0 <= pos) && (pos < j1);
+            const int nprior = max(0, min(j1, pos) - j0);
+            const int ntot = j1 - j0;
+            const uint16_t* kb = a.kv + ((size_t)(l * 2 + 0) * NKV + g) * a.maxctx * HD;
+            const uint16_t* vb = a.kv + ((size_t)(l * 2 + 1) * NKV + g) * a.maxctx * HD;
+            uint4 kr[ATT_SPQ], vr[ATT_SPQ];
             {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64, r16 = lane % 16;
-                (void)r16;
-                const int rb = w;
-                uint4 wv[CW2];
-                uint2 sbv[CW2];
-                const uint8_t* blk = P.wqkv + (size_t)rb * CPB2 * 1024;
-#pragma unroll
-                for (int i = 0; i < CW2; ++i) {
-                    const int c = wave * CW2 + i;
-                    wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
-                    sbv[i] = load_sb<FMT>(P.wqkv_sb, rb * 16 + r16, H, c);
-                }
-                // Layer 0 reads the embedding the commit wrote (already waited for above).
-                if (l > 0 && !wait_fan(S, sync, C_DOWN, round * (NWG / 2) / 16)) return;
-                stage_vec<FMT>(S, a.x, H, P.attn_norm);
-                float acc = 0.f;
-#pragma unroll
-                for (int i = 0; i < CW2; ++i) acc += chunk_mac<FMT>(S, wv[i], sbv[i], wave * CW2 + i, lane);
-                const float y = reduce_waves(S, acc);
-                if (wave == 0 && lane < 16) stf(a.qkv + rb * 16 + lane, y);
-                const int g = rb < 128 ? rb / 16 : rb < 192 ? (rb - 128) / 8 : (rb - 192) / 8;
-                arrive(sync, C_QKV + g);
-            }
-
-            // ---------------- attention: group g, slot range s ----------------------------
-            // The pos + 1 rows (cache rows 0..pos-1 and the new row pos) are split evenly over
-            // the group's 32 workgroups; the one whose range holds row pos writes it.
-            {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64, r16 = lane % 16;
-                (void)r16;
-                const int g = w / ATT_SPLITS, s = w % ATT_SPLITS;
-                const int tot = pos + 1;
-                const int chunk = (tot + ATT_SPLITS - 1) / ATT_SPLITS;
-                const int j0 = min(s * chunk, tot), j1 = min(j0 + chunk, tot);
-                const bool tail = (j0 <= pos) && (pos < j1);
-                const int nprior = max(0, min(j1, pos) - j0);
-                const int ntot = j1 - j0;
-                const int quad = tid / 16, ql = tid % 16;  // 32 quarter-waves, 8 dims per lane
-                const uint16_t* kb = a.kv + ((size_t)(l * 2 + 0) * NKV + g) * a.maxctx * HD;
-                const uint16_t* vb = a.kv + ((size_t)(l * 2 + 1) * NKV + g) * a.maxctx * HD;
-                // First block of K/V rows (ATT_SPQ slots per quarter-wave), issued before the wait.
-                // Only rows < pos are ever loaded: row pos is written during this step by another
-                // workgroup, and a line of it cached early would go stale.
-                uint4 kr[ATT_SPQ], vr[ATT_SPQ];
+                const int tid = my_tid(), quad = tid / 16, ql = tid % 16;
 #pragma unroll
                 for (int i = 0; i < ATT_SPQ; ++i) {
                     const int p = quad + 32 * i;
@@ -423,29 +496,78 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                         vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
                     }
                 }
-                if (!wait_single(S, sync, C_QKV + g, (round + 1) * 32)) return;
-                const float* rope = a.rope + (size_t)pos * 128;
-                if (wave < 2) {  // queries of heads 2g, 2g+1
-                    const int hh = wave;
-                    float x0 = ldf(a.qkv + (2 * g + hh) * HD + lane), x1 = ldf(a.qkv + (2 * g + hh) * HD + lane + 64);
-                    norm_rope(x0, x1, P.q_norm, rope, lane);
-                    const float qscale = 1.0f / sqrtf((float)HD);
-                    S.qs[hh][lane] = x0 * qscale;
-                    S.qs[hh][lane + 64] = x1 * qscale;
-                } else if (wave == 2 && tail) {  // the new K/V row of this group
-                    float k0 = ldf(a.qkv + H + g * HD + lane), k1 = ldf(a.qkv + H + g * HD + lane + 64);
-                    norm_rope(k0, k1, P.k_norm, rope, lane);
-                    const float v0 = ldf(a.qkv + H + NKV * HD + g * HD + lane);
-                    const float v1 = ldf(a.qkv + H + NKV * HD + g * HD + lane + 64);
-                    S.ktail[lane] = h2f(f2h(k0));
-                    S.ktail[lane + 64] = h2f(f2h(k1));
-                    S.vtail[lane] = h2f(f2h(v0));
-                    S.vtail[lane + 64] = h2f(f2h(v1));
+            }
+
+            // ---------------- QKV: row block w ---------------------------------------------
+            {
+                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
+                PK_TRACE(l, 0);
+                uint4 wv[CW2];
+                uint2 sbv[CW2];
+                load_block<FMT, CW2>(P.wqkv, P.wqkv_sb, w, H, wave, lane, wv, sbv);
+                if (l == 0) {
+                    stage_emb<FMT>(S, P.attn_norm);
+                } else if (!stage_packets<FMT, SRC_X>(S, ll + XP, 2 * r, H, P.attn_norm, err)) {
+                    return;
+                }
+                PK_TRACE(l, 1);
+                if (l > 0) PK_TRACE_MARKS(l, 0);
+                const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv, sbv, wave, lane));
+                if (wave == 0 && lane < 16) st64(ll + QKVP + w * 16 + lane, pack(y, r + 1));
+                PK_TRACE(l, 2);
+            }
+
+            // ---------------- attention: group g, split s ----------------------------------
+            {
+                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
+                const int quad = tid / 16, ql = tid % 16;  // 32 quarter-waves, 8 dims per lane
+                // Sentinels: the 32 QKV blocks of group g (q heads 2g, 2g+1: blocks 16g..16g+15;
+                // k: 128 + 8g..; v: 192 + 8g..), lane 0 of each.
+                if (!wait_sentinels(
+                        ll + QKVP, 32,
+                        [&](int t) {
+                            const int b = t < 16 ? 16 * g + t : t < 24 ? 128 + 8 * g + (t - 16) : 192 + 8 * g + (t - 24);
+                            return 16 * b;
+                        },
+                        r + 1, err))
+                    return;
+                // Queries of heads 2g, 2g+1 (waves 0, 1); the tail split's wave 2 also takes the
+                // new K and V rows of the group.
+                {
+                    const bool needs = wave < 2 || (wave == 2 && tail);
+                    const int qoff = (2 * g + wave) * HD + lane;
+                    const int koff = H + g * HD + lane, voff = H + NKV * HD + g * HD + lane;
+                    uint64_t p[4];
+                    bool ok = true;
+                    if (needs)
+                        ok = poll<4>(
+                            ll + QKVP,
+                            [&](int i) {
+                                if (wave < 2) return i < 2 ? qoff + 64 * i : -1;
+                                return i < 2 ? koff + 64 * i : voff + 64 * (i - 2);
+                            },
+                            r + 1, p, err);
+                    if (__syncthreads_or(!ok)) return;
+                    PK_TRACE(l, 3);
+                    const float* rope = a.rope + (size_t)pos * 128;
+                    if (wave < 2) {
+                        float x0 = val_of(p[0]), x1 = val_of(p[1]);
+                        norm_rope(x0, x1, P.q_norm, rope, lane);
+                        const float qscale = 1.0f / sqrtf((float)HD);
+                        S.qs[wave][lane] = x0 * qscale;
+                        S.qs[wave][lane + 64] = x1 * qscale;
+                    } else if (needs) {
+                        float k0 = val_of(p[0]), k1 = val_of(p[1]);
+                        norm_rope(k0, k1, P.k_norm, rope, lane);
+                        S.ktail[lane] = h2f(f2h(k0));
+                        S.ktail[lane + 64] = h2f(f2h(k1));
+                        S.vtail[lane] = h2f(f2h(val_of(p[2])));
+                        S.vtail[lane + 64] = h2f(f2h(val_of(p[3])));
+                    }
                 }
                 __syncthreads();
                 if (tail && tid < 128) {
-                    // The new cache row, written through to the coherence point (device-scope
-                    // stores) so that any workgroup reads it in the next step.
+                    // The new cache row (fp16), device-scope stores.
                     const float* src = tid < 64 ? S.ktail : S.vtail;
                     uint16_t* dst = (uint16_t*)(tid < 64 ? kb : vb) + (size_t)pos * HD;
                     const int d = 2 * (tid % 64);
@@ -479,13 +601,14 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                     const int pnew = tail ? pos - j0 - b0 : -1;
 #pragma unroll
                     for (int i = 0; i < ATT_SPQ; ++i) {
-                        const int p = quad + 32 * i;
-                        if (p == pnew) {
+                        if (quad + 32 * i == pnew) {
                             uint32_t kk[4], vv[4];
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
-                                kk[j] = (uint32_t)f2h(S.ktail[8 * ql + 2 * j]) | ((uint32_t)f2h(S.ktail[8 * ql + 2 * j + 1]) << 16);
-                                vv[j] = (uint32_t)f2h(S.vtail[8 * ql + 2 * j]) | ((uint32_t)f2h(S.vtail[8 * ql + 2 * j + 1]) << 16);
+                                kk[j] = (uint32_t)f2h(S.ktail[8 * ql + 2 * j]) |
+                                        ((uint32_t)f2h(S.ktail[8 * ql + 2 * j + 1]) << 16);
+                                vv[j] = (uint32_t)f2h(S.vtail[8 * ql + 2 * j]) |
+                                        ((uint32_t)f2h(S.vtail[8 * ql + 2 * j + 1]) << 16);
                             }
                             kr[i] = make_uint4(kk[0], kk[1], kk[2], kk[3]);
                             vr[i] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
@@ -513,8 +636,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                         }
                     }
                     __syncthreads();
-                    // Block softmax statistics: waves 0 and 1, one head each, ATT_BLOCK / 64 slots
-                    // per lane.
+                    // Block softmax statistics: waves 0 and 1, one head each.
                     if (wave < 2) {
                         float sv[ATT_BLOCK / 64];
                         float mb = -__builtin_inff();
@@ -534,7 +656,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                         }
                         ls = wave_sum(ls);
                         if (lane == 0) {
-                            S.misc[wave] = mn;  // new running max
+                            S.misc[wave] = mn;
                             S.misc[2 + wave] = ls;
                         }
                     }
@@ -579,223 +701,227 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
 #pragma unroll
                         for (int d = 0; d < 8; ++d) S.ored[wave][hh][8 * ql + d] = o[hh][d];
                 }
+                // The new cache row is acknowledged before this workgroup's next packet.
+                __builtin_amdgcn_s_waitcnt(0);
                 __syncthreads();
-                float* part = a.part + (size_t)(g * ATT_SPLITS + s) * 2 * PART;
+                uint64_t* part = ll + PARTP + (size_t)(g * ATT_SPLITS + s) * 2 * PART;
                 if (tid < 2 * HD) {
                     const int hh = tid / HD, d = tid % HD;
                     float acc = 0.f;
                     for (int ww = 0; ww < WAVES; ++ww) acc += S.ored[ww][hh][d];
-                    stf(part + hh * PART + d, acc);
+                    st64(part + hh * PART + d, pack(acc, r + 1));
                     if (d == 0) {
-                        stf(part + hh * PART + HD, m_run[hh]);
-                        stf(part + hh * PART + HD + 1, l_run[hh]);
+                        st64(part + hh * PART + HD, pack(m_run[hh], r + 1));
+                        st64(part + hh * PART + HD + 1, pack(l_run[hh], r + 1));
                     }
                 }
-                const unsigned old = arrive(sync, C_ATT + g);
-                if (tid == 0) S.flag = (old == (round + 1) * ATT_SPLITS - 1);
-                __syncthreads();
-                if (S.flag) {  // last split of this group to finish: merge the 32 partials
-                    const float* gp = a.part + (size_t)g * ATT_SPLITS * 2 * PART;
-                    if (tid < 2 * HD) {
-                        const int hh = tid / HD, d = tid % HD;
-                        float m[ATT_SPLITS], lv[ATT_SPLITS], ov[ATT_SPLITS];
-#pragma unroll
-                        for (int ss = 0; ss < ATT_SPLITS; ++ss) {  // all loads in flight at once
-                            const float* pp = gp + (ss * 2 + hh) * PART;
-                            m[ss] = ldf(pp + HD);
-                            lv[ss] = ldf(pp + HD + 1);
-                            ov[ss] = ldf(pp + d);
-                        }
-                        float mx = -__builtin_inff();
-#pragma unroll
-                        for (int ss = 0; ss < ATT_SPLITS; ++ss) mx = fmaxf(mx, m[ss]);
-                        float Lsum = 0.f, O = 0.f;
-#pragma unroll
-                        for (int ss = 0; ss < ATT_SPLITS; ++ss) {
-                            const float wgt = (m[ss] == -__builtin_inff()) ? 0.f : expf(m[ss] - mx);
-                            Lsum = fmaf(wgt, lv[ss], Lsum);
-                            O = fmaf(wgt, ov[ss], O);
-                        }
-                        stf(a.attn + (2 * g + hh) * HD + d, O / Lsum);
-                    }
-                    arrive(sync, C_MERGED);
-                }
+                PK_TRACE(l, 4);
             }
 
-            // ---------------- O projection: workgroups 0..127 ------------------------------
+            // ---------------- merge of group g: workgroups 248..255 ------------------------
+            // Thread t: half = t / 256 (splits 16 half .. 16 half + 15), head hh, element d; the
+            // threads with d < 16 also fetch (m, l) of split 16 half + d.  Each half is merged with
+            // its own maximum, then the two halves are combined.
+            if (w >= MERGER0) {
+                const int tid = my_tid();
+                const int half = tid / 256, hh = (tid / HD) & 1, d = tid % HD;
+                const uint64_t* gp = ll + PARTP + (size_t)g * ATT_SPLITS * 2 * PART;
+                // Sentinels: per split and head, the m packet and the o packet stored by the second
+                // wave of that head (element 64).
+                if (!wait_sentinels(
+                        gp, 4 * ATT_SPLITS,
+                        [](int t) { return ((t / 4) * 2 + (t % 4) / 2) * PART + ((t % 2) ? 64 : HD); }, r + 1,
+                        err))
+                    return;
+                uint64_t p[18];
+                const bool ok = poll<18>(
+                    gp,
+                    [&](int i) {
+                        if (i < 16) return ((half * 16 + i) * 2 + hh) * PART + d;
+                        return d < 16 ? ((half * 16 + d) * 2 + hh) * PART + HD + (i - 16) : -1;
+                    },
+                    r + 1, p, err);
+                if (__syncthreads_or(!ok)) return;
+                float* ml = &S.sc[0][0];  // [half][hh][16][2]
+                if (d < 16) {
+                    ml[((half * 2 + hh) * 16 + d) * 2] = val_of(p[16]);
+                    ml[((half * 2 + hh) * 16 + d) * 2 + 1] = val_of(p[17]);
+                }
+                __syncthreads();
+                const float* mlh = ml + (half * 2 + hh) * 32;
+                float mx = -__builtin_inff();
+#pragma unroll
+                for (int j = 0; j < 16; ++j) mx = fmaxf(mx, mlh[2 * j]);
+                float Lh = 0.f, Oh = 0.f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const float m = mlh[2 * j];
+                    const float wgt = (m == -__builtin_inff()) ? 0.f : expf(m - mx);
+                    Lh = fmaf(wgt, mlh[2 * j + 1], Lh);
+                    Oh = fmaf(wgt, val_of(p[j]), Oh);
+                }
+                S.ored[half][hh][d] = Oh;
+                if (d == 0) {
+                    S.misc[(half * 2 + hh) * 2] = mx;
+                    S.misc[(half * 2 + hh) * 2 + 1] = Lh;
+                }
+                __syncthreads();
+                if (half == 0) {
+                    const float m0 = S.misc[hh * 2], l0 = S.misc[hh * 2 + 1];
+                    const float m1 = S.misc[(2 + hh) * 2], l1 = S.misc[(2 + hh) * 2 + 1];
+                    const float M = fmaxf(m0, m1);  // finite: the split holding row pos is never empty
+                    const float w0 = (m0 == -__builtin_inff()) ? 0.f : expf(m0 - M);
+                    const float w1 = (m1 == -__builtin_inff()) ? 0.f : expf(m1 - M);
+                    const float out = (w0 * Oh + w1 * S.ored[1][hh][d]) / (w0 * l0 + w1 * l1);
+                    st64(ll + ATTNP + (2 * g + hh) * HD + d, pack(out, r + 1));
+                }
+                PK_TRACE(l, 5);
+            }
+
+            // ---------------- O projection + residual: workgroups 0..127 -------------------
             if (w < H / 16) {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64, r16 = lane % 16;
-                (void)r16;
-                const int rb = w;
+                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
                 uint4 wv[CW2];
                 uint2 sbv[CW2];
-                const uint8_t* blk = P.wo + (size_t)rb * CPB2 * 1024;
-#pragma unroll
-                for (int i = 0; i < CW2; ++i) {
-                    const int c = wave * CW2 + i;
-                    wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
-                    sbv[i] = load_sb<FMT>(P.wo_sb, rb * 16 + r16, H, c);
-                }
-                if (!wait_single(S, sync, C_MERGED, (round + 1) * NKV)) return;
-                stage_vec<FMT>(S, a.attn, H, nullptr);
-                float acc = 0.f;
-#pragma unroll
-                for (int i = 0; i < CW2; ++i) acc += chunk_mac<FMT>(S, wv[i], sbv[i], wave * CW2 + i, lane);
-                const float y = reduce_waves(S, acc);
+                load_block<FMT, CW2>(P.wo, P.wo_sb, w, H, wave, lane, wv, sbv);
+                if (!stage_packets<FMT, SRC_ATTN>(S, ll + ATTNP, r + 1, H, nullptr, err)) return;
+                PK_TRACE(l, 6);
+                PK_TRACE_MARKS(l, 1);
+                const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv, sbv, wave, lane));
                 if (wave == 0 && lane < 16) {
-                    float* xo = a.x + rb * 16 + lane;
-                    stf(xo, ldf(xo) + y);
+                    const float xn = S.xown[lane] + y;
+                    S.xown[lane] = xn;
+                    st64(ll + XP + w * 16 + lane, pack(xn, 2 * r + 1));
                 }
-                arrive(sync, C_O + (w % 16));
+                PK_TRACE(l, 7);
             }
 
-            // ---------------- gate|up + SwiGLU: blocks 3w .. 3w + 2 ------------------------
+            // ---------------- RMSNorm + gate|up + SwiGLU: blocks 3w .. 3w + 2 --------------
             {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64, r16 = lane % 16;
-                (void)r16;
+                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
                 uint4 wv[3][CW2];
                 uint2 sbv[3][CW2];
 #pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const int rb = 3 * w + j;
-                    const uint8_t* blk = P.wgu + (size_t)rb * CPB2 * 1024;
-#pragma unroll
-                    for (int i = 0; i < CW2; ++i) {
-                        const int c = wave * CW2 + i;
-                        wv[j][i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
-                        sbv[j][i] = load_sb<FMT>(P.wgu_sb, rb * 16 + r16, H, c);
-                    }
-                }
-                if (!wait_fan(S, sync, C_O, (round + 1) * (H / 16) / 16)) return;
-                stage_vec<FMT>(S, a.x, H, P.mlp_norm);
+                for (int j = 0; j < 3; ++j) load_block<FMT, CW2>(P.wgu, P.wgu_sb, 3 * w + j, H, wave, lane, wv[j], sbv[j]);
+                if (!stage_packets<FMT, SRC_X>(S, ll + XP, 2 * r + 1, H, P.mlp_norm, err)) return;
+                PK_TRACE(l, 8);
+                PK_TRACE_MARKS(l, 2);
 #pragma unroll
                 for (int j = 0; j < 3; ++j) {
-                    float acc = 0.f;
-#pragma unroll
-                    for (int i = 0; i < CW2; ++i) acc += chunk_mac<FMT>(S, wv[j][i], sbv[j][i], wave * CW2 + i, lane);
-                    const float y = reduce_waves(S, acc);
+                    const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv[j], sbv[j], wave, lane));
                     if (wave == 0) {
+                        // Block 3w + j: gate units 8 (3w + j) + 0..7 in lanes 0-7, their up rows in 8-15.
                         const float up = __shfl_xor(y, 8);
-                        if (lane < 8) stf(a.h + (3 * w + j) * 8 + lane, (y / (1.f + expf(-y))) * up);
+                        if (lane < 8)
+                            st64(ll + HP + (3 * w + j) * 8 + lane, pack((y / (1.f + expf(-y))) * up, r + 1));
                     }
                 }
-                arrive(sync, C_GU + (w % 16));
+                PK_TRACE(l, 9);
             }
 
             // ---------------- down + residual: workgroups 0..127 ---------------------------
             if (w < H / 16) {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64, r16 = lane % 16;
-                (void)r16;
-                const int rb = w;
+                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
                 uint4 wv[CW6];
                 uint2 sbv[CW6];
-                const uint8_t* blk = P.wd + (size_t)rb * CPB6 * 1024;
-#pragma unroll
-                for (int i = 0; i < CW6; ++i) {
-                    const int c = wave * CW6 + i;
-                    wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
-                    sbv[i] = load_sb<FMT>(P.wd_sb, rb * 16 + r16, FF, c);
-                }
-                if (!wait_fan(S, sync, C_GU, (round + 1) * NWG / 16)) return;
-                stage_vec<FMT>(S, a.h, FF, nullptr);
-                float acc = 0.f;
-#pragma unroll
-                for (int i = 0; i < CW6; ++i) acc += chunk_mac<FMT>(S, wv[i], sbv[i], wave * CW6 + i, lane);
-                const float y = reduce_waves(S, acc);
+                load_block<FMT, CW6>(P.wd, P.wd_sb, w, FF, wave, lane, wv, sbv);
+                if (!stage_packets<FMT, SRC_H>(S, ll + HP, r + 1, FF, nullptr, err)) return;
+                PK_TRACE(l, 10);
+                PK_TRACE_MARKS(l, 3);
+                const float y = reduce_waves(S, block_mac<FMT, CW6>(S, wv, sbv, wave, lane));
                 if (wave == 0 && lane < 16) {
-                    float* xo = a.x + rb * 16 + lane;
-                    stf(xo, ldf(xo) + y);
+                    const float xn = S.xown[lane] + y;
+                    S.xown[lane] = xn;
+                    st64(ll + XP + w * 16 + lane, pack(xn, 2 * r + 2));
                 }
-                arrive(sync, C_DOWN + (w % 16));
+                PK_TRACE(l, 11);
             }
         }
 
-        // ---------------- lm_head + argmax partials ---------------------------------------
+        // ---------------- final RMSNorm + lm_head + per-workgroup argmax ---------------------
         {
-            const int tid = my_tid(), lane = tid % 64, wave = tid / 64, r16 = lane % 16;
-            const unsigned round = (unsigned)((step + 1) * L);
-            constexpr int NRB = VOCAB / 16;
-            uint4 wv[CW2];
-            uint2 sbv[CW2];
-            int rb = w;
-            auto load_block = [&](int b) {
-                const uint8_t* blk = a.E + (size_t)b * CPB2 * 1024;
-#pragma unroll
-                for (int i = 0; i < CW2; ++i) {
-                    const int c = wave * CW2 + i;
-                    wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
-                    sbv[i] = load_sb<FMT>(a.Esb, b * 16 + r16, H, c);
-                }
-            };
-            load_block(rb);
-            if (!wait_fan(S, sync, C_DOWN, round * (NWG / 2) / 16)) return;
-            stage_vec<FMT>(S, a.x, H, a.final_norm);
+            const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
+            const unsigned r_last = (unsigned)(step * L + L - 1);
+            PK_TRACE(L, 0);
+            uint4 wv0[CW2], wv1[CW2];
+            uint2 sb0[CW2], sb1[CW2];
+            load_block<FMT, CW2>(a.E, a.Esb, w, H, wave, lane, wv0, sb0);
+            load_block<FMT, CW2>(a.E, a.Esb, w + NWG, H, wave, lane, wv1, sb1);
+            if (!stage_packets<FMT, SRC_X>(S, ll + XP, 2 * r_last + 2, H, a.final_norm, err)) return;
+            PK_TRACE(L, 1);
+            PK_TRACE_MARKS(L, 0);
             float best = -__builtin_inff();
             int besti = 0x7fffffff;
-            for (; rb < NRB; rb += NWG) {
-                uint4 cur[CW2];
-                uint2 csb[CW2];
-#pragma unroll
-                for (int i = 0; i < CW2; ++i) {
-                    cur[i] = wv[i];
-                    csb[i] = sbv[i];
+            // Two blocks in flight (static ping-pong buffers): a block computes while the block
+            // two ahead loads.  Blocks w + k * 256; every workgroup has at least 37.
+            for (int rb = w; rb < NRB; rb += 2 * NWG) {
+                {
+                    const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv0, sb0, wave, lane));
+                    if (wave == 0 && lane < 16) argmax_merge(best, besti, y, rb * 16 + lane);
+                    if (rb + 2 * NWG < NRB) load_block<FMT, CW2>(a.E, a.Esb, rb + 2 * NWG, H, wave, lane, wv0, sb0);
                 }
-                if (rb + NWG < NRB) load_block(rb + NWG);  // next block in flight while computing
-                float acc = 0.f;
-#pragma unroll
-                for (int i = 0; i < CW2; ++i) acc += chunk_mac<FMT>(S, cur[i], csb[i], wave * CW2 + i, lane);
-                const float y = reduce_waves(S, acc);
-                if (wave == 0 && lane < 16) argmax_merge(best, besti, y, rb * 16 + lane);
+                if (rb + NWG < NRB) {
+                    const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv1, sb1, wave, lane));
+                    if (wave == 0 && lane < 16) argmax_merge(best, besti, y, (rb + NWG) * 16 + lane);
+                    if (rb + 3 * NWG < NRB) load_block<FMT, CW2>(a.E, a.Esb, rb + 3 * NWG, H, wave, lane, wv1, sb1);
+                }
             }
             if (wave == 0) {
                 wave_argmax(best, besti);  // lanes >= 16 hold (-inf, INT_MAX)
                 if (lane == 0) {
-                    stf(a.pval + w, best);
-                    sti(a.pidx + w, besti);
+                    st64(ll + LMP + 2 * w, pack(best, (unsigned)step + 1));
+                    st64(ll + LMP + 2 * w + 1, pack_i(besti, (unsigned)step + 1));
                 }
             }
-            const unsigned old = arrive(sync, C_LM);
-            if (tid == 0) S.flag = (old == (unsigned)((step + 1) * NWG - 1));
+            PK_TRACE(L, 2);
+        }
+
+        // ---------------- greedy commit, evaluated by every workgroup ------------------------
+        {
+            const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
+            uint64_t p[2];
+            const bool ok = poll<2>(
+                ll + LMP, [&](int i) { return tid < NWG ? 2 * tid + i : -1; }, (unsigned)step + 1, p, err);
+            if (__syncthreads_or(!ok)) return;
+            float bv = tid < NWG ? val_of(p[0]) : -__builtin_inff();
+            int bi = tid < NWG ? (int)(uint32_t)p[1] : 0x7fffffff;
+            wave_argmax(bv, bi);
+            if (lane == 0) {
+                S.misc[wave] = bv;
+                S.imisc[wave] = bi;
+            }
             __syncthreads();
-            if (S.flag) {  // last workgroup: greedy commit (Shaders.swift:1501-1571)
-                if (wave == 0) {
-                    float bv = -__builtin_inff();
-                    int bi = 0x7fffffff;
-                    for (int i = lane; i < NWG; i += 64) argmax_merge(bv, bi, ldf(a.pval + i), ldi(a.pidx + i));
-                    wave_argmax(bv, bi);
-                    if (lane == 0) {
-                        State* st = a.st;
-                        int tok = bi;
-                        const bool bad = tok < 0 || tok >= VOCAB;  // no finite logit (NaN model)
-                        if (bad) tok = 0;
-                        const int stp = ldi(&st->step);
-                        int dn = 0;
-                        if (stp >= ldi(&st->maxsteps)) {
-                            dn = 1;
-                            S.misc[8] = -1.f;
-                        } else {
-                            a.out_tokens[stp] = tok;
-                            const int nstep = stp + 1;
-                            const int npos = pos + 1;
-                            sti(&st->pos, npos);
-                            sti(&st->step, nstep);
-                            sti(&st->vis_offset, -1);
-                            sti(&st->n, 1);
-                            dn = (bad || tok == ldi(&st->eos0) || tok == ldi(&st->eos1) ||
-                                  nstep >= ldi(&st->maxsteps) || npos + 2 > ldi(&st->maxctx));
-                            S.misc[8] = dn ? -1.f : (float)tok;
-                        }
-                        if (dn) sti(&st->done, 1);
-                    }
-                }
-                __syncthreads();
-                const float t = S.misc[8];
-                if (t >= 0.f) {
-                    const int tok = (int)t;
-                    for (int i = tid; i < H; i += THREADS) stf(a.x + i, dequant_tiled(FMT, a.E, a.Esb, (size_t)tok, i, H));
-                }
-                arrive(sync, C_COMMIT);
+            float b2 = S.misc[0];
+            int tok = S.imisc[0];
+            for (int ww = 1; ww < WAVES; ++ww) argmax_merge(b2, tok, S.misc[ww], S.imisc[ww]);
+            bool stop;
+            if (stp >= maxsteps) {  // nothing may be written past out_tokens[maxsteps - 1]
+                stop = true;
+            } else {
+                const bool bad = tok < 0 || tok >= VOCAB;  // no finite logit (NaN model): stop on token 0
+                if (bad) tok = 0;
+                if (w == 0 && tid == 0) a.out_tokens[stp] = tok;
+                stp += 1;
+                pos += 1;
+                stop = bad || tok == eos0 || tok == eos1 || stp >= maxsteps || pos + 2 > maxctx;
             }
+            if (w == 0 && tid == 0) {
+                st->pos = pos;
+                st->step = stp;
+                st->n = 1;
+                st->vis_offset = -1;
+                st->logits_rows = 0;
+                if (stop) st->done = 1;
+            }
+            PK_TRACE(L, 3);
+            if (stop) break;
+            // Next token's embedding (Shaders.swift:464-476), in every workgroup.
+            __syncthreads();  // every thread has read S.misc / S.imisc
+            for (int i = tid; i < H; i += THREADS) S.emb[i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)tok, i, H);
+            __syncthreads();
+            if (tid < 16 && w < H / 16) S.xown[tid] = S.emb[w * 16 + tid];
+            if (w == 0 && step == a.nsteps - 1)
+                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row for the host
         }
     }
 }
@@ -805,13 +931,21 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
 hipError_t launch_persistent(int fmt, const PersistArgs& a, hipStream_t s) {
     void* args[] = {(void*)&a};
     if (fmt == FMT_Q4)
-        return hipLaunchCooperativeKernel((const void*)pk::decode_kernel<FMT_Q4>, dim3(pk::NWG), dim3(pk::THREADS), args, 0, s);
+        return hipLaunchCooperativeKernel((const void*)pk::decode_kernel<FMT_Q4>, dim3(pk::NWG), dim3(pk::THREADS),
+                                          args, 0, s);
     if (fmt == FMT_Q8)
-        return hipLaunchCooperativeKernel((const void*)pk::decode_kernel<FMT_Q8>, dim3(pk::NWG), dim3(pk::THREADS), args, 0, s);
+        return hipLaunchCooperativeKernel((const void*)pk::decode_kernel<FMT_Q8>, dim3(pk::NWG), dim3(pk::THREADS),
+                                          args, 0, s);
     return hipErrorInvalidValue;
 }
 
-size_t persistent_sync_bytes() { return (size_t)pk::C_SLOTS * 64 * sizeof(unsigned); }
-int persistent_error_slot() { return pk::C_ERR * 64; }
+#ifdef ICUA_PERSIST_TRACE
+extern "C" int icua_debug_persist_trace(uint64_t* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(pk::g_trace), sizeof(pk::g_trace)) == hipSuccess ? 0 : -1;
+}
+#endif
+
+size_t persistent_sync_bytes() { return ((size_t)pk::PACKETS + 32) * sizeof(uint64_t); }
+int persistent_error_slot() { return pk::ERRW; }
 
 }  // namespace icua
