@@ -4,15 +4,16 @@
 //
 // Why.  As separate kernels a decode step is ~170 dependent launches whose fixed latency
 // (launch, cold weight fetch, prologue, drain: 5-10 us each) dominates the ~180 us the step's
-// bytes need at 8 TB/s.  Here every workgroup stays resident and, before it waits for a stage's
-// inputs, already has the loads of its slice of that stage's weights (and K/V rows) in flight.
+// bytes need at 8 TB/s.  Here every workgroup stays resident; weights, K/V rows and norm vectors
+// are requested one or two stages before they are needed, so HBM streams while the workgroups
+// wait for each other.
 //
 // Grid.  One 512-thread workgroup per CU (256).  Static work split per layer:
 //   QKV   256 row blocks of the fused q|k|v rows (Convert.swift:185-188), block w
 //   attn  KV group g = w % 8, split s = w / 8: the pos + 1 cache rows of the group (rows < pos and
 //         the new row) are spread evenly over the 32 splits; the split holding row pos writes it
-//   merge split 31 of group g (workgroup 248 + g, which has no O / down work) merges the 32
-//         partials of the group
+//   merge splits 28..31 of group g (workgroups 224..255, no O / down work) merge the 32
+//         partials of the group, a quarter of the group's output each
 //   O     128 row blocks, workgroups 0..127
 //   GU    768 row blocks (8 gate + 8 up rows each), blocks 3w .. 3w + 2
 //   down  128 row blocks (K = 6144), workgroups 0..127
@@ -20,19 +21,25 @@
 // commit (Shaders.swift:1501-1571), which every workgroup evaluates redundantly from the 256
 // argmax partials; workgroup 0 alone writes the control block and the token list.
 //
+// Roles inside a workgroup.  Waves 0-3 ("math") hold the weight tiles and K/V rows in registers
+// and run the matrix-core GEMV and attention arithmetic.  Waves 4-7 ("exchange") wait for the
+// inputs of each stage, stage them into LDS and slice them into matrix-core operands.  The split
+// exists because a wave's vector-memory counter retires in issue order: a poll issued behind a
+// wave's outstanding weight loads could not be seen before those loads land.  The exchange waves
+// never load weights, so they see an input as soon as it is written.
+//
 // Data exchange.  Every value that crosses workgroups travels as a 64-bit packet (fp32 value,
 // 32-bit round tag) written with one device-scope store and read with device-scope loads
-// (global_store/load_dwordx2 ... sc1: coherent across the XCDs' L2s without cache flushes).  A
-// consumer polls the packets it needs until each carries the tag of the round it expects, so the
-// data is its own flag: no fences, counters or store acknowledgements on the critical path.
-// A buffer is rewritten only after every consumer of its previous round has read it: each
-// producer first consumes outputs that, through the stage chain, every such consumer produced
-// after its read.  The packet area is zeroed before each launch and tags start at 1, so a tag
-// never matches stale data.  The one value read with plain loads across workgroups is the new
-// K/V cache row: it is stored device-scope, acknowledged before the writer's next packet, first
-// read a step later, and rows >= pos are never loaded early (a line cached early would go
-// stale).  Every poll is bounded: a timeout raises an error flag that makes all workgroups
-// leave, and the host reports it.
+// (global_store/load_dwordx2 ... sc1: coherent across the XCDs' L2s without cache flushes); the
+// exchange waves read consecutive packets in consecutive lanes and poll until each carries the
+// tag of the round they expect, so the data is its own flag.  A buffer is rewritten only after
+// every consumer of its previous round has read it: each producer first consumes outputs that,
+// through the stage chain, every such consumer produced after its read.  The packet area is
+// zeroed before each launch and tags start at 1, so a tag never matches stale data.  The one
+// value read with plain loads across workgroups is the new K/V cache row: it is stored
+// device-scope, acknowledged before the writer's next packet, first read a step later, and rows
+// >= pos are never loaded early (a line cached early would go stale).  Every poll is bounded: a
+// timeout raises an error flag that makes all workgroups leave, and the host reports it.
 #include "icua_device.h"
 #include "icua_kernels.h"
 #include "icua_persist.h"
@@ -43,13 +50,21 @@ namespace pk {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int THREADS = 512, WAVES = 8;
-constexpr int NWG = PERSIST_WGS;         // 256
-constexpr int ATT_SPLITS = NWG / NKV;    // 32
-constexpr int SPIN_LIMIT = 2000000;      // polls (>= ~1 us each) before a wait gives up
-constexpr int PART = HD + 2;             // partial of one head: o[128], m, l
-constexpr int ATT_SPQ = 8;               // cache slots per quarter-wave per block
-constexpr int ATT_BLOCK = 32 * ATT_SPQ;  // 256 slots per block
-constexpr int MERGER0 = NWG - NKV;       // workgroup 248 + g merges group g (its split 31)
+constexpr int MW = 4;                     // math waves 0..3
+constexpr int MT = MW * 64;               // math threads
+constexpr int CT = THREADS - MT;          // exchange threads (waves 4..7)
+constexpr int NWG = PERSIST_WGS;          // 256
+constexpr int ATT_SPLITS = NWG / NKV;     // 32
+constexpr int SPIN_LIMIT = 2000000;       // polls (>= ~1 us each) before a wait gives up
+constexpr int PART = HD + 2;              // partial of one head: o[128], m, l
+constexpr int ATT_QW = MT / 16;           // 16 quarter-waves of math threads
+constexpr int ATT_SPQ = 9;                // cache slots per quarter-wave per block
+constexpr int ATT_BLOCK = ATT_QW * ATT_SPQ;  // 144 slots per block
+constexpr int ATT_PAD = 192;              // score row length (3 per lane of a wave)
+constexpr int MERGE_PARTS = 4;            // workgroups merging one group's partials
+constexpr int MERGER0 = NWG - NKV * MERGE_PARTS;  // workgroups 224..255: splits 28..31 of each group
+static_assert(MERGER0 >= H / 16, "mergers must not have O / down work");
+static_assert(MERGER0 % NKV == 0, "mergers of group g are splits 28..31 of group g");
 
 // Packet area (64-bit packets), zeroed before every launch.
 constexpr int XP = 0;                 // residual x [H]
@@ -60,7 +75,7 @@ constexpr int LMP = HP + FF;          // argmax partials [NWG][2] (value, index)
 constexpr int PARTP = LMP + 2 * NWG;  // attention partials [NKV][32][2][PART]
 constexpr int PACKETS = PARTP + NKV * ATT_SPLITS * 2 * PART;
 constexpr int ERRW = PACKETS * 2;     // error flag (32-bit word index)
-static_assert(MERGER0 % NKV == 0, "merger of group g must be split 31 of group g");
+constexpr int GROUP_PARTS = ATT_SPLITS * 2 * PART;  // 8320 packets of one group's partials
 
 // threadIdx.x behind an empty asm: per-lane address math derived from it is recomputed where it
 // is used instead of being hoisted out of the step / layer loops and held live (which spills).
@@ -69,6 +84,9 @@ __device__ __forceinline__ int my_tid() {
     asm volatile("" : "+v"(t));
     return t;
 }
+
+// Wave index as a wave-uniform (scalar) value, so that role branches compile to scalar branches.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x / 64); }
 
 __device__ __forceinline__ uint64_t ld64(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -88,21 +106,24 @@ __device__ __forceinline__ void raise_err(unsigned* e) {
     __hip_atomic_store(e, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls packets p[i] = src[off(i)] (i < N; off(i) < 0: unused) until each carries `tag`.  Returns
-// false on timeout (after raising the error flag) or when another workgroup raised it.
-template <int N, typename Off>
-__device__ __forceinline__ bool poll(const uint64_t* src, Off off, unsigned tag, uint64_t (&p)[N], unsigned* err) {
+// Exchange threads: polls packets src[k], k = ct + CT * i < n (consecutive lanes read consecutive
+// packets), until each carries `tag`, then writes their values to dst[k].  false on timeout
+// (after raising the error flag) or when another workgroup raised it.
+template <int NP>
+__device__ __forceinline__ bool poll_vec(const uint64_t* src, int n, unsigned tag, float* dst, unsigned* err) {
+    const int ct = my_tid() - MT;
     const uint64_t filler = (uint64_t)tag << 32;
+    uint64_t p[NP];
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-        const int o = off(i);
-        p[i] = o >= 0 ? ld64(src + o) : filler;
+    for (int i = 0; i < NP; ++i) {
+        const int k = ct + CT * i;
+        p[i] = k < n ? ld64(src + k) : filler;
     }
     for (int it = 0;; ++it) {
         bool ok = true;
 #pragma unroll
-        for (int i = 0; i < N; ++i) ok &= tag_of(p[i]) == tag;
-        if (ok) return true;
+        for (int i = 0; i < NP; ++i) ok &= tag_of(p[i]) == tag;
+        if (ok) break;
         if (it >= SPIN_LIMIT) {
             raise_err(err);
             return false;
@@ -110,215 +131,178 @@ __device__ __forceinline__ bool poll(const uint64_t* src, Off off, unsigned tag,
         if ((it & 63) == 63 && load_err(err)) return false;
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (int i = 0; i < N; ++i)
-            if (tag_of(p[i]) != tag) p[i] = ld64(src + off(i));
-    }
-}
-
-// Waits until sentinel packet src[sent(t)] carries `tag` for every thread t < nsent (one packet
-// per producer store instruction), so that the bulk of a vector is read once instead of being
-// polled: polling whole vectors from every workgroup floods the fabric.  Whole-workgroup call.
-template <typename Sent>
-__device__ __forceinline__ bool wait_sentinels(const uint64_t* src, int nsent, Sent sent, unsigned tag,
-                                               unsigned* err) {
-    const int tid = my_tid();
-    bool ok = true;
-    if (tid < nsent) {
-        const uint64_t* q = src + sent(tid);
-        uint64_t p = ld64(q);
-        for (int it = 0; tag_of(p) != tag; ++it) {
-            if (it >= SPIN_LIMIT) {
-                raise_err(err);
-                ok = false;
-                break;
-            }
-            if ((it & 63) == 63 && load_err(err)) {
-                ok = false;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-            p = ld64(q);
-        }
-    }
-    return !__syncthreads_or(!ok);
-}
-
-// Producers of the packet vectors and their sentinels.  A sentinel only decides when to read
-// the vector; the tag check of every packet read afterwards is what guarantees the data.
-enum Src { SRC_X = 0, SRC_ATTN = 1, SRC_H = 2 };
-// x: workgroup p < 128 stores packets 16p .. 16p + 15 with one instruction.
-// attn: merger g stores head (2g + hh) elements d with waves 0-3 (64 elements each).
-// h: workgroup p < 256 stores 8 packets per block 3p + j, j = 0, 1, 2; its last block is polled.
-template <int SRC>
-__device__ __forceinline__ int sentinel_count() {
-    return SRC == SRC_X ? H / 16 : SRC == SRC_ATTN ? 4 * NKV : NWG;
-}
-template <int SRC>
-__device__ __forceinline__ int sentinel_of(int t) {
-    if constexpr (SRC == SRC_X) return 16 * t;
-    else if constexpr (SRC == SRC_ATTN) return (t / 4) * 2 * HD + (t % 4) * 64;
-    else return 8 * (3 * t + 2);
-}
-
-struct Shared {
-    uint8_t A[96 * 1024];  // activation operands (1 KiB per q4 group / 512 B per q8 group, K <= 6144)
-    float fx[192 * 2];     // per-group (2^(e-21), sum X * 2^(e-21))
-    float red[WAVES * 64];
-    float emb[H];          // embedding of the token being decoded
-    float xown[16];        // residual rows of this workgroup's O / down block (workgroups < 128)
-    float qs[2][HD];       // attention: two query heads
-    float ktail[HD], vtail[HD];
-    float sc[2][ATT_BLOCK];
-    float ored[WAVES][2][HD];
-    float misc[64];
-    int imisc[64];
-    uint64_t tmark[2];  // profiling builds: sentinel / packet times of the last vector staging
-};
-
-// ------------------------------------------------------------------------------------------
-// Activation staging for one token: 8 consecutive activations per unit, units u = tid and
-// tid + 512 (K / 8 units) -> optional RMSNorm -> 22-bit slices -> A operands.  Rows 0, 1, 2 of each
-// group tile hold the hi, mid, lo slices; rows 3..15 stay zero (zeroed at kernel start).
-
-template <int FMT>
-__device__ __forceinline__ void stage_vals(Shared& S, float (&v)[2][8], int K, const float* norm_w) {
-    constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
-    constexpr int TILE = (FMT == FMT_Q4) ? 1024 : 512;
-    const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
-    const int nunits = K / 8;
-    float scale = 1.f;
-    if (norm_w) {
-        float ss = 0.f;
-#pragma unroll
-        for (int it = 0; it < 2; ++it)
-            if (tid + it * THREADS < nunits)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) ss += v[it][i] * v[it][i];
-        ss = wave_sum(ss);
-        if (lane == 0) S.red[wave] = ss;
-        __syncthreads();
-        float tot = 0.f;
-        for (int w = 0; w < WAVES; ++w) tot += S.red[w];
-        scale = 1.0f / sqrtf(tot / (float)K + EPS);
-        __syncthreads();
+        for (int i = 0; i < NP; ++i)
+            if (tag_of(p[i]) != tag) p[i] = ld64(src + ct + CT * i);
     }
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int u = tid + it * THREADS;
-        if (it * THREADS >= nunits) break;  // uniform across the workgroup
-        const bool act = u < nunits;
-        const int k0 = (act ? u : 0) * 8;
-        float x[8];
-        if (norm_w && act) {
-            const float4 w0 = ((const float4*)(norm_w + k0))[0], w1 = ((const float4*)(norm_w + k0))[1];
-            x[0] = v[it][0] * scale * w0.x; x[1] = v[it][1] * scale * w0.y; x[2] = v[it][2] * scale * w0.z;
-            x[3] = v[it][3] * scale * w0.w; x[4] = v[it][4] * scale * w1.x; x[5] = v[it][5] * scale * w1.y;
-            x[6] = v[it][6] * scale * w1.z; x[7] = v[it][7] * scale * w1.w;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[i] = act ? v[it][i] : 0.f;
-        }
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
-        int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
-        bits = max(bits, dpp_i<DPP_XOR1>(bits));
-        bits = max(bits, dpp_i<DPP_XOR2>(bits));
-        if constexpr (G == 64) bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
-        int e = ((bits >> 23) & 0xFF) - 127;
-        if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
-        const int sh = 21 - e;
-        int X[8], xs = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            X[i] = (int)rintf(ldexpf(x[i], sh));
-            xs += X[i];
-        }
-        xs += dpp_i<DPP_XOR1>(xs);
-        xs += dpp_i<DPP_XOR2>(xs);
-        if constexpr (G == 64) xs += dpp_i<DPP_HALF_MIRROR>(xs);
-        if (!act) continue;
-        uint32_t sl[3][2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint32_t p0 = 0, p1 = 0, p2 = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int xv = X[4 * h + i];
-                const int lo = (int)(int8_t)(xv & 0xFF);
-                const int r1 = (xv - lo) >> 8;
-                const int mid = (int)(int8_t)(r1 & 0xFF);
-                const int hi = (r1 - mid) >> 8;
-                p0 |= (uint32_t)(lo & 0xFF) << (8 * i);
-                p1 |= (uint32_t)(mid & 0xFF) << (8 * i);
-                p2 |= (uint32_t)(hi & 0xFF) << (8 * i);
-            }
-            sl[0][h] = p0;
-            sl[1][h] = p1;
-            sl[2][h] = p2;
-        }
-        const int gl = k0 / G, kk = k0 % G;
-        uint8_t* A = S.A + gl * TILE;
-        if constexpr (FMT == FMT_Q4) {
-            const int q = kk / 16, j0 = kk % 16;
-            *(uint2*)(A + (0 + 16 * q) * 16 + j0) = make_uint2(sl[2][0], sl[2][1]);
-            *(uint2*)(A + (1 + 16 * q) * 16 + j0) = make_uint2(sl[1][0], sl[1][1]);
-            *(uint2*)(A + (2 + 16 * q) * 16 + j0) = make_uint2(sl[0][0], sl[0][1]);
-        } else {
-            const int q = kk / 8;
-            *(uint2*)(A + (0 + 16 * q) * 8) = make_uint2(sl[2][0], sl[2][1]);
-            *(uint2*)(A + (1 + 16 * q) * 8) = make_uint2(sl[1][0], sl[1][1]);
-            *(uint2*)(A + (2 + 16 * q) * 8) = make_uint2(sl[0][0], sl[0][1]);
-        }
-        if (kk == 0) {
-            const float f = ldexpf(1.0f, -sh);
-            S.fx[gl * 2] = f;
-            S.fx[gl * 2 + 1] = (float)xs * f;
-        }
+    for (int i = 0; i < NP; ++i) {
+        const int k = ct + CT * i;
+        if (k < n) dst[k] = val_of(p[i]);
     }
-    __syncthreads();
-}
-
-// Stages a packet vector of K values (round `tag`).  false (for the whole workgroup) on error.
-template <int FMT, int SRC>
-__device__ __forceinline__ bool stage_packets(Shared& S, const uint64_t* src, unsigned tag, int K, const float* norm_w,
-                              unsigned* err) {
-    if (!wait_sentinels(src, sentinel_count<SRC>(), [](int t) { return sentinel_of<SRC>(t); }, tag, err)) return false;
-#ifdef ICUA_PERSIST_TRACE
-    if (my_tid() == 0) S.tmark[0] = wall_clock64();
-#endif
-    const int tid = my_tid();
-    const int nunits = K / 8;
-    uint64_t p[16];
-    const bool ok = poll<16>(
-        src,
-        [&](int i) {
-            const int u = tid + (i / 8) * THREADS;
-            return u < nunits ? u * 8 + i % 8 : -1;
-        },
-        tag, p, err);
-    if (__syncthreads_or(!ok)) return false;
-#ifdef ICUA_PERSIST_TRACE
-    if (my_tid() == 0) S.tmark[1] = wall_clock64();
-#endif
-    float v[2][8];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i / 8][i % 8] = val_of(p[i]);
-    stage_vals<FMT>(S, v, K, norm_w);
     return true;
 }
 
-// Stages the embedding held in LDS (K = H).
-template <int FMT>
-__device__ __forceinline__ void stage_emb(Shared& S, const float* norm_w) {
-    const int tid = my_tid();
-    float v[2][8];
+// Exchange threads: as poll_vec, for packets src[map(k)] of a gathered vector (k < n).
+template <int NP, typename Map>
+__device__ __forceinline__ bool poll_map(const uint64_t* src, int n, Map map, unsigned tag, float* dst, unsigned* err) {
+    const int ct = my_tid() - MT;
+    const uint64_t filler = (uint64_t)tag << 32;
+    uint64_t p[NP];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        v[0][i] = tid < H / 8 ? S.emb[tid * 8 + i] : 0.f;
-        v[1][i] = 0.f;
+    for (int i = 0; i < NP; ++i) {
+        const int k = ct + CT * i;
+        p[i] = k < n ? ld64(src + map(k)) : filler;
     }
-    stage_vals<FMT>(S, v, H, norm_w);
+    for (int it = 0;; ++it) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) ok &= tag_of(p[i]) == tag;
+        if (ok) break;
+        if (it >= SPIN_LIMIT) {
+            raise_err(err);
+            return false;
+        }
+        if ((it & 63) == 63 && load_err(err)) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+            if (tag_of(p[i]) != tag) p[i] = ld64(src + map(ct + CT * i));
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int k = ct + CT * i;
+        if (k < n) dst[k] = val_of(p[i]);
+    }
+    return true;
+}
+
+struct Shared {
+    uint8_t A[96 * 1024];     // activation operands (1 KiB per q4 group / 512 B per q8 group, K <= 6144);
+                              // the merger's fp32 partials during the merge
+    float fx[192 * 2];        // per-group (2^(e-21), sum X * 2^(e-21))
+    float red[3 * MW * 64];   // math-wave partial sums (up to 3 blocks)
+    float vec[FF];            // input vector of the current stage (fp32)
+    float emb[H];             // embedding of the token being decoded
+    float nw[H];              // RMSNorm weights of the current stage
+    float xown[16];           // residual rows of this workgroup's O / down block (workgroups < 128)
+    float qs[2][HD];          // attention: two query heads
+    float ktail[HD], vtail[HD];
+    float sc[2][ATT_PAD];
+    float ored[MW][2][HD];
+    float misc[64];
+    int imisc[64];
+};
+
+// ------------------------------------------------------------------------------------------
+// Staging by the exchange threads: units of 8 consecutive activations (u = ct + CT * i, K / 8
+// units) -> optional RMSNorm with S.nw -> 22-bit slices -> A operands.  Rows 0, 1, 2 of each
+// group tile hold the hi, mid, lo slices; rows 3..15 stay zero (zeroed at kernel start).  Called
+// by the whole workgroup (math threads only pass the barriers).
+
+template <int FMT, int NU, bool MATH>
+__device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed) {
+    constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
+    constexpr int TILE = (FMT == FMT_Q4) ? 1024 : 512;
+    constexpr int K = NU * CT * 8;
+    const int tid = my_tid();
+    constexpr bool ex = !MATH;
+    const int ct = tid - MT, lane = tid % 64, cw = wave_id() - MW;
+    float v[NU][8];
+    float scale = 1.f;
+    if (ex) {
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const float4 a0 = ((const float4*)(src + (ct + CT * j) * 8))[0];
+            const float4 a1 = ((const float4*)(src + (ct + CT * j) * 8))[1];
+            v[j][0] = a0.x; v[j][1] = a0.y; v[j][2] = a0.z; v[j][3] = a0.w;
+            v[j][4] = a1.x; v[j][5] = a1.y; v[j][6] = a1.z; v[j][7] = a1.w;
+        }
+    }
+    if (normed) {
+        if (ex) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < NU; ++j)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
+            ss = wave_sum(ss);
+            if (lane == 0) S.misc[40 + cw] = ss;
+        }
+        __syncthreads();
+        if (ex) {
+            const float tot = (S.misc[40] + S.misc[41]) + (S.misc[42] + S.misc[43]);
+            scale = 1.0f / sqrtf(tot / (float)K + EPS);
+#pragma unroll
+            for (int j = 0; j < NU; ++j) {
+                const float* wn = S.nw + (ct + CT * j) * 8;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[j][i] = v[j][i] * scale * wn[i];
+            }
+        }
+    }
+    if (ex) {
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int k0 = (ct + CT * j) * 8;
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
+            int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
+            bits = max(bits, dpp_i<DPP_XOR1>(bits));
+            bits = max(bits, dpp_i<DPP_XOR2>(bits));
+            if constexpr (G == 64) bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
+            int e = ((bits >> 23) & 0xFF) - 127;
+            if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
+            const int sh = 21 - e;
+            int X[8], xs = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                X[i] = (int)rintf(ldexpf(v[j][i], sh));
+                xs += X[i];
+            }
+            xs += dpp_i<DPP_XOR1>(xs);
+            xs += dpp_i<DPP_XOR2>(xs);
+            if constexpr (G == 64) xs += dpp_i<DPP_HALF_MIRROR>(xs);
+            uint32_t sl[3][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int xv = X[4 * h + i];
+                    const int lo = (int)(int8_t)(xv & 0xFF);
+                    const int r1 = (xv - lo) >> 8;
+                    const int mid = (int)(int8_t)(r1 & 0xFF);
+                    const int hi = (r1 - mid) >> 8;
+                    p0 |= (uint32_t)(lo & 0xFF) << (8 * i);
+                    p1 |= (uint32_t)(mid & 0xFF) << (8 * i);
+                    p2 |= (uint32_t)(hi & 0xFF) << (8 * i);
+                }
+                sl[0][h] = p0;
+                sl[1][h] = p1;
+                sl[2][h] = p2;
+            }
+            const int gl = k0 / G, kk = k0 % G;
+            uint8_t* A = S.A + gl * TILE;
+            if constexpr (FMT == FMT_Q4) {
+                const int q = kk / 16, j0 = kk % 16;
+                *(uint2*)(A + (0 + 16 * q) * 16 + j0) = make_uint2(sl[2][0], sl[2][1]);
+                *(uint2*)(A + (1 + 16 * q) * 16 + j0) = make_uint2(sl[1][0], sl[1][1]);
+                *(uint2*)(A + (2 + 16 * q) * 16 + j0) = make_uint2(sl[0][0], sl[0][1]);
+            } else {
+                const int q = kk / 8;
+                *(uint2*)(A + (0 + 16 * q) * 8) = make_uint2(sl[2][0], sl[2][1]);
+                *(uint2*)(A + (1 + 16 * q) * 8) = make_uint2(sl[1][0], sl[1][1]);
+                *(uint2*)(A + (2 + 16 * q) * 8) = make_uint2(sl[0][0], sl[0][1]);
+            }
+            if (kk == 0) {
+                const float f = ldexpf(1.0f, -sh);
+                S.fx[gl * 2] = f;
+                S.fx[gl * 2 + 1] = (float)xs * f;
+            }
+        }
+    }
+    __syncthreads();
 }
 
 // One 1 KiB chunk of a 16-row block against the staged operands; returns the lane's partial
@@ -369,111 +353,131 @@ __device__ __forceinline__ uint2 load_sb(const uint8_t* sb, int row, int K, int 
         return make_uint2(*(const uint32_t*)(sb + ((size_t)row * (K / 32) + 2 * c) * 2), 0u);
 }
 
-// The CW chunks of wave `wave` of 16-row block rb (chunks wave * CW .. wave * CW + CW - 1).
+// This math wave's share (chunks mw * CW .. mw * CW + CW - 1) of 16-row block rb.
 template <int FMT, int CW>
-__device__ __forceinline__ void load_block(const uint8_t* w, const uint8_t* sb, int rb, int K, int wave, int lane,
-                                           uint4 (&wv)[CW], uint2 (&sbv)[CW]) {
-    constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
-    const int cpb = K / CHK;
-    const uint8_t* blk = w + (size_t)rb * cpb * 1024;
+struct WB {
+    uint4 wv[CW];
+    uint2 sb[CW];
+    __device__ __forceinline__ void load(const uint8_t* w, const uint8_t* sbp, int rb, int K, int mw, int lane) {
+        constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
+        const int cpb = K / CHK;
+        const uint8_t* blk = w + (size_t)rb * cpb * 1024;
 #pragma unroll
-    for (int i = 0; i < CW; ++i) {
-        const int c = wave * CW + i;
-        wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
-        sbv[i] = load_sb<FMT>(sb, rb * 16 + lane % 16, K, c);
+        for (int i = 0; i < CW; ++i) {
+            const int c = mw * CW + i;
+            wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
+            sb[i] = load_sb<FMT>(sbp, rb * 16 + lane % 16, K, c);
+        }
     }
-}
-
-template <int FMT, int CW>
-__device__ __forceinline__ float block_mac(const Shared& S, const uint4 (&wv)[CW], const uint2 (&sbv)[CW], int wave,
-                                           int lane) {
-    float acc = 0.f;
+    __device__ __forceinline__ float mac(const Shared& S, int mw, int lane) const {
+        float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < CW; ++i) acc += chunk_mac<FMT>(S, wv[i], sbv[i], wave * CW + i, lane);
-    return acc;
-}
+        for (int i = 0; i < CW; ++i) acc += chunk_mac<FMT>(S, wv[i], sb[i], mw * CW + i, lane);
+        return acc;
+    }
+};
 
-// Cross-wave sum of per-lane partials; returns the total in wave 0 (lanes 0-15 meaningful).
-__device__ __forceinline__ float reduce_waves(Shared& S, float acc) {
-    const int lane = my_tid() % 64, wave = my_tid() / 64;
-    S.red[wave * 64 + lane] = acc;
+// Sum of the math waves' per-lane partials (whole-workgroup call); the total is valid in math
+// wave 0 (lanes 0-15 meaningful).
+template <bool MATH>
+__device__ __forceinline__ float reduce_math(Shared& S, float acc) {
+    const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+    if (MATH) S.red[wave * 64 + lane] = acc;
     __syncthreads();
     float s = 0.f;
-    if (wave == 0)
-        for (int w = 0; w < WAVES; ++w) s += S.red[w * 64 + lane];
+    if (wave == 0) s = (S.red[lane] + S.red[64 + lane]) + (S.red[128 + lane] + S.red[192 + lane]);
     __syncthreads();
     return s;
 }
 
-__device__ __forceinline__ void norm_rope(float& a, float& b, const float* w, const float* cs, int lane) {
+// reduce_math for the three gate|up blocks at once (one pair of barriers).
+template <bool MATH>
+__device__ __forceinline__ void reduce_math3(Shared& S, const float (&acc)[3], float (&out)[3]) {
+    const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+    if (MATH) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) S.red[(j * MW + wave) * 64 + lane] = acc[j];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const float* r = S.red + j * MW * 64;
+            out[j] = (r[lane] + r[64 + lane]) + (r[128 + lane] + r[192 + lane]);
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void norm_rope(float& a, float& b, float w0, float w1, float c, float sn) {
     const float ss = wave_sum(a * a + b * b);
     const float scale = 1.0f / sqrtf(ss / (float)HD + EPS);
-    a = a * scale * w[lane];
-    b = b * scale * w[lane + 64];
-    const float c = cs[2 * lane], sn = cs[2 * lane + 1];
+    a = a * scale * w0;
+    b = b * scale * w1;
     const float a2 = a * c - b * sn, b2 = b * c + a * sn;
     a = a2;
     b = b2;
 }
 
+__device__ __forceinline__ void load_norm8(float (&n)[8], const float* p) {
+    const float4 n0 = ((const float4*)p)[0], n1 = ((const float4*)p)[1];
+    n[0] = n0.x; n[1] = n0.y; n[2] = n0.z; n[3] = n0.w;
+    n[4] = n1.x; n[5] = n1.y; n[6] = n1.z; n[7] = n1.w;
+}
+
 // ------------------------------------------------------------------------------------------
 // Stage timeline of the last step of a launch (per workgroup, per layer, 32 event slots; steady
-// clock), compiled only with -DICUA_PERSIST_TRACE for profiling builds.  Slots 16 + 2k and
-// 17 + 2k: sentinels seen and packets read by the k-th vector staging of the layer.
+// clock), compiled only with -DICUA_PERSIST_TRACE for profiling builds.  PK_TRACE is recorded by
+// math thread 0, PK_TRACE_X by exchange thread 0.
 #ifdef ICUA_PERSIST_TRACE
 __device__ uint64_t g_trace[NWG][MAX_LAYERS + 1][32];
-#define PK_TRACE(layer, ev)                                                                  \
-    do {                                                                                     \
-        if (step == a.nsteps - 1 && my_tid() == 0) g_trace[w][layer][ev] = wall_clock64(); \
-    } while (0)
-#define PK_TRACE_MARKS(layer, k)                                           \
-    do {                                                                   \
-        if (step == a.nsteps - 1 && my_tid() == 0) {                       \
-            g_trace[w][layer][16 + 2 * (k)] = S.tmark[0];                  \
-            g_trace[w][layer][17 + 2 * (k)] = S.tmark[1];                  \
-        }                                                                  \
+#define PK_TRACE_AT(layer, ev, t0)                                                            \
+    do {                                                                                      \
+        if (step == a.nsteps - 1 && my_tid() == (t0)) g_trace[w][layer][ev] = wall_clock64(); \
     } while (0)
 #else
-#define PK_TRACE(layer, ev) \
-    do {                    \
-    } while (0)
-#define PK_TRACE_MARKS(layer, k) \
-    do {                         \
+#define PK_TRACE_AT(layer, ev, t0) \
+    do {                           \
     } while (0)
 #endif
+#define PK_TRACE(layer, ev) PK_TRACE_AT(layer, ev, 0)
+#define PK_TRACE_X(layer, ev) PK_TRACE_AT(layer, ev, MT)
 
-template <int FMT>
-__global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
+// The decode loop of one role (MATH: waves 0-3, else waves 4-7).  Each role is compiled as its
+// own copy of the loop, so the register allocator never has to fit the math waves' weight tiles
+// and the exchange waves' poll buffers side by side.  Both copies execute the same sequence of
+// workgroup barriers (s_barrier counts waves, not call sites), so they stay in lockstep.
+template <int FMT, bool MATH>
+__device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int w, int pos, int stp) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
-    constexpr int CW2 = H / CHK / WAVES;   // chunks per wave, K = 2048
-    constexpr int CW6 = FF / CHK / WAVES;  // K = 6144
-    constexpr int NRB = VOCAB / 16;        // lm_head row blocks
-    __shared__ Shared S;
-    const int w = blockIdx.x;
+    constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
+    constexpr int CW6 = FF / CHK / MW;  // K = 6144
+    constexpr int NRB = VOCAB / 16;     // lm_head row blocks
+    constexpr int LM_DEPTH = (FMT == FMT_Q4) ? 4 : 2;  // lm_head blocks in flight
+    // Down tiles are requested when the down stage starts: holding them through the gate|up stage
+    // as well would not fit the math waves' registers.
+    constexpr bool EARLY_DOWN = false;
     uint64_t* ll = a.ll;
     unsigned* err = (unsigned*)a.ll + ERRW;
-    for (int i = my_tid(); i < (int)sizeof(S.A) / 4; i += THREADS) ((uint32_t*)S.A)[i] = 0u;
-
-    // Control block and the embedding of the first token (written before this launch).
     State* st = a.st;
-    if (st->done || st->n != 1) return;  // single-row passes only (checked by the host too)
-    int pos = st->pos, stp = st->step;
     const int maxsteps = st->maxsteps, eos0 = st->eos0, eos1 = st->eos1, maxctx = st->maxctx;
-    for (int i = my_tid(); i < H; i += THREADS) S.emb[i] = a.x[i];
-    if (my_tid() < 16 && w < H / 16) S.xown[my_tid()] = a.x[w * 16 + my_tid()];
+    const int L = a.nlayers;
+    float nreg[8];  // math threads: norm weights of the next normed stage (8 each)
+    if (MATH) load_norm8(nreg, a.layers[0].attn_norm + my_tid() * 8);
     __syncthreads();
 
-    const int L = a.nlayers;
     for (int step = 0; step < a.nsteps; ++step) {
         if (pos + 1 > maxctx) break;  // the commit stops earlier; guards the cache row
         for (int l = 0; l < L; ++l) {
             const LayerPtrs& P = a.layers[l];
             const unsigned r = (unsigned)(step * L + l);  // round of this layer
+            const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+            constexpr bool math = MATH;
+            const int mw = wave;  // math wave index (valid when math)
 
-            // Attention geometry of this workgroup (KV group g, split s) and its first block of
-            // K/V rows, issued before the QKV stage so that they stream in behind it.  The pos + 1
-            // rows of the group (rows < pos and the new row) are spread evenly over the 32 splits;
-            // the split holding row pos writes it.  Only rows < pos are loaded from the cache.
+            // Attention geometry of this workgroup: KV group g, split s.  The pos + 1 rows of the
+            // group (rows < pos and the new row) are spread evenly over the 32 splits; the split
+            // holding row pos writes it.  Only rows < pos are loaded from the cache.
             const int g = w % NKV, s = w / NKV;
             const int tot = pos + 1;
             const int chunk = (tot + ATT_SPLITS - 1) / ATT_SPLITS;
@@ -483,12 +487,32 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
             const int ntot = j1 - j0;
             const uint16_t* kb = a.kv + ((size_t)(l * 2 + 0) * NKV + g) * a.maxctx * HD;
             const uint16_t* vb = a.kv + ((size_t)(l * 2 + 1) * NKV + g) * a.maxctx * HD;
+            const int quad = tid / 16, ql = tid % 16;  // math threads: 16 quarter-waves, 8 dims per lane
+
+            // Math-wave register tiles of this layer.  Each is requested when its stage starts
+            // (while the exchange waves wait for the stage's input) or one stage earlier.
+            WB<FMT, CW2> wq, wo, wgu[3];
+            WB<FMT, CW6> wd;
+
+            // ---------------- QKV: row block w ---------------------------------------------
+            PK_TRACE(l, 0);
             uint4 kr[ATT_SPQ], vr[ATT_SPQ];
-            {
-                const int tid = my_tid(), quad = tid / 16, ql = tid % 16;
+            float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rs = 0.f;
+            // Exchange waves poll the stage input first; math waves skip that branch and issue
+            // their loads at once.  Keeping the loads after the poll in program order lets the
+            // poll's registers and the weight tiles share the register file.
+            bool ok_in = true;
+            if (l > 0 && !math) ok_in = poll_vec<H / CT>(ll + XP, H, 2 * r, S.vec, err);
+            if (math) {
+                // This layer's norm weights into LDS; then the QKV block and the loads for the
+                // stages ahead: the first block of K/V rows, the per-head norms and the rope row,
+                // the O block and the mlp norm.
+#pragma unroll
+                for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
+                wq.load(P.wqkv, P.wqkv_sb, w, H, mw, lane);
 #pragma unroll
                 for (int i = 0; i < ATT_SPQ; ++i) {
-                    const int p = quad + 32 * i;
+                    const int p = quad + ATT_QW * i;
                     kr[i] = make_uint4(0u, 0u, 0u, 0u);
                     vr[i] = kr[i];
                     if (p < nprior) {
@@ -496,152 +520,141 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                         vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
                     }
                 }
+                const float* rope = a.rope + (size_t)pos * 128;
+                qn0 = P.q_norm[lane];
+                qn1 = P.q_norm[lane + 64];
+                kn0 = P.k_norm[lane];
+                kn1 = P.k_norm[lane + 64];
+                rc = rope[2 * lane];
+                rs = rope[2 * lane + 1];
+                if (w < H / 16) wo.load(P.wo, P.wo_sb, w, H, mw, lane);
+                load_norm8(nreg, P.mlp_norm + tid * 8);
             }
-
-            // ---------------- QKV: row block w ---------------------------------------------
+            if (__syncthreads_or(!ok_in)) return;
+            PK_TRACE_X(l, 1);
+            stage_c<FMT, H / CT / 8, MATH>(S, l == 0 ? S.emb : S.vec, true);
             {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
-                PK_TRACE(l, 0);
-                uint4 wv[CW2];
-                uint2 sbv[CW2];
-                load_block<FMT, CW2>(P.wqkv, P.wqkv_sb, w, H, wave, lane, wv, sbv);
-                if (l == 0) {
-                    stage_emb<FMT>(S, P.attn_norm);
-                } else if (!stage_packets<FMT, SRC_X>(S, ll + XP, 2 * r, H, P.attn_norm, err)) {
-                    return;
-                }
-                PK_TRACE(l, 1);
-                if (l > 0) PK_TRACE_MARKS(l, 0);
-                const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv, sbv, wave, lane));
+                const float y = reduce_math<MATH>(S, math ? wq.mac(S, mw, lane) : 0.f);
                 if (wave == 0 && lane < 16) st64(ll + QKVP + w * 16 + lane, pack(y, r + 1));
-                PK_TRACE(l, 2);
             }
+            PK_TRACE(l, 2);
 
             // ---------------- attention: group g, split s ----------------------------------
             {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
-                const int quad = tid / 16, ql = tid % 16;  // 32 quarter-waves, 8 dims per lane
-                // Sentinels: the 32 QKV blocks of group g (q heads 2g, 2g+1: blocks 16g..16g+15;
-                // k: 128 + 8g..; v: 192 + 8g..), lane 0 of each.
-                if (!wait_sentinels(
-                        ll + QKVP, 32,
-                        [&](int t) {
-                            const int b = t < 16 ? 16 * g + t : t < 24 ? 128 + 8 * g + (t - 16) : 192 + 8 * g + (t - 24);
-                            return 16 * b;
+                bool ok = true;
+                if (!math)  // q heads 2g, 2g+1 -> vec[0..255], k -> vec[256..383], v -> vec[384..511]
+                    ok = poll_map<2>(
+                        ll + QKVP, 4 * HD,
+                        [&](int k) {
+                            return k < 2 * HD ? 2 * g * HD + k
+                                              : k < 3 * HD ? H + g * HD + (k - 2 * HD) : H + NKV * HD + g * HD + (k - 3 * HD);
                         },
-                        r + 1, err))
-                    return;
-                // Queries of heads 2g, 2g+1 (waves 0, 1); the tail split's wave 2 also takes the
-                // new K and V rows of the group.
-                {
-                    const bool needs = wave < 2 || (wave == 2 && tail);
-                    const int qoff = (2 * g + wave) * HD + lane;
-                    const int koff = H + g * HD + lane, voff = H + NKV * HD + g * HD + lane;
-                    uint64_t p[4];
-                    bool ok = true;
-                    if (needs)
-                        ok = poll<4>(
-                            ll + QKVP,
-                            [&](int i) {
-                                if (wave < 2) return i < 2 ? qoff + 64 * i : -1;
-                                return i < 2 ? koff + 64 * i : voff + 64 * (i - 2);
-                            },
-                            r + 1, p, err);
-                    if (__syncthreads_or(!ok)) return;
-                    PK_TRACE(l, 3);
-                    const float* rope = a.rope + (size_t)pos * 128;
-                    if (wave < 2) {
-                        float x0 = val_of(p[0]), x1 = val_of(p[1]);
-                        norm_rope(x0, x1, P.q_norm, rope, lane);
-                        const float qscale = 1.0f / sqrtf((float)HD);
-                        S.qs[wave][lane] = x0 * qscale;
-                        S.qs[wave][lane + 64] = x1 * qscale;
-                    } else if (needs) {
-                        float k0 = val_of(p[0]), k1 = val_of(p[1]);
-                        norm_rope(k0, k1, P.k_norm, rope, lane);
-                        S.ktail[lane] = h2f(f2h(k0));
-                        S.ktail[lane + 64] = h2f(f2h(k1));
-                        S.vtail[lane] = h2f(f2h(val_of(p[2])));
-                        S.vtail[lane + 64] = h2f(f2h(val_of(p[3])));
-                    }
+                        r + 1, S.vec, err);
+                if (__syncthreads_or(!ok)) return;
+            }
+            PK_TRACE_X(l, 3);
+            if (math) {
+                if (wave < 2) {
+                    float x0 = S.vec[wave * HD + lane], x1 = S.vec[wave * HD + lane + 64];
+                    norm_rope(x0, x1, qn0, qn1, rc, rs);
+                    const float qscale = 1.0f / sqrtf((float)HD);
+                    S.qs[wave][lane] = x0 * qscale;
+                    S.qs[wave][lane + 64] = x1 * qscale;
+                } else if (wave == 2 && tail) {
+                    float k0 = S.vec[2 * HD + lane], k1 = S.vec[2 * HD + lane + 64];
+                    norm_rope(k0, k1, kn0, kn1, rc, rs);
+                    S.ktail[lane] = h2f(f2h(k0));
+                    S.ktail[lane + 64] = h2f(f2h(k1));
+                    S.vtail[lane] = h2f(f2h(S.vec[3 * HD + lane]));
+                    S.vtail[lane + 64] = h2f(f2h(S.vec[3 * HD + lane + 64]));
                 }
-                __syncthreads();
-                if (tail && tid < 128) {
-                    // The new cache row (fp16), device-scope stores.
-                    const float* src = tid < 64 ? S.ktail : S.vtail;
-                    uint16_t* dst = (uint16_t*)(tid < 64 ? kb : vb) + (size_t)pos * HD;
-                    const int d = 2 * (tid % 64);
-                    const uint32_t v = (uint32_t)f2h(src[d]) | ((uint32_t)f2h(src[d + 1]) << 16);
-                    __hip_atomic_store((uint32_t*)(dst + d), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+            }
+            __syncthreads();
+            if (tail && !math && tid < MT + 128) {
+                // The new cache row (fp16), device-scope stores by exchange threads, acknowledged
+                // before this workgroup publishes its partials.
+                const int c = tid - MT;
+                const float* src = c < 64 ? S.ktail : S.vtail;
+                uint16_t* dst = (uint16_t*)(c < 64 ? kb : vb) + (size_t)pos * HD;
+                const int d = 2 * (c % 64);
+                const uint32_t v = (uint32_t)f2h(src[d]) | ((uint32_t)f2h(src[d + 1]) << 16);
+                __hip_atomic_store((uint32_t*)(dst + d), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_s_waitcnt(0);
+            }
+            {
                 float q[2][8];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                    for (int d = 0; d < 8; ++d) q[hh][d] = S.qs[hh][8 * ql + d];
                 float m_run[2] = {-__builtin_inff(), -__builtin_inff()}, l_run[2] = {0.f, 0.f};
                 float o[2][8];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int d = 0; d < 8; ++d) o[hh][d] = 0.f;
-                for (int b0 = 0; b0 < ntot; b0 += ATT_BLOCK) {
+                    for (int d = 0; d < 8; ++d) {
+                        q[hh][d] = math ? S.qs[hh][8 * ql + d] : 0.f;
+                        o[hh][d] = 0.f;
+                    }
+                PK_TRACE(l, 21);
+                for (int b0 = 0; b0 < ntot; b0 += ATT_BLOCK) {  // uniform over the workgroup
                     const int nb = min(ATT_BLOCK, ntot - b0);
-                    if (b0 > 0) {
+                    if (math) {
+                        if (b0 > 0) {
+#pragma unroll
+                            for (int i = 0; i < ATT_SPQ; ++i) {
+                                const int p = b0 + quad + ATT_QW * i;
+                                if (p < nprior) {
+                                    kr[i] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 8 * ql);
+                                    vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
+                                }
+                            }
+                        }
+                        // The new row (block slot pos - j0 - b0) comes from LDS, not from the cache.
+                        const int pnew = tail ? pos - j0 - b0 : -1;
 #pragma unroll
                         for (int i = 0; i < ATT_SPQ; ++i) {
-                            const int p = b0 + quad + 32 * i;
-                            if (p < nprior) {
-                                kr[i] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 8 * ql);
-                                vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
+                            if (quad + ATT_QW * i == pnew) {
+                                uint32_t kk[4], vv[4];
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) {
+                                    kk[j] = (uint32_t)f2h(S.ktail[8 * ql + 2 * j]) |
+                                            ((uint32_t)f2h(S.ktail[8 * ql + 2 * j + 1]) << 16);
+                                    vv[j] = (uint32_t)f2h(S.vtail[8 * ql + 2 * j]) |
+                                            ((uint32_t)f2h(S.vtail[8 * ql + 2 * j + 1]) << 16);
+                                }
+                                kr[i] = make_uint4(kk[0], kk[1], kk[2], kk[3]);
+                                vr[i] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
                             }
                         }
-                    }
-                    // The new row (block slot pos - j0 - b0) comes from LDS, not from the cache.
-                    const int pnew = tail ? pos - j0 - b0 : -1;
 #pragma unroll
-                    for (int i = 0; i < ATT_SPQ; ++i) {
-                        if (quad + 32 * i == pnew) {
-                            uint32_t kk[4], vv[4];
+                        for (int i = 0; i < ATT_SPQ; ++i) {
+                            const int p = quad + ATT_QW * i;
+                            const uint32_t dk[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+                            float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
-                                kk[j] = (uint32_t)f2h(S.ktail[8 * ql + 2 * j]) |
-                                        ((uint32_t)f2h(S.ktail[8 * ql + 2 * j + 1]) << 16);
-                                vv[j] = (uint32_t)f2h(S.vtail[8 * ql + 2 * j]) |
-                                        ((uint32_t)f2h(S.vtail[8 * ql + 2 * j + 1]) << 16);
+                                const f16x2 hk = as_h2(dk[j]);
+                                const float k0 = (float)hk.x, k1 = (float)hk.y;
+                                acc0 = fmaf(q[0][2 * j], k0, acc0);
+                                acc0 = fmaf(q[0][2 * j + 1], k1, acc0);
+                                acc1 = fmaf(q[1][2 * j], k0, acc1);
+                                acc1 = fmaf(q[1][2 * j + 1], k1, acc1);
                             }
-                            kr[i] = make_uint4(kk[0], kk[1], kk[2], kk[3]);
-                            vr[i] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
+                            acc0 = sum16(acc0);
+                            acc1 = sum16(acc1);
+                            if (ql == 0) {
+                                S.sc[0][p] = (p < nb) ? acc0 : -__builtin_inff();
+                                S.sc[1][p] = (p < nb) ? acc1 : -__builtin_inff();
+                            }
                         }
-                    }
-#pragma unroll
-                    for (int i = 0; i < ATT_SPQ; ++i) {
-                        const int p = quad + 32 * i;
-                        const uint32_t dk[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
-                        float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const f16x2 hk = as_h2(dk[j]);
-                            const float k0 = (float)hk.x, k1 = (float)hk.y;
-                            acc0 = fmaf(q[0][2 * j], k0, acc0);
-                            acc0 = fmaf(q[0][2 * j + 1], k1, acc0);
-                            acc1 = fmaf(q[1][2 * j], k0, acc1);
-                            acc1 = fmaf(q[1][2 * j + 1], k1, acc1);
-                        }
-                        acc0 = sum16(acc0);
-                        acc1 = sum16(acc1);
-                        if (ql == 0) {
-                            S.sc[0][p] = (p < nb) ? acc0 : -__builtin_inff();
-                            S.sc[1][p] = (p < nb) ? acc1 : -__builtin_inff();
-                        }
+                    } else if (tid < MT + 2 * (ATT_PAD - ATT_BLOCK)) {  // padding slots
+                        const int c = tid - MT;
+                        S.sc[c & 1][ATT_BLOCK + (c >> 1)] = -__builtin_inff();
                     }
                     __syncthreads();
-                    // Block softmax statistics: waves 0 and 1, one head each.
+                    // Block softmax statistics: math waves 0 and 1, one head each.
                     if (wave < 2) {
-                        float sv[ATT_BLOCK / 64];
+                        float sv[ATT_PAD / 64];
                         float mb = -__builtin_inff();
 #pragma unroll
-                        for (int i = 0; i < ATT_BLOCK / 64; ++i) {
+                        for (int i = 0; i < ATT_PAD / 64; ++i) {
                             sv[i] = S.sc[wave][lane + 64 * i];
                             mb = fmaxf(mb, sv[i]);
                         }
@@ -649,7 +662,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                         const float mn = fmaxf(m_run[wave], mb);
                         float ls = 0.f;
 #pragma unroll
-                        for (int i = 0; i < ATT_BLOCK / 64; ++i) {
+                        for (int i = 0; i < ATT_PAD / 64; ++i) {
                             const float e = (sv[i] == -__builtin_inff()) ? 0.f : expf(sv[i] - mn);
                             S.sc[wave][lane + 64 * i] = e;
                             ls += e;
@@ -661,209 +674,227 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                         }
                     }
                     __syncthreads();
+                    if (math) {
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const float mn = S.misc[hh];
-                        const float corr = (m_run[hh] == -__builtin_inff()) ? 0.f : expf(m_run[hh] - mn);
-                        l_run[hh] = l_run[hh] * corr + S.misc[2 + hh];
-                        m_run[hh] = mn;
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const float mn = S.misc[hh];
+                            const float corr = (m_run[hh] == -__builtin_inff()) ? 0.f : expf(m_run[hh] - mn);
+                            l_run[hh] = l_run[hh] * corr + S.misc[2 + hh];
+                            m_run[hh] = mn;
 #pragma unroll
-                        for (int d = 0; d < 8; ++d) o[hh][d] *= corr;
-                    }
+                            for (int d = 0; d < 8; ++d) o[hh][d] *= corr;
+                        }
 #pragma unroll
-                    for (int i = 0; i < ATT_SPQ; ++i) {
-                        const int p = quad + 32 * i;
-                        const float p0 = S.sc[0][p], p1 = S.sc[1][p];
-                        const uint32_t dv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+                        for (int i = 0; i < ATT_SPQ; ++i) {
+                            const int p = quad + ATT_QW * i;
+                            const float p0 = S.sc[0][p], p1 = S.sc[1][p];
+                            const uint32_t dv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const f16x2 hv = as_h2(dv[j]);
-                            const float v0 = (float)hv.x, v1 = (float)hv.y;
-                            o[0][2 * j] = fmaf(p0, v0, o[0][2 * j]);
-                            o[0][2 * j + 1] = fmaf(p0, v1, o[0][2 * j + 1]);
-                            o[1][2 * j] = fmaf(p1, v0, o[1][2 * j]);
-                            o[1][2 * j + 1] = fmaf(p1, v1, o[1][2 * j + 1]);
+                            for (int j = 0; j < 4; ++j) {
+                                const f16x2 hv = as_h2(dv[j]);
+                                const float v0 = (float)hv.x, v1 = (float)hv.y;
+                                o[0][2 * j] = fmaf(p0, v0, o[0][2 * j]);
+                                o[0][2 * j + 1] = fmaf(p0, v1, o[0][2 * j + 1]);
+                                o[1][2 * j] = fmaf(p1, v0, o[1][2 * j]);
+                                o[1][2 * j + 1] = fmaf(p1, v1, o[1][2 * j + 1]);
+                            }
                         }
                     }
                     __syncthreads();
                 }
-                // Reduce o over the 32 quarter-waves: 4 per wave by lane swaps, 8 waves via LDS.
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                    for (int d = 0; d < 8; ++d) {
-                        const float t1 = swap16_add(o[hh][d], o[hh][d]);
-                        o[hh][d] = swap32_add(t1, t1);
-                    }
-                if (lane < 16) {
+                PK_TRACE(l, 22);
+                // Reduce o over the 16 quarter-waves: 4 per wave by lane swaps, 4 waves via LDS.
+                if (math) {
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                        for (int d = 0; d < 8; ++d) S.ored[wave][hh][8 * ql + d] = o[hh][d];
+                        for (int d = 0; d < 8; ++d) {
+                            const float t1 = swap16_add(o[hh][d], o[hh][d]);
+                            o[hh][d] = swap32_add(t1, t1);
+                        }
+                    if (lane < 16) {
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                            for (int d = 0; d < 8; ++d) S.ored[mw][hh][8 * ql + d] = o[hh][d];
+                    }
                 }
-                // The new cache row is acknowledged before this workgroup's next packet.
-                __builtin_amdgcn_s_waitcnt(0);
                 __syncthreads();
-                uint64_t* part = ll + PARTP + (size_t)(g * ATT_SPLITS + s) * 2 * PART;
-                if (tid < 2 * HD) {
+                if (math) {
+                    uint64_t* part = ll + PARTP + (size_t)(g * ATT_SPLITS + s) * 2 * PART;
                     const int hh = tid / HD, d = tid % HD;
-                    float acc = 0.f;
-                    for (int ww = 0; ww < WAVES; ++ww) acc += S.ored[ww][hh][d];
+                    const float acc = (S.ored[0][hh][d] + S.ored[1][hh][d]) + (S.ored[2][hh][d] + S.ored[3][hh][d]);
                     st64(part + hh * PART + d, pack(acc, r + 1));
                     if (d == 0) {
                         st64(part + hh * PART + HD, pack(m_run[hh], r + 1));
                         st64(part + hh * PART + HD + 1, pack(l_run[hh], r + 1));
                     }
                 }
-                PK_TRACE(l, 4);
+                PK_TRACE(l, 20);
             }
+            PK_TRACE(l, 4);
 
-            // ---------------- merge of group g: workgroups 248..255 ------------------------
-            // Thread t: half = t / 256 (splits 16 half .. 16 half + 15), head hh, element d; the
-            // threads with d < 16 also fetch (m, l) of split 16 half + d.  Each half is merged with
-            // its own maximum, then the two halves are combined.
+            // ---------------- merge of group g: workgroups 224..255 ------------------------
+            // Split s = 28 + p of group g (workgroup 224 + 8p + g, no O / down work) merges part
+            // p = 0..3 of the group's output: head 2g + p / 2, elements 64 (p % 2) .. + 63.
             if (w >= MERGER0) {
-                const int tid = my_tid();
-                const int half = tid / 256, hh = (tid / HD) & 1, d = tid % HD;
-                const uint64_t* gp = ll + PARTP + (size_t)g * ATT_SPLITS * 2 * PART;
-                // Sentinels: per split and head, the m packet and the o packet stored by the second
-                // wave of that head (element 64).
-                if (!wait_sentinels(
-                        gp, 4 * ATT_SPLITS,
-                        [](int t) { return ((t / 4) * 2 + (t % 4) / 2) * PART + ((t % 2) ? 64 : HD); }, r + 1,
-                        err))
-                    return;
-                uint64_t p[18];
-                const bool ok = poll<18>(
-                    gp,
-                    [&](int i) {
-                        if (i < 16) return ((half * 16 + i) * 2 + hh) * PART + d;
-                        return d < 16 ? ((half * 16 + d) * 2 + hh) * PART + HD + (i - 16) : -1;
-                    },
-                    r + 1, p, err);
+                const int p = s - (ATT_SPLITS - MERGE_PARTS), hh = p / 2, d0 = 64 * (p % 2);
+                float* pl = (float*)S.A;  // [32][64 + 2]: o elements d0.., m, l of head hh per split
+                const uint64_t* gp = ll + PARTP + (size_t)g * GROUP_PARTS;
+                bool ok = true;
+                if (!math)
+                    ok = poll_map<(ATT_SPLITS * 66 + CT - 1) / CT>(
+                        gp, ATT_SPLITS * 66,
+                        [&](int k) {
+                            const int sj = k / 66, e = k % 66;
+                            return (sj * 2 + hh) * PART + (e < 64 ? d0 + e : HD + (e - 64));
+                        },
+                        r + 1, pl, err);
                 if (__syncthreads_or(!ok)) return;
-                float* ml = &S.sc[0][0];  // [half][hh][16][2]
-                if (d < 16) {
-                    ml[((half * 2 + hh) * 16 + d) * 2] = val_of(p[16]);
-                    ml[((half * 2 + hh) * 16 + d) * 2 + 1] = val_of(p[17]);
-                }
-                __syncthreads();
-                const float* mlh = ml + (half * 2 + hh) * 32;
-                float mx = -__builtin_inff();
-#pragma unroll
-                for (int j = 0; j < 16; ++j) mx = fmaxf(mx, mlh[2 * j]);
-                float Lh = 0.f, Oh = 0.f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const float m = mlh[2 * j];
+                PK_TRACE_X(l, 5);
+                // Split weights exp(m_s - max) and the normaliser (math wave 0, one lane per split).
+                if (math && wave == 0) {
+                    const int sl = lane % ATT_SPLITS;
+                    const float m = pl[sl * 66 + 64];
+                    const float mx = wave_max(m);  // finite: the split holding row pos is never empty
                     const float wgt = (m == -__builtin_inff()) ? 0.f : expf(m - mx);
-                    Lh = fmaf(wgt, mlh[2 * j + 1], Lh);
-                    Oh = fmaf(wgt, val_of(p[j]), Oh);
-                }
-                S.ored[half][hh][d] = Oh;
-                if (d == 0) {
-                    S.misc[(half * 2 + hh) * 2] = mx;
-                    S.misc[(half * 2 + hh) * 2 + 1] = Lh;
+                    const float lw = wave_sum(lane < ATT_SPLITS ? wgt * pl[sl * 66 + 65] : 0.f);
+                    if (lane < ATT_SPLITS) S.sc[0][lane] = wgt;
+                    if (lane == 0) S.misc[0] = 1.0f / lw;
                 }
                 __syncthreads();
-                if (half == 0) {
-                    const float m0 = S.misc[hh * 2], l0 = S.misc[hh * 2 + 1];
-                    const float m1 = S.misc[(2 + hh) * 2], l1 = S.misc[(2 + hh) * 2 + 1];
-                    const float M = fmaxf(m0, m1);  // finite: the split holding row pos is never empty
-                    const float w0 = (m0 == -__builtin_inff()) ? 0.f : expf(m0 - M);
-                    const float w1 = (m1 == -__builtin_inff()) ? 0.f : expf(m1 - M);
-                    const float out = (w0 * Oh + w1 * S.ored[1][hh][d]) / (w0 * l0 + w1 * l1);
-                    st64(ll + ATTNP + (2 * g + hh) * HD + d, pack(out, r + 1));
+                // Weighted sum of the split outputs: thread (q, e) over splits 8q .. 8q + 7, the
+                // eight quarters combined through LDS.
+                {
+                    const int q = tid / 64, e = tid % 64;
+                    float O = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int sj = q * 4 + j;
+                        O = fmaf(S.sc[0][sj], pl[sj * 66 + e], O);
+                    }
+                    float* q8 = &S.ored[0][0][0];  // [8][64]
+                    q8[q * 64 + e] = O;
+                    __syncthreads();
+                    if (tid < 64) {
+                        float t = 0.f;
+#pragma unroll
+                        for (int qq = 0; qq < 8; ++qq) t += q8[qq * 64 + tid];
+                        st64(ll + ATTNP + (2 * g + hh) * HD + d0 + tid, pack(t * S.misc[0], r + 1));
+                    }
                 }
-                PK_TRACE(l, 5);
+                PK_TRACE(l, 17);
+                __syncthreads();  // the partials in S.A are read before the next staging
+                PK_TRACE(l, 6);
             }
 
             // ---------------- O projection + residual: workgroups 0..127 -------------------
+            // The gate|up blocks are requested here, a stage early, by every workgroup.
+            {
+                bool ok = true;
+                if (w < H / 16 && !math) ok = poll_vec<H / CT>(ll + ATTNP, H, r + 1, S.vec, err);
+                if (math) {
+#pragma unroll
+                    for (int j = 0; j < 3; ++j) wgu[j].load(P.wgu, P.wgu_sb, 3 * w + j, H, mw, lane);
+                }
+                if (w < H / 16 && __syncthreads_or(!ok)) return;
+            }
             if (w < H / 16) {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
-                uint4 wv[CW2];
-                uint2 sbv[CW2];
-                load_block<FMT, CW2>(P.wo, P.wo_sb, w, H, wave, lane, wv, sbv);
-                if (!stage_packets<FMT, SRC_ATTN>(S, ll + ATTNP, r + 1, H, nullptr, err)) return;
-                PK_TRACE(l, 6);
-                PK_TRACE_MARKS(l, 1);
-                const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv, sbv, wave, lane));
+                PK_TRACE_X(l, 7);
+                stage_c<FMT, H / CT / 8, MATH>(S, S.vec, false);
+                const float y = reduce_math<MATH>(S, math ? wo.mac(S, mw, lane) : 0.f);
                 if (wave == 0 && lane < 16) {
                     const float xn = S.xown[lane] + y;
                     S.xown[lane] = xn;
                     st64(ll + XP + w * 16 + lane, pack(xn, 2 * r + 1));
                 }
-                PK_TRACE(l, 7);
+                PK_TRACE(l, 8);
             }
 
             // ---------------- RMSNorm + gate|up + SwiGLU: blocks 3w .. 3w + 2 --------------
             {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
-                uint4 wv[3][CW2];
-                uint2 sbv[3][CW2];
+                bool ok = true;
+                if (!math) ok = poll_vec<H / CT>(ll + XP, H, 2 * r + 1, S.vec, err);
+                if (math) {
 #pragma unroll
-                for (int j = 0; j < 3; ++j) load_block<FMT, CW2>(P.wgu, P.wgu_sb, 3 * w + j, H, wave, lane, wv[j], sbv[j]);
-                if (!stage_packets<FMT, SRC_X>(S, ll + XP, 2 * r + 1, H, P.mlp_norm, err)) return;
-                PK_TRACE(l, 8);
-                PK_TRACE_MARKS(l, 2);
+                    for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
+                    if (EARLY_DOWN && w < H / 16) wd.load(P.wd, P.wd_sb, w, FF, mw, lane);
+                    // The next layer's attention norm, or the final norm.
+                    load_norm8(nreg, (l + 1 < L ? a.layers[l + 1].attn_norm : a.final_norm) + tid * 8);
+                }
+                if (__syncthreads_or(!ok)) return;
+                PK_TRACE_X(l, 9);
+                stage_c<FMT, H / CT / 8, MATH>(S, S.vec, true);
+                PK_TRACE(l, 13);
+                float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
+                if (math) {
 #pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv[j], sbv[j], wave, lane));
-                    if (wave == 0) {
+                    for (int j = 0; j < 3; ++j) acc[j] = wgu[j].mac(S, mw, lane);
+                }
+                reduce_math3<MATH>(S, acc, y);
+                PK_TRACE(l, 14);
+                if (wave == 0) {
+#pragma unroll
+                    for (int j = 0; j < 3; ++j) {
                         // Block 3w + j: gate units 8 (3w + j) + 0..7 in lanes 0-7, their up rows in 8-15.
-                        const float up = __shfl_xor(y, 8);
+                        const float up = __shfl_xor(y[j], 8);
                         if (lane < 8)
-                            st64(ll + HP + (3 * w + j) * 8 + lane, pack((y / (1.f + expf(-y))) * up, r + 1));
+                            st64(ll + HP + (3 * w + j) * 8 + lane, pack((y[j] / (1.f + expf(-y[j]))) * up, r + 1));
                     }
                 }
-                PK_TRACE(l, 9);
+                PK_TRACE(l, 10);
             }
 
             // ---------------- down + residual: workgroups 0..127 ---------------------------
             if (w < H / 16) {
-                const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
-                uint4 wv[CW6];
-                uint2 sbv[CW6];
-                load_block<FMT, CW6>(P.wd, P.wd_sb, w, FF, wave, lane, wv, sbv);
-                if (!stage_packets<FMT, SRC_H>(S, ll + HP, r + 1, FF, nullptr, err)) return;
-                PK_TRACE(l, 10);
-                PK_TRACE_MARKS(l, 3);
-                const float y = reduce_waves(S, block_mac<FMT, CW6>(S, wv, sbv, wave, lane));
+                bool ok = true;
+                if (!math) ok = poll_vec<FF / CT>(ll + HP, FF, r + 1, S.vec, err);
+                if (!EARLY_DOWN && math) wd.load(P.wd, P.wd_sb, w, FF, mw, lane);
+                if (__syncthreads_or(!ok)) return;
+                PK_TRACE_X(l, 11);
+                stage_c<FMT, FF / CT / 8, MATH>(S, S.vec, false);
+                PK_TRACE(l, 18);
+                const float y = reduce_math<MATH>(S, math ? wd.mac(S, mw, lane) : 0.f);
+                PK_TRACE(l, 19);
                 if (wave == 0 && lane < 16) {
                     const float xn = S.xown[lane] + y;
                     S.xown[lane] = xn;
                     st64(ll + XP + w * 16 + lane, pack(xn, 2 * r + 2));
                 }
-                PK_TRACE(l, 11);
+                PK_TRACE(l, 12);
             }
         }
 
         // ---------------- final RMSNorm + lm_head + per-workgroup argmax ---------------------
         {
-            const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
+            const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+            constexpr bool math = MATH;
+            const int mw = wave;
             const unsigned r_last = (unsigned)(step * L + L - 1);
             PK_TRACE(L, 0);
-            uint4 wv0[CW2], wv1[CW2];
-            uint2 sb0[CW2], sb1[CW2];
-            load_block<FMT, CW2>(a.E, a.Esb, w, H, wave, lane, wv0, sb0);
-            load_block<FMT, CW2>(a.E, a.Esb, w + NWG, H, wave, lane, wv1, sb1);
-            if (!stage_packets<FMT, SRC_X>(S, ll + XP, 2 * r_last + 2, H, a.final_norm, err)) return;
-            PK_TRACE(L, 1);
-            PK_TRACE_MARKS(L, 0);
+            WB<FMT, CW2> wl[LM_DEPTH];  // blocks w + k * 256, LM_DEPTH in flight
+            bool ok = true;
+            if (!math) ok = poll_vec<H / CT>(ll + XP, H, 2 * r_last + 2, S.vec, err);
+            if (math) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
+#pragma unroll
+                for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, mw, lane);
+            }
+            if (__syncthreads_or(!ok)) return;
+            PK_TRACE_X(L, 1);
+            stage_c<FMT, H / CT / 8, MATH>(S, S.vec, true);
             float best = -__builtin_inff();
             int besti = 0x7fffffff;
-            // Two blocks in flight (static ping-pong buffers): a block computes while the block
-            // two ahead loads.  Blocks w + k * 256; every workgroup has at least 37.
-            for (int rb = w; rb < NRB; rb += 2 * NWG) {
-                {
-                    const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv0, sb0, wave, lane));
-                    if (wave == 0 && lane < 16) argmax_merge(best, besti, y, rb * 16 + lane);
-                    if (rb + 2 * NWG < NRB) load_block<FMT, CW2>(a.E, a.Esb, rb + 2 * NWG, H, wave, lane, wv0, sb0);
-                }
-                if (rb + NWG < NRB) {
-                    const float y = reduce_waves(S, block_mac<FMT, CW2>(S, wv1, sb1, wave, lane));
-                    if (wave == 0 && lane < 16) argmax_merge(best, besti, y, (rb + NWG) * 16 + lane);
-                    if (rb + 3 * NWG < NRB) load_block<FMT, CW2>(a.E, a.Esb, rb + 3 * NWG, H, wave, lane, wv1, sb1);
+            for (int rb0 = w; rb0 < NRB; rb0 += LM_DEPTH * NWG) {  // uniform over the workgroup
+#pragma unroll
+                for (int k = 0; k < LM_DEPTH; ++k) {
+                    const int rb = rb0 + k * NWG;
+                    if (rb < NRB) {
+                        const float y = reduce_math<MATH>(S, math ? wl[k].mac(S, mw, lane) : 0.f);
+                        if (wave == 0 && lane < 16) argmax_merge(best, besti, y, rb * 16 + lane);
+                        if (math && rb + LM_DEPTH * NWG < NRB) wl[k].load(a.E, a.Esb, rb + LM_DEPTH * NWG, H, mw, lane);
+                    }
                 }
             }
             if (wave == 0) {
@@ -874,17 +905,22 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                 }
             }
             PK_TRACE(L, 2);
+            if (math) load_norm8(nreg, a.layers[0].attn_norm + tid * 8);  // for the next step
         }
 
         // ---------------- greedy commit, evaluated by every workgroup ------------------------
         {
-            const int tid = my_tid(), lane = tid % 64, wave = tid / 64;
-            uint64_t p[2];
-            const bool ok = poll<2>(
-                ll + LMP, [&](int i) { return tid < NWG ? 2 * tid + i : -1; }, (unsigned)step + 1, p, err);
+            const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+            bool ok = true;
+            if (!MATH) ok = poll_vec<2>(ll + LMP, 2 * NWG, (unsigned)step + 1, S.vec, err);
             if (__syncthreads_or(!ok)) return;
-            float bv = tid < NWG ? val_of(p[0]) : -__builtin_inff();
-            int bi = tid < NWG ? (int)(uint32_t)p[1] : 0x7fffffff;
+            PK_TRACE_X(L, 3);
+            float bv = -__builtin_inff();
+            int bi = 0x7fffffff;
+            if (tid < NWG) {
+                bv = S.vec[2 * tid];
+                bi = (int)as_u32(S.vec[2 * tid + 1]);
+            }
             wave_argmax(bv, bi);
             if (lane == 0) {
                 S.misc[wave] = bv;
@@ -913,7 +949,6 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
                 st->logits_rows = 0;
                 if (stop) st->done = 1;
             }
-            PK_TRACE(L, 3);
             if (stop) break;
             // Next token's embedding (Shaders.swift:464-476), in every workgroup.
             __syncthreads();  // every thread has read S.misc / S.imisc
@@ -922,8 +957,25 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
             if (tid < 16 && w < H / 16) S.xown[tid] = S.emb[w * 16 + tid];
             if (w == 0 && step == a.nsteps - 1)
                 for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row for the host
+            PK_TRACE(L, 4);
         }
     }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
+    __shared__ Shared S;
+    const int w = blockIdx.x;
+    for (int i = my_tid(); i < (int)sizeof(S.A) / 4; i += THREADS) ((uint32_t*)S.A)[i] = 0u;
+    // Control block and the embedding of the first token (written before this launch).
+    const State* st = a.st;
+    if (st->done || st->n != 1) return;  // single-row passes only (checked by the host too)
+    for (int i = my_tid(); i < H; i += THREADS) S.emb[i] = a.x[i];
+    if (my_tid() < 16 && w < H / 16) S.xown[my_tid()] = a.x[w * 16 + my_tid()];
+    if (wave_id() < MW)
+        decode_loop<FMT, true>(a, S, w, st->pos, st->step);
+    else
+        decode_loop<FMT, false>(a, S, w, st->pos, st->step);
 }
 
 }  // namespace pk
