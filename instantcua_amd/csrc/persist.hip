@@ -453,7 +453,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
     constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
     constexpr int CW6 = FF / CHK / MW;  // K = 6144
     constexpr int NRB = VOCAB / 16;     // lm_head row blocks
-    constexpr int LM_DEPTH = (FMT == FMT_Q4) ? 4 : 2;  // lm_head blocks in flight
+    constexpr int CW8 = H / CHK / WAVES;  // lm_head chunks per wave (all eight waves)
+    constexpr int LM_DEPTH = 4;           // lm_head blocks in flight per wave
+    constexpr int LM_BLOCKS = (NRB + NWG - 1) / NWG;  // 38 block slots per workgroup
     // Down tiles are requested when the down stage starts: holding them through the gate|up stage
     // as well would not fit the math waves' registers.
     constexpr bool EARLY_DOWN = false;
@@ -869,40 +871,58 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
         {
             const int tid = my_tid(), lane = tid % 64, wave = wave_id();
             constexpr bool math = MATH;
-            const int mw = wave;
             const unsigned r_last = (unsigned)(step * L + L - 1);
             PK_TRACE(L, 0);
-            WB<FMT, CW2> wl[LM_DEPTH];  // blocks w + k * 256, LM_DEPTH in flight
+            // All eight waves stream the blocks w + k * 256 (chunks wave * CW8 ..), LM_DEPTH in
+            // flight per wave; the exchange waves issue theirs once their poll is done.  Each
+            // wave's per-block partial sums go to LDS; one reduction and argmax at the end.
+            WB<FMT, CW8> wl[LM_DEPTH];
             bool ok = true;
             if (!math) ok = poll_vec<H / CT>(ll + XP, H, 2 * r_last + 2, S.vec, err);
             if (math) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
-#pragma unroll
-                for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, mw, lane);
             }
+#pragma unroll
+            for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
             if (__syncthreads_or(!ok)) return;
             PK_TRACE_X(L, 1);
             stage_c<FMT, H / CT / 8, MATH>(S, S.vec, true);
-            float best = -__builtin_inff();
-            int besti = 0x7fffffff;
-            for (int rb0 = w; rb0 < NRB; rb0 += LM_DEPTH * NWG) {  // uniform over the workgroup
+            float* plm = (float*)(S.A + 64 * 1024);  // [LM_BLOCKS][WAVES][16] partial sums
+            for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
 #pragma unroll
                 for (int k = 0; k < LM_DEPTH; ++k) {
-                    const int rb = rb0 + k * NWG;
+                    const int kb = k0 + k, rb = w + kb * NWG;
                     if (rb < NRB) {
-                        const float y = reduce_math<MATH>(S, math ? wl[k].mac(S, mw, lane) : 0.f);
-                        if (wave == 0 && lane < 16) argmax_merge(best, besti, y, rb * 16 + lane);
-                        if (math && rb + LM_DEPTH * NWG < NRB) wl[k].load(a.E, a.Esb, rb + LM_DEPTH * NWG, H, mw, lane);
+                        const float y = wl[k].mac(S, wave, lane);
+                        if (lane < 16) plm[(kb * WAVES + wave) * 16 + lane] = y;
+                        if (rb + LM_DEPTH * NWG < NRB) wl[k].load(a.E, a.Esb, rb + LM_DEPTH * NWG, H, wave, lane);
                     }
                 }
             }
-            if (wave == 0) {
-                wave_argmax(best, besti);  // lanes >= 16 hold (-inf, INT_MAX)
-                if (lane == 0) {
-                    st64(ll + LMP + 2 * w, pack(best, (unsigned)step + 1));
-                    st64(ll + LMP + 2 * w + 1, pack_i(besti, (unsigned)step + 1));
+            __syncthreads();
+            float best = -__builtin_inff();
+            int besti = 0x7fffffff;
+            for (int e = tid; e < LM_BLOCKS * 16; e += THREADS) {  // (block, row) pairs
+                const int kb = e / 16, rw = e % 16;
+                if (w + kb * NWG < NRB) {
+                    const float* pp = plm + kb * WAVES * 16 + rw;
+                    float y = 0.f;
+#pragma unroll
+                    for (int wv = 0; wv < WAVES; ++wv) y += pp[wv * 16];
+                    argmax_merge(best, besti, y, (w + kb * NWG) * 16 + rw);
                 }
+            }
+            wave_argmax(best, besti);
+            if (lane == 0) {
+                S.misc[8 + wave] = best;
+                S.imisc[8 + wave] = besti;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                for (int wv = 1; wv < WAVES; ++wv) argmax_merge(best, besti, S.misc[8 + wv], S.imisc[8 + wv]);
+                st64(ll + LMP + 2 * w, pack(best, (unsigned)step + 1));
+                st64(ll + LMP + 2 * w + 1, pack_i(besti, (unsigned)step + 1));
             }
             PK_TRACE(L, 2);
             if (math) load_norm8(nreg, a.layers[0].attn_norm + tid * 8);  // for the next step
