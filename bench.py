@@ -33,6 +33,11 @@ HBM_PEAK = 8.0e12  # B/s, MI355X
 LAYERS = 28
 VIS_OFFSET, LLM_H, LLM_W = 16, 32, 32
 PREFILL = 4096
+# HBM bytes the persistent decode launch moves per algorithmic byte, from rocprofv3 FETCH_SIZE
+# (scaled by 1.983, the factor that makes it read a GEMV of known footprint correctly) plus
+# WRITE_SIZE over a 16-step launch at this context: 1.4970 GB per step against 1.4393 GB of
+# weights and K/V (profiles/decode_q4_4k_persistent_counters.md).
+DECODE_TRAFFIC_RATIO = 1.4970 / 1.4393
 
 
 def weight_bytes_per_token(fmt=WeightFormat.Q4) -> int:
@@ -106,6 +111,9 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="profiling runs: start decoding at the same 4096-slot context without the prefill "
+                         "(cache rows stay zero; same bytes per step), so a profile holds only the decode launch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU decode is a design note only",
@@ -125,11 +133,15 @@ def main():
     e.prepare_mrope(VIS_OFFSET, LLM_H, LLM_W)
     e.set_visual(vp.pooler.astype(np.float32), [d.astype(np.float32) for d in vp.deepstack])
 
-    t1 = time.perf_counter()
-    e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=W + K + 1)
-    prefill_wall = time.perf_counter() - t1
-    prefill_ms = e.last_timing["prefill_ms"]
-    log(f"prefill {PREFILL} tokens: {prefill_ms:.1f} ms (GPU events), {prefill_wall * 1e3:.1f} ms wall")
+    if args.no_prefill:
+        e.set_position(PREFILL, int(vp.tokens[-1]), 1, W + K + 1)
+        prefill_ms = float("nan")
+    else:
+        t1 = time.perf_counter()
+        e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=W + K + 1)
+        prefill_wall = time.perf_counter() - t1
+        prefill_ms = e.last_timing["prefill_ms"]
+        log(f"prefill {PREFILL} tokens: {prefill_ms:.1f} ms (GPU events), {prefill_wall * 1e3:.1f} ms wall")
 
     if W:
         e.decode_steps(W)
@@ -175,11 +187,12 @@ def main():
                    "batch": 1},
         "decode_roofline_frac": round(achieved / HBM_PEAK, 4),
         "decode_bytes_per_token": int(bytes_tok),
-        "prefill_tok_s": round(PREFILL / (prefill_ms / 1e3), 1),
-        "prefill_ms": round(prefill_ms, 2),
+        "prefill_tok_s": None if args.no_prefill else round(PREFILL / (prefill_ms / 1e3), 1),
+        "prefill_ms": None if args.no_prefill else round(prefill_ms, 2),
         # Dominant kernel: the persistent decode kernel (one launch runs the K timed steps).
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": int(launch_bytes * DECODE_TRAFFIC_RATIO) if e_persistent else None,
                      "kernel": "pk::decode_kernel<2> (q4 persistent decode)" if e_persistent
                                else "decode step graph (q4)",
                      "launch_ms": round(dec_ms, 4), "bytes_per_launch": int(launch_bytes)},
