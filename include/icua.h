@@ -32,6 +32,7 @@ enum {
     ICUA_FLAG_GRAMMAR_PAIRS = 1, /* forced syntax pairs + ')' stop of k_commit (Shaders.swift:1543-1560) */
     ICUA_FLAG_PREFIX_CACHE = 2,  /* reuse the KV of an identical pre-image prefix (Engine.swift:719-735) */
     ICUA_FLAG_GRAPH_DECODE = 4,  /* decode through the per-kernel HIP graph instead of the persistent kernel */
+    ICUA_FLAG_PASS_PREFILL = 8,  /* prefill q4 prompts in passes of 8 rows instead of the matrix-core GEMMs */
 };
 
 /* Decode control block, first twelve fields as `State` (Shaders.swift:41-54). */
@@ -82,7 +83,9 @@ int icua_set_visual(icua_engine* e, const float* pooler, const float* const* dee
 
 /* Engine.encodePrefill (Engine.swift:658-673) run to completion: embeds tokens[0..n) at cache
  * slots start_pos.., runs every decoder layer (DeepStack after layers 0-2 at the visual rows),
- * then lm_head + greedy commit of the first generated token.  Resets step/done.
+ * then lm_head + greedy commit of the first generated token.  Resets step/done.  q4 prompts
+ * longer than 8 rows run as many-token matrix-core GEMMs and flash attention in chunks of up to
+ * 4096 rows (unless ICUA_FLAG_PASS_PREFILL); other formats and short prompts run in passes of 8.
  * vis_offset is the row of the first image-pad token in `tokens` (-1: none).
  * write_logits: keep the first-token logits for icua_logits(). */
 int icua_prefill(icua_engine* e, const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new,

@@ -26,20 +26,6 @@ constexpr int ATT_THREADS = 256;
 constexpr int ATT_CH = 64;  // prior slots per split: 16 quarter-waves x 4 slots
 constexpr int PART_STRIDE = HD + 2;
 
-// Per-head RMSNorm(128) + RoPE of one 128-vector by one wave: lane i owns the rotation pair
-// (i, i + 64).
-__device__ __forceinline__ void norm_rope_pair(float& a, float& b, const float* w, const float* cs, int lane) {
-    const float ss = wave_sum(a * a + b * b);
-    const float scale = 1.0f / sqrtf(ss / (float)HD + EPS);
-    a = a * scale * w[lane];
-    b = b * scale * w[lane + 64];
-    const float c = cs[2 * lane], sn = cs[2 * lane + 1];
-    const float a2 = a * c - b * sn;
-    const float b2 = b * c + a * sn;
-    a = a2;
-    b = b2;
-}
-
 __device__ __forceinline__ void unpack8(const uint4 raw, float* out) {
     const uint32_t d4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll

@@ -5,7 +5,9 @@
 //
 // Differences by design: one HIP stream instead of Metal command buffers; one decode step is a
 // captured HIP graph replayed per token (the reference encodes 8 steps per command buffer);
-// prefill runs in passes of up to MAXM rows through the same kernels as decode.
+// q4 prompts longer than MAXM rows prefill through the matrix-core GEMMs and flash attention of
+// prefill.hip in chunks of up to PF_CHUNK rows; other prompts run in passes of up to MAXM rows
+// through the decode kernels.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -82,6 +84,8 @@ void mrope_table(int maxctx, int vis_offset, int llm_h, int llm_w, std::vector<f
     }
 }
 
+constexpr int PF_CHUNK = 4096;  // rows per matrix-core prefill chunk
+
 struct NullState {
     State* d = nullptr;
 };
@@ -129,6 +133,11 @@ struct icua_engine {
     unsigned* psync = nullptr;
     LayerPtrs* d_layers = nullptr;
     bool persist_ok = false;
+    // Matrix-core prefill buffers for chunks of up to pf_cap rows (allocated on first use).
+    int pf_cap = 0;
+    float *px = nullptr, *pqkv = nullptr, *patt = nullptr, *ph = nullptr, *pxf = nullptr;
+    uint8_t* pxa = nullptr;
+    uint16_t *pqh = nullptr, *pql = nullptr;
 
     uint16_t* kv_ptr(int l, int kind) const { return kv + ((size_t)l * 2 + kind) * NKV * (size_t)maxctx * HD; }
 
@@ -462,6 +471,113 @@ struct icua_engine {
         return 0;
     }
 
+    void free_pf() {
+        void* bufs[] = {px, pqkv, patt, ph, pxf, pxa, pqh, pql};
+        for (void* b : bufs)
+            if (b) (void)hipFree(b);
+        px = pqkv = patt = ph = pxf = nullptr;
+        pxa = nullptr;
+        pqh = pql = nullptr;
+        pf_cap = 0;
+    }
+
+    int ensure_pf(int rows) {
+        const int cap = (rows + 127) / 128 * 128;
+        if (cap <= pf_cap) return 0;
+        HIPCK(hipStreamSynchronize(stream));
+        free_pf();
+        HIPCK(hipMalloc(&px, sizeof(float) * cap * H));
+        HIPCK(hipMalloc(&pqkv, sizeof(float) * cap * QKV));
+        HIPCK(hipMalloc(&patt, sizeof(float) * cap * H));
+        HIPCK(hipMalloc(&ph, sizeof(float) * cap * FF));
+        HIPCK(hipMalloc(&pxa, (size_t)cap / 16 * (FF / 64) * 3 * 1024));
+        HIPCK(hipMalloc(&pxf, sizeof(float) * 2 * (size_t)cap / 16 * (FF / 64) * 16));
+        HIPCK(hipMalloc(&pqh, sizeof(uint16_t) * (size_t)cap * NH * HD));
+        HIPCK(hipMalloc(&pql, sizeof(uint16_t) * (size_t)cap * NH * HD));
+        // Rows beyond a chunk's M are read (never stored) by the attention kernel: keep them finite.
+        HIPCK(hipMemset(pqh, 0, sizeof(uint16_t) * (size_t)cap * NH * HD));
+        HIPCK(hipMemset(pql, 0, sizeof(uint16_t) * (size_t)cap * NH * HD));
+        pf_cap = cap;
+        return 0;
+    }
+
+    // One decoder layer over chunk rows [0, M) at cache slots p0.. (prompt rows row0..).
+    int enqueue_pf_layer(int l, int M, int Mpad, int p0, int row0, int vis_offset) {
+        const LayerW& w = L[l];
+        PfGemmArgs g{};
+        g.xa = pxa;
+        g.xf = pxf;
+        g.M = M;
+        g.Mpad = Mpad;
+        g.row0 = row0;
+        g.vis_offset = vis_offset;
+        g.n_vis = n_vis;
+        // 1. RMSNorm + fused QKV.
+        HIPCK(launch_pf_prep(H, 1, px, w.attn_norm, M, Mpad, pxa, pxf, stream));
+        g.w = w.wqkv;
+        g.sb = w.wqkv_sb;
+        g.N = QKV;
+        g.y = pqkv;
+        HIPCK(launch_pf_gemm(H, EPI_STORE, g, stream));
+        // 2. q/k norm + M-RoPE + KV write, causal flash attention.
+        PfQkArgs qa{pqkv, w.q_norm, w.k_norm, rope, kv_ptr(l, 0), kv_ptr(l, 1), pqh, pql, M, p0, maxctx};
+        HIPCK(launch_pf_qk(qa, stream));
+        PfAttnArgs aa{pqh, pql, kv_ptr(l, 0), kv_ptr(l, 1), patt, M, p0, maxctx};
+        HIPCK(launch_pf_attn(aa, stream));
+        // 3. O projection + residual.
+        HIPCK(launch_pf_prep(H, 0, patt, nullptr, M, Mpad, pxa, pxf, stream));
+        g.w = w.wo;
+        g.sb = w.wo_sb;
+        g.N = H;
+        g.y = px;
+        HIPCK(launch_pf_gemm(H, EPI_RESID, g, stream));
+        // 4. RMSNorm + gate|up + SwiGLU.
+        HIPCK(launch_pf_prep(H, 1, px, w.mlp_norm, M, Mpad, pxa, pxf, stream));
+        g.w = w.wgu;
+        g.sb = w.wgu_sb;
+        g.N = GU;
+        g.h = ph;
+        HIPCK(launch_pf_gemm(H, EPI_SWIGLU, g, stream));
+        // 5. Down projection + residual (+ DeepStack after layers 0-2 at visual rows).
+        HIPCK(launch_pf_prep(FF, 0, ph, nullptr, M, Mpad, pxa, pxf, stream));
+        g.w = w.wd;
+        g.sb = w.wd_sb;
+        g.N = H;
+        g.y = px;
+        g.ds = (has_ds && l < 3) ? ds[l] : nullptr;
+        HIPCK(launch_pf_gemm(FF, EPI_RESID, g, stream));
+        return 0;
+    }
+
+    // Matrix-core prefill of prompt rows [0, n) at slots start_pos.., then the last row's
+    // lm_head + commit as a one-row pass.  The state was written by prefill().
+    int prefill_chunks(int n, int start_pos, int vis_offset, int write_logits) {
+        if (ensure_pf(std::min(n, PF_CHUNK))) return -1;
+        int M = 0;
+        for (int c0 = 0; c0 < n; c0 += PF_CHUNK) {
+            M = std::min(PF_CHUNK, n - c0);
+            const int Mpad = (M + 127) / 128 * 128;
+            EmbedArgs ea{};
+            ea.toks = prompt;
+            ea.E = E;
+            ea.Esb = Esb;
+            ea.fmt = fmt;
+            ea.pooler = vis_offset >= 0 ? pooler : nullptr;
+            ea.row0 = c0;
+            ea.x = px;
+            ea.st = st;
+            ea.n = M;
+            HIPCK(launch_embed(ea, stream));
+            for (int l = 0; l < layers; ++l)
+                if (enqueue_pf_layer(l, M, Mpad, start_pos + c0, c0, vis_offset)) return -1;
+        }
+        HIPCK(hipMemcpyAsync(x, px + (size_t)(M - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, stream));
+        HIPCK(launch_set_pass(st, start_pos + n - 1, 1, write_logits ? 1 : 0, stream));
+        return enqueue_head(MAXM, 0);
+    }
+
+    bool use_pf(int n) const { return fmt == 2 && n > MAXM && !(flags & ICUA_FLAG_PASS_PREFILL); }
+
     int prefill(const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new, int write_logits) {
         if (n <= 0) return fail("empty prompt");
         if (max_new < 1) max_new = 1;
@@ -487,6 +603,22 @@ struct icua_engine {
         s.logits_rows = 0;
         if (write_state(s)) return -1;
         HIPCK(hipEventRecord(ev0, stream));
+        if (use_pf(n)) {
+            if (prefill_chunks(n, start_pos, vis_offset, write_logits)) return -1;
+        } else {
+            if (prefill_passes(n, start_pos, vis_offset, write_logits)) return -1;
+        }
+        HIPCK(hipEventRecord(ev1, stream));
+        HIPCK(hipEventSynchronize(ev1));
+        float ms = 0;
+        HIPCK(hipEventElapsedTime(&ms, ev0, ev1));
+        timing.prefill_ms = ms;
+        timing.prefill_tokens = n;
+        last_logits_rows = write_logits ? 1 : 0;
+        return 0;
+    }
+
+    int prefill_passes(int n, int start_pos, int vis_offset, int write_logits) {
         for (int r0 = 0; r0 < n; r0 += MAXM) {
             const int m = std::min(MAXM, n - r0);
             const bool last = (r0 + m == n);
@@ -505,15 +637,7 @@ struct icua_engine {
             for (int l = 0; l < layers; ++l)
                 if (enqueue_layer(l, MAXM, r0)) return -1;
         }
-        if (enqueue_head(MAXM, 0)) return -1;
-        HIPCK(hipEventRecord(ev1, stream));
-        HIPCK(hipEventSynchronize(ev1));
-        float ms = 0;
-        HIPCK(hipEventElapsedTime(&ms, ev0, ev1));
-        timing.prefill_ms = ms;
-        timing.prefill_tokens = n;
-        last_logits_rows = write_logits ? 1 : 0;
-        return 0;
+        return enqueue_head(MAXM, 0);
     }
 
     int decode_steps(int k, double* ms_out) {
@@ -591,6 +715,7 @@ void icua_engine_destroy(icua_engine* e) {
     void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->pval,
                     e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
                     e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_layers};
+    e->free_pf();
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (e->ev0) (void)hipEventDestroy(e->ev0);

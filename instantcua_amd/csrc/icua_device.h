@@ -100,6 +100,32 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (every lane gets the result).
+__device__ __forceinline__ float max_x4(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(as_u32(v), as_u32(v), false, false);
+    v = fmaxf(as_f32(r[0]), as_f32(r[1]));
+    auto q = __builtin_amdgcn_permlane32_swap(as_u32(v), as_u32(v), false, false);
+    return fmaxf(as_f32(q[0]), as_f32(q[1]));
+}
+__device__ __forceinline__ float sum_x4(float v) {
+    const float s = swap16_add(v, v);
+    return swap32_add(s, s);
+}
+
+// Per-head RMSNorm(128) + RoPE of one 128-vector by one wave: lane i owns the rotation pair
+// (i, i + 64).
+__device__ __forceinline__ void norm_rope_pair(float& a, float& b, const float* w, const float* cs, int lane) {
+    const float ss = wave_sum(a * a + b * b);
+    const float scale = 1.0f / sqrtf(ss / (float)HD + EPS);
+    a = a * scale * w[lane];
+    b = b * scale * w[lane + 64];
+    const float c = cs[2 * lane], sn = cs[2 * lane + 1];
+    const float a2 = a * c - b * sn;
+    const float b2 = b * c + a * sn;
+    a = a2;
+    b = b2;
+}
+
 // Transposed reduction of R row partials held by every lane (R = 4 or 8).  Afterwards the
 // total of row r is held by the lanes l with l / (64 / R) == r.
 template <int R>

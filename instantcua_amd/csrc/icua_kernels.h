@@ -91,6 +91,50 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 // Sets pos / n / logits_rows of the control block on the stream.
 hipError_t launch_set_pass(State* st, int pos, int n, int logits_rows, hipStream_t s);
 
+// ---- Matrix-core prefill (prefill.hip), q4 weights, passes of M <= Mpad tokens (Mpad % 128 == 0).
+// Activation operands of one GEMM input: 21-bit slices [Mpad / 16][K / 64][3][1 KiB] and
+// per-(token, group) factors [Mpad / 16][K / 64][16] float2.
+hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint8_t* xa,
+                          float* xf, hipStream_t s);
+
+struct PfGemmArgs {
+    const uint8_t* xa;      // activation slices (launch_pf_prep)
+    const float* xf;        // activation factors
+    const uint8_t* w;       // codes in 16-row MFMA tiles (launch_repack)
+    const uint8_t* sb;      // half2 (scale, bias) [N][K / 64], tiled row order
+    int N, M, Mpad;
+    float* y;               // EPI_STORE: y [M][N]; EPI_RESID: residual x [M][N] (+=)
+    float* h;               // EPI_SWIGLU: [M][FF]
+    const float* ds;        // EPI_RESID: DeepStack rows [n_vis][H] or null
+    int row0;               // prompt row of pass row 0
+    int vis_offset, n_vis;
+};
+// epi: EPI_STORE / EPI_RESID / EPI_SWIGLU; K = 2048 (any epilogue) or 6144 (EPI_RESID).
+hipError_t launch_pf_gemm(int K, int epi, const PfGemmArgs& a, hipStream_t s);
+
+struct PfQkArgs {
+    const float* qkv;       // raw fused QKV rows [M][QKV]
+    const float* q_norm;
+    const float* k_norm;
+    const float* rope;      // [maxctx][64] (cos, sin)
+    uint16_t* kc;           // this layer's K / V cache [NKV][maxctx][HD] fp16
+    uint16_t* vc;
+    uint16_t* qh;           // queries, pre-scaled, fp16 hi / lo parts [Mpad][NH][HD]
+    uint16_t* ql;
+    int M, p0, maxctx;      // rows of the pass at cache slots p0 .. p0 + M - 1
+};
+hipError_t launch_pf_qk(const PfQkArgs& a, hipStream_t s);
+
+struct PfAttnArgs {
+    const uint16_t* qh;
+    const uint16_t* ql;
+    const uint16_t* kc;
+    const uint16_t* vc;
+    float* out;             // attention rows [M][H] fp32
+    int M, p0, maxctx;
+};
+hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s);
+
 // Bit-exact dequantisation of rows [row0, row0 + rows) to fp32 (w = s*q + b / s*q / half),
 // from the row-major .icua layout (tiled = 0) or the GEMV tile layout (tiled = 1).
 hipError_t launch_dequant(int fmt, const uint8_t* w, const uint8_t* sb, int K, int row0, int rows, float* out,

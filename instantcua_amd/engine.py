@@ -27,6 +27,7 @@ MAXM = 8
 FLAG_GRAMMAR_PAIRS = 1
 FLAG_PREFIX_CACHE = 2
 FLAG_GRAPH_DECODE = 4
+FLAG_PASS_PREFILL = 8
 
 EXPORTS = [
     "icua_last_error", "icua_engine_create", "icua_engine_create_from_memory", "icua_engine_destroy",
@@ -257,6 +258,15 @@ class Engine:
     @graph_decode.setter
     def graph_decode(self, v: bool):
         self.set_flags((self._flags | FLAG_GRAPH_DECODE) if v else (self._flags & ~FLAG_GRAPH_DECODE))
+
+    @property
+    def pass_prefill(self) -> bool:
+        """Prefill q4 prompts in passes of 8 rows instead of the matrix-core GEMMs."""
+        return bool(self._flags & FLAG_PASS_PREFILL)
+
+    @pass_prefill.setter
+    def pass_prefill(self, v: bool):
+        self.set_flags((self._flags | FLAG_PASS_PREFILL) if v else (self._flags & ~FLAG_PASS_PREFILL))
 
     def set_flags(self, flags: int) -> None:
         _check(lib().icua_set_flags(self._h, flags))

@@ -50,3 +50,17 @@ def compare_greedy(gpu_tokens, ref_tokens, ref_margins, ref_top=None):
                 f"greedy divergence at step {i}: gpu {gpu_tokens[i]} oracle {ref_tokens[i]} "
                 f"(oracle top-2 margin {ref_margins[i]:.4g})")
     return n, "identical"
+
+
+def fp16_close(got, ref, max_ulp=1, row_tol=1e-6, frac_over_1ulp=0.0):
+    """fp16 cache rows [..., HD]: every value within max_ulp fp16 ulps of itself or row_tol of its
+    row's largest magnitude, and at most frac_over_1ulp of the values more than one ulp away."""
+    g = np.asarray(got).astype(np.float32)
+    r = np.asarray(ref).astype(np.float32)
+    ulp = np.spacing(np.abs(r).astype(np.float16)).astype(np.float32)
+    rowmax = np.abs(r).max(axis=-1, keepdims=True)
+    d = np.abs(g - r)
+    bad = d > np.maximum(max_ulp * ulp, row_tol * rowmax)
+    assert not bad.any(), f"{bad.sum()} cache values beyond {max_ulp} ulp / {row_tol:g} of the row"
+    over = (d > ulp).mean()
+    assert over <= frac_over_1ulp, f"{over:.3g} of the cache values beyond one ulp"

@@ -1,0 +1,118 @@
+"""GPU parity of the matrix-core prefill (int8-sliced GEMMs, flash attention, chunking) against
+the oracle and against the 8-row pass path, through the C ABI."""
+import numpy as np
+import pytest
+
+from conftest import compare_greedy, fp16_close, rel_err
+from instantcua_amd import synth
+from instantcua_amd.engine import Engine
+from instantcua_amd.modelfile import Dims, WeightFormat
+
+pytestmark = pytest.mark.gpu
+
+LAYERS = 2
+
+
+@pytest.fixture(scope="module")
+def q4_small():
+    return synth.build_model_image(WeightFormat.Q4, n_layers=LAYERS, tag="q4-small")
+
+
+def _kv_close(got_rows, ref_rows, layer):
+    # Layer 0's K/V come from one projection of the embedding: fp32-level differences only
+    # flip fp16 rounding boundaries, or move a value near zero (RoPE cancellation) by a few of
+    # its own ulps but less than 1e-6 of its row.  Layer 1 inherits layer 0's fp16-cache reads
+    # and summation order, so small values of a row can be several of their own ulps off
+    # (bounded against the row scale, as in the decode-path tests).
+    if layer == 0:
+        fp16_close(got_rows, ref_rows, max_ulp=1, row_tol=1e-6, frac_over_1ulp=1e-3)
+    else:
+        fp16_close(got_rows, ref_rows, max_ulp=2, row_tol=2e-3, frac_over_1ulp=5e-2)
+
+
+@pytest.mark.parametrize("n", [9, 130, 400])
+def test_prefill_matches_oracle(oracle_mod, q4_small, n):
+    """Prompts of one partial 16-row block up to several 128-row tiles: first logits, every
+    prompt K/V row of both layers and the greedy continuation."""
+    toks = synth.random_tokens(n, f"pf-oracle-{n}")
+    steps = 6
+    om = oracle_mod.OracleModel(q4_small, n + 16)
+    ref, margins, first = om.generate(toks, steps)
+    with Engine(image=q4_small, max_context=n + 16, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        assert not e.pass_prefill
+        tok0 = e.prefill(toks, max_new=steps, write_logits=True)
+        lg = e.logits(1)[0]
+        kv = {(l, k): e.read_kv(l, k, 0, n) for l in range(LAYERS) for k in range(2)}
+        e.decode_steps(steps - 1)
+        got = e.tokens(steps)
+        t = e.last_timing
+    assert rel_err(lg, first) < 1e-2  # the stated logits tolerance
+    assert rel_err(lg, first) < 1e-4, f"first-logit rel err {rel_err(lg, first):.3g}"
+    assert tok0 == ref[0]
+    for (l, k), rows in kv.items():
+        _kv_close(rows, om.kv(l, k)[:, :n], l)
+    cnt, note = compare_greedy(got, ref, margins, first.max() * np.ones(steps))
+    print(f"n {n}: {cnt}/{steps} identical ({note}); prefill {t['prefill_ms']:.2f} ms")
+
+
+def test_prefill_continuation_at_offset(oracle_mod, q4_small):
+    """A second prefill call at start_pos 200 attends over the cache rows of the first."""
+    toks = synth.random_tokens(500, "pf-offset")
+    om = oracle_mod.OracleModel(q4_small, 512)
+    ref_lg = om.run_pass(toks, 0, logits_rows=1)[0]
+    with Engine(image=q4_small, max_context=512, max_steps=8) as e:
+        e.eos = (-1, -1)
+        e.prefill(toks[:200], max_new=2)
+        e.prefill(toks[200:], start_pos=200, max_new=2, write_logits=True)
+        lg = e.logits(1)[0]
+        st = e.state()
+        kv = {(l, k): e.read_kv(l, k, 0, 500) for l in range(LAYERS) for k in range(2)}
+    assert st["pos"] == 500 and st["step"] == 1
+    assert rel_err(lg, ref_lg) < 1e-4, rel_err(lg, ref_lg)
+    for (l, k), rows in kv.items():
+        _kv_close(rows, om.kv(l, k)[:, :500], l)
+
+
+def test_visual_prefill_matches_oracle(oracle_mod, q4_small):
+    """Image-pad rows over several 16-row blocks: visual embeddings, 3D M-RoPE, DeepStack."""
+    vp = synth.visual_prompt(300, vis_offset=16, llm_h=8, llm_w=16, tag="pf-vis")
+    pooler = vp.pooler.astype(np.float32)
+    ds = [d.astype(np.float32) for d in vp.deepstack]
+    steps = 6
+    om = oracle_mod.OracleModel(q4_small, 320)
+    om.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
+    ref, margins, first = om.generate(vp.tokens, steps, pooler=pooler, vis_offset=vp.vis_offset, deepstack=ds)
+    with Engine(image=q4_small, max_context=320, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
+        e.set_visual(pooler, ds)
+        e.prefill(vp.tokens, vis_offset=vp.vis_offset, max_new=steps, write_logits=True)
+        lg = e.logits(1)[0]
+        kv1 = e.read_kv(1, 0, 0, 300)
+        e.decode_steps(steps - 1)
+        got = e.tokens(steps)
+    assert rel_err(lg, first) < 1e-4, rel_err(lg, first)
+    _kv_close(kv1, om.kv(1, 0)[:, :300], 1)
+    compare_greedy(got, ref, margins, first.max() * np.ones(steps))
+
+
+def test_two_chunks_match_pass_path(q4_small):
+    """4296 rows = a full 4096-row chunk + 200: the matrix-core path against the 8-row passes
+    (the same oracle-checked decode kernels) on first logits and every cache row of layer 1."""
+    n = 4096 + 200
+    toks = synth.random_tokens(n, "pf-chunks")
+    out = {}
+    for passes in (False, True):
+        with Engine(image=q4_small, max_context=n + 8, max_steps=4) as e:
+            e.eos = (-1, -1)
+            e.pass_prefill = passes
+            tok0 = e.prefill(toks, max_new=2, write_logits=True)
+            out[passes] = (tok0, e.logits(1)[0], e.read_kv(1, 0, 0, n), e.read_kv(1, 1, 0, n),
+                           e.last_timing["prefill_ms"])
+    mm, ps = out[False], out[True]
+    print(f"prefill {n} rows: matrix-core {mm[4]:.1f} ms, passes {ps[4]:.1f} ms")
+    assert rel_err(mm[1], ps[1]) < 1e-4, rel_err(mm[1], ps[1])
+    assert mm[0] == ps[0]
+    for kind in (2, 3):
+        fp16_close(mm[kind], ps[kind], max_ulp=2, row_tol=2e-3, frac_over_1ulp=5e-2)
