@@ -135,9 +135,8 @@ struct icua_engine {
     bool persist_ok = false;
     // Matrix-core prefill buffers for chunks of up to pf_cap rows (allocated on first use).
     int pf_cap = 0;
-    float *px = nullptr, *pqkv = nullptr, *patt = nullptr, *ph = nullptr, *pxf = nullptr;
-    uint8_t* pxa = nullptr;
-    uint16_t *pqh = nullptr, *pql = nullptr;
+    float *px = nullptr, *pqkv = nullptr, *patt = nullptr, *ph = nullptr, *pxs = nullptr, *pts = nullptr;
+    uint16_t *pxa = nullptr, *pqh = nullptr, *pql = nullptr;
 
     uint16_t* kv_ptr(int l, int kind) const { return kv + ((size_t)l * 2 + kind) * NKV * (size_t)maxctx * HD; }
 
@@ -472,12 +471,11 @@ struct icua_engine {
     }
 
     void free_pf() {
-        void* bufs[] = {px, pqkv, patt, ph, pxf, pxa, pqh, pql};
+        void* bufs[] = {px, pqkv, patt, ph, pxs, pts, pxa, pqh, pql};
         for (void* b : bufs)
             if (b) (void)hipFree(b);
-        px = pqkv = patt = ph = pxf = nullptr;
-        pxa = nullptr;
-        pqh = pql = nullptr;
+        px = pqkv = patt = ph = pxs = pts = nullptr;
+        pxa = pqh = pql = nullptr;
         pf_cap = 0;
     }
 
@@ -490,8 +488,9 @@ struct icua_engine {
         HIPCK(hipMalloc(&pqkv, sizeof(float) * cap * QKV));
         HIPCK(hipMalloc(&patt, sizeof(float) * cap * H));
         HIPCK(hipMalloc(&ph, sizeof(float) * cap * FF));
-        HIPCK(hipMalloc(&pxa, (size_t)cap / 16 * (FF / 64) * 3 * 1024));
-        HIPCK(hipMalloc(&pxf, sizeof(float) * 2 * (size_t)cap / 16 * (FF / 64) * 16));
+        HIPCK(hipMalloc(&pxa, sizeof(uint16_t) * 2 * (size_t)cap * FF));
+        HIPCK(hipMalloc(&pxs, sizeof(float) * (size_t)cap * (FF / 64)));
+        HIPCK(hipMalloc(&pts, sizeof(float) * (size_t)cap));
         HIPCK(hipMalloc(&pqh, sizeof(uint16_t) * (size_t)cap * NH * HD));
         HIPCK(hipMalloc(&pql, sizeof(uint16_t) * (size_t)cap * NH * HD));
         // Rows beyond a chunk's M are read (never stored) by the attention kernel: keep them finite.
@@ -506,14 +505,15 @@ struct icua_engine {
         const LayerW& w = L[l];
         PfGemmArgs g{};
         g.xa = pxa;
-        g.xf = pxf;
+        g.xs = pxs;
+        g.ts = pts;
         g.M = M;
         g.Mpad = Mpad;
         g.row0 = row0;
         g.vis_offset = vis_offset;
         g.n_vis = n_vis;
         // 1. RMSNorm + fused QKV.
-        HIPCK(launch_pf_prep(H, 1, px, w.attn_norm, M, Mpad, pxa, pxf, stream));
+        HIPCK(launch_pf_prep(H, 1, px, w.attn_norm, M, Mpad, pxa, pxs, pts, stream));
         g.w = w.wqkv;
         g.sb = w.wqkv_sb;
         g.N = QKV;
@@ -525,21 +525,21 @@ struct icua_engine {
         PfAttnArgs aa{pqh, pql, kv_ptr(l, 0), kv_ptr(l, 1), patt, M, p0, maxctx};
         HIPCK(launch_pf_attn(aa, stream));
         // 3. O projection + residual.
-        HIPCK(launch_pf_prep(H, 0, patt, nullptr, M, Mpad, pxa, pxf, stream));
+        HIPCK(launch_pf_prep(H, 0, patt, nullptr, M, Mpad, pxa, pxs, pts, stream));
         g.w = w.wo;
         g.sb = w.wo_sb;
         g.N = H;
         g.y = px;
         HIPCK(launch_pf_gemm(H, EPI_RESID, g, stream));
         // 4. RMSNorm + gate|up + SwiGLU.
-        HIPCK(launch_pf_prep(H, 1, px, w.mlp_norm, M, Mpad, pxa, pxf, stream));
+        HIPCK(launch_pf_prep(H, 1, px, w.mlp_norm, M, Mpad, pxa, pxs, pts, stream));
         g.w = w.wgu;
         g.sb = w.wgu_sb;
         g.N = GU;
         g.h = ph;
         HIPCK(launch_pf_gemm(H, EPI_SWIGLU, g, stream));
         // 5. Down projection + residual (+ DeepStack after layers 0-2 at visual rows).
-        HIPCK(launch_pf_prep(FF, 0, ph, nullptr, M, Mpad, pxa, pxf, stream));
+        HIPCK(launch_pf_prep(FF, 0, ph, nullptr, M, Mpad, pxa, pxs, pts, stream));
         g.w = w.wd;
         g.sb = w.wd_sb;
         g.N = H;

@@ -92,14 +92,15 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 hipError_t launch_set_pass(State* st, int pos, int n, int logits_rows, hipStream_t s);
 
 // ---- Matrix-core prefill (prefill.hip), q4 weights, passes of M <= Mpad tokens (Mpad % 128 == 0).
-// Activation operands of one GEMM input: 21-bit slices [Mpad / 16][K / 64][3][1 KiB] and
-// per-(token, group) factors [Mpad / 16][K / 64][16] float2.
-hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint8_t* xa,
-                          float* xf, hipStream_t s);
+// Activation operands of one GEMM input: fp16 hi / lo parts of the row-scaled activations
+// [Mpad / 16][K / 32][2][64][8], group sums [Mpad / 16][K / 64][16] and row scales [Mpad].
+hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint16_t* xa,
+                          float* xs, float* ts, hipStream_t s);
 
 struct PfGemmArgs {
-    const uint8_t* xa;      // activation slices (launch_pf_prep)
-    const float* xf;        // activation factors
+    const uint16_t* xa;     // activation operands (launch_pf_prep)
+    const float* xs;        // group sums
+    const float* ts;        // row scales
     const uint8_t* w;       // codes in 16-row MFMA tiles (launch_repack)
     const uint8_t* sb;      // half2 (scale, bias) [N][K / 64], tiled row order
     int N, M, Mpad;

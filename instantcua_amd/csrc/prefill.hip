@@ -5,13 +5,13 @@
 // math per tools/reference/qwen3vl_ref.py:243-292 (fp32 activations, fp16 KV cache).
 //
 // Projections.  y[t][r] = sum_g (s_rg sum_{k in g} q_rk x_tk + b_rg sum_{k in g} x_tk).  A prep
-// kernel writes every activation row as exactly-rounded 21-bit integers per 64-group,
-// X = rint(x 2^(20-e_g)) (e_g = exponent of the group's largest |x|), split into three signed
-// bytes X = 65536 hi + 256 mid + lo, in the A-operand layout of v_mfma_i32_16x16x64_i8.  The
-// GEMM multiplies 16 tokens x 16 weight rows x 64 K per instruction and chains the slices in
-// the int32 accumulator: U = ((C_hi << 8) + C_mid) << 8) + C_lo = sum_k q_k X_k exactly
-// (|U| <= 64 * 15 * 2^21 < 2^31), then y += (s f) float(U) + b (f sum X), f = 2^(e_g-20).  The
-// only roundings are the 21-bit activation quantisation and fp32 group scaling.
+// kernel scales every activation row by a power of two that puts its largest |x| in
+// [2^14, 2^15) and splits it into fp16 hi + lo parts (x'' = hi + lo to ~22 bits; the scaling
+// keeps every part that matters far above the fp16 subnormal range).  The GEMM runs
+// v_mfma_f32_16x16x32_f16 on (hi, lo) x the integer codes, which are exact in fp16, so each
+// 64-group's sum C_g = sum_k q_k x''_k comes out of one accumulator chain; the group
+// epilogue is acc += s C_g + b X_g (X_g = sum_k x''_k), and the row scale 2^(E_t - 14) is
+// applied once at the end.
 //
 // Attention.  Causal GQA flash attention on v_mfma_f32_16x16x32_f16: scores are computed
 // transposed (S^T = K Q^T) so that the probabilities come out of the accumulator already in
@@ -23,23 +23,23 @@
 
 namespace icua {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------------------------------
-// Activation operands.  XA: [Mpad / 16][K / 64][3 slices (hi, mid, lo)][64 lanes][16 B], lane l
-// holding token 16 tb + l % 16, K = 64 g + 16 (l / 16) + 0..15.  XF: [Mpad / 16][K / 64][16]
-// float2 (f = 2^(e - 20), f * sum X).  One workgroup per token row (rows >= M are zero).
+// Activation operands.  XA: [Mpad / 16][K / 32][2 (hi, lo)][64 lanes][8 halves], lane l
+// holding token 16 tb + l % 16, K = 32 ks + 8 (l / 16) + 0..7.  XS: [Mpad / 16][K / 64][16]
+// group sums of hi + lo.  TS: [Mpad] row scales 2^(E_t - 14).  One workgroup per token row
+// (rows >= M are zero).
 
 template <int K, bool NORM>
 __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ src, const float* __restrict__ norm_w,
-                                                      int M, uint8_t* __restrict__ xa, float2* __restrict__ xf) {
+                                                      int M, uint16_t* __restrict__ xa, float* __restrict__ xs,
+                                                      float* __restrict__ ts) {
     constexpr int NU = K / 8 / 256;  // units of 8 activations per thread
-    constexpr int NG = K / 64;
+    constexpr int NG = K / 64, NKS = K / 32;
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-    __shared__ float red[4];
+    __shared__ float red[8];
     float v[NU][8];
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
@@ -73,182 +73,225 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
             for (int i = 0; i < 8; ++i) v[j][i] = v[j][i] * scale * w[i];
         }
     }
+    // Row exponent: largest |x| in [2^E, 2^(E+1)).
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < NU; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
+    amax = wave_max(amax);
+    if (lane == 0) red[4 + wave] = amax;
+    __syncthreads();
+    const float rmax = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+    const int E = (rmax > 0.f) ? ((int)((as_u32(rmax) >> 23) & 0xFF) - 127) : 0;
+    const int sh = 14 - E;
     const int tb = t >> 4, tr = t & 15;
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
         const int k0 = (tid + 256 * j) * 8;
-        // Group max over the 8 adjacent lanes holding the group's 64 values.
-        float amax = 0.f;
+        uint32_t hw[4], lw[4];
+        float gs = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
-        int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
-        bits = max(bits, dpp_i<DPP_XOR1>(bits));
-        bits = max(bits, dpp_i<DPP_XOR2>(bits));
-        bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
-        int e = ((bits >> 23) & 0xFF) - 127;
-        if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
-        const int sh = 20 - e;
-        int X[8], xs = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            X[i] = (int)rintf(ldexpf(v[j][i], sh));
-            xs += X[i];
+        for (int i = 0; i < 4; ++i) {
+            const float x0 = ldexpf(v[j][2 * i], sh), x1 = ldexpf(v[j][2 * i + 1], sh);
+            const f16 h0 = (f16)x0, h1 = (f16)x1;
+            const f16 l0 = (f16)(x0 - (float)h0), l1 = (f16)(x1 - (float)h1);
+            gs += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
+            hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
         }
-        xs += dpp_i<DPP_XOR1>(xs);
-        xs += dpp_i<DPP_XOR2>(xs);
-        xs += dpp_i<DPP_HALF_MIRROR>(xs);
-        // Balanced byte slices: X = 65536 hi + 256 mid + lo, mid and lo in [-128, 127], |hi| <= 32.
-        uint32_t sl[3][2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint32_t p0 = 0, p1 = 0, p2 = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int x = X[4 * h + i];
-                const int lo = (int)(int8_t)(x & 0xFF);
-                const int r1 = (x - lo) >> 8;
-                const int mid = (int)(int8_t)(r1 & 0xFF);
-                const int hi = (r1 - mid) >> 8;
-                p0 |= (uint32_t)(lo & 0xFF) << (8 * i);
-                p1 |= (uint32_t)(mid & 0xFF) << (8 * i);
-                p2 |= (uint32_t)(hi & 0xFF) << (8 * i);
-            }
-            sl[0][h] = p0;
-            sl[1][h] = p1;
-            sl[2][h] = p2;
-        }
-        const int g = k0 / 64, kk = k0 % 64;
-        uint8_t* base = xa + (size_t)(tb * NG + g) * 3 * 1024 + (tr + 16 * (kk / 16)) * 16 + kk % 16;
-        *(uint2*)(base) = make_uint2(sl[2][0], sl[2][1]);
-        *(uint2*)(base + 1024) = make_uint2(sl[1][0], sl[1][1]);
-        *(uint2*)(base + 2048) = make_uint2(sl[0][0], sl[0][1]);
-        if (kk == 0) {
-            const float f = ldexpf(1.0f, -sh);
-            xf[(size_t)(tb * NG + g) * 16 + tr] = make_float2(f, (float)xs * f);
-        }
+        // Group sums over the 8 adjacent lanes holding the group's 64 values.
+        gs += dpp<DPP_XOR1>(gs);
+        gs += dpp<DPP_XOR2>(gs);
+        gs += dpp<DPP_HALF_MIRROR>(gs);
+        const int ks = k0 / 32, qq = (k0 % 32) / 8;
+        uint16_t* base = xa + ((size_t)(tb * NKS + ks) * 2) * 512 + (tr + 16 * qq) * 8;
+        *(uint4*)base = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *(uint4*)(base + 512) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        if (k0 % 64 == 0) xs[(size_t)(tb * NG + k0 / 64) * 16 + tr] = gs;
     }
+    if (tid == 0) ts[t] = ldexpf(1.0f, -sh);
 }
 
 // ------------------------------------------------------------------------------------------
-// q4 GEMM: a workgroup of 8 waves computes 128 tokens x 128 weight rows.  Wave w owns token
-// block 8 tm + w (16 tokens) against all 8 row blocks; the row blocks' 1 KiB code chunks and
-// scales of each 128-K step are staged once in LDS (double-buffered) and shared by the waves,
-// the wave's activation slices stream from global memory straight into registers.  Tiles are
+// q4 GEMM: a workgroup of 8 waves computes 128 tokens x 128 weight rows; wave w owns token
+// blocks 8 tm + 2 (w % 4), + 1 (32 tokens) against row blocks 4 (w / 4) .. + 3 (64 rows), two
+// waves per SIMD.  Each 128-K step, the code chunks of the 8 row blocks are unpacked once into
+// fp16 B operands in LDS (double-buffered) and shared by the waves; the waves' activation
+// operands stream from global memory straight into registers one 64-group ahead.  Tiles are
 // numbered token-tile-major and dealt to the 8 XCDs in contiguous ranges, so the workgroups of
 // one XCD share token tiles in its L2.
 
 template <int K, int EPI>
 __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
-    constexpr int NG = K / 64, NC = K / 128;
+    constexpr int NG = K / 64, NKS = K / 32, NC = K / 128;
     const int TN = a.N / 128, TM = a.Mpad / 128, T = TM * TN;
     const int per = (T + 7) / 8;
     const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (tile >= T) return;
     const int tm = tile / TN, tn = tile % TN;
 
-    __shared__ uint4 Bs[2][8][64];
-    __shared__ uint32_t SBs[2][2][128];  // [buffer][group of the step][row]
+    __shared__ uint4 Bs[2][8][4][64];   // fp16 codes: [buffer][row block][k-step][lane]
+    __shared__ float2 SBs[2][2][128];   // (scale, bias): [buffer][group of the step][row]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;
-    const int tb = tm * 8 + wave;
-    const uint8_t* xa = a.xa + (size_t)tb * NG * 3 * 1024 + lane * 16;
-    const float* xf = a.xf + ((size_t)tb * NG * 16 + 4 * q) * 2;
-    const uint8_t* wsrc = a.w + (size_t)(tn * 8 + wave) * NC * 1024 + lane * 16;
-    const uint32_t* sbsrc = (const uint32_t*)a.sb + (size_t)(tn * 128 + (tid & 127)) * NG + (tid >> 7);
+    const int tb0 = tm * 8 + 2 * (wave & 3), rb0 = 4 * (wave >> 2);
+    const uint16_t* xa = a.xa + (size_t)tb0 * NKS * 1024 + lane * 8;   // token block tb0 (+ NKS * 1024 for tb0 + 1)
+    const float* xsp = a.xs + ((size_t)tb0 * NG) * 16 + 4 * q;
+    // Staging: thread t unpacks nibble lane t % 64 of row block t / 64.
+    const int srb = tid >> 6;
+    const uint8_t* wsrc = a.w + (size_t)(tn * 8 + srb) * NC * 1024 + lane * 16;
+    const uint32_t* sbsrc = (const uint32_t*)a.sb + (size_t)(tn * 128 + (tid & 127)) * NG + ((tid >> 7) & 1);
 
-    float acc[8][4];
+    f32x4 acc[2][4];
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[rb][i] = 0.f;
+        for (int r = 0; r < 4; ++r) acc[i][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    uint4 Ac[2][3], An[2][3];
-    float4 Fc[2][2], Fn[2][2];
-    uint4 Bn;
+    // Activation operands of one 64-group (two k-steps), prefetched one group ahead.
+    uint4 Ac[2][2][2], An[2][2][2];  // [token block][k-step of the group][hi, lo]
+    float4 Xc[2], Xn[2];             // [token block]: group sums of tokens 4 q .. 4 q + 3
+    uint4 Wn;
     uint32_t SBn = 0;
-    auto gload = [&](int c, uint4(&A)[2][3], float4(&F)[2][2]) {
+    auto aload = [&](int g, uint4(&A)[2][2][2], float4(&X)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl)
+                    A[i][kk][hl] = *(const uint4*)(xa + (size_t)i * NKS * 1024 + ((size_t)(2 * g + kk) * 2 + hl) * 512);
+            X[i] = *(const float4*)(xsp + ((size_t)i * NG + g) * 16);
+        }
+    };
+    auto wload = [&](int c) {
+        Wn = *(const uint4*)(wsrc + (size_t)c * 1024);
+        if (tid < 256) SBn = sbsrc[2 * c];
+    };
+    // Nibble lane L (row L % 16, 16-K slot L / 16 of each group) -> fp16 lanes (L % 16) + 16 (2 (slot % 2) + h)
+    // of k-step 2 gg + slot / 2, h = 0 for K 0..7 of the slot, 1 for K 8..15.
+    auto lstore = [&](int b) {
+        const int r = lane & 15, slot = lane >> 4;
+        const uint32_t dd[4] = {Wn.x, Wn.y, Wn.z, Wn.w};
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
 #pragma unroll
-            for (int s = 0; s < 3; ++s) A[gg][s] = *(const uint4*)(xa + ((size_t)(2 * c + gg) * 3 + s) * 1024);
-            F[gg][0] = *(const float4*)(xf + (size_t)(2 * c + gg) * 32);
-            F[gg][1] = *(const float4*)(xf + (size_t)(2 * c + gg) * 32 + 4);
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t d = dd[2 * gg + h];
+                uint32_t o[4];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    // K 8 h + 2 j, + 1 are the low nibbles of bytes 2 j, 2 j + 1; K 8 h + 4 + 2 j, + 1 the
+                    // high ones.  Bytes spread to 16-bit lanes, a nibble or'ed into 0x6400 is the fp16
+                    // value 1024 + q, and one packed fp16 subtraction leaves q exactly.
+                    const uint32_t sp = __builtin_amdgcn_perm(d, d, 0x0C000C00u | ((2u * j + 1u) << 16) | (2u * j));
+                    const f16x2 k1024 = {(f16)1024.f, (f16)1024.f};
+                    o[j] = h2_bits(as_h2((sp & 0x000F000Fu) | 0x64006400u) - k1024);
+                    o[2 + j] = h2_bits(as_h2(((sp >> 4) & 0x000F000Fu) | 0x64006400u) - k1024);
+                }
+                Bs[b][srb][2 * gg + (slot >> 1)][r + 16 * (2 * (slot & 1) + h)] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
         }
-        Bn = *(const uint4*)(wsrc + (size_t)c * 1024);
-        if (tid < 256) SBn = sbsrc[2 * c];
+        if (tid < 256) {
+            const f16x2 sb2 = as_h2(SBn);
+            SBs[b][tid >> 7][tid & 127] = make_float2((float)sb2.x, (float)sb2.y);
+        }
     };
-    auto lstore = [&](int b) {
-        Bs[b][wave][lane] = Bn;
-        if (tid < 256) SBs[b][tid >> 7][tid & 127] = SBn;
+    // One 64-group: the wave's 8 B fragments first, then 4 x 2 accumulator chains of 4 MFMAs.
+    auto group = [&](int b, int gg) {
+        v8h Bf[4][2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) Bf[r][kk] = __builtin_bit_cast(v8h, Bs[b][rb0 + r][2 * gg + kk][lane]);
+        float2 sb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sb[r] = SBs[b][gg][(rb0 + r) * 16 + r16];
+        f32x4 C[4][2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        C[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, Ac[i][kk][hl]), Bf[r][kk],
+                                                                         C[r][i], 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float xg[4] = {Xc[i].x, Xc[i].y, Xc[i].z, Xc[i].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], fmaf(sb[r].y, xg[e], acc[i][r][e]));
+            }
+    };
+    auto advance = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                Ac[i][kk][0] = An[i][kk][0];
+                Ac[i][kk][1] = An[i][kk][1];
+            }
+            Xc[i] = Xn[i];
+        }
     };
 
-    gload(0, Ac, Fc);
+    aload(0, Ac, Xc);
+    wload(0);
     lstore(0);
     __syncthreads();
     for (int c = 0; c < NC; ++c) {
         const int b = c & 1;
-        if (c + 1 < NC) gload(c + 1, An, Fn);
-#pragma unroll
-        for (int rb = 0; rb < 8; ++rb) {
-            const uint4 bw = Bs[b][rb][lane];
-#pragma unroll
-            for (int gg = 0; gg < 2; ++gg) {
-                const uint32_t d0 = gg ? bw.z : bw.x, d1 = gg ? bw.w : bw.y;
-                v4i B;
-                B[0] = (int)(d0 & 0x0F0F0F0Fu);
-                B[1] = (int)((d0 >> 4) & 0x0F0F0F0Fu);
-                B[2] = (int)(d1 & 0x0F0F0F0Fu);
-                B[3] = (int)((d1 >> 4) & 0x0F0F0F0Fu);
-                const v4i zero = {0, 0, 0, 0};
-                v4i U = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, Ac[gg][0]), B, zero, 0, 0, 0);
-                U = __builtin_bit_cast(v4i, __builtin_bit_cast(v4u, U) << 8u);
-                U = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, Ac[gg][1]), B, U, 0, 0, 0);
-                U = __builtin_bit_cast(v4i, __builtin_bit_cast(v4u, U) << 8u);
-                U = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, Ac[gg][2]), B, U, 0, 0, 0);
-                const f16x2 sbv = as_h2(SBs[b][gg][rb * 16 + r16]);
-                const float s = (float)sbv.x, bias = (float)sbv.y;
-                const float f[4] = {Fc[gg][0].x, Fc[gg][0].z, Fc[gg][1].x, Fc[gg][1].z};
-                const float xs[4] = {Fc[gg][0].y, Fc[gg][0].w, Fc[gg][1].y, Fc[gg][1].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(s * f[i], (float)U[i], fmaf(bias, xs[i], acc[rb][i]));
-            }
-        }
-        if (c + 1 < NC) {
-            lstore(b ^ 1);
-#pragma unroll
-            for (int gg = 0; gg < 2; ++gg) {
-#pragma unroll
-                for (int s = 0; s < 3; ++s) Ac[gg][s] = An[gg][s];
-                Fc[gg][0] = Fn[gg][0];
-                Fc[gg][1] = Fn[gg][1];
-            }
-        }
+        // The next step's codes (the last step reloads step 0 into the idle buffer: no branch).
+        wload(c + 1 < NC ? c + 1 : 0);
+        aload(2 * c + 1, An, Xn);
+        group(b, 0);
+        advance();
+        aload(2 * c + 2 < NG ? 2 * c + 2 : 0, An, Xn);
+        group(b, 1);
+        lstore(b ^ 1);
+        advance();
         __syncthreads();
     }
 
-    // Epilogue: lane holds tokens 16 tb + 4 q + i of weight row 128 tn + 16 rb + r16.
+    // Epilogue: lane holds tokens 16 tb + 4 q + e of weight row 128 tn + 16 rb + r16.
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb) {
-        const int row = tn * 128 + rb * 16 + r16;
+    for (int i = 0; i < 2; ++i) {
+        const int tq = (tb0 + i) * 16 + 4 * q;
+        const float4 tsv = *(const float4*)(a.ts + tq);
+        const float tsc[4] = {tsv.x, tsv.y, tsv.z, tsv.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = tb * 16 + 4 * q + i;
-            const float y = acc[rb][i];
-            if constexpr (EPI == EPI_STORE) {
-                if (t < a.M) a.y[(size_t)t * a.N + row] = y;
-            } else if constexpr (EPI == EPI_RESID) {
-                if (t < a.M) {
-                    float* xo = a.y + (size_t)t * a.N + row;
-                    float v = *xo + y;
-                    if (a.ds) {  // DeepStack residual of a visual row (Shaders.swift:696-707)
-                        const int vrow = a.row0 + t - a.vis_offset;
-                        if (a.vis_offset >= 0 && vrow >= 0 && vrow < a.n_vis) v = v + a.ds[(size_t)vrow * H + row];
+        for (int r = 0; r < 4; ++r) {
+            const int rb = rb0 + r;
+            const int row = tn * 128 + rb * 16 + r16;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = tq + e;
+                const float y = acc[i][r][e] * tsc[e];
+                if constexpr (EPI == EPI_STORE) {
+                    if (t < a.M) a.y[(size_t)t * a.N + row] = y;
+                } else if constexpr (EPI == EPI_RESID) {
+                    if (t < a.M) {
+                        float* xo = a.y + (size_t)t * a.N + row;
+                        float v = *xo + y;
+                        if (a.ds) {  // DeepStack residual of a visual row (Shaders.swift:696-707)
+                            const int vrow = a.row0 + t - a.vis_offset;
+                            if (a.vis_offset >= 0 && vrow >= 0 && vrow < a.n_vis) v = v + a.ds[(size_t)vrow * H + row];
+                        }
+                        *xo = v;
                     }
-                    *xo = v;
+                } else {  // EPI_SWIGLU: block 8 tn + rb = gate units 8 (8 tn + rb) + 0..7, then their up rows
+                    const float up = __shfl_xor(y, 8);
+                    if (t < a.M && r16 < 8) a.h[(size_t)t * FF + (tn * 8 + rb) * 8 + r16] = (y / (1.f + expf(-y))) * up;
                 }
-            } else {  // EPI_SWIGLU: block 8 tn + rb = gate units 8 (8 tn + rb) + 0..7, then their up rows
-                const float up = __shfl_xor(y, 8);
-                if (t < a.M && r16 < 8) a.h[(size_t)t * FF + (tn * 8 + rb) * 8 + r16] = (y / (1.f + expf(-y))) * up;
             }
         }
     }
@@ -457,16 +500,15 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
 
 // ------------------------------------------------------------------------------------------
 
-hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint8_t* xa,
-                          float* xf, hipStream_t s) {
+hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint16_t* xa,
+                          float* xs, float* ts, hipStream_t s) {
     if (M < 1 || Mpad < M || Mpad % 128) return hipErrorInvalidValue;
-    float2* f2 = (float2*)xf;
     if (K == H && norm)
-        hipLaunchKernelGGL((pf_prep_kernel<H, true>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, f2);
+        hipLaunchKernelGGL((pf_prep_kernel<H, true>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
     else if (K == H)
-        hipLaunchKernelGGL((pf_prep_kernel<H, false>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, f2);
+        hipLaunchKernelGGL((pf_prep_kernel<H, false>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
     else if (K == FF && !norm)
-        hipLaunchKernelGGL((pf_prep_kernel<FF, false>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, f2);
+        hipLaunchKernelGGL((pf_prep_kernel<FF, false>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
