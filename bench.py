@@ -60,10 +60,9 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def gemv_roofline(iters=200):
-    """Isolated q4 dequant-GEMV at the gate+up shape (the largest per-layer matrix), rotating
-    distinct weight copies (> 256 MB) so the Infinity Cache cannot serve repeats."""
-    K, N = Dims.hidden, Dims.gu_rows
+def gemv_roofline(iters=200, K=Dims.hidden, N=Dims.gu_rows):
+    """Isolated q4 dequant-GEMV (default: the gate+up shape, the largest per-layer matrix),
+    rotating distinct weight copies (> 256 MB) so the Infinity Cache cannot serve repeats."""
     m = synth.make_matrix(WeightFormat.Q4, N, K, tag="bench-gemv")
     per = m.codes.nbytes + m.sb.nbytes
     copies = max(2, int(np.ceil(300e6 / per)))
@@ -105,6 +104,79 @@ def cpu_baseline(img, ctx, seconds=10.0):
             "sample": f"{n} decode steps of the 28-layer q4 decoder at {ctx}-token context (oracle, fp64 accumulation)"}
 
 
+# Speculative verify workload: 8 random drafts over 8192 cache rows of a 28-layer q8 decoder.
+VERIFY_CTX, VERIFY_M = 8192, 8
+# Isolated q4 GEMV sweep (K, N): fused QKV, O, gate+up, down, lm_head.
+GEMV_SHAPES = [(2048, 4096), (2048, 2048), (2048, 12288), (6144, 2048), (2048, 151936)]
+# Algorithmic FLOPs of the 4096-row prefill: the decoder layers' projections for every row
+# (the last row's lm_head is a GEMV) plus causal attention (q.k and p.v over i + 1 slots).
+PREFILL_FLOPS = (2 * PREFILL * LAYERS * (Dims.qkv_rows * Dims.hidden + Dims.hidden * Dims.hidden
+                                         + Dims.gu_rows * Dims.hidden + Dims.hidden * Dims.ff)
+                 + LAYERS * 16 * (PREFILL * (PREFILL + 1) // 2) * Dims.head_dim * 2 * 2)
+MFMA_F16_PEAK = 2.5e15  # dense fp16 matrix-core FLOP/s, MI355X
+
+
+def verify_bytes_per_pass() -> int:
+    return weight_bytes_per_token(WeightFormat.Q8) + kv_bytes_per_token(VERIFY_CTX)
+
+
+def run_verify(K, W):
+    """K timed verify passes (each: 8 draft rows at slots 8192..8199, per-row argmax) of the
+    28-layer q8 decoder over 8192 cache rows of fp16 N(0, 1)."""
+    img = synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="bench-q8")
+    e = eng.Engine(image=img, max_context=VERIFY_CTX + VERIFY_M + 8, max_steps=8)
+    for l in range(LAYERS):
+        for kind in (0, 1):
+            e.write_kv(l, kind, 0, synth.fp16_normal((Dims.kv_heads, VERIFY_CTX, Dims.head_dim), f"bench-verify-kv{kind}", l))
+    drafts = [synth.random_tokens(VERIFY_M, "bench-verify-draft", i) for i in range(W + K)]
+    e.set_position(VERIFY_CTX, int(drafts[0][0]), 0, 4)
+    for i in range(W):
+        e.verify(drafts[i])
+    eng.lib().icua_device_sync()
+    t0 = time.perf_counter()
+    for i in range(K):
+        e.verify(drafts[W + i])
+    eng.lib().icua_device_sync()
+    dt = (time.perf_counter() - t0) / K
+    e.close()
+    nbytes = verify_bytes_per_pass()
+    achieved = nbytes / dt
+    log(f"verify: {dt * 1e3:.3f} ms per pass of {VERIFY_M} drafts, {achieved / 1e9:.0f} GB/s")
+    return {
+        "metric": "speculative verify passes/s (q8 28-layer decoder, 8 drafts, 8192 ctx)",
+        "value": round(1.0 / dt, 2), "unit": "passes/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q8 weights, int codes x fp activations, fp32 accumulate, fp16 KV",
+        "data": "synthetic (seeded random-init q8 weights, fp16 N(0,1) cache rows, random draft ids)",
+        "config": {"workload": "28-layer q8 g32 decoder, one pass of 8 draft tokens over 8192 cache rows",
+                   "context": VERIFY_CTX, "drafts": VERIFY_M},
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "kernel": "whole verify pass (host wall clock per synchronous call)", "bytes_per_pass": nbytes},
+    }
+
+
+def run_gemv(iters):
+    rows = []
+    for K, N in GEMV_SHAPES:
+        g = gemv_roofline(iters, K, N)
+        rate = g["bytes"] / (g["us"] * 1e-6)
+        rows.append({"K": K, "N": N, "us": round(g["us"], 3), "bytes": g["bytes"], "GB_s": round(rate / 1e9, 1),
+                     "frac": round(rate / HBM_PEAK, 4)})
+        log(f"q4 GEMV {K}x{N}: {g['us']:.2f} us, {rate / 1e9:.0f} GB/s")
+    big = rows[-1]
+    return {
+        "metric": "isolated q4 dequant-GEMV GB/s (M=1)", "value": big["GB_s"], "unit": "GB/s", "n_gpus": 1,
+        "steps": iters, "warmup": 0, "ms_per_step": round(big["us"] / 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4 weights, int codes x fp32 activations",
+        "data": "synthetic (seeded q4 g64 codes and scales, fp16 N(0,1) activations)",
+        "config": {"workload": "q4 GEMV sweep over the decoder shapes, > 300 MB of rotated weight copies per shape"},
+        "roofline": {"bound": "hbm", "achieved": big["GB_s"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": big["frac"], "traffic": None, "kernel": "gemv_kernel q4 lm_head shape"},
+        "shapes": rows,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,11 +186,20 @@ def main():
     ap.add_argument("--no-prefill", action="store_true",
                     help="profiling runs: start decoding at the same 4096-slot context without the prefill "
                          "(cache rows stay zero; same bytes per step), so a profile holds only the decode launch")
+    ap.add_argument("--workload", choices=["decode", "verify", "gemv"], default="decode",
+                    help="decode: the 4k-context q4 decode (default); verify: 8-draft q8 verify over 8192 rows; "
+                         "gemv: isolated q4 GEMV sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU decode is a design note only",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.workload == "verify":
+        print(json.dumps(run_verify(args.steps, args.warmup)))
+        return
+    if args.workload == "gemv":
+        print(json.dumps(run_gemv(200)))
+        return
 
     K, W = args.steps, args.warmup
     t0 = time.time()
@@ -189,6 +270,8 @@ def main():
         "decode_bytes_per_token": int(bytes_tok),
         "prefill_tok_s": None if args.no_prefill else round(PREFILL / (prefill_ms / 1e3), 1),
         "prefill_ms": None if args.no_prefill else round(prefill_ms, 2),
+        # Prefill is matrix-core bound: algorithmic FLOPs / time against the dense fp16 peak.
+        "prefill_mfma_frac": None if args.no_prefill else round(PREFILL_FLOPS / (prefill_ms * 1e-3) / MFMA_F16_PEAK, 4),
         # Dominant kernel: the persistent decode kernel (one launch runs the K timed steps).
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),

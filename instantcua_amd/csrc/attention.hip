@@ -211,9 +211,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a) {
 
 }
 
-// Merge of the split partials (flash-decoding): one workgroup per KV group.
-// Runs as its own kernel: the kernel boundary publishes the partials of every split, which is
-// far cheaper on a multi-XCD device than a device-scope fence in each split workgroup.
+// Merge of the split partials (flash-decoding): one workgroup per (KV group, token x head row),
+// grid (NKV, 2 MT).  Runs as its own kernel: the kernel boundary publishes the partials of every
+// split, which is far cheaper on a multi-XCD device than a device-scope fence in each split
+// workgroup.  Thread t weights split t (t < S); the 128 output elements are summed by two
+// halves of the workgroup over interleaved splits, combined in a fixed order.
 template <int MT>
 __global__ __launch_bounds__(ATT_THREADS) void attention_merge_kernel(AttnArgs a, int splits) {
     const State* st = a.st;
@@ -222,44 +224,54 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_merge_kernel(AttnArgs a
     const int pos = st->pos;
     const int S = (pos + ATT_CH - 1) / ATT_CH + 1;
     if (pos < 0 || pos + M > st->maxctx || S > splits) return;
-    const int g = blockIdx.x;
+    const int g = blockIdx.x, row = blockIdx.y;
+    if (row >= 2 * M) return;
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
-    __shared__ float wts[2 * MT][16384 / ATT_CH + 1];
-    __shared__ float Lsum[2 * MT];
+    constexpr int NS = 16384 / ATT_CH + 1;
+    __shared__ float wts[NS];
+    __shared__ float red[2][ATT_THREADS / WAVE];
+    __shared__ float half[HD];
     const size_t split_stride = (size_t)MAXM * 2 * PART_STRIDE;
-    const float* gpart = a.part + (size_t)g * splits * split_stride;
-    for (int row = wave; row < 2 * M; row += ATT_THREADS / WAVE) {
-        float mx = -__builtin_inff();
-        for (int ss = lane; ss < S; ss += WAVE) mx = fmaxf(mx, gpart[ss * split_stride + row * PART_STRIDE + HD]);
-        mx = wave_max(mx);
-        float L = 0.f;
-        for (int ss = lane; ss < S; ss += WAVE) {
-            const float* pp = gpart + ss * split_stride + row * PART_STRIDE;
-            const float m = pp[HD];
-            const float w = (m == -__builtin_inff()) ? 0.f : expf(m - mx);
-            wts[row][ss] = w;
-            L += w * pp[HD + 1];
-        }
-        L = wave_sum(L);
-        if (lane == 0) Lsum[row] = L;
-    }
+    const float* rp = a.part + (size_t)g * splits * split_stride + row * PART_STRIDE;
+    // Split maxima and weights: thread t handles splits t, t + 256 (S <= 257).
+    float mloc = -__builtin_inff();
+    for (int ss = tid; ss < S; ss += ATT_THREADS) mloc = fmaxf(mloc, rp[ss * split_stride + HD]);
+    mloc = wave_max(mloc);
+    if (lane == 0) red[0][wave] = mloc;
     __syncthreads();
-    for (int idx = tid; idx < 2 * M * HD; idx += ATT_THREADS) {
-        const int row = idx / HD, d = idx % HD;
-        const float* pp = gpart + row * PART_STRIDE + d;
-        const float* w = wts[row];
-        float O = 0.f;
-        int ss = 0;
-        for (; ss + 8 <= S; ss += 8) {
-            float v[8];
+    float mx = red[0][0];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = pp[(ss + u) * split_stride];
+    for (int w = 1; w < ATT_THREADS / WAVE; ++w) mx = fmaxf(mx, red[0][w]);
+    float L = 0.f;
+    for (int ss = tid; ss < S; ss += ATT_THREADS) {
+        const float m = rp[ss * split_stride + HD];
+        const float wgt = (m == -__builtin_inff()) ? 0.f : expf(m - mx);
+        wts[ss] = wgt;
+        L += wgt * rp[ss * split_stride + HD + 1];
+    }
+    L = wave_sum(L);
+    if (lane == 0) red[1][wave] = L;
+    __syncthreads();
+    float Lsum = 0.f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) O = fmaf(w[ss + u], v[u], O);
-        }
-        for (; ss < S; ++ss) O = fmaf(w[ss], pp[ss * split_stride], O);
+    for (int w = 0; w < ATT_THREADS / WAVE; ++w) Lsum += red[1][w];
+    // Weighted sum: threads (h, d), h = tid / 128 takes splits h, h + 2, ...
+    const int h = tid / HD, d = tid % HD;
+    float O = 0.f;
+    int ss = h;
+    for (; ss + 6 < S; ss += 8) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = rp[(ss + 2 * u) * split_stride + d];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) O = fmaf(wts[ss + 2 * u], v[u], O);
+    }
+    for (; ss < S; ss += 2) O = fmaf(wts[ss], rp[ss * split_stride + d], O);
+    if (h == 1) half[d] = O;
+    __syncthreads();
+    if (h == 0) {
         const int t = row / 2, hh = row % 2;
-        a.out[(size_t)t * H + (2 * g + hh) * HD + d] = O / Lsum[row];
+        a.out[(size_t)t * H + (2 * g + hh) * HD + d] = (O + half[d]) / Lsum;
     }
 }
 
@@ -270,10 +282,10 @@ hipError_t launch_attention(const AttnArgs& a, int mt, int splits, hipStream_t s
     const dim3 grid(splits, NKV);
     if (mt == 1) {
         hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(ATT_THREADS), 0, s, a);
-        hipLaunchKernelGGL(attention_merge_kernel<1>, dim3(NKV), dim3(ATT_THREADS), 0, s, a, splits);
+        hipLaunchKernelGGL(attention_merge_kernel<1>, dim3(NKV, 2), dim3(ATT_THREADS), 0, s, a, splits);
     } else {
         hipLaunchKernelGGL(attention_kernel<MAXM>, grid, dim3(ATT_THREADS), 0, s, a);
-        hipLaunchKernelGGL(attention_merge_kernel<MAXM>, dim3(NKV), dim3(ATT_THREADS), 0, s, a, splits);
+        hipLaunchKernelGGL(attention_merge_kernel<MAXM>, dim3(NKV, 2 * MAXM), dim3(ATT_THREADS), 0, s, a, splits);
     }
     return hipGetLastError();
 }
