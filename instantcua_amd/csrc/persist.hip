@@ -65,6 +65,7 @@ constexpr int MERGE_PARTS = 4;            // workgroups merging one group's part
 constexpr int MERGER0 = NWG - NKV * MERGE_PARTS;  // workgroups 224..255: splits 28..31 of each group
 static_assert(MERGER0 >= H / 16, "mergers must not have O / down work");
 static_assert(MERGER0 % NKV == 0, "mergers of group g are splits 28..31 of group g");
+static_assert((FF / 128) % MW == 0 && FF / 64 / MW == 24, "down block: 12 chunks and 24 scale groups per math wave");
 
 // Packet area (64-bit packets), zeroed before every launch.
 constexpr int XP = 0;                 // residual x [H]
@@ -98,6 +99,12 @@ __device__ __forceinline__ uint64_t pack(float v, unsigned tag) { return (uint64
 __device__ __forceinline__ uint64_t pack_i(int v, unsigned tag) { return (uint64_t)(uint32_t)v | ((uint64_t)tag << 32); }
 __device__ __forceinline__ unsigned tag_of(uint64_t p) { return (unsigned)(p >> 32); }
 __device__ __forceinline__ float val_of(uint64_t p) { return as_f32((uint32_t)p); }
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l
+// (lds is wave-uniform).  Counted by the issuing wave's vector-memory counter.
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
 
 __device__ __forceinline__ unsigned load_err(const unsigned* e) {
     return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -176,9 +183,17 @@ __device__ __forceinline__ bool poll_map(const uint64_t* src, int n, Map map, un
     return true;
 }
 
+// Compact activation operands: per group the hi, mid, lo slices of its 4 K-slots (q4: 16 bytes
+// each, 192 B per 64-group; q8: 8 bytes each, 96 B per 32-group), K <= 6144.
+constexpr int A_BYTES = 18432;
+// q4 down block of a workgroup in LDS: 48 chunks of 1 KiB, then the 16 rows' (scale, bias) in
+// four per-wave parts of 16 x 96 B.
+constexpr int WD_CODES = (FF / 128) * 1024, WD_SB = 16 * (FF / 64) * 4;
+
 struct Shared {
-    uint8_t A[96 * 1024];     // activation operands (1 KiB per q4 group / 512 B per q8 group, K <= 6144);
-                              // the merger's fp32 partials during the merge
+    uint8_t A[A_BYTES];       // activation operands; the merger's fp32 partials during the merge
+    uint8_t wdb[WD_CODES + WD_SB];  // q4 down block (streamed in during the stages before down); lm_head partial sums
+    uint32_t zero[4];         // operand rows 3..15 of every tile (16 zero bytes)
     float fx[192 * 2];        // per-group (2^(e-21), sum X * 2^(e-21))
     float red[3 * MW * 64];   // math-wave partial sums (up to 3 blocks)
     float vec[FF];            // input vector of the current stage (fp32)
@@ -195,14 +210,14 @@ struct Shared {
 
 // ------------------------------------------------------------------------------------------
 // Staging by the exchange threads: units of 8 consecutive activations (u = ct + CT * i, K / 8
-// units) -> optional RMSNorm with S.nw -> 22-bit slices -> A operands.  Rows 0, 1, 2 of each
-// group tile hold the hi, mid, lo slices; rows 3..15 stay zero (zeroed at kernel start).  Called
-// by the whole workgroup (math threads only pass the barriers).
+// units) -> optional RMSNorm with S.nw -> 22-bit slices -> compact A operands (rows 0, 1, 2 of a
+// group's tile: the hi, mid, lo slices; rows 3..15 read S.zero).  Called by the whole workgroup
+// (math threads only pass the barriers).
 
 template <int FMT, int NU, bool MATH>
 __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed) {
     constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
-    constexpr int TILE = (FMT == FMT_Q4) ? 1024 : 512;
+    constexpr int TILE = (FMT == FMT_Q4) ? 192 : 96;
     constexpr int K = NU * CT * 8;
     const int tid = my_tid();
     constexpr bool ex = !MATH;
@@ -286,14 +301,14 @@ __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed
             uint8_t* A = S.A + gl * TILE;
             if constexpr (FMT == FMT_Q4) {
                 const int q = kk / 16, j0 = kk % 16;
-                *(uint2*)(A + (0 + 16 * q) * 16 + j0) = make_uint2(sl[2][0], sl[2][1]);
-                *(uint2*)(A + (1 + 16 * q) * 16 + j0) = make_uint2(sl[1][0], sl[1][1]);
-                *(uint2*)(A + (2 + 16 * q) * 16 + j0) = make_uint2(sl[0][0], sl[0][1]);
+                *(uint2*)(A + (3 * q + 0) * 16 + j0) = make_uint2(sl[2][0], sl[2][1]);
+                *(uint2*)(A + (3 * q + 1) * 16 + j0) = make_uint2(sl[1][0], sl[1][1]);
+                *(uint2*)(A + (3 * q + 2) * 16 + j0) = make_uint2(sl[0][0], sl[0][1]);
             } else {
                 const int q = kk / 8;
-                *(uint2*)(A + (0 + 16 * q) * 8) = make_uint2(sl[2][0], sl[2][1]);
-                *(uint2*)(A + (1 + 16 * q) * 8) = make_uint2(sl[1][0], sl[1][1]);
-                *(uint2*)(A + (2 + 16 * q) * 8) = make_uint2(sl[0][0], sl[0][1]);
+                *(uint2*)(A + (3 * q + 0) * 8) = make_uint2(sl[2][0], sl[2][1]);
+                *(uint2*)(A + (3 * q + 1) * 8) = make_uint2(sl[1][0], sl[1][1]);
+                *(uint2*)(A + (3 * q + 2) * 8) = make_uint2(sl[0][0], sl[0][1]);
             }
             if (kk == 0) {
                 const float f = ldexpf(1.0f, -sh);
@@ -305,42 +320,102 @@ __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed
     __syncthreads();
 }
 
-// One 1 KiB chunk of a 16-row block against the staged operands; returns the lane's partial
-// (lanes 0-15 hold rows 0-15 of the block).
+// One 1 KiB chunk of a 16-row block against the staged operands, in phases so that a batch of
+// chunks issues all of its LDS reads before the first multiply: ops_load reads the chunk's two
+// operand tiles (row lane % 16 of K-slot lane / 16: rows 0-2 are the slices, rows 3-15 read the
+// zero block) and group factors; ops_mfma forms the integer sums, ops_scale the lane's partial.
 template <int FMT>
-__device__ __forceinline__ float chunk_mac(const Shared& S, uint4 wv, uint2 sbv, int c, int lane) {
-    float acc = 0.f;
-    if constexpr (FMT == FMT_Q4) {
+struct ChunkOps {
+    v4i A[2];     // q4: operand tiles of groups 2c, 2c + 1 (q8 uses the low 8 bytes)
+    float f[4];   // (2^(e-21), sum X 2^(e-21)) of both groups
+};
+
+template <int FMT>
+__device__ __forceinline__ ChunkOps<FMT> ops_load(const Shared& S, int c, int lane) {
+    ChunkOps<FMT> o;
+    const int r = lane & 15, q = lane >> 4;
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
+    for (int hh = 0; hh < 2; ++hh) {
+        const int gl = 2 * c + hh;
+        if constexpr (FMT == FMT_Q4) {
+            const uint8_t* ap = r < 3 ? S.A + gl * 192 + (3 * q + r) * 16 : (const uint8_t*)S.zero;
+            o.A[hh] = *(const v4i*)ap;
+        } else {
+            const uint8_t* ap = r < 3 ? S.A + gl * 96 + (3 * q + r) * 8 : (const uint8_t*)S.zero;
+            const long v = *(const long*)ap;
+            o.A[hh] = v4i{(int)(uint32_t)v, (int)(uint32_t)((uint64_t)v >> 32), 0, 0};
+        }
+        const float2 fx = *(const float2*)(S.fx + gl * 2);
+        o.f[2 * hh] = fx.x;
+        o.f[2 * hh + 1] = fx.y;
+    }
+    return o;
+}
+
+// Integer partial sums of both groups of a chunk (q4: v_mfma_i32_16x16x64_i8, q8: 16x16x32).
+template <int FMT>
+__device__ __forceinline__ void ops_mfma(const ChunkOps<FMT>& o, uint4 wv, v4i (&C)[2]) {
+    const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        if constexpr (FMT == FMT_Q4) {
             const uint32_t d0 = hh ? wv.z : wv.x, d1 = hh ? wv.w : wv.y;
             v4i B;
             B[0] = (int)(d0 & 0x0F0F0F0Fu);
             B[1] = (int)((d0 >> 4) & 0x0F0F0F0Fu);
             B[2] = (int)(d1 & 0x0F0F0F0Fu);
             B[3] = (int)((d1 >> 4) & 0x0F0F0F0Fu);
-            const int gl = 2 * c + hh;
-            const v4i A = *(const v4i*)(S.A + gl * 1024 + lane * 16);
-            const v4i zero = {0, 0, 0, 0};
-            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero, 0, 0, 0);
-            const float Sv = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
-            const f16x2 sb2 = as_h2(hh ? sbv.y : sbv.x);
-            acc = fmaf((float)sb2.x * S.fx[gl * 2], Sv, fmaf((float)sb2.y, S.fx[gl * 2 + 1], acc));
-        }
-    } else {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
+            C[hh] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[hh], B, zero, 0, 0, 0);
+        } else {
             const long B = (long)(hh ? ((uint64_t)wv.w << 32 | wv.z) : ((uint64_t)wv.y << 32 | wv.x));
-            const int gl = 2 * c + hh;
-            const long A = *(const long*)(S.A + gl * 512 + lane * 8);
-            const v4i zero = {0, 0, 0, 0};
-            const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
-            const float Sv = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
+            const long A = (long)((uint64_t)(uint32_t)o.A[hh][0] | ((uint64_t)(uint32_t)o.A[hh][1] << 32));
+            C[hh] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+        }
+    }
+}
+
+// Group scaling of a chunk's integer sums: the lane's partial (lanes 0-15 hold rows 0-15).
+template <int FMT>
+__device__ __forceinline__ float ops_scale(const ChunkOps<FMT>& o, const v4i (&C)[2], uint2 sbv) {
+    float acc = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const float Sv = fmaf((float)C[hh][0], 65536.f, fmaf((float)C[hh][1], 256.f, (float)C[hh][2]));
+        if constexpr (FMT == FMT_Q4) {
+            const f16x2 sb2 = as_h2(hh ? sbv.y : sbv.x);
+            // The two groups' terms are independent; they meet in one add.
+            acc += fmaf((float)sb2.x * o.f[2 * hh], Sv, (float)sb2.y * o.f[2 * hh + 1]);
+        } else {
             const f16x2 s2 = as_h2(sbv.x);
-            acc = fmaf((hh ? (float)s2.y : (float)s2.x) * S.fx[gl * 2], Sv, acc);
+            acc += (hh ? (float)s2.y : (float)s2.x) * o.f[2 * hh] * Sv;
         }
     }
     return acc;
+}
+
+// Pairwise sum of N values (fixed order).
+template <int N>
+__device__ __forceinline__ float tree_sum(float (&v)[N]) {
+#pragma unroll
+    for (int w = 1; w < N; w *= 2)
+#pragma unroll
+        for (int i = 0; i + w < N; i += 2 * w) v[i] += v[i + w];
+    return v[0];
+}
+
+// Chunks c0 + i (i < N) against weights wv / sbv: all LDS reads, then all multiplies, then the
+// group scaling (no multiply result is consumed right after its issue).  Partials into part[i].
+template <int FMT, int N>
+__device__ __forceinline__ void mac_batch(const Shared& S, const uint4* wv, const uint2* sbv, int c0, int lane,
+                                          float* part) {
+    ChunkOps<FMT> o[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = ops_load<FMT>(S, c0 + i, lane);
+    v4i C[N][2];
+#pragma unroll
+    for (int i = 0; i < N; ++i) ops_mfma<FMT>(o[i], wv[i], C[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) part[i] = ops_scale<FMT>(o[i], C[i], sbv[i]);
 }
 
 // Scales of chunk c of tiled row `row`: q4 chunk = 128 K (two half2 (scale, bias) of 64-K
@@ -369,13 +444,55 @@ struct WB {
             sb[i] = load_sb<FMT>(sbp, rb * 16 + lane % 16, K, c);
         }
     }
+    // Batches of up to 4 chunks issue their LDS reads together; partials summed pairwise.
     __device__ __forceinline__ float mac(const Shared& S, int mw, int lane) const {
-        float acc = 0.f;
+        constexpr int NB = CW < 4 ? CW : 4;
+        static_assert(CW % NB == 0, "chunk batches");
+        float part[CW];
 #pragma unroll
-        for (int i = 0; i < CW; ++i) acc += chunk_mac<FMT>(S, wv[i], sb[i], mw * CW + i, lane);
-        return acc;
+        for (int b = 0; b < CW; b += NB) mac_batch<FMT, NB>(S, wv + b, sb + b, mw * CW + b, lane, part + b);
+        return tree_sum<CW>(part);
     }
 };
+
+// q4 down block of workgroup w straight into S.wdb (math wave mw requests the 12 chunks and the
+// scale columns it multiplies later, so each wave reads back only its own requests).
+__device__ __forceinline__ void wd_request(Shared& S, const uint8_t* wd, const uint8_t* wd_sb, int w, int mw, int lane) {
+    constexpr int NC = FF / 128, CWD = NC / MW;  // 48 chunks, 12 per wave
+    const uint8_t* blk = wd + (size_t)w * NC * 1024;
+#pragma unroll
+    for (int i = 0; i < CWD; ++i) {
+        const int c = mw * CWD + i;
+        lds_dma16(blk + (size_t)c * 1024 + lane * 16, S.wdb + c * 1024);
+    }
+    // Scales: rows 16 w + r, groups 24 mw .. 24 mw + 23 (96 B per row) -> 16 x 96 B at
+    // WD_CODES + 1536 mw; lane j of the two requests carries row j / 6, 16 B part j % 6.
+    uint8_t* dst = S.wdb + WD_CODES + mw * 1536;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int j = 64 * k + lane;
+        if (j < 96)
+            lds_dma16(wd_sb + ((size_t)(16 * w + j / 6) * (FF / 64) + 24 * mw) * 4 + 16 * (j % 6), dst + 1024 * k);
+    }
+}
+
+// The math wave's share of the q4 down block from S.wdb (after its requests have landed).
+template <int FMT>
+__device__ __forceinline__ float wd_mac_lds(const Shared& S, int mw, int lane) {
+    constexpr int CWD = FF / 128 / MW;
+    const uint8_t* sbr = S.wdb + WD_CODES + mw * 1536 + 96 * (lane & 15);
+    uint4 wv[CWD];
+    uint2 sbv[CWD];
+#pragma unroll
+    for (int i = 0; i < CWD; ++i) {
+        wv[i] = *(const uint4*)(S.wdb + (mw * CWD + i) * 1024 + lane * 16);
+        sbv[i] = *(const uint2*)(sbr + 8 * i);
+    }
+    float part[CWD];
+#pragma unroll
+    for (int b = 0; b < CWD; b += 4) mac_batch<FMT, 4>(S, wv + b, sbv + b, mw * CWD + b, lane, part + b);
+    return tree_sum<CWD>(part);
+}
 
 // Sum of the math waves' per-lane partials (whole-workgroup call); the total is valid in math
 // wave 0 (lanes 0-15 meaningful).
@@ -733,6 +850,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                     }
                 }
                 PK_TRACE(l, 20);
+                // q4: this layer's down block streams into LDS during merge, O and gate|up.
+                if constexpr (FMT == FMT_Q4) {
+                    if (math && w < H / 16) wd_request(S, P.wd, P.wd_sb, w, mw, lane);
+                }
             }
             PK_TRACE(l, 4);
 
@@ -851,12 +972,24 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             if (w < H / 16) {
                 bool ok = true;
                 if (!math) ok = poll_vec<FF / CT>(ll + HP, FF, r + 1, S.vec, err);
-                if (!EARLY_DOWN && math) wd.load(P.wd, P.wd_sb, w, FF, mw, lane);
+                if (FMT != FMT_Q4 && !EARLY_DOWN && math) wd.load(P.wd, P.wd_sb, w, FF, mw, lane);
                 if (__syncthreads_or(!ok)) return;
                 PK_TRACE_X(l, 11);
                 stage_c<FMT, FF / CT / 8, MATH>(S, S.vec, false);
                 PK_TRACE(l, 18);
-                const float y = reduce_math<MATH>(S, math ? wd.mac(S, mw, lane) : 0.f);
+                float yd = 0.f;
+                if (math) {
+                    if constexpr (FMT == FMT_Q4) {
+                        __builtin_amdgcn_s_waitcnt(0);  // this wave's down-block requests have landed
+                        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                        PK_TRACE(l, 23);
+                        yd = wd_mac_lds<FMT>(S, mw, lane);
+                        PK_TRACE(l, 24);
+                    } else {
+                        yd = wd.mac(S, mw, lane);
+                    }
+                }
+                const float y = reduce_math<MATH>(S, yd);
                 PK_TRACE(l, 19);
                 if (wave == 0 && lane < 16) {
                     const float xn = S.xown[lane] + y;
@@ -888,7 +1021,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             if (__syncthreads_or(!ok)) return;
             PK_TRACE_X(L, 1);
             stage_c<FMT, H / CT / 8, MATH>(S, S.vec, true);
-            float* plm = (float*)(S.A + 64 * 1024);  // [LM_BLOCKS][WAVES][16] partial sums
+            float* plm = (float*)S.wdb;  // [LM_BLOCKS][WAVES][16] partial sums
             for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
 #pragma unroll
                 for (int k = 0; k < LM_DEPTH; ++k) {
@@ -986,7 +1119,7 @@ template <int FMT>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     __shared__ Shared S;
     const int w = blockIdx.x;
-    for (int i = my_tid(); i < (int)sizeof(S.A) / 4; i += THREADS) ((uint32_t*)S.A)[i] = 0u;
+    if (my_tid() < 4) S.zero[my_tid()] = 0u;
     // Control block and the embedding of the first token (written before this launch).
     const State* st = a.st;
     if (st->done || st->n != 1) return;  // single-row passes only (checked by the host too)
