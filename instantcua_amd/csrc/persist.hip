@@ -850,10 +850,6 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                     }
                 }
                 PK_TRACE(l, 20);
-                // q4: this layer's down block streams into LDS during merge, O and gate|up.
-                if constexpr (FMT == FMT_Q4) {
-                    if (math && w < H / 16) wd_request(S, P.wd, P.wd_sb, w, mw, lane);
-                }
             }
             PK_TRACE(l, 4);
 
@@ -932,6 +928,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                     st64(ll + XP + w * 16 + lane, pack(xn, 2 * r + 1));
                 }
                 PK_TRACE(l, 8);
+                // q4: this layer's down block streams into LDS while the gate|up input is awaited
+                // and during gate|up (the math waves would otherwise idle at the next barrier).
+                if constexpr (FMT == FMT_Q4) {
+                    if (math) wd_request(S, P.wd, P.wd_sb, w, mw, lane);
+                }
             }
 
             // ---------------- RMSNorm + gate|up + SwiGLU: blocks 3w .. 3w + 2 --------------
