@@ -100,6 +100,9 @@ __device__ __forceinline__ uint64_t pack_i(int v, unsigned tag) { return (uint64
 __device__ __forceinline__ unsigned tag_of(uint64_t p) { return (unsigned)(p >> 32); }
 __device__ __forceinline__ float val_of(uint64_t p) { return as_f32((uint32_t)p); }
 
+// 2^x (v_exp_f32): the persistent attention keeps scores in base-2 units.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l
 // (lds is wave-uniform).  Counted by the issuing wave's vector-memory counter.
 __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
@@ -676,7 +679,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                 if (wave < 2) {
                     float x0 = S.vec[wave * HD + lane], x1 = S.vec[wave * HD + lane + 64];
                     norm_rope(x0, x1, qn0, qn1, rc, rs);
-                    const float qscale = 1.0f / sqrtf((float)HD);
+                    // 1/sqrt(128) and log2(e): scores come out in base-2 units, so every softmax
+                    // exponential of this split and of the merge is one v_exp_f32.
+                    const float qscale = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
                     S.qs[wave][lane] = x0 * qscale;
                     S.qs[wave][lane + 64] = x1 * qscale;
                 } else if (wave == 2 && tail) {
@@ -701,6 +706,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                 __builtin_amdgcn_s_waitcnt(0);
             }
             {
+                // Online softmax per quarter-wave (its 9 slots of every block) in registers; the
+                // 16 quarter-waves' (max, sum, o) are combined by lane swaps and once through LDS.
                 float q[2][8];
                 float m_run[2] = {-__builtin_inff(), -__builtin_inff()}, l_run[2] = {0.f, 0.f};
                 float o[2][8];
@@ -712,9 +719,13 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                         o[hh][d] = 0.f;
                     }
                 PK_TRACE(l, 21);
-                for (int b0 = 0; b0 < ntot; b0 += ATT_BLOCK) {  // uniform over the workgroup
-                    const int nb = min(ATT_BLOCK, ntot - b0);
-                    if (math) {
+                if (math) {
+#ifdef ICUA_PERSIST_TRACE
+                    __builtin_amdgcn_s_waitcnt(0);
+                    PK_TRACE(l, 25);
+#endif
+                    for (int b0 = 0; b0 < ntot; b0 += ATT_BLOCK) {
+                        const int nb = min(ATT_BLOCK, ntot - b0);
                         if (b0 > 0) {
 #pragma unroll
                             for (int i = 0; i < ATT_SPQ; ++i) {
@@ -742,6 +753,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                                 vr[i] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
                             }
                         }
+                        // Scores of the quarter-wave's slots (every lane of the quarter holds all 9).
+                        float sc[2][ATT_SPQ];
 #pragma unroll
                         for (int i = 0; i < ATT_SPQ; ++i) {
                             const int p = quad + ATT_QW * i;
@@ -758,95 +771,86 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                             }
                             acc0 = sum16(acc0);
                             acc1 = sum16(acc1);
-                            if (ql == 0) {
-                                S.sc[0][p] = (p < nb) ? acc0 : -__builtin_inff();
-                                S.sc[1][p] = (p < nb) ? acc1 : -__builtin_inff();
-                            }
+                            sc[0][i] = (p < nb) ? acc0 : -__builtin_inff();
+                            sc[1][i] = (p < nb) ? acc1 : -__builtin_inff();
                         }
-                    } else if (tid < MT + 2 * (ATT_PAD - ATT_BLOCK)) {  // padding slots
-                        const int c = tid - MT;
-                        S.sc[c & 1][ATT_BLOCK + (c >> 1)] = -__builtin_inff();
-                    }
-                    __syncthreads();
-                    // Block softmax statistics: math waves 0 and 1, one head each.
-                    if (wave < 2) {
-                        float sv[ATT_PAD / 64];
-                        float mb = -__builtin_inff();
-#pragma unroll
-                        for (int i = 0; i < ATT_PAD / 64; ++i) {
-                            sv[i] = S.sc[wave][lane + 64 * i];
-                            mb = fmaxf(mb, sv[i]);
-                        }
-                        mb = wave_max(mb);
-                        const float mn = fmaxf(m_run[wave], mb);
-                        float ls = 0.f;
-#pragma unroll
-                        for (int i = 0; i < ATT_PAD / 64; ++i) {
-                            const float e = (sv[i] == -__builtin_inff()) ? 0.f : expf(sv[i] - mn);
-                            S.sc[wave][lane + 64 * i] = e;
-                            ls += e;
-                        }
-                        ls = wave_sum(ls);
-                        if (lane == 0) {
-                            S.misc[wave] = mn;
-                            S.misc[2 + wave] = ls;
-                        }
-                    }
-                    __syncthreads();
-                    if (math) {
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh) {
-                            const float mn = S.misc[hh];
-                            const float corr = (m_run[hh] == -__builtin_inff()) ? 0.f : expf(m_run[hh] - mn);
-                            l_run[hh] = l_run[hh] * corr + S.misc[2 + hh];
-                            m_run[hh] = mn;
+                            float mb = m_run[hh];
+#pragma unroll
+                            for (int i = 0; i < ATT_SPQ; ++i) mb = fmaxf(mb, sc[hh][i]);
+                            // mb is finite as soon as the quarter has seen one valid slot.
+                            const float corr = (m_run[hh] == -__builtin_inff()) ? 0.f : ex2(m_run[hh] - mb);
+                            float ls = 0.f;
+#pragma unroll
+                            for (int i = 0; i < ATT_SPQ; ++i) {
+                                sc[hh][i] = (sc[hh][i] == -__builtin_inff()) ? 0.f : ex2(sc[hh][i] - mb);
+                                ls += sc[hh][i];
+                            }
+                            l_run[hh] = l_run[hh] * corr + ls;
+                            m_run[hh] = mb;
 #pragma unroll
                             for (int d = 0; d < 8; ++d) o[hh][d] *= corr;
                         }
 #pragma unroll
                         for (int i = 0; i < ATT_SPQ; ++i) {
-                            const int p = quad + ATT_QW * i;
-                            const float p0 = S.sc[0][p], p1 = S.sc[1][p];
                             const uint32_t dv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
                                 const f16x2 hv = as_h2(dv[j]);
                                 const float v0 = (float)hv.x, v1 = (float)hv.y;
-                                o[0][2 * j] = fmaf(p0, v0, o[0][2 * j]);
-                                o[0][2 * j + 1] = fmaf(p0, v1, o[0][2 * j + 1]);
-                                o[1][2 * j] = fmaf(p1, v0, o[1][2 * j]);
-                                o[1][2 * j + 1] = fmaf(p1, v1, o[1][2 * j + 1]);
+                                o[0][2 * j] = fmaf(sc[0][i], v0, o[0][2 * j]);
+                                o[0][2 * j + 1] = fmaf(sc[0][i], v1, o[0][2 * j + 1]);
+                                o[1][2 * j] = fmaf(sc[1][i], v0, o[1][2 * j]);
+                                o[1][2 * j + 1] = fmaf(sc[1][i], v1, o[1][2 * j + 1]);
                             }
                         }
                     }
-                    __syncthreads();
-                }
-                PK_TRACE(l, 22);
-                // Reduce o over the 16 quarter-waves: 4 per wave by lane swaps, 4 waves via LDS.
-                if (math) {
+                    // Combine the wave's 4 quarter-waves (lanes l, l ^ 16, l ^ 32, l ^ 48 hold the
+                    // same dims): rescale to their common max, then sum.
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh)
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const float mw4 = max_x4(m_run[hh]);
+                        const float f = (m_run[hh] == -__builtin_inff()) ? 0.f : ex2(m_run[hh] - mw4);
+                        l_run[hh] = sum_x4(l_run[hh] * f);
 #pragma unroll
-                        for (int d = 0; d < 8; ++d) {
-                            const float t1 = swap16_add(o[hh][d], o[hh][d]);
-                            o[hh][d] = swap32_add(t1, t1);
-                        }
+                        for (int d = 0; d < 8; ++d) o[hh][d] = sum_x4(o[hh][d] * f);
+                        m_run[hh] = mw4;
+                    }
                     if (lane < 16) {
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                             for (int d = 0; d < 8; ++d) S.ored[mw][hh][8 * ql + d] = o[hh][d];
                     }
+                    if (lane == 0) {
+                        S.misc[16 + 4 * mw] = m_run[0];
+                        S.misc[17 + 4 * mw] = m_run[1];
+                        S.misc[18 + 4 * mw] = l_run[0];
+                        S.misc[19 + 4 * mw] = l_run[1];
+                    }
                 }
+                PK_TRACE(l, 22);
                 __syncthreads();
                 if (math) {
+                    // The split's partial: the 4 waves rescaled to their common max.
                     uint64_t* part = ll + PARTP + (size_t)(g * ATT_SPLITS + s) * 2 * PART;
                     const int hh = tid / HD, d = tid % HD;
-                    const float acc = (S.ored[0][hh][d] + S.ored[1][hh][d]) + (S.ored[2][hh][d] + S.ored[3][hh][d]);
+                    float mx = -__builtin_inff();
+#pragma unroll
+                    for (int ww = 0; ww < MW; ++ww) mx = fmaxf(mx, S.misc[16 + 4 * ww + hh]);
+                    float acc = 0.f, lsum = 0.f;
+#pragma unroll
+                    for (int ww = 0; ww < MW; ++ww) {
+                        const float mwv = S.misc[16 + 4 * ww + hh];
+                        const float f = (mwv == -__builtin_inff()) ? 0.f : ex2(mwv - mx);
+                        acc = fmaf(S.ored[ww][hh][d], f, acc);
+                        lsum = fmaf(S.misc[18 + 4 * ww + hh], f, lsum);
+                    }
                     st64(part + hh * PART + d, pack(acc, r + 1));
                     if (d == 0) {
-                        st64(part + hh * PART + HD, pack(m_run[hh], r + 1));
-                        st64(part + hh * PART + HD + 1, pack(l_run[hh], r + 1));
+                        st64(part + hh * PART + HD, pack(mx, r + 1));
+                        st64(part + hh * PART + HD + 1, pack(lsum, r + 1));
                     }
                 }
                 PK_TRACE(l, 20);
@@ -876,7 +880,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                     const int sl = lane % ATT_SPLITS;
                     const float m = pl[sl * 66 + 64];
                     const float mx = wave_max(m);  // finite: the split holding row pos is never empty
-                    const float wgt = (m == -__builtin_inff()) ? 0.f : expf(m - mx);
+                    const float wgt = (m == -__builtin_inff()) ? 0.f : ex2(m - mx);
                     const float lw = wave_sum(lane < ATT_SPLITS ? wgt * pl[sl * 66 + 65] : 0.f);
                     if (lane < ATT_SPLITS) S.sc[0][lane] = wgt;
                     if (lane == 0) S.misc[0] = 1.0f / lw;
