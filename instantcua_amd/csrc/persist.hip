@@ -9,7 +9,8 @@
 // wait for each other.
 //
 // Grid.  One 512-thread workgroup per CU (256).  Static work split per layer:
-//   QKV   256 row blocks of the fused q|k|v rows (Convert.swift:185-188), block w
+//   QKV   256 row blocks of the fused q|k|v rows (Convert.swift:185-188): blocks w - 128 and w
+//         in workgroups 128..255 (workgroups 0..127 run down, just before)
 //   attn  KV group g = w % 8, split s = w / 8: the pos + 1 cache rows of the group (rows < pos and
 //         the new row) are spread evenly over the 32 splits; the split holding row pos writes it
 //   merge splits 28..31 of group g (workgroups 224..255, no O / down work) merge the 32
@@ -510,18 +511,19 @@ __device__ __forceinline__ float reduce_math(Shared& S, float acc) {
     return s;
 }
 
-// reduce_math for the three gate|up blocks at once (one pair of barriers).
-template <bool MATH>
-__device__ __forceinline__ void reduce_math3(Shared& S, const float (&acc)[3], float (&out)[3]) {
+// reduce_math for N <= 3 blocks at once (one pair of barriers).
+template <bool MATH, int N>
+__device__ __forceinline__ void reduce_math_n(Shared& S, const float (&acc)[N], float (&out)[N]) {
+    static_assert(N <= 3, "S.red holds three blocks");
     const int tid = my_tid(), lane = tid % 64, wave = wave_id();
     if (MATH) {
 #pragma unroll
-        for (int j = 0; j < 3; ++j) S.red[(j * MW + wave) * 64 + lane] = acc[j];
+        for (int j = 0; j < N; ++j) S.red[(j * MW + wave) * 64 + lane] = acc[j];
     }
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
+        for (int j = 0; j < N; ++j) {
             const float* r = S.red + j * MW * 64;
             out[j] = (r[lane] + r[64 + lane]) + (r[128 + lane] + r[192 + lane]);
         }
@@ -613,10 +615,14 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
 
             // Math-wave register tiles of this layer.  Each is requested when its stage starts
             // (while the exchange waves wait for the stage's input) or one stage earlier.
-            WB<FMT, CW2> wq, wo, wgu[3];
+            // wx: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127).
+            WB<FMT, CW2> wx[2], wgu[3];
             WB<FMT, CW6> wd;
 
-            // ---------------- QKV: row block w ---------------------------------------------
+            // ---------------- QKV: row blocks w - 128 and w (workgroups 128..255) ------------
+            // Workgroups 0..127 run down, so their next-layer loads would be issued just before
+            // an x poll and queue ahead of it; they take no QKV block and need no x here.
+            const bool qkv_wg = w >= NWG / 2;
             PK_TRACE(l, 0);
             uint4 kr[ATT_SPQ], vr[ATT_SPQ];
             float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rs = 0.f;
@@ -624,14 +630,19 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             // their loads at once.  Keeping the loads after the poll in program order lets the
             // poll's registers and the weight tiles share the register file.
             bool ok_in = true;
-            if (l > 0 && !math) ok_in = poll_vec<H / CT>(ll + XP, H, 2 * r, S.vec, err);
+            if (l > 0 && !math && qkv_wg) ok_in = poll_vec<H / CT>(ll + XP, H, 2 * r, S.vec, err);
             if (math) {
-                // This layer's norm weights into LDS; then the QKV block and the loads for the
+                // This layer's norm weights into LDS; then the QKV blocks and the loads for the
                 // stages ahead: the first block of K/V rows, the per-head norms and the rope row,
                 // the O block and the mlp norm.
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
-                wq.load(P.wqkv, P.wqkv_sb, w, H, mw, lane);
+                if (qkv_wg) {
+                    wx[0].load(P.wqkv, P.wqkv_sb, w - NWG / 2, H, mw, lane);
+                    wx[1].load(P.wqkv, P.wqkv_sb, w, H, mw, lane);
+                } else {
+                    wx[0].load(P.wo, P.wo_sb, w, H, mw, lane);
+                }
 #pragma unroll
                 for (int i = 0; i < ATT_SPQ; ++i) {
                     const int p = quad + ATT_QW * i;
@@ -649,15 +660,22 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                 kn1 = P.k_norm[lane + 64];
                 rc = rope[2 * lane];
                 rs = rope[2 * lane + 1];
-                if (w < H / 16) wo.load(P.wo, P.wo_sb, w, H, mw, lane);
                 load_norm8(nreg, P.mlp_norm + tid * 8);
             }
             if (__syncthreads_or(!ok_in)) return;
             PK_TRACE_X(l, 1);
-            stage_c<FMT, H / CT / 8, MATH>(S, l == 0 ? S.emb : S.vec, true);
-            {
-                const float y = reduce_math<MATH>(S, math ? wq.mac(S, mw, lane) : 0.f);
-                if (wave == 0 && lane < 16) st64(ll + QKVP + w * 16 + lane, pack(y, r + 1));
+            if (qkv_wg) {
+                stage_c<FMT, H / CT / 8, MATH>(S, l == 0 ? S.emb : S.vec, true);
+                float acc[2] = {0.f, 0.f}, y[2] = {0.f, 0.f};
+                if (math) {
+                    acc[0] = wx[0].mac(S, mw, lane);
+                    acc[1] = wx[1].mac(S, mw, lane);
+                }
+                reduce_math_n<MATH, 2>(S, acc, y);
+                if (wave == 0 && lane < 16) {
+                    st64(ll + QKVP + (w - NWG / 2) * 16 + lane, pack(y[0], r + 1));
+                    st64(ll + QKVP + w * 16 + lane, pack(y[1], r + 1));
+                }
             }
             PK_TRACE(l, 2);
 
@@ -925,7 +943,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             if (w < H / 16) {
                 PK_TRACE_X(l, 7);
                 stage_c<FMT, H / CT / 8, MATH>(S, S.vec, false);
-                const float y = reduce_math<MATH>(S, math ? wo.mac(S, mw, lane) : 0.f);
+                const float y = reduce_math<MATH>(S, math ? wx[0].mac(S, mw, lane) : 0.f);
                 if (wave == 0 && lane < 16) {
                     const float xn = S.xown[lane] + y;
                     S.xown[lane] = xn;
@@ -959,7 +977,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
 #pragma unroll
                     for (int j = 0; j < 3; ++j) acc[j] = wgu[j].mac(S, mw, lane);
                 }
-                reduce_math3<MATH>(S, acc, y);
+                reduce_math_n<MATH, 3>(S, acc, y);
                 PK_TRACE(l, 14);
                 if (wave == 0) {
 #pragma unroll
