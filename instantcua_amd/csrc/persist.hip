@@ -57,7 +57,7 @@ constexpr int CT = THREADS - MT;          // exchange threads (waves 4..7)
 constexpr int NWG = PERSIST_WGS;          // 256
 constexpr int ATT_SPLITS = NWG / NKV;     // 32
 constexpr int SPIN_LIMIT = 2000000;       // polls (>= ~1 us each) before a wait gives up
-constexpr int PART = HD + 2;              // partial of one head: o[128], m, l
+constexpr int PART2 = HD / 2 + 1;         // packets of one head's partial: o pairs, (l, m)
 constexpr int ATT_QW = MT / 16;           // 16 quarter-waves of math threads
 constexpr int ATT_SPQ = 9;                // cache slots per quarter-wave per block
 constexpr int ATT_BLOCK = ATT_QW * ATT_SPQ;  // 144 slots per block
@@ -66,18 +66,24 @@ constexpr int MERGE_PARTS = 4;            // workgroups merging one group's part
 constexpr int MERGER0 = NWG - NKV * MERGE_PARTS;  // workgroups 224..255: splits 28..31 of each group
 static_assert(MERGER0 >= H / 16, "mergers must not have O / down work");
 static_assert(MERGER0 % NKV == 0, "mergers of group g are splits 28..31 of group g");
-static_assert((FF / 128) % MW == 0 && FF / 64 / MW == 24, "down block: 12 chunks and 24 scale groups per math wave");
+// Down is split along K: workgroup w < 128 multiplies K 0..3071 of row block w, workgroup
+// w + 128 K 3072..6143 of the same rows.
+constexpr int FFH = FF / 2;
+static_assert(FFH / 128 / MW == 6 && FFH / 64 / MW == 12, "q4 down half: 6 chunks and 12 scale groups per math wave");
 
-// Packet area (64-bit packets), zeroed before every launch.
-constexpr int XP = 0;                 // residual x [H]
-constexpr int QKVP = XP + H;          // fused q|k|v [QKV]
-constexpr int ATTNP = QKVP + QKV;     // merged attention [H]
-constexpr int HP = ATTNP + H;         // SwiGLU activations [FF]
-constexpr int LMP = HP + FF;          // argmax partials [NWG][2] (value, index)
-constexpr int PARTP = LMP + 2 * NWG;  // attention partials [NKV][32][2][PART]
-constexpr int PACKETS = PARTP + NKV * ATT_SPLITS * 2 * PART;
-constexpr int ERRW = PACKETS * 2;     // error flag (32-bit word index)
-constexpr int GROUP_PARTS = ATT_SPLITS * 2 * PART;  // 8320 packets of one group's partials
+// Packet area (64-bit packets of two values, elements 2k and 2k + 1 of a vector in packet k),
+// zeroed before every launch.  The residual after a layer is x = XP + XDP: XP carries the lower
+// half's sum added to the residual, XDP the upper half's sum.
+constexpr int XP = 0;                   // residual x [H / 2] (after O: complete; after down: + lower half)
+constexpr int XDP = XP + H / 2;         // upper-half down sums [H / 2]
+constexpr int QKVP = XDP + H / 2;       // fused q|k|v [QKV / 2]
+constexpr int ATTNP = QKVP + QKV / 2;   // merged attention [H / 2]
+constexpr int HP = ATTNP + H / 2;       // SwiGLU activations [FF / 2]
+constexpr int LMP = HP + FF / 2;        // argmax partials [NWG] (index, value)
+constexpr int PARTP = LMP + NWG;        // attention partials [NKV][32][2][PART2]
+constexpr int PACKETS = PARTP + NKV * ATT_SPLITS * 2 * PART2;
+constexpr int ERRW = PACKETS * 2;       // error flag (32-bit word index)
+constexpr int GROUP_PARTS = ATT_SPLITS * 2 * PART2;  // 4160 packets of one group's partials
 
 // threadIdx.x behind an empty asm: per-lane address math derived from it is recomputed where it
 // is used instead of being hoisted out of the step / layer loops and held live (which spills).
@@ -96,10 +102,20 @@ __device__ __forceinline__ uint64_t ld64(const uint64_t* p) {
 __device__ __forceinline__ void st64(uint64_t* p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint64_t pack(float v, unsigned tag) { return (uint64_t)as_u32(v) | ((uint64_t)tag << 32); }
-__device__ __forceinline__ uint64_t pack_i(int v, unsigned tag) { return (uint64_t)(uint32_t)v | ((uint64_t)tag << 32); }
-__device__ __forceinline__ unsigned tag_of(uint64_t p) { return (unsigned)(p >> 32); }
-__device__ __forceinline__ float val_of(uint64_t p) { return as_f32((uint32_t)p); }
+// A packet holds two fp32 values and is written by one 64-bit store (single-copy atomic: a
+// reader sees both values of one store).  The low word is value a rounded to a 19-bit mantissa
+// whose low 4 bits carry the tag of the round (1..15: the round number mod 15, plus one; a
+// cleared packet carries 0); the high word is value b, exact.  A packet is rewritten once per
+// round of its area and a poll can only meet its own round or the two before it, so 15 tags
+// never alias.
+__device__ __forceinline__ unsigned tag4(unsigned round) { return round % 15u + 1u; }
+__device__ __forceinline__ float q19(float v) { return as_f32((as_u32(v) + 8u) & ~0xFu); }
+__device__ __forceinline__ uint64_t pack2(float a, float b, unsigned round) {
+    return (uint64_t)(as_u32(q19(a)) | tag4(round)) | ((uint64_t)as_u32(b) << 32);
+}
+__device__ __forceinline__ unsigned tag_of(uint64_t p) { return (unsigned)p & 0xFu; }
+__device__ __forceinline__ float lo_of(uint64_t p) { return as_f32((uint32_t)p & ~0xFu); }
+__device__ __forceinline__ float hi_of(uint64_t p) { return as_f32((uint32_t)(p >> 32)); }
 
 // 2^x (v_exp_f32): the persistent attention keeps scores in base-2 units.
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -117,24 +133,23 @@ __device__ __forceinline__ void raise_err(unsigned* e) {
     __hip_atomic_store(e, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Exchange threads: polls packets src[k], k = ct + CT * i < n (consecutive lanes read consecutive
-// packets), until each carries `tag`, then writes their values to dst[k].  false on timeout
-// (after raising the error flag) or when another workgroup raised it.
-template <int NP>
-__device__ __forceinline__ bool poll_vec(const uint64_t* src, int n, unsigned tag, float* dst, unsigned* err) {
-    const int ct = my_tid() - MT;
-    const uint64_t filler = (uint64_t)tag << 32;
-    uint64_t p[NP];
+// Exchange threads: loads the packets at(i) (i < NP; nullptr: no packet) until each carries the
+// tag of `round`.  false on timeout (after raising the error flag) or when another workgroup
+// raised it.
+template <int NP, typename At>
+__device__ __forceinline__ bool spin_tags(uint64_t (&p)[NP], At at, unsigned round, unsigned* err) {
+    const unsigned tag = tag4(round);
+    const uint64_t filler = tag;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        const int k = ct + CT * i;
-        p[i] = k < n ? ld64(src + k) : filler;
+        const uint64_t* q = at(i);
+        p[i] = q ? ld64(q) : filler;
     }
     for (int it = 0;; ++it) {
         bool ok = true;
 #pragma unroll
         for (int i = 0; i < NP; ++i) ok &= tag_of(p[i]) == tag;
-        if (ok) break;
+        if (ok) return true;
         if (it >= SPIN_LIMIT) {
             raise_err(err);
             return false;
@@ -143,46 +158,57 @@ __device__ __forceinline__ bool poll_vec(const uint64_t* src, int n, unsigned ta
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int i = 0; i < NP; ++i)
-            if (tag_of(p[i]) != tag) p[i] = ld64(src + ct + CT * i);
+            if (tag_of(p[i]) != tag) p[i] = ld64(at(i));  // a filler always carries the tag
     }
+}
+
+// Exchange threads: polls packets src[k], k = ct + CT * i < n (consecutive lanes read consecutive
+// packets), until each carries the tag of `round`, then writes their values to dst[2k], dst[2k + 1].
+template <int NP>
+__device__ __forceinline__ bool poll_vec(const uint64_t* src, int n, unsigned round, float* dst, unsigned* err) {
+    const int ct = my_tid() - MT;
+    uint64_t p[NP];
+    if (!spin_tags(p, [&](int i) { return ct + CT * i < n ? src + ct + CT * i : nullptr; }, round, err)) return false;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         const int k = ct + CT * i;
-        if (k < n) dst[k] = val_of(p[i]);
+        if (k < n) {
+            dst[2 * k] = lo_of(p[i]);
+            dst[2 * k + 1] = hi_of(p[i]);
+        }
     }
     return true;
 }
 
 // Exchange threads: as poll_vec, for packets src[map(k)] of a gathered vector (k < n).
 template <int NP, typename Map>
-__device__ __forceinline__ bool poll_map(const uint64_t* src, int n, Map map, unsigned tag, float* dst, unsigned* err) {
+__device__ __forceinline__ bool poll_map(const uint64_t* src, int n, Map map, unsigned round, float* dst, unsigned* err) {
     const int ct = my_tid() - MT;
-    const uint64_t filler = (uint64_t)tag << 32;
     uint64_t p[NP];
+    if (!spin_tags(p, [&](int i) { return ct + CT * i < n ? src + map(ct + CT * i) : nullptr; }, round, err))
+        return false;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         const int k = ct + CT * i;
-        p[i] = k < n ? ld64(src + map(k)) : filler;
-    }
-    for (int it = 0;; ++it) {
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) ok &= tag_of(p[i]) == tag;
-        if (ok) break;
-        if (it >= SPIN_LIMIT) {
-            raise_err(err);
-            return false;
+        if (k < n) {
+            dst[2 * k] = lo_of(p[i]);
+            dst[2 * k + 1] = hi_of(p[i]);
         }
-        if ((it & 63) == 63 && load_err(err)) return false;
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int i = 0; i < NP; ++i)
-            if (tag_of(p[i]) != tag) p[i] = ld64(src + map(ct + CT * i));
     }
+    return true;
+}
+
+// Exchange threads: as poll_vec for n = NP * CT packets, the sums of two packet vectors a, b.
+template <int NP>
+__device__ __forceinline__ bool poll_sum(const uint64_t* a, const uint64_t* b, unsigned round, float* dst, unsigned* err) {
+    const int ct = my_tid() - MT;
+    uint64_t p[2 * NP];
+    if (!spin_tags(p, [&](int i) { return (i < NP ? a : b) + ct + CT * (i % NP); }, round, err)) return false;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
         const int k = ct + CT * i;
-        if (k < n) dst[k] = val_of(p[i]);
+        dst[2 * k] = lo_of(p[i]) + lo_of(p[NP + i]);
+        dst[2 * k + 1] = hi_of(p[i]) + hi_of(p[NP + i]);
     }
     return true;
 }
@@ -190,13 +216,14 @@ __device__ __forceinline__ bool poll_map(const uint64_t* src, int n, Map map, un
 // Compact activation operands: per group the hi, mid, lo slices of its 4 K-slots (q4: 16 bytes
 // each, 192 B per 64-group; q8: 8 bytes each, 96 B per 32-group), K <= 6144.
 constexpr int A_BYTES = 18432;
-// q4 down block of a workgroup in LDS: 48 chunks of 1 KiB, then the 16 rows' (scale, bias) in
-// four per-wave parts of 16 x 96 B.
-constexpr int WD_CODES = (FF / 128) * 1024, WD_SB = 16 * (FF / 64) * 4;
+// Down half-block of a workgroup in LDS: 1 KiB chunks (q4 24, q8 48), then the 16 rows' scales
+// in four per-wave parts of 16 x 48 B (q4: 12 (scale, bias) pairs, q8: 24 scales per row).
+constexpr int WD_CODES = (FFH / 64) * 1024, WD_SB = 16 * MW * 48;
+static_assert(((VOCAB / 16 + NWG - 1) / NWG) * WAVES * 16 * 4 <= WD_CODES + WD_SB, "lm_head partial sums fit S.wdb");
 
 struct Shared {
     uint8_t A[A_BYTES];       // activation operands; the merger's fp32 partials during the merge
-    uint8_t wdb[WD_CODES + WD_SB];  // q4 down block (streamed in during the stages before down); lm_head partial sums
+    uint8_t wdb[WD_CODES + WD_SB];  // q4 down half-block (streamed in before down); lm_head partial sums
     uint32_t zero[4];         // operand rows 3..15 of every tile (16 zero bytes)
     float fx[192 * 2];        // per-group (2^(e-21), sum X * 2^(e-21))
     float red[3 * MW * 64];   // math-wave partial sums (up to 3 blocks)
@@ -204,6 +231,7 @@ struct Shared {
     float emb[H];             // embedding of the token being decoded
     float nw[H];              // RMSNorm weights of the current stage
     float xown[16];           // residual rows of this workgroup's O / down block (workgroups < 128)
+    float xhi[16];            // the upper-half down sums of those rows from the previous layer
     float qs[2][HD];          // attention: two query heads
     float ktail[HD], vtail[HD];
     float sc[2][ATT_PAD];
@@ -213,24 +241,32 @@ struct Shared {
 };
 
 // ------------------------------------------------------------------------------------------
-// Staging by the exchange threads: units of 8 consecutive activations (u = ct + CT * i, K / 8
-// units) -> optional RMSNorm with S.nw -> 22-bit slices -> compact A operands (rows 0, 1, 2 of a
-// group's tile: the hi, mid, lo slices; rows 3..15 read S.zero).  Called by the whole workgroup
-// (math threads only pass the barriers).
+// Staging by the exchange threads: units of 8 consecutive activations (u = ct + CT * j < K / 8)
+// -> optional RMSNorm with S.nw -> 22-bit slices -> compact A operands (rows 0, 1, 2 of a group's
+// tile: the hi, mid, lo slices; rows 3..15 read S.zero).  Called by the whole workgroup (math
+// threads only pass the barriers).  When K / 8 is not a multiple of CT the last unit row is held
+// by the first exchange waves only (whole waves, so whole groups).
 
-template <int FMT, int NU, bool MATH>
+template <int FMT, int K, bool MATH>
 __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed) {
     constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
     constexpr int TILE = (FMT == FMT_Q4) ? 192 : 96;
-    constexpr int K = NU * CT * 8;
+    constexpr int NU = (K / 8 + CT - 1) / CT;
+    static_assert((K / 8) % 64 == 0, "units of whole waves");
     const int tid = my_tid();
     constexpr bool ex = !MATH;
     const int ct = tid - MT, lane = tid % 64, cw = wave_id() - MW;
+    auto has = [&](int j) { return (K / 8) % CT == 0 || ct + CT * j < K / 8; };
     float v[NU][8];
     float scale = 1.f;
     if (ex) {
 #pragma unroll
         for (int j = 0; j < NU; ++j) {
+            if (!has(j)) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
+                continue;
+            }
             const float4 a0 = ((const float4*)(src + (ct + CT * j) * 8))[0];
             const float4 a1 = ((const float4*)(src + (ct + CT * j) * 8))[1];
             v[j][0] = a0.x; v[j][1] = a0.y; v[j][2] = a0.z; v[j][3] = a0.w;
@@ -253,6 +289,7 @@ __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed
             scale = 1.0f / sqrtf(tot / (float)K + EPS);
 #pragma unroll
             for (int j = 0; j < NU; ++j) {
+                if (!has(j)) continue;
                 const float* wn = S.nw + (ct + CT * j) * 8;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[j][i] = v[j][i] * scale * wn[i];
@@ -262,6 +299,7 @@ __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed
     if (ex) {
 #pragma unroll
         for (int j = 0; j < NU; ++j) {
+            if (!has(j)) continue;
             const int k0 = (ct + CT * j) * 8;
             float amax = 0.f;
 #pragma unroll
@@ -432,25 +470,39 @@ __device__ __forceinline__ uint2 load_sb(const uint8_t* sb, int row, int K, int 
         return make_uint2(*(const uint32_t*)(sb + ((size_t)row * (K / 32) + 2 * c) * 2), 0u);
 }
 
-// This math wave's share (chunks mw * CW .. mw * CW + CW - 1) of 16-row block rb.
+// Chunks per batch of a wave's CW chunks (at most 4).
+constexpr int batch_of(int cw) { return cw <= 4 ? cw : cw % 4 == 0 ? 4 : cw % 3 == 0 ? 3 : 2; }
+
+// This math wave's share (chunks c0 + mw * CW .. c0 + mw * CW + CW - 1) of 16-row block rb; the
+// staged operands start at chunk c0.
 template <int FMT, int CW>
 struct WB {
     uint4 wv[CW];
     uint2 sb[CW];
-    __device__ __forceinline__ void load(const uint8_t* w, const uint8_t* sbp, int rb, int K, int mw, int lane) {
+    __device__ __forceinline__ void load(const uint8_t* w, const uint8_t* sbp, int rb, int K, int mw, int lane,
+                                         int c0 = 0) {
         constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
         const int cpb = K / CHK;
         const uint8_t* blk = w + (size_t)rb * cpb * 1024;
 #pragma unroll
         for (int i = 0; i < CW; ++i) {
-            const int c = mw * CW + i;
+            const int c = c0 + mw * CW + i;
             wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
             sb[i] = load_sb<FMT>(sbp, rb * 16 + lane % 16, K, c);
         }
     }
-    // Batches of up to 4 chunks issue their LDS reads together; partials summed pairwise.
+    // Ends the live range of the tile's registers (no instruction): a tile loaded under a
+    // condition is otherwise kept alive across every path where the condition is false.
+    __device__ __forceinline__ void forget() {
+#pragma unroll
+        for (int i = 0; i < CW; ++i) {
+            asm volatile("" : "=v"(wv[i].x), "=v"(wv[i].y), "=v"(wv[i].z), "=v"(wv[i].w));
+            asm volatile("" : "=v"(sb[i].x), "=v"(sb[i].y));
+        }
+    }
+    // Batches of chunks issue their LDS reads together; partials summed pairwise.
     __device__ __forceinline__ float mac(const Shared& S, int mw, int lane) const {
-        constexpr int NB = CW < 4 ? CW : 4;
+        constexpr int NB = batch_of(CW);
         static_assert(CW % NB == 0, "chunk batches");
         float part[CW];
 #pragma unroll
@@ -459,42 +511,48 @@ struct WB {
     }
 };
 
-// q4 down block of workgroup w straight into S.wdb (math wave mw requests the 12 chunks and the
-// scale columns it multiplies later, so each wave reads back only its own requests).
-__device__ __forceinline__ void wd_request(Shared& S, const uint8_t* wd, const uint8_t* wd_sb, int w, int mw, int lane) {
-    constexpr int NC = FF / 128, CWD = NC / MW;  // 48 chunks, 12 per wave
-    const uint8_t* blk = wd + (size_t)w * NC * 1024;
+// Down half-block `half` of row block rb straight into S.wdb (math wave mw requests the chunks
+// and the scale columns it multiplies later, so each wave reads back only its own requests).
+template <int FMT>
+__device__ __forceinline__ void wd_request(Shared& S, const uint8_t* wd, const uint8_t* wd_sb, int rb, int half,
+                                           int mw, int lane) {
+    constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
+    constexpr int NC = FF / CHK, CWD = FFH / CHK / MW;  // chunks per row block, per wave
+    const uint8_t* blk = wd + ((size_t)rb * NC + half * (NC / 2)) * 1024;
 #pragma unroll
     for (int i = 0; i < CWD; ++i) {
         const int c = mw * CWD + i;
         lds_dma16(blk + (size_t)c * 1024 + lane * 16, S.wdb + c * 1024);
     }
-    // Scales: rows 16 w + r, groups 24 mw .. 24 mw + 23 (96 B per row) -> 16 x 96 B at
-    // WD_CODES + 1536 mw; lane j of the two requests carries row j / 6, 16 B part j % 6.
-    uint8_t* dst = S.wdb + WD_CODES + mw * 1536;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int j = 64 * k + lane;
-        if (j < 96)
-            lds_dma16(wd_sb + ((size_t)(16 * w + j / 6) * (FF / 64) + 24 * mw) * 4 + 16 * (j % 6), dst + 1024 * k);
-    }
+    // Scales (FF / 16 bytes per row in both formats): rows 16 rb + r, bytes 192 half + 48 mw ..
+    // + 47 -> 16 x 48 B at WD_CODES + 768 mw; lane j < 48 carries row j / 3, 16 B part j % 3.
+    if (lane < 48)
+        lds_dma16(wd_sb + (size_t)(16 * rb + lane / 3) * (FF / 16) + 192 * half + 48 * mw + 16 * (lane % 3),
+                  S.wdb + WD_CODES + mw * 768);
 }
 
-// The math wave's share of the q4 down block from S.wdb (after its requests have landed).
+// The math wave's share of the down half-block from S.wdb (after its requests have landed), in
+// batches of chunks.
 template <int FMT>
 __device__ __forceinline__ float wd_mac_lds(const Shared& S, int mw, int lane) {
-    constexpr int CWD = FF / 128 / MW;
-    const uint8_t* sbr = S.wdb + WD_CODES + mw * 1536 + 96 * (lane & 15);
-    uint4 wv[CWD];
-    uint2 sbv[CWD];
-#pragma unroll
-    for (int i = 0; i < CWD; ++i) {
-        wv[i] = *(const uint4*)(S.wdb + (mw * CWD + i) * 1024 + lane * 16);
-        sbv[i] = *(const uint2*)(sbr + 8 * i);
-    }
+    constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
+    constexpr int CWD = FFH / CHK / MW, NB = batch_of(CWD);
+    const uint8_t* sbr = S.wdb + WD_CODES + mw * 768 + 48 * (lane & 15);
     float part[CWD];
 #pragma unroll
-    for (int b = 0; b < CWD; b += 4) mac_batch<FMT, 4>(S, wv + b, sbv + b, mw * CWD + b, lane, part + b);
+    for (int b = 0; b < CWD; b += NB) {
+        uint4 wv[NB];
+        uint2 sbv[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            wv[i] = *(const uint4*)(S.wdb + (mw * CWD + b + i) * 1024 + lane * 16);
+            if constexpr (FMT == FMT_Q4)
+                sbv[i] = *(const uint2*)(sbr + 8 * (b + i));
+            else
+                sbv[i] = make_uint2(*(const uint32_t*)(sbr + 4 * (b + i)), 0u);
+        }
+        mac_batch<FMT, NB>(S, wv, sbv, mw * CWD + b, lane, part + b);
+    }
     return tree_sum<CWD>(part);
 }
 
@@ -541,6 +599,22 @@ __device__ __forceinline__ void norm_rope(float& a, float& b, float w0, float w1
     b = b2;
 }
 
+// Math threads: the cached K/V rows j0 + quad + 16 i (< j0 + nprior) of one split, 8 dims
+// (16 B) per lane; zeros past the split.
+__device__ __forceinline__ void load_kv_rows(uint4 (&kr)[ATT_SPQ], uint4 (&vr)[ATT_SPQ], const uint16_t* kb,
+                                             const uint16_t* vb, int j0, int nprior, int quad, int ql) {
+#pragma unroll
+    for (int i = 0; i < ATT_SPQ; ++i) {
+        const int p = quad + ATT_QW * i;
+        kr[i] = make_uint4(0u, 0u, 0u, 0u);
+        vr[i] = kr[i];
+        if (p < nprior) {
+            kr[i] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 8 * ql);
+            vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
+        }
+    }
+}
+
 __device__ __forceinline__ void load_norm8(float (&n)[8], const float* p) {
     const float4 n0 = ((const float4*)p)[0], n1 = ((const float4*)p)[1];
     n[0] = n0.x; n[1] = n0.y; n[2] = n0.z; n[3] = n0.w;
@@ -573,14 +647,10 @@ template <int FMT, bool MATH>
 __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int w, int pos, int stp) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
-    constexpr int CW6 = FF / CHK / MW;  // K = 6144
     constexpr int NRB = VOCAB / 16;     // lm_head row blocks
     constexpr int CW8 = H / CHK / WAVES;  // lm_head chunks per wave (all eight waves)
     constexpr int LM_DEPTH = 4;           // lm_head blocks in flight per wave
     constexpr int LM_BLOCKS = (NRB + NWG - 1) / NWG;  // 38 block slots per workgroup
-    // Down tiles are requested when the down stage starts: holding them through the gate|up stage
-    // as well would not fit the math waves' registers.
-    constexpr bool EARLY_DOWN = false;
     uint64_t* ll = a.ll;
     unsigned* err = (unsigned*)a.ll + ERRW;
     State* st = a.st;
@@ -588,10 +658,21 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
     const int L = a.nlayers;
     float nreg[8];  // math threads: norm weights of the next normed stage (8 each)
     if (MATH) load_norm8(nreg, a.layers[0].attn_norm + my_tid() * 8);
+    // Math waves: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127) of
+    // the current layer.
+    WB<FMT, CW2> wx[2];
     __syncthreads();
 
     for (int step = 0; step < a.nsteps; ++step) {
         if (pos + 1 > maxctx) break;  // the commit stops earlier; guards the cache row
+        if (MATH) {
+            wx[0].forget();
+            wx[1].forget();
+        }
+        if (MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
+            wx[0].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w - NWG / 2, H, wave_id(), my_tid() % 64);
+            wx[1].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w, H, wave_id(), my_tid() % 64);
+        }
         for (int l = 0; l < L; ++l) {
             const LayerPtrs& P = a.layers[l];
             const unsigned r = (unsigned)(step * L + l);  // round of this layer
@@ -613,15 +694,15 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             const uint16_t* vb = a.kv + ((size_t)(l * 2 + 1) * NKV + g) * a.maxctx * HD;
             const int quad = tid / 16, ql = tid % 16;  // math threads: 16 quarter-waves, 8 dims per lane
 
-            // Math-wave register tiles of this layer.  Each is requested when its stage starts
-            // (while the exchange waves wait for the stage's input) or one stage earlier.
-            // wx: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127).
-            WB<FMT, CW2> wx[2], wgu[3];
-            WB<FMT, CW6> wd;
+            // Math-wave register tiles: each is requested while the exchange waves wait for the
+            // input of its stage or of an earlier one.  The down half-block streams into LDS.
+            WB<FMT, CW2> wgu[3];
 
             // ---------------- QKV: row blocks w - 128 and w (workgroups 128..255) ------------
-            // Workgroups 0..127 run down, so their next-layer loads would be issued just before
-            // an x poll and queue ahead of it; they take no QKV block and need no x here.
+            // Workgroups 0..127 need no x here.  Loads issued just before the x poll of
+            // workgroups 128..255 would queue ahead of it on their CU: their QKV blocks are
+            // requested during the previous layer's down stage (layer 0's at the start of the
+            // step) and their K/V rows after the QKV publish.
             const bool qkv_wg = w >= NWG / 2;
             PK_TRACE(l, 0);
             uint4 kr[ATT_SPQ], vr[ATT_SPQ];
@@ -630,28 +711,16 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             // their loads at once.  Keeping the loads after the poll in program order lets the
             // poll's registers and the weight tiles share the register file.
             bool ok_in = true;
-            if (l > 0 && !math && qkv_wg) ok_in = poll_vec<H / CT>(ll + XP, H, 2 * r, S.vec, err);
+            if (l > 0 && !math && qkv_wg) ok_in = poll_sum<H / 2 / CT>(ll + XP, ll + XDP, 2 * r, S.vec, err);
             if (math) {
                 // This layer's norm weights into LDS; then the QKV blocks and the loads for the
                 // stages ahead: the first block of K/V rows, the per-head norms and the rope row,
                 // the O block and the mlp norm.
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
-                if (qkv_wg) {
-                    wx[0].load(P.wqkv, P.wqkv_sb, w - NWG / 2, H, mw, lane);
-                    wx[1].load(P.wqkv, P.wqkv_sb, w, H, mw, lane);
-                } else {
+                if (!qkv_wg) {
                     wx[0].load(P.wo, P.wo_sb, w, H, mw, lane);
-                }
-#pragma unroll
-                for (int i = 0; i < ATT_SPQ; ++i) {
-                    const int p = quad + ATT_QW * i;
-                    kr[i] = make_uint4(0u, 0u, 0u, 0u);
-                    vr[i] = kr[i];
-                    if (p < nprior) {
-                        kr[i] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 8 * ql);
-                        vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
-                    }
+                    load_kv_rows(kr, vr, kb, vb, j0, nprior, quad, ql);
                 }
                 const float* rope = a.rope + (size_t)pos * 128;
                 qn0 = P.q_norm[lane];
@@ -665,17 +734,21 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             if (__syncthreads_or(!ok_in)) return;
             PK_TRACE_X(l, 1);
             if (qkv_wg) {
-                stage_c<FMT, H / CT / 8, MATH>(S, l == 0 ? S.emb : S.vec, true);
+                stage_c<FMT, H, MATH>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[2] = {0.f, 0.f}, y[2] = {0.f, 0.f};
                 if (math) {
                     acc[0] = wx[0].mac(S, mw, lane);
                     acc[1] = wx[1].mac(S, mw, lane);
                 }
                 reduce_math_n<MATH, 2>(S, acc, y);
-                if (wave == 0 && lane < 16) {
-                    st64(ll + QKVP + (w - NWG / 2) * 16 + lane, pack(y[0], r + 1));
-                    st64(ll + QKVP + w * 16 + lane, pack(y[1], r + 1));
+                if (wave == 0) {  // rows 2i, 2i + 1 of a block in packet i (even lanes)
+                    const float n0 = __shfl_xor(y[0], 1), n1 = __shfl_xor(y[1], 1);
+                    if (lane < 16 && !(lane & 1)) {
+                        st64(ll + QKVP + (w - NWG / 2) * 8 + lane / 2, pack2(y[0], n0, r + 1));
+                        st64(ll + QKVP + w * 8 + lane / 2, pack2(y[1], n1, r + 1));
+                    }
                 }
+                if (math) load_kv_rows(kr, vr, kb, vb, j0, nprior, quad, ql);
             }
             PK_TRACE(l, 2);
 
@@ -683,11 +756,13 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             {
                 bool ok = true;
                 if (!math)  // q heads 2g, 2g+1 -> vec[0..255], k -> vec[256..383], v -> vec[384..511]
-                    ok = poll_map<2>(
-                        ll + QKVP, 4 * HD,
-                        [&](int k) {
-                            return k < 2 * HD ? 2 * g * HD + k
-                                              : k < 3 * HD ? H + g * HD + (k - 2 * HD) : H + NKV * HD + g * HD + (k - 3 * HD);
+                    ok = poll_map<1>(
+                        ll + QKVP, 2 * HD,
+                        [&](int k) {  // packet of gathered elements 2k, 2k + 1
+                            const int e = 2 * k;
+                            return (e < 2 * HD ? 2 * g * HD + e
+                                               : e < 3 * HD ? H + g * HD + (e - 2 * HD)
+                                                            : H + NKV * HD + g * HD + (e - 3 * HD)) / 2;
                         },
                         r + 1, S.vec, err);
                 if (__syncthreads_or(!ok)) return;
@@ -852,7 +927,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                 __syncthreads();
                 if (math) {
                     // The split's partial: the 4 waves rescaled to their common max.
-                    uint64_t* part = ll + PARTP + (size_t)(g * ATT_SPLITS + s) * 2 * PART;
+                    uint64_t* part = ll + PARTP + (size_t)(g * ATT_SPLITS + s) * 2 * PART2;
                     const int hh = tid / HD, d = tid % HD;
                     float mx = -__builtin_inff();
 #pragma unroll
@@ -865,11 +940,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                         acc = fmaf(S.ored[ww][hh][d], f, acc);
                         lsum = fmaf(S.misc[18 + 4 * ww + hh], f, lsum);
                     }
-                    st64(part + hh * PART + d, pack(acc, r + 1));
-                    if (d == 0) {
-                        st64(part + hh * PART + HD, pack(mx, r + 1));
-                        st64(part + hh * PART + HD + 1, pack(lsum, r + 1));
-                    }
+                    // o pairs (even lanes), then (l, m) with the maximum exact.
+                    const float acc_n = __shfl_xor(acc, 1);
+                    if (!(d & 1)) st64(part + hh * PART2 + d / 2, pack2(acc, acc_n, r + 1));
+                    if (d == 0) st64(part + hh * PART2 + HD / 2, pack2(lsum, mx, r + 1));
                 }
                 PK_TRACE(l, 20);
             }
@@ -880,15 +954,15 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             // p = 0..3 of the group's output: head 2g + p / 2, elements 64 (p % 2) .. + 63.
             if (w >= MERGER0) {
                 const int p = s - (ATT_SPLITS - MERGE_PARTS), hh = p / 2, d0 = 64 * (p % 2);
-                float* pl = (float*)S.A;  // [32][64 + 2]: o elements d0.., m, l of head hh per split
+                float* pl = (float*)S.A;  // [32][64 + 2]: o elements d0.., l, m of head hh per split
                 const uint64_t* gp = ll + PARTP + (size_t)g * GROUP_PARTS;
                 bool ok = true;
                 if (!math)
-                    ok = poll_map<(ATT_SPLITS * 66 + CT - 1) / CT>(
-                        gp, ATT_SPLITS * 66,
+                    ok = poll_map<(ATT_SPLITS * 33 + CT - 1) / CT>(
+                        gp, ATT_SPLITS * 33,
                         [&](int k) {
-                            const int sj = k / 66, e = k % 66;
-                            return (sj * 2 + hh) * PART + (e < 64 ? d0 + e : HD + (e - 64));
+                            const int sj = k / 33, e = k % 33;
+                            return (sj * 2 + hh) * PART2 + (e < 32 ? d0 / 2 + e : HD / 2);
                         },
                         r + 1, pl, err);
                 if (__syncthreads_or(!ok)) return;
@@ -896,10 +970,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                 // Split weights exp(m_s - max) and the normaliser (math wave 0, one lane per split).
                 if (math && wave == 0) {
                     const int sl = lane % ATT_SPLITS;
-                    const float m = pl[sl * 66 + 64];
+                    const float m = pl[sl * 66 + 65];
                     const float mx = wave_max(m);  // finite: the split holding row pos is never empty
                     const float wgt = (m == -__builtin_inff()) ? 0.f : ex2(m - mx);
-                    const float lw = wave_sum(lane < ATT_SPLITS ? wgt * pl[sl * 66 + 65] : 0.f);
+                    const float lw = wave_sum(lane < ATT_SPLITS ? wgt * pl[sl * 66 + 64] : 0.f);
                     if (lane < ATT_SPLITS) S.sc[0][lane] = wgt;
                     if (lane == 0) S.misc[0] = 1.0f / lw;
                 }
@@ -921,7 +995,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                         float t = 0.f;
 #pragma unroll
                         for (int qq = 0; qq < 8; ++qq) t += q8[qq * 64 + tid];
-                        st64(ll + ATTNP + (2 * g + hh) * HD + d0 + tid, pack(t * S.misc[0], r + 1));
+                        const float v = t * S.misc[0], vn = __shfl_xor(v, 1);
+                        if (!(tid & 1)) st64(ll + ATTNP + ((2 * g + hh) * HD + d0 + tid) / 2, pack2(v, vn, r + 1));
                     }
                 }
                 PK_TRACE(l, 17);
@@ -930,10 +1005,18 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             }
 
             // ---------------- O projection + residual: workgroups 0..127 -------------------
-            // The gate|up blocks are requested here, a stage early, by every workgroup.
+            // The gate|up blocks are requested here, a stage early, by every workgroup.  The
+            // residual of the O rows is xown (previous x + lower-half down sums) + xhi (the
+            // upper-half sums, long published): the same two terms every x reader adds.
             {
                 bool ok = true;
-                if (w < H / 16 && !math) ok = poll_vec<H / CT>(ll + ATTNP, H, r + 1, S.vec, err);
+                if (w < H / 16 && !math) {
+                    if (l > 0)
+                        ok = poll_vec<1>(ll + XDP + w * 8, 8, 2 * r, S.xhi, err);
+                    else if (tid - MT < 16)
+                        S.xhi[tid - MT] = 0.f;
+                    ok = ok && poll_vec<H / 2 / CT>(ll + ATTNP, H / 2, r + 1, S.vec, err);
+                }
                 if (math) {
 #pragma unroll
                     for (int j = 0; j < 3; ++j) wgu[j].load(P.wgu, P.wgu_sb, 3 * w + j, H, mw, lane);
@@ -942,35 +1025,35 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             }
             if (w < H / 16) {
                 PK_TRACE_X(l, 7);
-                stage_c<FMT, H / CT / 8, MATH>(S, S.vec, false);
+                stage_c<FMT, H, MATH>(S, S.vec, false);
                 const float y = reduce_math<MATH>(S, math ? wx[0].mac(S, mw, lane) : 0.f);
-                if (wave == 0 && lane < 16) {
-                    const float xn = S.xown[lane] + y;
-                    S.xown[lane] = xn;
-                    st64(ll + XP + w * 16 + lane, pack(xn, 2 * r + 1));
+                if (wave == 0) {  // the owner keeps the residual as published (even rows rounded)
+                    const float xn = lane < 16 ? (S.xown[lane] + S.xhi[lane]) + y : 0.f;
+                    const float xo = __shfl_xor(xn, 1);
+                    if (lane < 16) {
+                        S.xown[lane] = (lane & 1) ? xn : q19(xn);
+                        if (!(lane & 1)) st64(ll + XP + w * 8 + lane / 2, pack2(xn, xo, 2 * r + 1));
+                    }
                 }
                 PK_TRACE(l, 8);
-                // q4: this layer's down block streams into LDS while the gate|up input is awaited
-                // and during gate|up (the math waves would otherwise idle at the next barrier).
-                if constexpr (FMT == FMT_Q4) {
-                    if (math) wd_request(S, P.wd, P.wd_sb, w, mw, lane);
-                }
             }
+            // This layer's down half-block streams into LDS while the gate|up input is awaited
+            // and during gate|up (the math waves would otherwise idle at the next barrier).
+            if (math) wd_request<FMT>(S, P.wd, P.wd_sb, w % (NWG / 2), w / (NWG / 2), mw, lane);
 
             // ---------------- RMSNorm + gate|up + SwiGLU: blocks 3w .. 3w + 2 --------------
             {
                 bool ok = true;
-                if (!math) ok = poll_vec<H / CT>(ll + XP, H, 2 * r + 1, S.vec, err);
+                if (!math) ok = poll_vec<H / 2 / CT>(ll + XP, H / 2, 2 * r + 1, S.vec, err);
                 if (math) {
 #pragma unroll
                     for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
-                    if (EARLY_DOWN && w < H / 16) wd.load(P.wd, P.wd_sb, w, FF, mw, lane);
                     // The next layer's attention norm, or the final norm.
                     load_norm8(nreg, (l + 1 < L ? a.layers[l + 1].attn_norm : a.final_norm) + tid * 8);
                 }
                 if (__syncthreads_or(!ok)) return;
                 PK_TRACE_X(l, 9);
-                stage_c<FMT, H / CT / 8, MATH>(S, S.vec, true);
+                stage_c<FMT, H, MATH>(S, S.vec, true);
                 PK_TRACE(l, 13);
                 float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
                 if (math) {
@@ -984,40 +1067,50 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                     for (int j = 0; j < 3; ++j) {
                         // Block 3w + j: gate units 8 (3w + j) + 0..7 in lanes 0-7, their up rows in 8-15.
                         const float up = __shfl_xor(y[j], 8);
-                        if (lane < 8)
-                            st64(ll + HP + (3 * w + j) * 8 + lane, pack((y[j] / (1.f + expf(-y[j]))) * up, r + 1));
+                        const float hv = (y[j] / (1.f + expf(-y[j]))) * up, hn = __shfl_xor(hv, 1);
+                        if (lane < 8 && !(lane & 1)) st64(ll + HP + (3 * w + j) * 4 + lane / 2, pack2(hv, hn, r + 1));
                     }
                 }
                 PK_TRACE(l, 10);
             }
 
-            // ---------------- down + residual: workgroups 0..127 ---------------------------
-            if (w < H / 16) {
+            // ---------------- down: K half w / 128 of row block w % 128 --------------------
+            {
+                const int rb = w % (NWG / 2), half = w / (NWG / 2);
                 bool ok = true;
-                if (!math) ok = poll_vec<FF / CT>(ll + HP, FF, r + 1, S.vec, err);
-                if (FMT != FMT_Q4 && !EARLY_DOWN && math) wd.load(P.wd, P.wd_sb, w, FF, mw, lane);
+                if (!math) ok = poll_vec<FFH / 2 / CT>(ll + HP + half * (FFH / 2), FFH / 2, r + 1, S.vec, err);
+                if (math) {
+                    wx[0].forget();
+                    wx[1].forget();
+                }
+                if (math && qkv_wg && l + 1 < L) {  // the next layer's QKV blocks
+                    const LayerPtrs& Pn = a.layers[l + 1];
+                    wx[0].load(Pn.wqkv, Pn.wqkv_sb, w - NWG / 2, H, mw, lane);
+                    wx[1].load(Pn.wqkv, Pn.wqkv_sb, w, H, mw, lane);
+                }
                 if (__syncthreads_or(!ok)) return;
                 PK_TRACE_X(l, 11);
-                stage_c<FMT, FF / CT / 8, MATH>(S, S.vec, false);
+                stage_c<FMT, FFH, MATH>(S, S.vec, false);
                 PK_TRACE(l, 18);
                 float yd = 0.f;
                 if (math) {
-                    if constexpr (FMT == FMT_Q4) {
-                        __builtin_amdgcn_s_waitcnt(0);  // this wave's down-block requests have landed
-                        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-                        PK_TRACE(l, 23);
-                        yd = wd_mac_lds<FMT>(S, mw, lane);
-                        PK_TRACE(l, 24);
-                    } else {
-                        yd = wd.mac(S, mw, lane);
-                    }
+                    // This wave's down-block requests have landed (and the QKV prefetch, issued
+                    // after them, too: vector memory counts complete in order).
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                    PK_TRACE(l, 23);
+                    yd = wd_mac_lds<FMT>(S, mw, lane);
+                    PK_TRACE(l, 24);
                 }
                 const float y = reduce_math<MATH>(S, yd);
                 PK_TRACE(l, 19);
-                if (wave == 0 && lane < 16) {
-                    const float xn = S.xown[lane] + y;
-                    S.xown[lane] = xn;
-                    st64(ll + XP + w * 16 + lane, pack(xn, 2 * r + 2));
+                if (wave == 0) {
+                    const float v = lane < 16 ? (half == 0 ? S.xown[lane] + y : y) : 0.f;
+                    const float vn = __shfl_xor(v, 1);
+                    if (lane < 16) {
+                        if (half == 0) S.xown[lane] = (lane & 1) ? v : q19(v);
+                        if (!(lane & 1)) st64(ll + (half == 0 ? XP : XDP) + rb * 8 + lane / 2, pack2(v, vn, 2 * r + 2));
+                    }
                 }
                 PK_TRACE(l, 12);
             }
@@ -1034,7 +1127,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             // wave's per-block partial sums go to LDS; one reduction and argmax at the end.
             WB<FMT, CW8> wl[LM_DEPTH];
             bool ok = true;
-            if (!math) ok = poll_vec<H / CT>(ll + XP, H, 2 * r_last + 2, S.vec, err);
+            if (!math) ok = poll_sum<H / 2 / CT>(ll + XP, ll + XDP, 2 * r_last + 2, S.vec, err);
             if (math) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
@@ -1043,7 +1136,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
             if (__syncthreads_or(!ok)) return;
             PK_TRACE_X(L, 1);
-            stage_c<FMT, H / CT / 8, MATH>(S, S.vec, true);
+            stage_c<FMT, H, MATH>(S, S.vec, true);
             float* plm = (float*)S.wdb;  // [LM_BLOCKS][WAVES][16] partial sums
             for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
 #pragma unroll
@@ -1077,8 +1170,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             __syncthreads();
             if (tid == 0) {
                 for (int wv = 1; wv < WAVES; ++wv) argmax_merge(best, besti, S.misc[8 + wv], S.imisc[8 + wv]);
-                st64(ll + LMP + 2 * w, pack(best, (unsigned)step + 1));
-                st64(ll + LMP + 2 * w + 1, pack_i(besti, (unsigned)step + 1));
+                // (index << 4 | tag, value): the value exact, ids < 2^27 exact in the low word.
+                const uint32_t lo = ((uint32_t)min(besti, 0x07FFFFFF) << 4) | tag4((unsigned)step + 1);
+                st64(ll + LMP + w, (uint64_t)lo | ((uint64_t)as_u32(best) << 32));
             }
             PK_TRACE(L, 2);
             if (math) load_norm8(nreg, a.layers[0].attn_norm + tid * 8);  // for the next step
@@ -1088,14 +1182,14 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
         {
             const int tid = my_tid(), lane = tid % 64, wave = wave_id();
             bool ok = true;
-            if (!MATH) ok = poll_vec<2>(ll + LMP, 2 * NWG, (unsigned)step + 1, S.vec, err);
+            if (!MATH) ok = poll_vec<NWG / CT>(ll + LMP, NWG, (unsigned)step + 1, S.vec, err);
             if (__syncthreads_or(!ok)) return;
             PK_TRACE_X(L, 3);
             float bv = -__builtin_inff();
             int bi = 0x7fffffff;
             if (tid < NWG) {
-                bv = S.vec[2 * tid];
-                bi = (int)as_u32(S.vec[2 * tid + 1]);
+                bv = S.vec[2 * tid + 1];
+                bi = (int)(as_u32(S.vec[2 * tid]) >> 4);
             }
             wave_argmax(bv, bi);
             if (lane == 0) {
