@@ -241,122 +241,94 @@ struct Shared {
 };
 
 // ------------------------------------------------------------------------------------------
-// Staging by the exchange threads: units of 8 consecutive activations (u = ct + CT * j < K / 8)
-// -> optional RMSNorm with S.nw -> 22-bit slices -> compact A operands (rows 0, 1, 2 of a group's
-// tile: the hi, mid, lo slices; rows 3..15 read S.zero).  Called by the whole workgroup (math
-// threads only pass the barriers).  When K / 8 is not a multiple of CT the last unit row is held
-// by the first exchange waves only (whole waves, so whole groups).
+// Staging by the whole workgroup: units of 4 consecutive activations (u = tid + THREADS * j <
+// K / 4) -> optional RMSNorm with S.nw -> 22-bit slices -> compact A operands (rows 0, 1, 2 of a
+// group's tile: the hi, mid, lo slices; rows 3..15 read S.zero).  A group is 16 (q4) or 8 (q8)
+// consecutive lanes, so its maximum and sum are DPP row reductions.  When K / 4 is not a
+// multiple of THREADS the last unit row is held by the first waves only (whole waves, so whole
+// groups).
 
 template <int FMT, int K, bool MATH>
 __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed) {
     constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
     constexpr int TILE = (FMT == FMT_Q4) ? 192 : 96;
-    constexpr int NU = (K / 8 + CT - 1) / CT;
-    static_assert((K / 8) % 64 == 0, "units of whole waves");
-    const int tid = my_tid();
-    constexpr bool ex = !MATH;
-    const int ct = tid - MT, lane = tid % 64, cw = wave_id() - MW;
-    auto has = [&](int j) { return (K / 8) % CT == 0 || ct + CT * j < K / 8; };
-    float v[NU][8];
-    float scale = 1.f;
-    if (ex) {
+    constexpr int NU = (K / 4 + THREADS - 1) / THREADS;
+    static_assert((K / 4) % 64 == 0, "units of whole waves");
+    const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+    auto has = [&](int j) { return (K / 4) % THREADS == 0 || tid + THREADS * j < K / 4; };
+    float v[NU][4];
 #pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            if (!has(j)) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
-                continue;
-            }
-            const float4 a0 = ((const float4*)(src + (ct + CT * j) * 8))[0];
-            const float4 a1 = ((const float4*)(src + (ct + CT * j) * 8))[1];
-            v[j][0] = a0.x; v[j][1] = a0.y; v[j][2] = a0.z; v[j][3] = a0.w;
-            v[j][4] = a1.x; v[j][5] = a1.y; v[j][6] = a1.z; v[j][7] = a1.w;
-        }
+    for (int j = 0; j < NU; ++j) {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (has(j)) a = ((const float4*)src)[tid + THREADS * j];
+        v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
     }
     if (normed) {
-        if (ex) {
-            float ss = 0.f;
+        float ss = 0.f;
 #pragma unroll
-            for (int j = 0; j < NU; ++j)
+        for (int j = 0; j < NU; ++j)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
-            ss = wave_sum(ss);
-            if (lane == 0) S.misc[40 + cw] = ss;
-        }
+            for (int i = 0; i < 4; ++i) ss += v[j][i] * v[j][i];
+        ss = wave_sum(ss);
+        if (lane == 0) S.misc[40 + wave] = ss;
         __syncthreads();
-        if (ex) {
-            const float tot = (S.misc[40] + S.misc[41]) + (S.misc[42] + S.misc[43]);
-            scale = 1.0f / sqrtf(tot / (float)K + EPS);
-#pragma unroll
-            for (int j = 0; j < NU; ++j) {
-                if (!has(j)) continue;
-                const float* wn = S.nw + (ct + CT * j) * 8;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[j][i] = v[j][i] * scale * wn[i];
-            }
-        }
-    }
-    if (ex) {
+        const float tot = ((S.misc[40] + S.misc[41]) + (S.misc[42] + S.misc[43])) +
+                          ((S.misc[44] + S.misc[45]) + (S.misc[46] + S.misc[47]));
+        const float scale = 1.0f / sqrtf(tot / (float)K + EPS);
 #pragma unroll
         for (int j = 0; j < NU; ++j) {
             if (!has(j)) continue;
-            const int k0 = (ct + CT * j) * 8;
-            float amax = 0.f;
+            const float4 wn = ((const float4*)S.nw)[tid + THREADS * j];
+            v[j][0] = v[j][0] * scale * wn.x;
+            v[j][1] = v[j][1] * scale * wn.y;
+            v[j][2] = v[j][2] * scale * wn.z;
+            v[j][3] = v[j][3] * scale * wn.w;
+        }
+    }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
-            int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
-            bits = max(bits, dpp_i<DPP_XOR1>(bits));
-            bits = max(bits, dpp_i<DPP_XOR2>(bits));
-            if constexpr (G == 64) bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
-            int e = ((bits >> 23) & 0xFF) - 127;
-            if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
-            const int sh = 21 - e;
-            int X[8], xs = 0;
+    for (int j = 0; j < NU; ++j) {
+        if (!has(j)) continue;
+        const int k0 = (tid + THREADS * j) * 4;
+        float amax = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                X[i] = (int)rintf(ldexpf(v[j][i], sh));
-                xs += X[i];
-            }
-            xs += dpp_i<DPP_XOR1>(xs);
-            xs += dpp_i<DPP_XOR2>(xs);
-            if constexpr (G == 64) xs += dpp_i<DPP_HALF_MIRROR>(xs);
-            uint32_t sl[3][2];
+        for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
+        int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
+        bits = max(bits, dpp_i<DPP_XOR1>(bits));
+        bits = max(bits, dpp_i<DPP_XOR2>(bits));
+        bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
+        if constexpr (G == 64) bits = max(bits, dpp_i<DPP_MIRROR>(bits));
+        int e = ((bits >> 23) & 0xFF) - 127;
+        if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
+        const int sh = 21 - e;
+        int xs = 0;
+        uint32_t p0 = 0, p1 = 0, p2 = 0;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint32_t p0 = 0, p1 = 0, p2 = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int xv = X[4 * h + i];
-                    const int lo = (int)(int8_t)(xv & 0xFF);
-                    const int r1 = (xv - lo) >> 8;
-                    const int mid = (int)(int8_t)(r1 & 0xFF);
-                    const int hi = (r1 - mid) >> 8;
-                    p0 |= (uint32_t)(lo & 0xFF) << (8 * i);
-                    p1 |= (uint32_t)(mid & 0xFF) << (8 * i);
-                    p2 |= (uint32_t)(hi & 0xFF) << (8 * i);
-                }
-                sl[0][h] = p0;
-                sl[1][h] = p1;
-                sl[2][h] = p2;
-            }
-            const int gl = k0 / G, kk = k0 % G;
-            uint8_t* A = S.A + gl * TILE;
-            if constexpr (FMT == FMT_Q4) {
-                const int q = kk / 16, j0 = kk % 16;
-                *(uint2*)(A + (3 * q + 0) * 16 + j0) = make_uint2(sl[2][0], sl[2][1]);
-                *(uint2*)(A + (3 * q + 1) * 16 + j0) = make_uint2(sl[1][0], sl[1][1]);
-                *(uint2*)(A + (3 * q + 2) * 16 + j0) = make_uint2(sl[0][0], sl[0][1]);
-            } else {
-                const int q = kk / 8;
-                *(uint2*)(A + (3 * q + 0) * 8) = make_uint2(sl[2][0], sl[2][1]);
-                *(uint2*)(A + (3 * q + 1) * 8) = make_uint2(sl[1][0], sl[1][1]);
-                *(uint2*)(A + (3 * q + 2) * 8) = make_uint2(sl[0][0], sl[0][1]);
-            }
-            if (kk == 0) {
-                const float f = ldexpf(1.0f, -sh);
-                S.fx[gl * 2] = f;
-                S.fx[gl * 2 + 1] = (float)xs * f;
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int xv = (int)rintf(ldexpf(v[j][i], sh));
+            xs += xv;
+            const int lo = (int)(int8_t)(xv & 0xFF);
+            const int r1 = (xv - lo) >> 8;
+            const int mid = (int)(int8_t)(r1 & 0xFF);
+            const int hi = (r1 - mid) >> 8;
+            p0 |= (uint32_t)(lo & 0xFF) << (8 * i);
+            p1 |= (uint32_t)(mid & 0xFF) << (8 * i);
+            p2 |= (uint32_t)(hi & 0xFF) << (8 * i);
+        }
+        xs += dpp_i<DPP_XOR1>(xs);
+        xs += dpp_i<DPP_XOR2>(xs);
+        xs += dpp_i<DPP_HALF_MIRROR>(xs);
+        if constexpr (G == 64) xs += dpp_i<DPP_MIRROR>(xs);
+        const int gl = k0 / G, kk = k0 % G;
+        uint8_t* A = S.A + gl * TILE;
+        constexpr int SLOT = (FMT == FMT_Q4) ? 16 : 8;  // bytes of a K-slot row
+        const int q = kk / SLOT, j0 = kk % SLOT;
+        *(uint32_t*)(A + (3 * q + 0) * SLOT + j0) = p2;
+        *(uint32_t*)(A + (3 * q + 1) * SLOT + j0) = p1;
+        *(uint32_t*)(A + (3 * q + 2) * SLOT + j0) = p0;
+        if (kk == 0) {
+            const float f = ldexpf(1.0f, -sh);
+            S.fx[gl * 2] = f;
+            S.fx[gl * 2 + 1] = (float)xs * f;
         }
     }
     __syncthreads();
