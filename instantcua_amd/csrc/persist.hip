@@ -10,34 +10,38 @@
 //
 // Grid.  One 512-thread workgroup per CU (256).  Static work split per layer:
 //   QKV   256 row blocks of the fused q|k|v rows (Convert.swift:185-188): blocks w - 128 and w
-//         in workgroups 128..255 (workgroups 0..127 run down, just before)
+//         in workgroups 128..255
 //   attn  KV group g = w % 8, split s = w / 8: the pos + 1 cache rows of the group (rows < pos and
 //         the new row) are spread evenly over the 32 splits; the split holding row pos writes it
-//   merge splits 28..31 of group g (workgroups 224..255, no O / down work) merge the 32
-//         partials of the group, a quarter of the group's output each
+//   merge splits 28..31 of group g (workgroups 224..255, no O work) merge the 32 partials of
+//         the group, a quarter of the group's output each
 //   O     128 row blocks, workgroups 0..127
 //   GU    768 row blocks (8 gate + 8 up rows each), blocks 3w .. 3w + 2
-//   down  128 row blocks (K = 6144), workgroups 0..127
+//   down  128 row blocks split along K: workgroup w takes K half w / 128 of block w % 128
 // then lm_head over 9496 row blocks (w, w + 256, ...) with a per-workgroup argmax, and the greedy
 // commit (Shaders.swift:1501-1571), which every workgroup evaluates redundantly from the 256
 // argmax partials; workgroup 0 alone writes the control block and the token list.
 //
 // Roles inside a workgroup.  Waves 0-3 ("math") hold the weight tiles and K/V rows in registers
-// and run the matrix-core GEMV and attention arithmetic.  Waves 4-7 ("exchange") wait for the
-// inputs of each stage, stage them into LDS and slice them into matrix-core operands.  The split
-// exists because a wave's vector-memory counter retires in issue order: a poll issued behind a
-// wave's outstanding weight loads could not be seen before those loads land.  The exchange waves
-// never load weights, so they see an input as soon as it is written.
+// and run the matrix-core GEMV and the attention arithmetic (VALU-bound: spreading it over all
+// eight waves only shares the same four SIMDs).  Waves 4-7 ("exchange") wait for the inputs of
+// each stage; all eight waves stage them into LDS as matrix-core operands.  The
+// split exists because a wave's vector-memory counter retires in issue order and a CU's memory
+// pipeline is shared: a poll issued behind outstanding weight loads could not be seen before
+// those loads land.  So bulk loads are issued where no poll follows on the CU: the next layer's
+// QKV blocks while h is awaited, K/V rows after the QKV publish (workgroups 128..255), the down
+// half-block into LDS after the O publish.
 //
-// Data exchange.  Every value that crosses workgroups travels as a 64-bit packet (fp32 value,
-// 32-bit round tag) written with one device-scope store and read with device-scope loads
-// (global_store/load_dwordx2 ... sc1: coherent across the XCDs' L2s without cache flushes); the
-// exchange waves read consecutive packets in consecutive lanes and poll until each carries the
-// tag of the round they expect, so the data is its own flag.  A buffer is rewritten only after
-// every consumer of its previous round has read it: each producer first consumes outputs that,
-// through the stage chain, every such consumer produced after its read.  The packet area is
-// zeroed before each launch and tags start at 1, so a tag never matches stale data.  The one
-// value read with plain loads across workgroups is the new K/V cache row: it is stored
+// Data exchange.  Every value that crosses workgroups travels in a 64-bit packet of two values
+// written with one device-scope store and read with device-scope loads (global_store/load_dwordx2
+// ... sc1: coherent across the XCDs' L2s without cache flushes).  The low word is value a rounded
+// to a 19-bit mantissa whose low 4 bits carry the tag of the round (1..15), the high word value b
+// exact.  The exchange waves read consecutive packets in consecutive lanes and poll until each
+// carries the tag of the round they expect, so the data is its own flag.  A buffer is rewritten
+// only after every consumer of its previous round has read it: each producer first consumes
+// outputs that, through the stage chain, every such consumer produced after its read.  The packet
+// area is zeroed before each launch and tags start at 1, so a tag never matches stale data.  The
+// one value read with plain loads across workgroups is the new K/V cache row: it is stored
 // device-scope, acknowledged before the writer's next packet, first read a step later, and rows
 // >= pos are never loaded early (a line cached early would go stale).  Every poll is bounded: a
 // timeout raises an error flag that makes all workgroups leave, and the host reports it.
