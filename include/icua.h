@@ -160,6 +160,21 @@ int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb
  * the row-major .icua layout (tiled = 0) or the repacked layout (tiled = 1). */
 int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out, int tiled);
 
+/* ---- converter quantisers (Convert.swift:214-320, Converter.quantizeQ8 / quantizeQ4Raw) ---- */
+/* Quantises the row-major fp32 matrix d_m [rows][cols] into the .icua layout, bit-exact with the
+ * reference's float32 arithmetic:
+ *   ICUA_FMT_Q8: symmetric, group 32 along K: d_codes int8 [rows][cols], d_sb fp16 scales
+ *                [rows][cols/32] (quantizeQ8, Convert.swift:215-241).
+ *   ICUA_FMT_Q4: affine, group 64: d_codes packed [rows][cols/2] (q[2j] | q[2j+1] << 4), d_sb fp16
+ *                (scale, bias) [rows][cols/64][2], each pair from the 5 x 5 clip grid with a
+ *                least-squares refit (quantizeQ4Raw / quantGroup, Convert.swift:243-320).
+ * cols must be a multiple of the group size.  All pointers are device buffers. */
+int icua_quantize(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb);
+/* Times `iters` back-to-back icua_quantize launches on the same buffers; *avg_us per call (HIP
+ * events on the launch stream). */
+int icua_quantize_bench(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb, int iters,
+                        double* avg_us);
+
 #ifdef __cplusplus
 }
 #endif

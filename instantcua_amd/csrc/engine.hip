@@ -1089,6 +1089,53 @@ int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb
     return 0;
 }
 
+static int quant_check(int fmt, const float* d_m, int rows, int cols, const void* d_codes, const void* d_sb) {
+    if (fmt != FMT_Q4 && fmt != FMT_Q8) return fail("quantize: format must be q8 (1) or q4 (2)");
+    const int gsz = fmt == FMT_Q4 ? 64 : 32;
+    if (rows <= 0 || cols <= 0 || cols % gsz) return fail("quantize: cols must be a positive multiple of " +
+                                                         std::to_string(gsz));
+    if ((int64_t)rows * cols > ((int64_t)1 << 40)) return fail("quantize: matrix too large");
+    if (!d_m || !d_codes || !d_sb) return fail("quantize: null buffer");
+    return 0;
+}
+
+int icua_quantize(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb) {
+    if (quant_check(fmt, d_m, rows, cols, d_codes, d_sb)) return -1;
+    uint8_t* none = nullptr;
+    if (fmt == FMT_Q4) HIPCK(hipMalloc(&none, (size_t)rows * (cols / 64)));
+    const hipError_t e = launch_quant(fmt, d_m, rows, cols, d_codes, d_sb, none, nullptr);
+    const hipError_t e2 = hipDeviceSynchronize();
+    if (none) (void)hipFree(none);
+    HIPCK(e);
+    HIPCK(e2);
+    return 0;
+}
+
+int icua_quantize_bench(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb, int iters,
+                        double* avg_us) {
+    if (quant_check(fmt, d_m, rows, cols, d_codes, d_sb)) return -1;
+    if (iters < 1 || !avg_us) return fail("bad arguments");
+    uint8_t* none = nullptr;
+    if (fmt == FMT_Q4) HIPCK(hipMalloc(&none, (size_t)rows * (cols / 64)));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = launch_quant(fmt, d_m, rows, cols, d_codes, d_sb, none, nullptr);  // warm-up
+    if (e == hipSuccess) e = hipEventRecord(e0, nullptr);
+    for (int i = 0; i < iters && e == hipSuccess; ++i) e = launch_quant(fmt, d_m, rows, cols, d_codes, d_sb, none, nullptr);
+    if (e == hipSuccess) e = hipEventRecord(e1, nullptr);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipDeviceSynchronize();
+    if (none) (void)hipFree(none);
+    HIPCK(e);
+    *avg_us = (double)ms * 1000.0 / iters;
+    return 0;
+}
+
 int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0, int rows, float* d_out, int tiled) {
     if (fmt < 0 || fmt > 2) return fail("bad format");
     if (K <= 0 || K % 64 || rows < 0 || row0 < 0) return fail("bad shape");

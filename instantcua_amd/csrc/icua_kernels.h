@@ -141,4 +141,9 @@ hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t* w, const uint8_t* sb, int K, int row0, int rows, float* out,
                           int tiled, hipStream_t s);
 
+// Converter quantisers (Convert.swift:214-320) of a row-major fp32 matrix [rows][cols]: q8 codes
+// + fp16 scales, or q4 packed codes + fp16 (scale, bias); `none` is a scratch byte per q4 group.
+hipError_t launch_quant(int fmt, const float* m, int64_t rows, int64_t cols, void* codes, void* sb, uint8_t* none,
+                        hipStream_t s);
+
 }  // namespace icua

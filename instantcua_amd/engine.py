@@ -36,6 +36,7 @@ EXPORTS = [
     "icua_read_state", "icua_read_tokens", "icua_logits", "icua_timing", "icua_layer_step",
     "icua_read_kv", "icua_write_kv", "icua_read_buffer", "icua_dev_alloc", "icua_dev_free", "icua_memcpy_h2d",
     "icua_memcpy_d2h", "icua_device_sync", "icua_repack", "icua_gemv", "icua_gemv_bench", "icua_dequant",
+    "icua_quantize", "icua_quantize_bench",
 ]
 
 
@@ -102,6 +103,8 @@ def lib() -> C.CDLL:
         L.icua_gemv_bench.argtypes = [i32, vp, vp, i32, i32, i32, vp, vp, i32, C.POINTER(C.c_double)]
         L.icua_dequant.argtypes = [i32, vp, vp, i32, i32, i32, vp, i32]
         L.icua_repack.argtypes = [i32, vp, vp, i32, i32, vp, vp]
+        L.icua_quantize.argtypes = [i32, vp, i32, i32, vp, vp]
+        L.icua_quantize_bench.argtypes = [i32, vp, i32, i32, vp, vp, i32, C.POINTER(C.c_double)]
         _lib = L
     return _lib
 

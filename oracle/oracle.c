@@ -553,3 +553,120 @@ int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, in
     free(logits);
     return rc;
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* Quantisers of the converter (Convert.swift:214-320), float32 arithmetic in the reference's
+ * order: sums run over i = 0..n-1, no contraction (the Makefile builds with
+ * -ffp-contract=off), division correctly rounded, `.rounded()` = roundf (half away from zero),
+ * Float16(x) = round to nearest even (or_f2h). */
+
+/* Swift's min / max on Float: min(x, y) = y < x ? y : x, max(x, y) = y >= x ? y : x. */
+static float sw_min(float x, float y) { return y < x ? y : x; }
+static float sw_max(float x, float y) { return y >= x ? y : x; }
+
+void or_quant_q8(const float* m, int rows, int cols, int8_t* codes, uint16_t* scales) {
+    const int groups = cols / 32;
+#pragma omp parallel for schedule(static)
+    for (int ci = 0; ci < (rows + 63) / 64; ++ci) {
+        for (int r = ci * 64; r < rows && r < (ci + 1) * 64; ++r) {
+            for (int g = 0; g < groups; ++g) {
+                const float* src = m + (size_t)r * cols + (size_t)g * 32;
+                float amax = 0.0f;
+                for (int i = 0; i < 32; ++i) amax = sw_max(amax, fabsf(src[i]));
+                uint16_t sh = or_f2h(amax / 127.0f);
+                if (or_h2f(sh) * 127.0f < amax) sh = (uint16_t)(sh + 1u); /* Convert.swift:229 */
+                const float s = or_h2f(sh);
+                scales[(size_t)r * groups + g] = sh;
+                const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+                for (int i = 0; i < 32; ++i)
+                    codes[(size_t)r * cols + (size_t)g * 32 + i] =
+                        (int8_t)sw_max(-127.0f, sw_min(127.0f, roundf(src[i] * inv)));
+            }
+        }
+    }
+}
+
+/* quantGroup (Convert.swift:273-319).  q_out keeps its contents when no candidate is accepted
+ * (every candidate's fp16 scale rounds to 0): the caller's array then still holds the codes of
+ * the chunk's previous group, as in the reference. */
+static void quant_group_q4(const float* w, uint8_t* q_out, uint16_t* s_out, uint16_t* b_out) {
+    static const float clips[5] = {0.0f, 0.03f, 0.06f, 0.1f, 0.15f};
+    float mn = w[0], mx = w[0];
+    for (int i = 1; i < 64; ++i) {
+        mn = sw_min(mn, w[i]);
+        mx = sw_max(mx, w[i]);
+    }
+    if (mx - mn < 1e-12f) {
+        memset(q_out, 0, 64);
+        *s_out = 0;
+        *b_out = or_f2h(mn);
+        return;
+    }
+    float best_err = INFINITY;
+    uint16_t best_s = 0, best_b = 0;
+    uint8_t q[64];
+    const float range = mx - mn;
+    for (int ai = 0; ai < 5; ++ai) {
+        for (int cj = 0; cj < 5; ++cj) {
+            const float lo = mn + clips[ai] * range, hi = mx - clips[cj] * range;
+            if (hi <= lo) continue;
+            float s = (hi - lo) / 15.0f, b = lo;
+            /* Iteration 0 of the reference's two: the codes and the least-squares refit.  Its
+             * iteration 1 only recomputes codes that the error pass below overwrites. */
+            {
+                const float inv = 1.0f / s;
+                float sq = 0.0f, sw = 0.0f, sqq = 0.0f, sqw = 0.0f;
+                for (int i = 0; i < 64; ++i) {
+                    const float v = sw_min(15.0f, sw_max(0.0f, roundf((w[i] - b) * inv)));
+                    sq += v;
+                    sw += w[i];
+                    sqq += v * v;
+                    sqw += v * w[i];
+                }
+                const float den = 64.0f * sqq - sq * sq;
+                if (den > 0.0f) {
+                    const float s2 = (64.0f * sqw - sq * sw) / den;
+                    if (s2 > 0.0f) {
+                        s = s2;
+                        b = (sw - s2 * sq) / 64.0f;
+                    }
+                }
+            }
+            const uint16_t sh = or_f2h(s), bh = or_f2h(b);
+            const float sf = or_h2f(sh), bf = or_h2f(bh);
+            if (sf <= 0.0f) continue;
+            const float inv = 1.0f / sf;
+            float err = 0.0f;
+            for (int i = 0; i < 64; ++i) {
+                const float v = sw_min(15.0f, sw_max(0.0f, roundf((w[i] - bf) * inv)));
+                q[i] = (uint8_t)v;
+                const float d = sf * v + bf - w[i];
+                err += d * d;
+            }
+            if (err < best_err) {
+                best_err = err;
+                best_s = sh;
+                best_b = bh;
+                memcpy(q_out, q, 64);
+            }
+        }
+    }
+    *s_out = best_s;
+    *b_out = best_b;
+}
+
+void or_quant_q4(const float* m, int rows, int cols, uint8_t* packed, uint16_t* sb) {
+    const int groups = cols / 64;
+#pragma omp parallel for schedule(static)
+    for (int ci = 0; ci < (rows + 63) / 64; ++ci) {
+        uint8_t q[64];
+        memset(q, 0, 64); /* one code array per 64-row chunk (Convert.swift:251) */
+        for (int r = ci * 64; r < rows && r < (ci + 1) * 64; ++r) {
+            for (int g = 0; g < groups; ++g) {
+                const size_t base = (size_t)r * cols + (size_t)g * 64;
+                quant_group_q4(m + base, q, &sb[((size_t)r * groups + g) * 2], &sb[((size_t)r * groups + g) * 2 + 1]);
+                for (int j = 0; j < 32; ++j) packed[base / 2 + j] = (uint8_t)(q[2 * j] | (q[2 * j + 1] << 4));
+            }
+        }
+    }
+}

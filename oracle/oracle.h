@@ -108,6 +108,17 @@ int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, in
                 int n_vis, const float* const* deepstack, int steps, int32_t* out_tokens,
                 float* margins, float* out_first_logits);
 
+/* Group-wise quantisers of the .icua converter, restated in float32 with the reference's
+ * operation order (Sources/Engine/Convert.swift:214-320; built with -ffp-contract=off).
+ * m is row-major [rows][cols].
+ *  or_quant_q8: symmetric, group 32 (Convert.swift:215-241): codes int8 [rows][cols], scales
+ *      fp16 [rows][cols / 32].
+ *  or_quant_q4: affine, group 64 (Convert.swift:243-320): packed codes [rows][cols / 2],
+ *      (scale, bias) fp16 [rows][cols / 64][2].
+ * Both process 64-row chunks independently (the reference's concurrentPerform iterations). */
+void or_quant_q8(const float* m, int rows, int cols, int8_t* codes, uint16_t* scales);
+void or_quant_q4(const float* m, int rows, int cols, uint8_t* packed, uint16_t* sb);
+
 /* Threads used by the OpenMP regions (0 = library default). */
 void or_set_threads(int n);
 int or_get_threads(void);

@@ -63,6 +63,8 @@ def lib():
         L.or_argmax.argtypes = [_f32p, C.c_int]
         L.or_generate.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
                                   _i32p, C.c_void_p, C.c_void_p]
+        L.or_quant_q8.argtypes = [_f32p, C.c_int, C.c_int, C.c_void_p, _u16p]
+        L.or_quant_q4.argtypes = [_f32p, C.c_int, C.c_int, _u8p, _u16p]
         L.or_set_threads.argtypes = [C.c_int]
         L.or_get_threads.restype = C.c_int
         _lib = L
@@ -103,6 +105,27 @@ def gemv(fmt: int, codes: np.ndarray, sb: np.ndarray, N: int, K: int, x: np.ndar
     sb = np.ascontiguousarray(sb, dtype=np.uint8)
     lib().or_gemv(fmt, np.ascontiguousarray(codes, dtype=np.uint8), _ptr(sb), N, K, x, n, y)
     return y
+
+
+def quant_q8(m: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """quantizeQ8 (Convert.swift:215-241): int8 codes [rows][cols], fp16 bits [rows][cols/32]."""
+    m = np.ascontiguousarray(m, dtype=np.float32)
+    rows, cols = m.shape
+    codes = np.empty((rows, cols), dtype=np.int8)
+    scales = np.empty((rows, cols // 32), dtype=np.uint16)
+    lib().or_quant_q8(m, rows, cols, _ptr(codes), scales)
+    return codes, scales
+
+
+def quant_q4(m: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """quantizeQ4Raw (Convert.swift:243-320): packed codes [rows][cols/2], (scale, bias) fp16
+    bits [rows][cols/64][2]."""
+    m = np.ascontiguousarray(m, dtype=np.float32)
+    rows, cols = m.shape
+    packed = np.empty((rows, cols // 2), dtype=np.uint8)
+    sb = np.empty((rows, cols // 64, 2), dtype=np.uint16)
+    lib().or_quant_q4(m, rows, cols, packed, sb)
+    return packed, sb
 
 
 def mrope_table(maxctx: int, vis_offset: int, llm_h: int, llm_w: int) -> np.ndarray:
