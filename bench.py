@@ -27,7 +27,7 @@ sys.path.insert(0, ROOT)
 
 from instantcua_amd import engine as eng  # noqa: E402
 from instantcua_amd import synth  # noqa: E402
-from instantcua_amd.modelfile import Dims, WeightFormat  # noqa: E402
+from instantcua_amd.modelfile import Dims, WeightFormat, matrix_bytes  # noqa: E402
 
 HBM_PEAK = 8.0e12  # B/s, MI355X
 LAYERS = 28
@@ -177,6 +177,81 @@ def run_gemv(iters):
     }
 
 
+# Converter workload: the language backbone's matrices quantised from fp32 resident in HBM
+# (name, rows, cols, matrices per model).
+QUANT_SHAPES = [("QKV", Dims.qkv_rows, Dims.hidden, LAYERS), ("O", Dims.hidden, Dims.hidden, LAYERS),
+                ("gate/up", Dims.gu_rows, Dims.hidden, LAYERS), ("down", Dims.hidden, Dims.ff, LAYERS),
+                ("embed", Dims.vocab, Dims.hidden, 1)]
+# Float32 operations of the q4 search per 64-group (Convert.swift:273-319): 25 clip candidates x
+# (64 elements x (10 in the code/refit pass + 10 in the error pass) + ~30 scalar), plus the
+# group's min, max and sum.
+Q4_OPS_PER_GROUP = 25 * (64 * 20 + 30) + 3 * 64
+VALU_F32_PEAK = 256 * 64 * 2.4e9  # non-packed fp32 lane operations/s, MI355X (packed forms unused)
+Q8_BYTES_PER_ELEM = 4 + 1 + 2 / 32  # fp32 in, int8 code and fp16 scale per 32 out
+
+
+def run_quant(iters):
+    """Times icua_quantize (q4 and q8) on each backbone shape; totals are per whole backbone."""
+    rows, tot = [], {"q4": 0.0, "q8": 0.0}
+    params = sum(r * c * n for _, r, c, n in QUANT_SHAPES)
+    for name, R, C, count in QUANT_SHAPES:
+        m = (np.random.default_rng(R + C).standard_normal((R, C), dtype=np.float32) * 0.02)
+        dm = eng.DeviceBuffer.from_array(m)
+        del m
+        for fmt, key in ((WeightFormat.Q4, "q4"), (WeightFormat.Q8, "q8")):
+            cb, sbb = matrix_bytes(fmt, R, C)
+            dc, ds = eng.DeviceBuffer(cb), eng.DeviceBuffer(sbb)
+            us = eng.C.c_double()
+            n_it = max(2, iters if R * C < 64 << 20 else iters // 4)
+            eng._check(eng.lib().icua_quantize_bench(fmt, dm.ptr, R, C, dc.ptr, ds.ptr, n_it, eng.C.byref(us)))
+            us = us.value
+            dc.free()
+            ds.free()
+            tot[key] += us * count
+            if key == "q4":
+                ops = R * C // 64 * Q4_OPS_PER_GROUP
+                rate = {"Gops_s": round(ops / us / 1e3, 1), "frac_valu": round(ops / (us * 1e-6) / VALU_F32_PEAK, 4)}
+            else:
+                b = R * C * Q8_BYTES_PER_ELEM
+                rate = {"GB_s": round(b / us / 1e3, 1), "frac_hbm": round(b / (us * 1e-6) / HBM_PEAK, 4)}
+            rows.append({"matrix": name, "rows": R, "cols": C, "fmt": key, "us": round(us, 2), **rate})
+            log(f"quantise {key} {name} {R}x{C}: {us:.1f} us {rate}")
+        dm.free()
+    # The oracle (C, all host threads) on the gate/up matrix.
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    oracle.build()
+    m = (np.random.default_rng(1).standard_normal((Dims.gu_rows, Dims.hidden), dtype=np.float32) * 0.02)
+    t0 = time.perf_counter()
+    oracle.quant_q4(m)
+    dt = time.perf_counter() - t0
+    gu = next(r for r in rows if r["matrix"] == "gate/up" and r["fmt"] == "q4")
+    q4_ops = sum(r * c // 64 * Q4_OPS_PER_GROUP * n for _, r, c, n in QUANT_SHAPES)
+    value = params / (tot["q4"] * 1e-6)
+    log(f"whole backbone: q4 {tot['q4'] / 1e3:.1f} ms, q8 {tot['q8'] / 1e3:.1f} ms; oracle q4 gate/up {dt:.2f} s")
+    return {
+        "metric": "q4 converter quantisation, weights/s (Qwen3-VL-2B language backbone)",
+        "value": round(value), "unit": "weights/s", "n_gpus": 1, "steps": iters, "warmup": 1,
+        "ms_per_step": round(tot["q4"] / 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (the reference's float32 arithmetic, bit-exact)",
+        "data": "synthetic (seeded fp32 N(0, 0.02) matrices of the backbone shapes, resident in HBM)",
+        "config": {"workload": "quantise the 28-layer backbone (QKV, O, gate/up, down per layer, the embedding) "
+                               "from fp32 to q4 g64 and to q8 g32", "params": params,
+                   "q8_ms": round(tot["q8"] / 1e3, 3)},
+        "roofline": {"bound": "valu", "achieved": round(q4_ops / (tot["q4"] * 1e-6) / 1e12, 2),
+                     "peak": VALU_F32_PEAK / 1e12, "unit": "Tops/s",
+                     "frac": round(q4_ops / (tot["q4"] * 1e-6) / VALU_F32_PEAK, 4), "traffic": None,
+                     "kernel": "quant_q4_kernel (one lane per 64-group, 25 clip candidates)",
+                     "ops_per_group": Q4_OPS_PER_GROUP},
+        "cpu_baseline": {"value": round(Dims.gu_rows * Dims.hidden / dt), "unit": "weights/s",
+                         "cores": oracle.get_threads(), "kind": "port",
+                         "sample": "q4 quantisation of one 12288 x 2048 gate/up matrix by the oracle (C, float32)",
+                         "gpu_same_matrix_us": gu["us"]},
+        "shapes": rows,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -186,9 +261,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true",
                     help="profiling runs: start decoding at the same 4096-slot context without the prefill "
                          "(cache rows stay zero; same bytes per step), so a profile holds only the decode launch")
-    ap.add_argument("--workload", choices=["decode", "verify", "gemv"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "verify", "gemv", "quant"], default="decode",
                     help="decode: the 4k-context q4 decode (default); verify: 8-draft q8 verify over 8192 rows; "
-                         "gemv: isolated q4 GEMV sweep")
+                         "gemv: isolated q4 GEMV sweep; quant: converter quantisers over the backbone shapes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU decode is a design note only",
@@ -199,6 +274,9 @@ def main():
         return
     if args.workload == "gemv":
         print(json.dumps(run_gemv(200)))
+        return
+    if args.workload == "quant":
+        print(json.dumps(run_quant(20)))
         return
 
     K, W = args.steps, args.warmup

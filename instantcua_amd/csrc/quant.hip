@@ -3,8 +3,8 @@
 // own (no contraction), sums run in index order, division is correctly rounded, `.rounded()` is
 // roundf (half away from zero) and Float16(x) rounds to nearest even (v_cvt_f16_f32).
 //
-// q8 (quantizeQ8, 215-241): one lane per element; the 32 lanes of a group find its maximum with
-// shuffles (max is exact in any order), derive the scale and write their own code.
+// q8 (quantizeQ8, 215-241): four elements per lane; the 8 lanes of a group find its maximum with
+// shuffles (max is exact in any order), derive the scale and write their own codes.
 // q4 (quantizeQ4Raw / quantGroup, 243-320): one lane per 64-group, the group in registers.  The
 // lane runs the reference's 5 x 5 clip grid: codes and one least-squares refit of (s, b), fp16
 // rounding of both, the squared error of the rounded pair; the first candidate of least error
@@ -27,19 +27,25 @@ constexpr int QT = 256;  // threads per workgroup
 __global__ __launch_bounds__(QT) void quant_q8_kernel(const float* __restrict__ m, int64_t n, int8_t* __restrict__ codes,
                                                       uint16_t* __restrict__ scales) {
 #pragma clang fp contract(off)
-    const int64_t i = (int64_t)blockIdx.x * QT + threadIdx.x;  // element (row-major), group i / 32
-    const bool in = i < n;                                      // n % 32 == 0: groups are whole
-    const float w = in ? m[i] : 0.0f;
-    float amax = fabsf(w);
+    // Four consecutive elements per lane (one 16-byte load); group i / 32 = 8 lanes.
+    const int64_t i4 = ((int64_t)blockIdx.x * QT + threadIdx.x) * 4;
+    const bool in = i4 < n;  // n % 32 == 0: groups are whole
+    const float4 w = in ? *(const float4*)(m + i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float amax = sw_max(sw_max(fabsf(w.x), fabsf(w.y)), sw_max(fabsf(w.z), fabsf(w.w)));
 #pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = sw_max(amax, __shfl_xor(amax, o));
+    for (int o = 1; o < 8; o <<= 1) amax = sw_max(amax, __shfl_xor(amax, o));
     uint16_t sh = f2h(amax / 127.0f);
     if (h2f(sh) * 127.0f < amax) sh = (uint16_t)(sh + 1u);  // Convert.swift:229
     const float s = h2f(sh);
     const float inv = s > 0.0f ? 1.0f / s : 0.0f;
     if (in) {
-        codes[i] = (int8_t)sw_max(-127.0f, sw_min(127.0f, roundf(w * inv)));
-        if ((i & 31) == 0) scales[i >> 5] = sh;
+        const float v[4] = {w.x, w.y, w.z, w.w};
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            word |= (uint32_t)(uint8_t)(int8_t)sw_max(-127.0f, sw_min(127.0f, roundf(v[k] * inv))) << (8 * k);
+        *(uint32_t*)(codes + i4) = word;
+        if ((i4 & 31) == 0) scales[i4 >> 5] = sh;
     }
 }
 
@@ -172,8 +178,8 @@ hipError_t launch_quant(int fmt, const float* m, int64_t rows, int64_t cols, voi
                         hipStream_t s) {
     const int64_t n = rows * cols;
     if (fmt == FMT_Q8) {
-        hipLaunchKernelGGL(quant_q8_kernel, dim3((unsigned)((n + QT - 1) / QT)), dim3(QT), 0, s, m, n, (int8_t*)codes,
-                           (uint16_t*)sb);
+        hipLaunchKernelGGL(quant_q8_kernel, dim3((unsigned)((n / 4 + QT - 1) / QT)), dim3(QT), 0, s, m, n,
+                           (int8_t*)codes, (uint16_t*)sb);
         return hipGetLastError();
     }
     if (fmt != FMT_Q4) return hipErrorInvalidValue;
