@@ -554,6 +554,45 @@ int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, in
     return rc;
 }
 
+static int first_step_action(int tok) {
+    return tok == 3678 || tok == 7241 || tok == 12476 || tok == 10855 || tok == 11862 || tok == 1339 || tok == 1472 ||
+           tok == 24769;
+}
+
+int or_generate_commit(or_model* m, const int32_t* toks, int n, const float* pooler, int vis_offset, int n_vis,
+                       const float* const* deepstack, int max_steps, int eos0, int eos1, int grammar,
+                       int32_t* out_tokens) {
+    float* logits = (float*)malloc(sizeof(float) * OR_VOCAB);
+    int32_t pass[2];
+    const int32_t* pt = toks;
+    int pn = n, pos = 0, step = 0;
+    for (;;) {
+        if (step >= max_steps) break;
+        if (or_pass(m, pt, pn, pos, pooler, vis_offset, n_vis, deepstack, 1, logits)) {
+            free(logits);
+            return -1;
+        }
+        pooler = NULL; /* the visual rows belong to the prompt pass only */
+        deepstack = NULL;
+        vis_offset = -1;
+        n_vis = 0;
+        const int tok = or_argmax(logits, OR_VOCAB);
+        pos += pn;
+        out_tokens[step++] = tok;
+        if (tok == eos0 || tok == eos1 || (grammar && tok == 8) || step >= max_steps) break;
+        pass[0] = tok;
+        pt = pass;
+        pn = 1;
+        if (grammar && ((step == 1 && first_step_action(tok)) || tok == 11)) {
+            pass[1] = tok == 11 ? 220 : 7;
+            out_tokens[step++] = pass[1];
+            pn = 2;
+        }
+    }
+    free(logits);
+    return step;
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* Quantisers of the converter (Convert.swift:214-320), float32 arithmetic in the reference's
  * order: sums run over i = 0..n-1, no contraction (the Makefile builds with

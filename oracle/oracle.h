@@ -108,6 +108,20 @@ int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, in
                 int n_vis, const float* const* deepstack, int steps, int32_t* out_tokens,
                 float* margins, float* out_first_logits);
 
+/* The reference's token loop (Engine.swift:741-817) with its commit rules (Shaders.swift:
+ * 1531-1561): prefill `toks` (n) at slot 0 with the visual inputs as in or_pass, then passes
+ * until a stop.  Each pass commits the argmax of its last row (ties to the lowest id) as
+ * out_tokens[step++] and stops on eos0 / eos1 / max_steps, and on token 8 (")") when `grammar`
+ * is set.  With `grammar`, a token 11, or one of {3678, 7241, 12476, 10855, 11862, 1339, 1472,
+ * 24769} at step 1, is followed by a forced token (220 after 11, else 7) written as the next
+ * out_tokens entry, and the next pass carries both tokens.  A pass that would start with
+ * step >= max_steps (a forced token took the last slot) ends the loop: the reference commits one
+ * more token there, past its max_steps-entry buffer.  Returns the number of tokens written
+ * (out_tokens holds max_steps), or -1 on error. */
+int or_generate_commit(or_model* m, const int32_t* toks, int n, const float* pooler, int vis_offset, int n_vis,
+                       const float* const* deepstack, int max_steps, int eos0, int eos1, int grammar,
+                       int32_t* out_tokens);
+
 /* Group-wise quantisers of the .icua converter, restated in float32 with the reference's
  * operation order (Sources/Engine/Convert.swift:214-320; built with -ffp-contract=off).
  * m is row-major [rows][cols].

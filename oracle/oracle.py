@@ -63,6 +63,8 @@ def lib():
         L.or_argmax.argtypes = [_f32p, C.c_int]
         L.or_generate.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
                                   _i32p, C.c_void_p, C.c_void_p]
+        L.or_generate_commit.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                         C.c_int, C.c_int, C.c_int, C.c_int, _i32p]
         L.or_quant_q8.argtypes = [_f32p, C.c_int, C.c_int, C.c_void_p, _u16p]
         L.or_quant_q4.argtypes = [_f32p, C.c_int, C.c_int, _u8p, _u16p]
         L.or_set_threads.argtypes = [C.c_int]
@@ -217,6 +219,19 @@ class OracleModel:
         if rc:
             raise RuntimeError("oracle: " + lib().or_last_error().decode())
         return out[:logits_rows]
+
+    def generate_commit(self, toks, max_steps: int, eos=(-1, -1), grammar: bool = False, pooler=None,
+                        vis_offset: int = -1, deepstack=None) -> np.ndarray:
+        """The reference's token loop with its commit rules (or_generate_commit)."""
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        pool, keep, ds_ptr = self._visual(pooler, deepstack)
+        n_vis = 0 if pool is None else pool.shape[0]
+        out = np.zeros(max_steps, dtype=np.int32)
+        n = lib().or_generate_commit(self.h, toks, toks.size, _ptr(pool), vis_offset, n_vis, ds_ptr, max_steps,
+                                     int(eos[0]), int(eos[1]), int(grammar), out)
+        if n < 0:
+            raise RuntimeError("oracle: " + lib().or_last_error().decode())
+        return out[:n]
 
     def generate(self, toks, steps: int, pooler=None, vis_offset: int = -1, deepstack=None):
         """Greedy tokens, top-2 margins and first logits (prefill at slot 0, no EOS stop)."""

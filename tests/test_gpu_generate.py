@@ -1,0 +1,139 @@
+"""GPU parity of the generate API's host semantics (Engine.swift:696-827): the commit rules with
+grammar pairs and the ")" stop (Shaders.swift:1531-1561), the system-prompt KV prefix cache
+(Engine.swift:719-735) and the timing record, through the C ABI."""
+import numpy as np
+import pytest
+
+from conftest import compare_greedy
+from instantcua_amd import synth
+from instantcua_amd.engine import Engine
+from instantcua_amd.modelfile import Dims, TensorID, WeightFormat
+
+pytestmark = pytest.mark.gpu
+
+
+def scale_embedding_rows(img: np.ndarray, scales: dict) -> np.ndarray:
+    """Copy of a q4 image whose tied-embedding rows `tok` are multiplied by `c` (their fp16
+    (scale, bias) words), so that those tokens win the argmax often."""
+    img = img.copy()
+    table = np.frombuffer(img[16:16 + 16 * TensorID.count].tobytes(), dtype="<u8").reshape(-1, 2)
+    off = int(table[TensorID.embed_sb, 0])
+    n = Dims.vocab * (Dims.hidden // 64) * 4
+    sb = img[off:off + n].view(np.float16).reshape(Dims.vocab, Dims.hidden // 64, 2)
+    for tok, c in scales.items():
+        sb[tok] = (sb[tok].astype(np.float32) * c).astype(np.float16)
+    return img
+
+
+@pytest.fixture(scope="module")
+def grammar_base():
+    return synth.build_model_image(WeightFormat.Q4, n_layers=2, tag="q4-grammar")
+
+
+# (row scales, prompt seed, the rule the sequence must show)
+GRAMMAR_CASES = [
+    ({11: 8, 3678: 16, 8: 3}, 5, "step-1 action then 11"),
+    ({11: 10, 3678: 10, 8: 4}, 2, "stop on )"),
+    ({11: 8, 3678: 8, 8: 3}, 3, "11 pairs"),
+]
+
+
+@pytest.mark.parametrize("scales,seed,rule", GRAMMAR_CASES)
+def test_grammar_pairs_match_the_oracle(oracle_mod, grammar_base, scales, seed, rule):
+    img = scale_embedding_rows(grammar_base, scales)
+    toks = synth.random_tokens(9, "gram", seed)
+    steps = 20
+    om = oracle_mod.OracleModel(img, 128)
+    ref = [int(t) for t in om.generate_commit(toks, steps, grammar=True)]
+    # The case exercises its rule.
+    if rule == "step-1 action then 11":
+        assert ref[:2] == [3678, 7] and any(a == 11 and b == 220 for a, b in zip(ref, ref[1:])), ref
+    elif rule == "stop on )":
+        assert ref[-1] == 8 and len(ref) < steps, ref
+    else:
+        assert sum(a == 11 and b == 220 for a, b in zip(ref, ref[1:])) >= 3, ref
+    with Engine(image=img, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.grammar_pairs = True
+        got = e.generate(toks, max_new_tokens=steps)
+        st = e.state()
+    assert got == ref, (got, ref)
+    assert st["done"] == 1 and st["step"] == len(ref)
+
+
+def test_without_grammar_pairs_no_token_is_forced(oracle_mod, grammar_base):
+    """The same model without the flag: plain greedy, ")" does not stop, nothing is forced."""
+    img = scale_embedding_rows(grammar_base, {11: 8, 3678: 16, 8: 3})
+    toks = synth.random_tokens(9, "gram", 5)
+    steps = 12
+    om = oracle_mod.OracleModel(img, 128)
+    ref = [int(t) for t in om.generate_commit(toks, steps, grammar=False)]
+    assert ref[0] == 3678 and ref[1] != 7
+    with Engine(image=img, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        got = e.generate(toks, max_new_tokens=steps)
+    assert got == ref
+
+
+@pytest.fixture(scope="module")
+def q4_small():
+    return synth.build_model_image(WeightFormat.Q4, n_layers=2, tag="q4-small")
+
+
+def test_prefix_cache_reuses_the_system_prompt(oracle_mod, q4_small):
+    """Two prompts with the same text prefix before the image: the second prefills only from the
+    first image row, and decodes the tokens of a fresh engine and of the oracle."""
+    vp1 = synth.visual_prompt(40, vis_offset=6, llm_h=4, llm_w=4, tag="pfx1")
+    vp2 = synth.visual_prompt(44, vis_offset=6, llm_h=4, llm_w=4, tag="pfx2")
+    vp2.tokens[:6] = vp1.tokens[:6]
+    steps = 10
+    ds2 = [d.astype(np.float32) for d in vp2.deepstack]
+    with Engine(image=q4_small, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.use_prefix_cache = True
+        e.prepare_mrope(vp1.vis_offset, vp1.llm_h, vp1.llm_w)
+        e.set_visual(vp1.pooler.astype(np.float32), [d.astype(np.float32) for d in vp1.deepstack])
+        first = e.generate(vp1.tokens, vis_offset=vp1.vis_offset, max_new_tokens=steps)
+        t1 = e.last_timing
+        e.prepare_mrope(vp2.vis_offset, vp2.llm_h, vp2.llm_w)
+        e.set_visual(vp2.pooler.astype(np.float32), ds2)
+        cached = e.generate(vp2.tokens, vis_offset=vp2.vis_offset, max_new_tokens=steps)
+        t2 = e.last_timing
+    assert len(first) == steps and t1["prefill_tokens"] == 40
+    assert t2["prefill_tokens"] == 44 - 6, t2
+    with Engine(image=q4_small, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.prepare_mrope(vp2.vis_offset, vp2.llm_h, vp2.llm_w)
+        e.set_visual(vp2.pooler.astype(np.float32), ds2)
+        fresh = e.generate(vp2.tokens, vis_offset=vp2.vis_offset, max_new_tokens=steps)
+        assert e.last_timing["prefill_tokens"] == 44
+    assert cached == fresh
+    om = oracle_mod.OracleModel(q4_small, 128)
+    om.prepare_mrope(vp2.vis_offset, vp2.llm_h, vp2.llm_w)
+    ref, margins, lg = om.generate(vp2.tokens, steps, pooler=vp2.pooler.astype(np.float32),
+                                   vis_offset=vp2.vis_offset, deepstack=ds2)
+    compare_greedy(np.array(cached), ref, margins, lg.max() * np.ones(steps))
+
+
+def test_prefix_cache_misses_on_a_new_prefix(q4_small):
+    vp1 = synth.visual_prompt(30, vis_offset=4, llm_h=2, llm_w=4, tag="pfx3")
+    vp2 = synth.visual_prompt(30, vis_offset=4, llm_h=2, llm_w=4, tag="pfx4")
+    with Engine(image=q4_small, max_context=64, max_steps=4) as e:
+        e.eos = (-1, -1)
+        e.use_prefix_cache = True
+        for vp, want in ((vp1, 30), (vp2, 30), (vp2, 26)):
+            e.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
+            e.set_visual(vp.pooler.astype(np.float32), None)
+            e.generate(vp.tokens, vis_offset=vp.vis_offset, max_new_tokens=4)
+            assert e.last_timing["prefill_tokens"] == want
+
+
+def test_generate_timing_record(q4_small):
+    toks = synth.random_tokens(12, "timing")
+    with Engine(image=q4_small, max_context=64, max_steps=16) as e:
+        e.eos = (-1, -1)
+        out = e.generate(toks, max_new_tokens=16)
+        t = e.last_timing
+    assert len(out) == 16 and t["generated_tokens"] == 16 and t["prefill_tokens"] == 12
+    assert t["prefill_ms"] > 0 and t["decode_ms"] > 0 and t["vision_ms"] == 0
+    assert t["total_ms"] >= t["decode_ms"]

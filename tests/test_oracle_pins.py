@@ -325,3 +325,61 @@ def test_greedy_decode_is_consistent_with_passes(oracle_mod):
         srt = np.sort(lg)
         assert abs((srt[-1] - srt[-2]) - margins[s]) < 1e-6
     assert seq == list(out)
+
+
+def _scaled_embedding(img, scales):
+    from instantcua_amd.modelfile import TensorID as T
+    img = img.copy()
+    table = np.frombuffer(img[16:16 + 16 * T.count].tobytes(), dtype="<u8").reshape(-1, 2)
+    off = int(table[T.embed_sb, 0])
+    sb = img[off:off + Dims.vocab * (Dims.hidden // 64) * 4].view(np.float16).reshape(Dims.vocab, -1, 2)
+    for tok, c in scales.items():
+        sb[tok] = (sb[tok].astype(np.float32) * c).astype(np.float16)
+    return img
+
+
+def test_commit_loop_without_grammar_is_plain_greedy(oracle_mod):
+    img = synth.build_model_image(WeightFormat.Q4, n_layers=1, tag="pin5")
+    toks = synth.random_tokens(6, "pin5")
+    a = oracle_mod.OracleModel(img, 32).generate_commit(toks, 5)
+    b, _, _ = oracle_mod.OracleModel(img, 32).generate(toks, 5)
+    assert np.array_equal(a, b)
+    # EOS ends the loop with the EOS token as its last entry.
+    c = oracle_mod.OracleModel(img, 32).generate_commit(toks, 5, eos=(int(b[2]), -1))
+    assert list(c) == list(b[:3])
+
+
+def test_commit_loop_grammar_pairs_replay_as_explicit_passes(oracle_mod):
+    """With grammar pairs the loop equals explicit passes: a forced token follows 11 (220) or a
+    step-1 action token (7), the next pass carries both tokens at consecutive slots and commits
+    its last row's argmax; ")" (8) ends the loop."""
+    img = _scaled_embedding(synth.build_model_image(WeightFormat.Q4, n_layers=1, tag="pin6"),
+                            {11: 8, 3678: 16, 8: 3})
+    actions = {3678, 7241, 12476, 10855, 11862, 1339, 1472, 24769}
+    fired = set()
+    for seed in range(6):
+        toks = synth.random_tokens(7, "pin6", seed)
+        out = [int(t) for t in oracle_mod.OracleModel(img, 64).generate_commit(toks, 14, grammar=True)]
+        om = oracle_mod.OracleModel(img, 64)
+        pos, step, seq = 0, 0, []
+        pass_toks = np.asarray(toks, np.int32)
+        while step < 14:
+            tok = int(om.run_pass(pass_toks, pos)[0].argmax())
+            pos += pass_toks.size
+            seq.append(tok)
+            step += 1
+            if tok == 8 or step >= 14:
+                break
+            if (step == 1 and tok in actions) or tok == 11:
+                forced = 220 if tok == 11 else 7
+                seq.append(forced)
+                step += 1
+                pass_toks = np.array([tok, forced], np.int32)
+            else:
+                pass_toks = np.array([tok], np.int32)
+        assert out == seq, (seed, out, seq)
+        assert 8 not in out[:-1]
+        fired |= {"pair 11" for a, b in zip(out, out[1:]) if (a, b) == (11, 220)}
+        fired |= {"stop )"} if out[-1] == 8 else set()
+        fired |= {"action"} if out[:2] == [3678, 7] else set()
+    assert fired >= {"pair 11", "stop )"}, fired  # the scaled rows make the rules fire
