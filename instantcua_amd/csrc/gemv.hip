@@ -61,46 +61,62 @@ struct TileT<FMT_F16> {
     static constexpr int TOK = 8;
 };
 
-// LDS: activation operands of one segment and pass (32 KiB int8 / 64 KiB f16), per-(token,
-// group) factors, per-token RMSNorm scales and the cross-wave partial sums.
+// LDS: activation operands of one segment for every pass of the launch (32 KiB int8 / 64 KiB
+// f16 per pass), per-(token, group) factors, per-token RMSNorm scales, the cross-wave partial
+// sums and the per-wave sums of squares.
 template <int FMT>
 struct Smem {
     static constexpr int A_BYTES = (FMT == FMT_F16) ? 65536 : 32768;
     static constexpr int NG = SEG / TileT<FMT>::G;
     static constexpr int TOK = TileT<FMT>::TOK;
-    static constexpr int bytes(int ks) { return A_BYTES + TOK * NG * 8 + MAXM * 4 + ks * 64 * 2 * 4 + 64; }
+    static constexpr int FX = TOK * NG * 2;  // floats of one pass's group factors
+    static constexpr int passes(int mt) { return (mt + TOK - 1) / TOK; }
+    static constexpr int bytes(int ks, int mt) {
+        return passes(mt) * (A_BYTES + FX * 4) + MAXM * 4 + ks * 64 * 2 * 4 + ks * MAXM * 4;
+    }
 };
 
-// Stages the activation operands of segment `seg`, tokens [t0, t0 + TOK) of the pass.
-template <int FMT, int K, int PRO>
+// Stages the activation operands of segment `seg`, tokens [t0, t0 + TOK) of the pass, with NTHR
+// threads.  Each thread's units are loaded first (one memory round trip), then sliced.
+template <int FMT, int K, int PRO, int NTHR>
 __device__ __forceinline__ void stage(const GemvArgs& a, int seg, int t0, int M, int row0, uint8_t* Alds, float* fx,
                                       const float* nscale) {
     constexpr int TOK = TileT<FMT>::TOK;
     constexpr int G = TileT<FMT>::G;
     constexpr int NG = SEG / G;
-    const int tid = threadIdx.x, nthr = blockDim.x;
+    constexpr int NU = TOK * (SEG / 8) / NTHR;  // units per thread
+    static_assert(TOK * (SEG / 8) % NTHR == 0, "whole units per thread");
+    const int tid = threadIdx.x;
     // One unit = 8 consecutive activations of one token; the units of a group sit in adjacent
     // lanes (G / 8 of them), so the group reductions are DPP steps.
-    for (int u = tid; u < TOK * (SEG / 8); u += nthr) {
+    float vv[NU][8];
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+        const int u = tid + NTHR * j;
         const int tl = u / (SEG / 8);
         const int k0 = (u % (SEG / 8)) * 8;  // within the segment
         const int t = t0 + tl;
-        float v[8];
-        if (t < M) {
-            const float* xr = a.x + (size_t)(row0 + t) * K + seg * SEG + k0;
-            const float4 p0 = ((const float4*)xr)[0], p1 = ((const float4*)xr)[1];
-            v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
-            v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-            if constexpr (PRO == PRO_NORM) {
-                const float sc = nscale[t];
-                const float* w = a.norm_w + seg * SEG + k0;
-                const float4 w0 = ((const float4*)w)[0], w1 = ((const float4*)w)[1];
-                v[0] = v[0] * sc * w0.x; v[1] = v[1] * sc * w0.y; v[2] = v[2] * sc * w0.z; v[3] = v[3] * sc * w0.w;
-                v[4] = v[4] * sc * w1.x; v[5] = v[5] * sc * w1.y; v[6] = v[6] * sc * w1.z; v[7] = v[7] * sc * w1.w;
-            }
-        } else {
+        // Rows past the pass read row M - 1 and are zeroed: the loads stay unconditional, so the
+        // compiler issues all of them before the first use.
+        const float* xr = a.x + (size_t)(row0 + min(t, M - 1)) * K + seg * SEG + k0;
+        const float4 p0 = ((const float4*)xr)[0], p1 = ((const float4*)xr)[1];
+        const bool in = t < M;
+        vv[j][0] = in ? p0.x : 0.f; vv[j][1] = in ? p0.y : 0.f; vv[j][2] = in ? p0.z : 0.f; vv[j][3] = in ? p0.w : 0.f;
+        vv[j][4] = in ? p1.x : 0.f; vv[j][5] = in ? p1.y : 0.f; vv[j][6] = in ? p1.z : 0.f; vv[j][7] = in ? p1.w : 0.f;
+    }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    for (int j = 0; j < NU; ++j) {
+        const int u = tid + NTHR * j;
+        const int tl = u / (SEG / 8);
+        const int k0 = (u % (SEG / 8)) * 8;  // within the segment
+        const int t = t0 + tl;
+        float* v = vv[j];
+        if constexpr (PRO == PRO_NORM) {
+            const float sc = nscale[min(t, M - 1)];
+            const float* w = a.norm_w + seg * SEG + k0;
+            const float4 w0 = ((const float4*)w)[0], w1 = ((const float4*)w)[1];
+            v[0] = v[0] * sc * w0.x; v[1] = v[1] * sc * w0.y; v[2] = v[2] * sc * w0.z; v[3] = v[3] * sc * w0.w;
+            v[4] = v[4] * sc * w1.x; v[5] = v[5] * sc * w1.y; v[6] = v[6] * sc * w1.z; v[7] = v[7] * sc * w1.w;
         }
         if constexpr (FMT == FMT_F16) {
             // rows m = 2 tl + {hi, lo}; chunk c = k0 / 32, K-slot q = (k0 % 32) / 8.
@@ -213,43 +229,56 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
     }
     if (M > MT) M = MT;
     const int npass = (M + T::TOK - 1) / T::TOK;
+    constexpr int NP = Smem<FMT>::passes(MT);
 
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t* Alds = smem;
-    float* fx = (float*)(smem + Smem<FMT>::A_BYTES);
-    float* nscale = fx + T::TOK * NG * 2;
+    uint8_t* Alds = smem;                                           // [NP][A_BYTES]
+    float* fx = (float*)(smem + NP * Smem<FMT>::A_BYTES);           // [NP][FX]
+    float* nscale = fx + NP * Smem<FMT>::FX;
     float* part = nscale + MAXM;      // [KS][2][64]
-    float* red = part + KS * 2 * 64;  // [16]
+    float* red = part + KS * 2 * 64;  // [KS][MAXM]
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
 
-    // RMSNorm scale of every token over the full K, once per workgroup.
+    // RMSNorm scale of every token over the full K, once per workgroup; the tokens' loads are
+    // issued together and reduced in one round.
     if constexpr (PRO == PRO_NORM) {
-        for (int t = 0; t < M; ++t) {
-            const float* xr = a.x + (size_t)(row0 + t) * K;
-            float ss = 0.f;
-            for (int k = tid; k < K; k += KS * 64) {
-                const float v = xr[k];
-                ss += v * v;
+        float ss[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) ss[t] = 0.f;
+#pragma unroll
+        for (int k = tid; k < K; k += KS * 64) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {  // unconditional loads (row clamped), zero past the pass
+                const float v = a.x[(size_t)(row0 + min(t, M - 1)) * K + k];
+                ss[t] += t < M ? v * v : 0.f;
             }
-            ss = wave_sum(ss);
-            if (lane == 0) red[wave] = ss;
-            __syncthreads();
-            if (tid == 0) {
-                float tot = 0.f;
-                for (int w = 0; w < KS; ++w) tot += red[w];
-                nscale[t] = 1.0f / sqrtf(tot / (float)K + EPS);
-            }
-            __syncthreads();
         }
-    }
-
-    const int nrb = (EPI == EPI_SWIGLU) ? (FF / 8) : (a.N / 16);
-    const bool stage_once = (NSEG == 1) && (npass == 1);
-    if (stage_once) {
-        stage<FMT, K, PRO>(a, 0, 0, M, row0, Alds, fx, nscale);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const float w = wave_sum(ss[t]);
+            if (lane == 0) red[wave * MAXM + t] = w;
+        }
+        __syncthreads();
+        if (tid < M) {
+            float tot = 0.f;
+            for (int w = 0; w < KS; ++w) tot += red[w * MAXM + tid];
+            nscale[tid] = 1.0f / sqrtf(tot / (float)K + EPS);
+        }
         __syncthreads();
     }
+
+    // Activation operands of every pass, staged once per segment (once per launch when K fits
+    // one segment).
+    auto stage_all = [&](int seg) {
+        for (int p = 0; p < npass; ++p)
+            stage<FMT, K, PRO, KS * 64>(a, seg, p * T::TOK, M, row0, Alds + p * Smem<FMT>::A_BYTES,
+                                        fx + p * Smem<FMT>::FX, nscale);
+    };
+    const int nrb = (EPI == EPI_SWIGLU) ? (FF / 8) : (a.N / 16);
+    // K in one segment: staged once, right after the first row block's weight loads are issued.
+    constexpr bool stage_once = (NSEG == 1);
+    bool staged = false;
 
     float best_v[MT];
     int best_i[MT];
@@ -283,12 +312,15 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
                 else
                     sbv[i] = make_uint2(0u, 0u);
             }
+            if (!stage_once || !staged) {
+                if (!stage_once) __syncthreads();
+                stage_all(seg);
+                __syncthreads();
+                staged = true;
+            }
             for (int p = 0; p < npass; ++p) {
-                if (!stage_once) {
-                    __syncthreads();
-                    stage<FMT, K, PRO>(a, seg, p * T::TOK, M, row0, Alds, fx, nscale);
-                    __syncthreads();
-                }
+                const uint8_t* Ap = Alds + p * Smem<FMT>::A_BYTES;
+                const float* fxp = fx + p * Smem<FMT>::FX;
                 float pacc = 0.f, pacc2 = 0.f;
 #pragma unroll
                 for (int i = 0; i < CPW; ++i) {
@@ -304,12 +336,12 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
                             B[2] = (int)(d1 & 0x0F0F0F0Fu);
                             B[3] = (int)((d1 >> 4) & 0x0F0F0F0Fu);
                             const int gl = 2 * cs + hh;
-                            const v4i A = *(const v4i*)(Alds + gl * 1024 + lane * 16);
+                            const v4i A = *(const v4i*)(Ap + gl * 1024 + lane * 16);
                             const v4i zero = {0, 0, 0, 0};
                             const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero, 0, 0, 0);
                             const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
                             const f16x2 sb2 = as_h2(hh ? sbv[i].y : sbv[i].x);
-                            const float f = fx[(lg * NG + gl) * 2], X = fx[(lg * NG + gl) * 2 + 1];
+                            const float f = fxp[(lg * NG + gl) * 2], X = fxp[(lg * NG + gl) * 2 + 1];
                             pacc = fmaf((float)sb2.x * f, S, fmaf((float)sb2.y, X, pacc));
                         }
                     } else if constexpr (FMT == FMT_Q8) {
@@ -318,17 +350,17 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
                             const long B = (long)(hh ? ((uint64_t)wv[i].w << 32 | wv[i].z)
                                                      : ((uint64_t)wv[i].y << 32 | wv[i].x));
                             const int gl = 2 * cs + hh;
-                            const long A = *(const long*)(Alds + gl * 512 + lane * 8);
+                            const long A = *(const long*)(Ap + gl * 512 + lane * 8);
                             const v4i zero = {0, 0, 0, 0};
                             const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
                             const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
                             const f16x2 s2 = as_h2(sbv[i].x);
                             const float s = hh ? (float)s2.y : (float)s2.x;
-                            pacc = fmaf(s * fx[(lg * NG + gl) * 2], S, pacc);
+                            pacc = fmaf(s * fxp[(lg * NG + gl) * 2], S, pacc);
                         }
                     } else {
                         const v8h B = __builtin_bit_cast(v8h, wv[i]);
-                        const v8h A = *(const v8h*)(Alds + cs * 1024 + lane * 16);
+                        const v8h A = *(const v8h*)(Ap + cs * 1024 + lane * 16);
                         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
                         const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, zero, 0, 0, 0);
                         pacc += C[0] + C[1];
@@ -415,7 +447,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
 
 template <int FMT, int K, int KS, int MT, int PRO, int EPI>
 static hipError_t launch_one(const GemvArgs& a, int blocks, hipStream_t s) {
-    const size_t lds = Smem<FMT>::bytes(KS);
+    const size_t lds = Smem<FMT>::bytes(KS, MT);
     auto kern = gemv_kernel<FMT, K, KS, MT, PRO, EPI>;
     static bool attr_set = false;
     if (!attr_set) {
