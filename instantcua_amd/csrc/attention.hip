@@ -211,6 +211,210 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a) {
 
 }
 
+// Multi-row passes (verify, short prompts): the same 64-slot splits on the matrix cores.  The 16
+// (token, head) rows of a KV group, column c = 2 t + head, are the B operand of
+// S^T = K . Q^T (v_mfma_f32_16x16x32_f16, q split into fp16 hi + lo parts); wave w scores the
+// split's keys 16 w .. 16 w + 15, and its accumulator (lane l: keys 4 (l / 16) + i, column l % 16)
+// is directly the B operand of O^T = V^T . P^T (v_mfma_f32_16x16x16_f16, P split hi + lo) with V
+// transposed in LDS.  The four waves' (m, l, o) are combined into the partial that the merge
+// kernel reads.  Masked keys (past the split's cache rows, or later tokens of the pass in the
+// tail split) hold finite rows, so p = 0 contributes exactly nothing.
+constexpr int VA_KROW = 136, VA_VROW = 72, VA_QROW = 136;  // padded LDS rows (halves)
+
+__global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a) {
+    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+    typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+    const State* st = a.st;
+    if (st->done) return;
+    const int M = a.m_fixed > 0 ? a.m_fixed : (st->n < MAXM ? st->n : MAXM);
+    const int pos = st->pos;
+    const int maxctx = st->maxctx;
+    const int S = (pos + ATT_CH - 1) / ATT_CH + 1;
+    const int s = blockIdx.x, g = blockIdx.y;
+    if (pos < 0 || pos + M > maxctx || S > (int)gridDim.x) return;  // host-checked; stay inside the cache
+    if (s >= S) return;
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, q4 = lane >> 4, r16 = lane & 15;
+    const bool tail = (s == S - 1);
+    const int j0 = s * ATT_CH;
+    const int P = tail ? M : min(ATT_CH, pos - j0);  // keys of this split
+
+    // K tile (keys x dims) and V^T (dims x keys); after the products, the waves' o over both.
+    constexpr int KS_BYTES = ATT_CH * VA_KROW * 2, VT_BYTES = HD * VA_VROW * 2;
+    constexpr int OW_BYTES = (ATT_THREADS / WAVE) * 16 * HD * 4;
+    static_assert(KS_BYTES + VT_BYTES >= OW_BYTES, "the waves' o fit over the K / V tiles");
+    __shared__ __align__(16) uint8_t kv_lds[KS_BYTES + VT_BYTES];
+    uint16_t* Ks = (uint16_t*)kv_lds;
+    uint16_t* Vt = (uint16_t*)(kv_lds + KS_BYTES);
+    __shared__ __align__(16) uint16_t Qh[16 * VA_QROW], Ql[16 * VA_QROW];
+    __shared__ float wm[ATT_THREADS / WAVE][16], wl[ATT_THREADS / WAVE][16];
+
+    const uint16_t* kbase = a.kc + (size_t)g * maxctx * HD;
+    const uint16_t* vbase = a.vc + (size_t)g * maxctx * HD;
+
+    // Prior keys: K row tid / 4, dims 32 (tid % 4) .. + 31; V keys 4 (tid / 32) + i (+ 32),
+    // dims 4 (tid % 32) .. + 3, transposed in registers.  Rows past the split read its first row.
+    uint4 kr[4];
+    uint2 vr[2][4];
+    if (!tail) {
+        const int kk = tid >> 2;
+        const uint4* kp = (const uint4*)(kbase + (size_t)(j0 + (kk < P ? kk : 0)) * HD + 32 * (tid & 3));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = kp[i];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int vk = 32 * h + 4 * (tid >> 5) + i;
+                vr[h][i] = *(const uint2*)(vbase + (size_t)(j0 + (vk < P ? vk : 0)) * HD + 4 * (tid & 31));
+            }
+    }
+
+    // Query columns: normalised, rotated, scaled rows split into fp16 hi + lo; zero past the pass.
+    const float qscale = 1.0f / sqrtf((float)HD);
+    for (int c = wave; c < 16; c += ATT_THREADS / WAVE) {
+        const int t = c >> 1, hh = c & 1;
+        float x0 = 0.f, x1 = 0.f;
+        if (t < M) {
+            const float* src = a.qkv + (size_t)t * QKV + (2 * g + hh) * HD;
+            x0 = src[lane];
+            x1 = src[lane + 64];
+            norm_rope_pair(x0, x1, a.q_norm, a.rope + (size_t)(pos + t) * 128, lane);
+            x0 *= qscale;
+            x1 *= qscale;
+        }
+        const f16 h0 = (f16)x0, h1 = (f16)x1;
+        Qh[c * VA_QROW + lane] = __builtin_bit_cast(uint16_t, h0);
+        Qh[c * VA_QROW + lane + 64] = __builtin_bit_cast(uint16_t, h1);
+        Ql[c * VA_QROW + lane] = __builtin_bit_cast(uint16_t, (f16)(x0 - (float)h0));
+        Ql[c * VA_QROW + lane + 64] = __builtin_bit_cast(uint16_t, (f16)(x1 - (float)h1));
+    }
+    if (tail) {
+        // The pass's new rows: per-head RMSNorm + RoPE on K, fp16 K/V into the cache and into
+        // the split's tiles; keys M .. 63 are zero rows.
+        for (int t = wave; t < ATT_CH; t += ATT_THREADS / WAVE) {
+            uint16_t hk0 = 0, hk1 = 0, hv0 = 0, hv1 = 0;
+            if (t < M) {
+                const float* ksrc = a.qkv + (size_t)t * QKV + H + g * HD;
+                const float* vsrc = a.qkv + (size_t)t * QKV + H + NKV * HD + g * HD;
+                float k0 = ksrc[lane], k1 = ksrc[lane + 64];
+                norm_rope_pair(k0, k1, a.k_norm, a.rope + (size_t)(pos + t) * 128, lane);
+                hk0 = f2h(k0);
+                hk1 = f2h(k1);
+                hv0 = f2h(vsrc[lane]);
+                hv1 = f2h(vsrc[lane + 64]);
+                uint16_t* kd = a.kc + ((size_t)g * maxctx + pos + t) * HD;
+                uint16_t* vd = a.vc + ((size_t)g * maxctx + pos + t) * HD;
+                kd[lane] = hk0;
+                kd[lane + 64] = hk1;
+                vd[lane] = hv0;
+                vd[lane + 64] = hv1;
+            }
+            Ks[t * VA_KROW + lane] = hk0;
+            Ks[t * VA_KROW + lane + 64] = hk1;
+            Vt[lane * VA_VROW + t] = hv0;
+            Vt[(lane + 64) * VA_VROW + t] = hv1;
+        }
+    } else {
+        uint4* kd = (uint4*)(Ks + (tid >> 2) * VA_KROW + 32 * (tid & 3));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kd[i] = kr[i];
+        const int d0 = 4 * (tid & 31);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k0 = 32 * h + 4 * (tid >> 5);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t e[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) e[i] = ((j < 2 ? vr[h][i].x : vr[h][i].y) >> (16 * (j & 1))) & 0xFFFFu;
+                *(uint2*)(Vt + (d0 + j) * VA_VROW + k0) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+            }
+        }
+    }
+    __syncthreads();
+
+    // Scores of this wave's 16 keys against the 16 columns.
+    const int kt = 16 * wave;
+    f32x4 Sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const v8h kf = *(const v8h*)(Ks + (kt + r16) * VA_KROW + 32 * ks + 8 * q4);
+        const v8h qh = *(const v8h*)(Qh + r16 * VA_QROW + 32 * ks + 8 * q4);
+        const v8h ql = *(const v8h*)(Ql + r16 * VA_QROW + 32 * ks + 8 * q4);
+        Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh, Sc, 0, 0, 0);
+        Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql, Sc, 0, 0, 0);
+    }
+    const int col = r16, ct = col >> 1;
+    float mb = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int key = kt + 4 * q4 + i;
+        const bool valid = key < P && ct < M && (!tail || key <= ct);
+        if (!valid) Sc[i] = -__builtin_inff();
+        mb = fmaxf(mb, Sc[i]);
+    }
+    mb = max_x4(mb);
+    float p[4], ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        p[i] = (Sc[i] == -__builtin_inff()) ? 0.f : expf(Sc[i] - mb);
+        ls += p[i];
+    }
+    ls = sum_x4(ls);
+    v4h Ph, Pl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const f16 h = (f16)p[i];
+        Ph[i] = h;
+        Pl[i] = (f16)(p[i] - (float)h);
+    }
+    f32x4 O[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        const v4h vf = *(const v4h*)(Vt + (16 * dt + r16) * VA_VROW + kt + 4 * q4);
+        O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Ph, O[dt], 0, 0, 0);
+        O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Pl, O[dt], 0, 0, 0);
+    }
+    if (q4 == 0) {
+        wm[wave][col] = mb;
+        wl[wave][col] = ls;
+    }
+    __syncthreads();  // every wave's operand reads are done: the K / V tiles become the waves' o
+    float* ow = (float*)kv_lds;  // [4 waves][16 columns][128 dims]
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+        *(float4*)(ow + ((size_t)wave * 16 + col) * HD + 16 * dt + 4 * q4) = make_float4(O[dt][0], O[dt][1], O[dt][2], O[dt][3]);
+    __syncthreads();
+    // Partial of row c = 2 t + head: thread (c = tid / 16, dims 8 (tid % 16) .. + 7).
+    {
+        const int c = tid >> 4, d0 = 8 * (tid & 15);
+        if ((c >> 1) < M) {
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int w = 0; w < ATT_THREADS / WAVE; ++w) mx = fmaxf(mx, wm[w][c]);
+            float f[ATT_THREADS / WAVE], lsum = 0.f;
+#pragma unroll
+            for (int w = 0; w < ATT_THREADS / WAVE; ++w) {
+                f[w] = (wm[w][c] == -__builtin_inff()) ? 0.f : expf(wm[w][c] - mx);
+                lsum = fmaf(wl[w][c], f[w], lsum);
+            }
+            float* dst = a.part + ((size_t)(g * gridDim.x + s) * MAXM * 2 + c) * PART_STRIDE;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                float acc = 0.f;
+#pragma unroll
+                for (int w = 0; w < ATT_THREADS / WAVE; ++w) acc = fmaf(ow[((size_t)w * 16 + c) * HD + d0 + d], f[w], acc);
+                dst[d0 + d] = acc;
+            }
+            if (d0 == 0) {
+                dst[HD] = mx;
+                dst[HD + 1] = lsum;
+            }
+        }
+    }
+}
+
 // Merge of the split partials (flash-decoding): one workgroup per (KV group, token x head row),
 // grid (NKV, 2 MT).  Runs as its own kernel: the kernel boundary publishes the partials of every
 // split, which is far cheaper on a multi-XCD device than a device-scope fence in each split
@@ -284,7 +488,7 @@ hipError_t launch_attention(const AttnArgs& a, int mt, int splits, hipStream_t s
         hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(ATT_THREADS), 0, s, a);
         hipLaunchKernelGGL(attention_merge_kernel<1>, dim3(NKV, 2), dim3(ATT_THREADS), 0, s, a, splits);
     } else {
-        hipLaunchKernelGGL(attention_kernel<MAXM>, grid, dim3(ATT_THREADS), 0, s, a);
+        hipLaunchKernelGGL(attention_mfma_kernel, grid, dim3(ATT_THREADS), 0, s, a);
         hipLaunchKernelGGL(attention_merge_kernel<MAXM>, dim3(NKV, 2 * MAXM), dim3(ATT_THREADS), 0, s, a, splits);
     }
     return hipGetLastError();
