@@ -211,14 +211,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a) {
 
 }
 
-// Multi-row passes (verify, short prompts): the same 64-slot splits on the matrix cores.  The 16
-// (token, head) rows of a KV group, column c = 2 t + head, are the B operand of
-// S^T = K . Q^T (v_mfma_f32_16x16x32_f16, q split into fp16 hi + lo parts); wave w scores the
-// split's keys 16 w .. 16 w + 15, and its accumulator (lane l: keys 4 (l / 16) + i, column l % 16)
-// is directly the B operand of O^T = V^T . P^T (v_mfma_f32_16x16x16_f16, P split hi + lo) with V
-// transposed in LDS.  The four waves' (m, l, o) are combined into the partial that the merge
-// kernel reads.  Masked keys (past the split's cache rows, or later tokens of the pass in the
-// tail split) hold finite rows, so p = 0 contributes exactly nothing.
+// Multi-row passes (verify, short prompts) on the matrix cores, in splits of up to 256 prior
+// slots (four blocks of 64, double-buffered through LDS) plus the tail split of the pass's new
+// rows.  The 16 (token, head) rows of a KV group, column c = 2 t + head, are the B operand of
+// S^T = K . Q^T (v_mfma_f32_16x16x32_f16, q split into fp16 hi + lo parts); wave w scores keys
+// 16 w .. 16 w + 15 of each block, and its accumulator (lane l: keys 4 (l / 16) + i, column
+// l % 16) is directly the B operand of O^T = V^T . P^T (v_mfma_f32_16x16x16_f16, P split hi + lo)
+// with V transposed in LDS.  Each wave keeps an online softmax over its keys; the four waves'
+// (m, l, o) are combined into the partial that the merge kernel reads.  Masked keys (past the
+// split's cache rows, or later tokens of the pass in the tail split) hold finite rows, so p = 0
+// contributes exactly nothing.
+constexpr int VA_CH = 4 * ATT_CH;                          // prior slots per split
 constexpr int VA_KROW = 136, VA_VROW = 72, VA_QROW = 136;  // padded LDS rows (halves)
 
 __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a) {
@@ -229,34 +232,34 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
     const int M = a.m_fixed > 0 ? a.m_fixed : (st->n < MAXM ? st->n : MAXM);
     const int pos = st->pos;
     const int maxctx = st->maxctx;
-    const int S = (pos + ATT_CH - 1) / ATT_CH + 1;
+    const int S = (pos + VA_CH - 1) / VA_CH + 1;
     const int s = blockIdx.x, g = blockIdx.y;
     if (pos < 0 || pos + M > maxctx || S > (int)gridDim.x) return;  // host-checked; stay inside the cache
     if (s >= S) return;
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, q4 = lane >> 4, r16 = lane & 15;
     const bool tail = (s == S - 1);
-    const int j0 = s * ATT_CH;
-    const int P = tail ? M : min(ATT_CH, pos - j0);  // keys of this split
+    const int j0 = s * VA_CH;
+    const int P = tail ? M : min(VA_CH, pos - j0);  // keys of this split
+    const int nblk = (P + ATT_CH - 1) / ATT_CH;
 
-    // K tile (keys x dims) and V^T (dims x keys); after the products, the waves' o over both.
-    constexpr int KS_BYTES = ATT_CH * VA_KROW * 2, VT_BYTES = HD * VA_VROW * 2;
+    // Two K tiles (keys x dims) and V^T tiles (dims x keys); after the products, the waves' o.
+    constexpr int KS_BYTES = ATT_CH * VA_KROW * 2, VT_BYTES = HD * VA_VROW * 2, BUF = KS_BYTES + VT_BYTES;
     constexpr int OW_BYTES = (ATT_THREADS / WAVE) * 16 * HD * 4;
-    static_assert(KS_BYTES + VT_BYTES >= OW_BYTES, "the waves' o fit over the K / V tiles");
-    __shared__ __align__(16) uint8_t kv_lds[KS_BYTES + VT_BYTES];
-    uint16_t* Ks = (uint16_t*)kv_lds;
-    uint16_t* Vt = (uint16_t*)(kv_lds + KS_BYTES);
+    static_assert(2 * BUF >= OW_BYTES, "the waves' o fit over the K / V tiles");
+    __shared__ __align__(16) uint8_t kv_lds[2 * BUF];
     __shared__ __align__(16) uint16_t Qh[16 * VA_QROW], Ql[16 * VA_QROW];
     __shared__ float wm[ATT_THREADS / WAVE][16], wl[ATT_THREADS / WAVE][16];
 
     const uint16_t* kbase = a.kc + (size_t)g * maxctx * HD;
     const uint16_t* vbase = a.vc + (size_t)g * maxctx * HD;
 
-    // Prior keys: K row tid / 4, dims 32 (tid % 4) .. + 31; V keys 4 (tid / 32) + i (+ 32),
-    // dims 4 (tid % 32) .. + 3, transposed in registers.  Rows past the split read its first row.
+    // Prior keys of block b: K row tid / 4, dims 32 (tid % 4) .. + 31; V keys 4 (tid / 32) + i
+    // (+ 32), dims 4 (tid % 32) .. + 3, transposed in registers.  Rows past the split read its
+    // first row.
     uint4 kr[4];
     uint2 vr[2][4];
-    if (!tail) {
-        const int kk = tid >> 2;
+    auto gload = [&](int b) {
+        const int kk = 64 * b + (tid >> 2);
         const uint4* kp = (const uint4*)(kbase + (size_t)(j0 + (kk < P ? kk : 0)) * HD + 32 * (tid & 3));
 #pragma unroll
         for (int i = 0; i < 4; ++i) kr[i] = kp[i];
@@ -264,10 +267,30 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int vk = 32 * h + 4 * (tid >> 5) + i;
+                const int vk = 64 * b + 32 * h + 4 * (tid >> 5) + i;
                 vr[h][i] = *(const uint2*)(vbase + (size_t)(j0 + (vk < P ? vk : 0)) * HD + 4 * (tid & 31));
             }
-    }
+    };
+    auto lstore = [&](int buf) {
+        uint16_t* Ks = (uint16_t*)(kv_lds + buf * BUF);
+        uint16_t* Vt = (uint16_t*)(kv_lds + buf * BUF + KS_BYTES);
+        uint4* kd = (uint4*)(Ks + (tid >> 2) * VA_KROW + 32 * (tid & 3));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kd[i] = kr[i];
+        const int d0 = 4 * (tid & 31);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k0 = 32 * h + 4 * (tid >> 5);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t e[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) e[i] = ((j < 2 ? vr[h][i].x : vr[h][i].y) >> (16 * (j & 1))) & 0xFFFFu;
+                *(uint2*)(Vt + (d0 + j) * VA_VROW + k0) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+            }
+        }
+    };
+    if (!tail) gload(0);
 
     // Query columns: normalised, rotated, scaled rows split into fp16 hi + lo; zero past the pass.
     const float qscale = 1.0f / sqrtf((float)HD);
@@ -290,7 +313,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
     }
     if (tail) {
         // The pass's new rows: per-head RMSNorm + RoPE on K, fp16 K/V into the cache and into
-        // the split's tiles; keys M .. 63 are zero rows.
+        // block 0's tiles; keys M .. 63 are zero rows.
+        uint16_t* Ks = (uint16_t*)kv_lds;
+        uint16_t* Vt = (uint16_t*)(kv_lds + KS_BYTES);
         for (int t = wave; t < ATT_CH; t += ATT_THREADS / WAVE) {
             uint16_t hk0 = 0, hk1 = 0, hv0 = 0, hv1 = 0;
             if (t < M) {
@@ -315,73 +340,73 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
             Vt[(lane + 64) * VA_VROW + t] = hv1;
         }
     } else {
-        uint4* kd = (uint4*)(Ks + (tid >> 2) * VA_KROW + 32 * (tid & 3));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kd[i] = kr[i];
-        const int d0 = 4 * (tid & 31);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int k0 = 32 * h + 4 * (tid >> 5);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t e[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) e[i] = ((j < 2 ? vr[h][i].x : vr[h][i].y) >> (16 * (j & 1))) & 0xFFFFu;
-                *(uint2*)(Vt + (d0 + j) * VA_VROW + k0) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
-            }
-        }
+        lstore(0);
     }
     __syncthreads();
 
-    // Scores of this wave's 16 keys against the 16 columns.
-    const int kt = 16 * wave;
-    f32x4 Sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        const v8h kf = *(const v8h*)(Ks + (kt + r16) * VA_KROW + 32 * ks + 8 * q4);
-        const v8h qh = *(const v8h*)(Qh + r16 * VA_QROW + 32 * ks + 8 * q4);
-        const v8h ql = *(const v8h*)(Ql + r16 * VA_QROW + 32 * ks + 8 * q4);
-        Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh, Sc, 0, 0, 0);
-        Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql, Sc, 0, 0, 0);
-    }
-    const int col = r16, ct = col >> 1;
-    float mb = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int key = kt + 4 * q4 + i;
-        const bool valid = key < P && ct < M && (!tail || key <= ct);
-        if (!valid) Sc[i] = -__builtin_inff();
-        mb = fmaxf(mb, Sc[i]);
-    }
-    mb = max_x4(mb);
-    float p[4], ls = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        p[i] = (Sc[i] == -__builtin_inff()) ? 0.f : expf(Sc[i] - mb);
-        ls += p[i];
-    }
-    ls = sum_x4(ls);
-    v4h Ph, Pl;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const f16 h = (f16)p[i];
-        Ph[i] = h;
-        Pl[i] = (f16)(p[i] - (float)h);
-    }
+    // Online softmax of this wave's keys (16 per block) for its lane's column.
+    const int col = r16, ct = col >> 1, kt = 16 * wave;
+    float m_run = -__builtin_inff(), l_run = 0.f;
     f32x4 O[8];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-        const v4h vf = *(const v4h*)(Vt + (16 * dt + r16) * VA_VROW + kt + 4 * q4);
-        O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Ph, O[dt], 0, 0, 0);
-        O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Pl, O[dt], 0, 0, 0);
+    for (int dt = 0; dt < 8; ++dt) O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < nblk; ++b) {
+        const int buf = b & 1;
+        if (b + 1 < nblk) gload(b + 1);
+        const uint16_t* Ks = (const uint16_t*)(kv_lds + buf * BUF);
+        const uint16_t* Vt = (const uint16_t*)(kv_lds + buf * BUF + KS_BYTES);
+        f32x4 Sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const v8h kf = *(const v8h*)(Ks + (kt + r16) * VA_KROW + 32 * ks + 8 * q4);
+            const v8h qh = *(const v8h*)(Qh + r16 * VA_QROW + 32 * ks + 8 * q4);
+            const v8h ql = *(const v8h*)(Ql + r16 * VA_QROW + 32 * ks + 8 * q4);
+            Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh, Sc, 0, 0, 0);
+            Sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql, Sc, 0, 0, 0);
+        }
+        float mb = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = 64 * b + kt + 4 * q4 + i;
+            const bool valid = key < P && ct < M && (!tail || key <= ct);
+            if (!valid) Sc[i] = -__builtin_inff();
+            mb = fmaxf(mb, Sc[i]);
+        }
+        mb = max_x4(mb);
+        const float m_new = fmaxf(m_run, mb);
+        const float corr = (m_run == -__builtin_inff()) ? 0.f : expf(m_run - m_new);
+        float p[4], ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = (Sc[i] == -__builtin_inff()) ? 0.f : expf(Sc[i] - m_new);
+            ls += p[i];
+        }
+        ls = sum_x4(ls);
+        l_run = l_run * corr + ls;
+        m_run = m_new;
+        v4h Ph, Pl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f16 h = (f16)p[i];
+            Ph[i] = h;
+            Pl[i] = (f16)(p[i] - (float)h);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const v4h vf = *(const v4h*)(Vt + (16 * dt + r16) * VA_VROW + kt + 4 * q4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[dt][i] *= corr;
+            O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Ph, O[dt], 0, 0, 0);
+            O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Pl, O[dt], 0, 0, 0);
+        }
+        if (b + 1 < nblk) lstore(buf ^ 1);
+        __syncthreads();
     }
     if (q4 == 0) {
-        wm[wave][col] = mb;
-        wl[wave][col] = ls;
+        wm[wave][col] = m_run;
+        wl[wave][col] = l_run;
     }
-    __syncthreads();  // every wave's operand reads are done: the K / V tiles become the waves' o
-    float* ow = (float*)kv_lds;  // [4 waves][16 columns][128 dims]
+    float* ow = (float*)kv_lds;  // [4 waves][16 columns][128 dims]; every tile read is done
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
         *(float4*)(ow + ((size_t)wave * 16 + col) * HD + 16 * dt + 4 * q4) = make_float4(O[dt][0], O[dt][1], O[dt][2], O[dt][3]);
@@ -421,12 +446,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
 // workgroup.  Thread t weights split t (t < S); the 128 output elements are summed by two
 // halves of the workgroup over interleaved splits, combined in a fixed order.
 template <int MT>
-__global__ __launch_bounds__(ATT_THREADS) void attention_merge_kernel(AttnArgs a, int splits) {
+__global__ __launch_bounds__(ATT_THREADS) void attention_merge_kernel(AttnArgs a, int splits, int chunk) {
     const State* st = a.st;
     if (st->done) return;
     const int M = a.m_fixed > 0 ? a.m_fixed : (st->n < MT ? st->n : MT);
     const int pos = st->pos;
-    const int S = (pos + ATT_CH - 1) / ATT_CH + 1;
+    const int S = (pos + chunk - 1) / chunk + 1;  // prior splits of `chunk` slots + the tail split
     if (pos < 0 || pos + M > st->maxctx || S > splits) return;
     const int g = blockIdx.x, row = blockIdx.y;
     if (row >= 2 * M) return;
@@ -486,10 +511,12 @@ hipError_t launch_attention(const AttnArgs& a, int mt, int splits, hipStream_t s
     const dim3 grid(splits, NKV);
     if (mt == 1) {
         hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(ATT_THREADS), 0, s, a);
-        hipLaunchKernelGGL(attention_merge_kernel<1>, dim3(NKV, 2), dim3(ATT_THREADS), 0, s, a, splits);
+        hipLaunchKernelGGL(attention_merge_kernel<1>, dim3(NKV, 2), dim3(ATT_THREADS), 0, s, a, splits, ATT_CH);
     } else {
-        hipLaunchKernelGGL(attention_mfma_kernel, grid, dim3(ATT_THREADS), 0, s, a);
-        hipLaunchKernelGGL(attention_merge_kernel<MAXM>, dim3(NKV, 2 * MAXM), dim3(ATT_THREADS), 0, s, a, splits);
+        // splits - 1 prior splits of 64 slots cover the cache: so do ceil((splits - 1) / 4) of 256.
+        const int vs = (splits - 1 + 3) / 4 + 1;
+        hipLaunchKernelGGL(attention_mfma_kernel, dim3(vs, NKV), dim3(ATT_THREADS), 0, s, a);
+        hipLaunchKernelGGL(attention_merge_kernel<MAXM>, dim3(NKV, 2 * MAXM), dim3(ATT_THREADS), 0, s, a, vs, VA_CH);
     }
     return hipGetLastError();
 }
