@@ -177,6 +177,77 @@ def run_gemv(iters):
     }
 
 
+# Vision workload: the reference's default 640 x 384 frame (24 x 40 patches, 240 visual rows)
+# through the 24-block tower and the four mergers (Engine.swift:317-473).
+VISION_GRID = (24, 40)
+
+
+def vision_flops(gh: int, gw: int) -> int:
+    """Algorithmic FLOPs of one frame: every projection (2 per multiply-add) and attention's
+    q.k and p.v over all patch pairs of each of the 16 heads."""
+    npt, nvis = gh * gw, gh * gw // 4
+    blk = 2 * npt * 1024 * (3072 + 1024 + 4096 + 4096) + 2 * 2 * 16 * npt * npt * 64
+    return 2 * npt * 768 * 1024 + 24 * blk + 4 * 2 * nvis * 4096 * (4096 + 2048)
+
+
+def vision_cpu_baseline(img, budget_s: float = 20.0):
+    """The oracle tower (C, fp64 accumulation, all host threads) on 8 x 8-patch frames for about
+    budget_s, scaled to 640 x 384 frames by the FLOP ratio."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    oracle.build()
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+    rgb = synth.random_rgb(8, 8, "bench-vision-cpu")
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.vision(img, rgb)
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= 8:
+            break
+    dt = (time.perf_counter() - t0) / n
+    scale = vision_flops(8, 8) / vision_flops(*VISION_GRID)
+    return {"value": round(scale / dt, 4), "unit": "images/s", "cores": oracle.get_threads(), "kind": "port",
+            "sample": f"{n} oracle frames of 8 x 8 patches ({dt:.2f} s each), scaled by FLOPs to 24 x 40"}
+
+
+def run_vision(K, W, cpu: bool = True):
+    """K timed frames of 640 x 384 through the vision tower and mergers (fp16 weights)."""
+    img = synth.build_model_image(WeightFormat.Q4, n_layers=1, tag="bench-vision", vision=True)
+    e = eng.Engine(image=img, max_context=64, max_steps=4)
+    gh, gw = VISION_GRID
+    frames = [synth.random_rgb(gh, gw, "bench-vision", i) for i in range(2)]
+    for i in range(W):
+        e.vision(frames[i % 2])
+    ms = []
+    t0 = time.perf_counter()
+    for i in range(K):
+        e.vision(frames[i % 2])
+        ms.append(e.last_timing["vision_ms"])
+    wall = (time.perf_counter() - t0) / K
+    e.close()
+    gpu_ms = float(np.mean(ms))
+    flops = vision_flops(gh, gw)
+    achieved = flops / (gpu_ms * 1e-3)
+    log(f"vision: {gpu_ms:.3f} ms per 640x384 frame on the stream ({wall * 1e3:.3f} ms wall), "
+        f"{achieved / 1e12:.1f} TFLOP/s")
+    line = {
+        "metric": "vision tower frames/s (640x384, 24 blocks + 4 mergers)",
+        "value": round(1e3 / gpu_ms, 2), "unit": "images/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(gpu_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 operands, fp32 accumulate",
+        "data": "synthetic (seeded random-init fp16 vision weights, random RGB frames)",
+        "config": {"workload": "Qwen3-VL vision tower on one 640 x 384 RGB frame: 960 patches, 240 visual rows",
+                   "grid": [gh, gw]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": MFMA_F16_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK, 4), "traffic": None,
+                     "kernel": "whole tower (HIP events around the launches)", "flops_per_frame": flops},
+    }
+    if cpu:
+        line["cpu_baseline"] = vision_cpu_baseline(img)
+    return line
+
+
 # Converter workload: the language backbone's matrices quantised from fp32 resident in HBM
 # (name, rows, cols, matrices per model).
 QUANT_SHAPES = [("QKV", Dims.qkv_rows, Dims.hidden, LAYERS), ("O", Dims.hidden, Dims.hidden, LAYERS),
@@ -261,9 +332,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true",
                     help="profiling runs: start decoding at the same 4096-slot context without the prefill "
                          "(cache rows stay zero; same bytes per step), so a profile holds only the decode launch")
-    ap.add_argument("--workload", choices=["decode", "verify", "gemv", "quant"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "verify", "gemv", "quant", "vision"], default="decode",
                     help="decode: the 4k-context q4 decode (default); verify: 8-draft q8 verify over 8192 rows; "
-                         "gemv: isolated q4 GEMV sweep; quant: converter quantisers over the backbone shapes")
+                         "gemv: isolated q4 GEMV sweep; quant: converter quantisers over the backbone shapes; "
+                         "vision: the vision tower on a 640x384 frame")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU decode is a design note only",
@@ -274,6 +346,9 @@ def main():
         return
     if args.workload == "gemv":
         print(json.dumps(run_gemv(200)))
+        return
+    if args.workload == "vision":
+        print(json.dumps(run_vision(args.steps, args.warmup)))
         return
     if args.workload == "quant":
         print(json.dumps(run_quant(20)))

@@ -33,6 +33,7 @@ enum {
     ICUA_FLAG_PREFIX_CACHE = 2,  /* reuse the KV of an identical pre-image prefix (Engine.swift:719-735) */
     ICUA_FLAG_GRAPH_DECODE = 4,  /* decode through the per-kernel HIP graph instead of the persistent kernel */
     ICUA_FLAG_PASS_PREFILL = 8,  /* prefill q4 prompts in passes of 8 rows instead of the matrix-core GEMMs */
+    ICUA_FLAG_VISION_DELTA_CACHE = 16, /* icua_generate_vision skips the encoder on an identical frame (Engine.swift:707-716) */
 };
 
 /* Decode control block, first twelve fields as `State` (Shaders.swift:41-54). */
@@ -51,7 +52,7 @@ typedef struct {
     int32_t format, layers, max_context, max_pass, max_steps;
     int64_t weight_bytes, kv_bytes;
     int32_t persistent_decode; /* 1 if icua_decode_steps can use the persistent kernel on this device */
-    int32_t reserved;
+    int32_t vision; /* 1 if the model file holds the vision tower and its mergers */
 } icua_info_t;
 
 /* Last error message of the calling thread ("" if none). */
@@ -105,6 +106,19 @@ int icua_decode_steps(icua_engine* e, int k);
 int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, int max_new,
                   int32_t* out_tokens, int* n_out);
 
+/* Engine.encodeVision (Engine.swift:317-473): runs the vision tower and its mergers on an RGB8
+ * frame [height][width][3] (sides multiples of 32, at most 1024 16 x 16 patches) and keeps its
+ * outputs as the visual rows of the next prefill: pooler and the three DeepStack sets,
+ * (height / 32) * (width / 32) rows each.  Fails if the model file has no vision tower. */
+int icua_vision(icua_engine* e, const uint8_t* rgb, int width, int height);
+
+/* Engine.generateVision (Engine.swift:696-827): icua_vision on the frame (skipped with
+ * ICUA_FLAG_VISION_DELTA_CACHE when the frame, by its 8-byte-word FNV hash and its size, equals
+ * the last one), vis_offset = first 151655 (<|image_pad|>) in tokens, the M-RoPE table of the
+ * (height / 32) x (width / 32) grid, then icua_generate.  The timing record includes vision_ms. */
+int icua_generate_vision(icua_engine* e, const uint8_t* rgb, int width, int height, const int32_t* tokens, int n,
+                         int max_new, int32_t* out_tokens, int* n_out);
+
 /* Speculative verify: m <= 8 draft tokens at the current position in one pass with a causal
  * tail; out_argmax[m] gets each row's greedy token; out_logits ([m][151936]) may be NULL.
  * The cache keeps the drafts' K/V; the position is left unchanged (the caller accepts a prefix
@@ -134,8 +148,16 @@ int icua_write_kv(icua_engine* e, int layer, int kind, int slot0, int nslots, co
 
 /* Pass activations of the last layer run (Engine.swift:24 x, qkvBuf, attn, hbuf): for tests.
  * ICUA_BUF_X fp32 [8][2048]; ICUA_BUF_QKV fp32 [8][4096] raw fused QKV rows; ICUA_BUF_ATTN fp32
- * [8][2048] attention output; ICUA_BUF_MLP fp32 [8][6144] SwiGLU output. */
-enum { ICUA_BUF_X = 0, ICUA_BUF_QKV = 1, ICUA_BUF_ATTN = 2, ICUA_BUF_MLP = 3 };
+ * [8][2048] attention output; ICUA_BUF_MLP fp32 [8][6144] SwiGLU output; ICUA_BUF_POOLER and
+ * ICUA_BUF_DEEPSTACK0 + i fp32 [n_vis][2048], the visual rows of the next prefill. */
+enum {
+    ICUA_BUF_X = 0,
+    ICUA_BUF_QKV = 1,
+    ICUA_BUF_ATTN = 2,
+    ICUA_BUF_MLP = 3,
+    ICUA_BUF_POOLER = 4,
+    ICUA_BUF_DEEPSTACK0 = 5
+};
 int icua_read_buffer(icua_engine* e, int which, void* dst, size_t bytes);
 
 /* ---- standalone kernels on device buffers (isolated dequant-GEMV sweep, codec checks) ---- */

@@ -256,41 +256,41 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
     // Prior keys of block b: K row tid / 4, dims 32 (tid % 4) .. + 31; V keys 4 (tid / 32) + i
     // (+ 32), dims 4 (tid % 32) .. + 3, transposed in registers.  Rows past the split read its
     // first row.
+    // Register-staged block loads (macros, not lambdas: register arrays captured by reference,
+    // or filled under a condition, stay in scratch memory).
+    // The tail split's tiles come from the pass's own rows; its register loads read cache row 0.
+    const int lrow0 = tail ? 0 : j0, lP = tail ? 1 : P;
     uint4 kr[4];
     uint2 vr[2][4];
-    auto gload = [&](int b) {
-        const int kk = 64 * b + (tid >> 2);
-        const uint4* kp = (const uint4*)(kbase + (size_t)(j0 + (kk < P ? kk : 0)) * HD + 32 * (tid & 3));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kr[i] = kp[i];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int vk = 64 * b + 32 * h + 4 * (tid >> 5) + i;
-                vr[h][i] = *(const uint2*)(vbase + (size_t)(j0 + (vk < P ? vk : 0)) * HD + 4 * (tid & 31));
-            }
-    };
-    auto lstore = [&](int buf) {
-        uint16_t* Ks = (uint16_t*)(kv_lds + buf * BUF);
-        uint16_t* Vt = (uint16_t*)(kv_lds + buf * BUF + KS_BYTES);
-        uint4* kd = (uint4*)(Ks + (tid >> 2) * VA_KROW + 32 * (tid & 3));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kd[i] = kr[i];
-        const int d0 = 4 * (tid & 31);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int k0 = 32 * h + 4 * (tid >> 5);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t e[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) e[i] = ((j < 2 ? vr[h][i].x : vr[h][i].y) >> (16 * (j & 1))) & 0xFFFFu;
-                *(uint2*)(Vt + (d0 + j) * VA_VROW + k0) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
-            }
-        }
-    };
-    if (!tail) gload(0);
+#define VA_GLOAD(b_)                                                                                  \
+    do {                                                                                              \
+        const int kk_ = 64 * (b_) + (tid >> 2);                                                       \
+        const uint4* kp_ = (const uint4*)(kbase + (size_t)(lrow0 + (kk_ < lP ? kk_ : 0)) * HD + 32 * (tid & 3)); \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) kr[i] = kp_[i];                                 \
+        _Pragma("unroll") for (int h = 0; h < 2; ++h)                                                 \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                           \
+                const int vk = 64 * (b_) + 32 * h + 4 * (tid >> 5) + i;                                \
+                vr[h][i] = *(const uint2*)(vbase + (size_t)(lrow0 + (vk < lP ? vk : 0)) * HD + 4 * (tid & 31)); \
+            }                                                                                         \
+    } while (0)
+#define VA_LSTORE(buf_)                                                                               \
+    do {                                                                                              \
+        uint16_t* Ks_ = (uint16_t*)(kv_lds + (buf_) * BUF);                                           \
+        uint16_t* Vt_ = (uint16_t*)(kv_lds + (buf_) * BUF + KS_BYTES);                                \
+        uint4* kd_ = (uint4*)(Ks_ + (tid >> 2) * VA_KROW + 32 * (tid & 3));                           \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) kd_[i] = kr[i];                                 \
+        const int d0_ = 4 * (tid & 31);                                                               \
+        _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                               \
+            const int k0_ = 32 * h + 4 * (tid >> 5);                                                  \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                           \
+                uint32_t e[4];                                                                        \
+                _Pragma("unroll") for (int i = 0; i < 4; ++i)                                         \
+                    e[i] = ((j < 2 ? vr[h][i].x : vr[h][i].y) >> (16 * (j & 1))) & 0xFFFFu;           \
+                *(uint2*)(Vt_ + (d0_ + j) * VA_VROW + k0_) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16)); \
+            }                                                                                         \
+        }                                                                                             \
+    } while (0)
+    VA_GLOAD(0);
 
     // Query columns: normalised, rotated, scaled rows split into fp16 hi + lo; zero past the pass.
     const float qscale = 1.0f / sqrtf((float)HD);
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
             Vt[(lane + 64) * VA_VROW + t] = hv1;
         }
     } else {
-        lstore(0);
+        VA_LSTORE(0);
     }
     __syncthreads();
 
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
     for (int dt = 0; dt < 8; ++dt) O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int b = 0; b < nblk; ++b) {
         const int buf = b & 1;
-        if (b + 1 < nblk) gload(b + 1);
+        VA_GLOAD(min(b + 1, nblk - 1));  // unconditional (see above); the last reloads block nblk - 1
         const uint16_t* Ks = (const uint16_t*)(kv_lds + buf * BUF);
         const uint16_t* Vt = (const uint16_t*)(kv_lds + buf * BUF + KS_BYTES);
         f32x4 Sc = {0.f, 0.f, 0.f, 0.f};
@@ -399,9 +399,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
             O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Ph, O[dt], 0, 0, 0);
             O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Pl, O[dt], 0, 0, 0);
         }
-        if (b + 1 < nblk) lstore(buf ^ 1);
+        VA_LSTORE(buf ^ 1);  // the last fills the idle buffer, read by no one
         __syncthreads();
     }
+#undef VA_GLOAD
+#undef VA_LSTORE
     if (q4 == 0) {
         wm[wave][col] = m_run;
         wl[wave][col] = l_run;

@@ -137,6 +137,19 @@ struct icua_engine {
     int pf_cap = 0;
     float *px = nullptr, *pqkv = nullptr, *patt = nullptr, *ph = nullptr, *pxs = nullptr, *pts = nullptr;
     uint16_t *pxa = nullptr, *pqh = nullptr, *pql = nullptr;
+    // Vision tower, when the image holds it: weights, work buffers (one allocation, on first
+    // use), the host copy of the position table, the prepared grid and the frame hash.
+    uint8_t* d_vision = nullptr;
+    size_t vision_bytes = 0;
+    VitWeights vw{};
+    VitBuffers vb{};
+    void* vbuf = nullptr;
+    std::vector<float> vit_pos_host;
+    int vgrid[2] = {0, 0};
+    int vis_cap = 0;  // rows of pooler / ds
+    uint64_t rgb_hash = 0;
+    int rgb_dims[2] = {0, 0};
+    bool has_cached_vision = false;
 
     uint16_t* kv_ptr(int l, int kind) const { return kv + ((size_t)l * 2 + kind) * NKV * (size_t)maxctx * HD; }
 
@@ -403,7 +416,192 @@ struct icua_engine {
         s.vis_offset = -1;
         if (write_state(s)) return -1;
         if (init_persistent()) return -1;
+        if (init_vision(img, len, tab)) return -1;
         return prepare_mrope(-1, 1, 1);
+    }
+
+    // Vision tensors (ModelFile.swift:64-87, Convert.swift:97-152): copied as they are into one
+    // device block.  An image without them (slot 0 empty) loads as a text-only model.
+    int init_vision(const uint8_t* img, size_t len, const uint64_t* tab) {
+        if (tab[1] == 0) return 0;
+        struct Want {
+            int id;
+            size_t bytes;
+        };
+        std::vector<Want> want = {{0, (size_t)VH * VPATCH * 2}, {1, (size_t)VH * 4}, {2, (size_t)VPOS * VPOS * VH * 4}};
+        for (int l = 0; l < VLAYERS; ++l) {
+            const int b = 3 + 12 * l;
+            const size_t sz[12] = {VH * 4,          VH * 4, (size_t)VQKV * VH * 2, VQKV * 4,
+                                   (size_t)VH * VH * 2, VH * 4, VH * 4,                VH * 4,
+                                   (size_t)VFF * VH * 2, VFF * 4, (size_t)VH * VFF * 2, VH * 4};
+            for (int k = 0; k < 12; ++k) want.push_back({b + k, sz[k]});
+        }
+        for (int d = 0; d < 4; ++d) {
+            const int b = 3 + 12 * VLAYERS + 6 * d;
+            const size_t nn = d < 3 ? MH : VH;  // DeepStack mergers normalise 4096 columns
+            const size_t sz[6] = {nn * 4, nn * 4, (size_t)MH * MH * 2, MH * 4, (size_t)H * MH * 2, H * 4};
+            for (int k = 0; k < 6; ++k) want.push_back({b + k, sz[k]});
+        }
+        std::vector<size_t> off(want.size());
+        size_t total = 0;
+        for (size_t i = 0; i < want.size(); ++i) {
+            const uint64_t o = tab[2 * want[i].id], sz = tab[2 * want[i].id + 1];
+            if (sz != want[i].bytes || o + sz > len)
+                return fail("vision tensor " + std::to_string(want[i].id) + ": size " + std::to_string(sz) + ", want " +
+                            std::to_string(want[i].bytes));
+            total = (total + 255) & ~(size_t)255;
+            off[i] = total;
+            total += want[i].bytes;
+        }
+        HIPCK(hipMalloc(&d_vision, total));
+        vision_bytes = total;
+        for (size_t i = 0; i < want.size(); ++i)
+            HIPCK(hipMemcpy(d_vision + off[i], img + tab[2 * want[i].id], want[i].bytes, hipMemcpyHostToDevice));
+        auto F = [&](size_t i) { return (const float*)(d_vision + off[i]); };
+        auto W = [&](size_t i) { return (const uint16_t*)(d_vision + off[i]); };
+        vw.patch_w = W(0);
+        vw.patch_b = F(1);
+        for (int l = 0; l < VLAYERS; ++l) {
+            const size_t b = 3 + 12 * l;
+            VitBlock& B = vw.blk[l];
+            B.n1w = F(b);
+            B.n1b = F(b + 1);
+            B.qkvw = W(b + 2);
+            B.qkvb = F(b + 3);
+            B.projw = W(b + 4);
+            B.projb = F(b + 5);
+            B.n2w = F(b + 6);
+            B.n2b = F(b + 7);
+            B.fc1w = W(b + 8);
+            B.fc1b = F(b + 9);
+            B.fc2w = W(b + 10);
+            B.fc2b = F(b + 11);
+        }
+        for (int d = 0; d < 4; ++d) {
+            const size_t b = 3 + 12 * VLAYERS + 6 * d;
+            VitMerger& M = vw.mg[d];
+            M.nw = F(b);
+            M.nb = F(b + 1);
+            M.fc1w = W(b + 2);
+            M.fc1b = F(b + 3);
+            M.fc2w = W(b + 4);
+            M.fc2b = F(b + 5);
+        }
+        vit_pos_host.resize((size_t)VPOS * VPOS * VH);
+        std::memcpy(vit_pos_host.data(), img + tab[2 * 2], vit_pos_host.size() * 4);
+        return 0;
+    }
+
+    // Visual rows for n rows (pooler and the three DeepStack sets), kept when large enough.
+    int ensure_visual_rows(int n) {
+        if (n <= vis_cap) return 0;
+        if (pooler) (void)hipFree(pooler);
+        for (auto& d : ds)
+            if (d) {
+                (void)hipFree(d);
+                d = nullptr;
+            }
+        pooler = nullptr;
+        vis_cap = 0;
+        HIPCK(hipMalloc(&pooler, sizeof(float) * (size_t)n * H));
+        for (auto& d : ds) HIPCK(hipMalloc(&d, sizeof(float) * (size_t)n * H));
+        vis_cap = n;
+        return 0;
+    }
+
+    // prepareVisionGrid (Engine.swift:189-246): the interpolated position table and the 2D RoPE
+    // table of a gh x gw grid in merge-block order, in the engine's float32 operation order.
+    int prepare_vision_grid(int gh, int gw) {
+#pragma clang fp contract(off)
+        if (vgrid[0] == gh && vgrid[1] == gw) return 0;
+        const int np = gh * gw, mw = gw / 2;
+        std::vector<float> pos((size_t)np * VH), rope((size_t)np * 64);
+        float invf[16];
+        for (int i = 0; i < 16; ++i) invf[i] = (float)(1.0 / std::pow(10000.0, (double)(2 * i) / 32.0));
+        for (int p = 0; p < np; ++p) {
+            const int blk = p / 4, in = p % 4;
+            const int r = (blk / mw) * 2 + in / 2, c = (blk % mw) * 2 + in % 2;
+            const float y = (float)r * (float)(VPOS - 1) / (float)std::max(1, gh - 1);
+            const float xx = (float)c * (float)(VPOS - 1) / (float)std::max(1, gw - 1);
+            const int y0 = (int)std::floor(y), x0 = (int)std::floor(xx);
+            const int y1 = std::min(VPOS - 1, y0 + 1), x1 = std::min(VPOS - 1, x0 + 1);
+            const float dy = y - (float)y0, dx = xx - (float)x0;
+            const float w00 = (1.0f - dy) * (1.0f - dx), w01 = (1.0f - dy) * dx, w10 = dy * (1.0f - dx), w11 = dy * dx;
+            const float* p00 = vit_pos_host.data() + (size_t)(y0 * VPOS + x0) * VH;
+            const float* p01 = vit_pos_host.data() + (size_t)(y0 * VPOS + x1) * VH;
+            const float* p10 = vit_pos_host.data() + (size_t)(y1 * VPOS + x0) * VH;
+            const float* p11 = vit_pos_host.data() + (size_t)(y1 * VPOS + x1) * VH;
+            float* d = pos.data() + (size_t)p * VH;
+            for (int k = 0; k < VH; ++k) {
+                float t = w00 * p00[k];  // one rounding per operation, as the engine
+                t = t + w01 * p01[k];
+                t = t + w10 * p10[k];
+                t = t + w11 * p11[k];
+                d[k] = t;
+            }
+            float* rr = rope.data() + (size_t)p * 64;
+            for (int i = 0; i < 16; ++i) {
+                const double ah = (double)((float)r * invf[i]), aw = (double)((float)c * invf[i]);
+                rr[2 * i] = (float)std::cos(ah);
+                rr[2 * i + 1] = (float)std::sin(ah);
+                rr[2 * (16 + i)] = (float)std::cos(aw);
+                rr[2 * (16 + i) + 1] = (float)std::sin(aw);
+            }
+        }
+        HIPCK(hipMemcpy((void*)vb.pos, pos.data(), pos.size() * 4, hipMemcpyHostToDevice));
+        HIPCK(hipMemcpy((void*)vb.rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice));
+        vgrid[0] = gh;
+        vgrid[1] = gw;
+        return 0;
+    }
+
+    // encodeVision (Engine.swift:317-473) of an RGB8 frame [height][width][3].
+    int vision(const uint8_t* rgb, int width, int height, double* ms) {
+        if (!d_vision) return fail("the model file has no vision tower");
+        if (width <= 0 || height <= 0 || width % 32 || height % 32)
+            return fail("image sides must be positive multiples of 32");
+        const int gh = height / 16, gw = width / 16, np = gh * gw;
+        if (np > NPATCH_MAX) return fail("image has more than 1024 patches");
+        if (!vbuf) {
+            const size_t n = NPATCH_MAX;
+            const size_t sz[] = {n * 256 * 3, n * VPATCH * 2, n * VH * 4, n * VH * 2, (size_t)VNH * n * VHD * 2,
+                                 (size_t)VNH * n * VHD * 2, (size_t)VNH * VHD * n * 2, n * VH * 2, n * VFF * 2,
+                                 n * VH * 4, n * 64 * 4};
+            size_t o[11], total = 0;
+            for (int i = 0; i < 11; ++i) {
+                o[i] = total;
+                total += (sz[i] + 255) & ~(size_t)255;
+            }
+            HIPCK(hipMalloc(&vbuf, total));
+            HIPCK(hipMemset(vbuf, 0, total));  // padded key rows of q / k / v stay finite
+            uint8_t* b = (uint8_t*)vbuf;
+            vb.rgb = b + o[0];
+            vb.patches = (uint16_t*)(b + o[1]);
+            vb.x = (float*)(b + o[2]);
+            vb.xn = (uint16_t*)(b + o[3]);
+            vb.q = (uint16_t*)(b + o[4]);
+            vb.k = (uint16_t*)(b + o[5]);
+            vb.vt = (uint16_t*)(b + o[6]);
+            vb.attn = (uint16_t*)(b + o[7]);
+            vb.h = (uint16_t*)(b + o[8]);
+            vb.pos = (const float*)(b + o[9]);
+            vb.rope = (const float*)(b + o[10]);
+        }
+        if (ensure_visual_rows(NPATCH_MAX / 4)) return -1;
+        vb.pooler = pooler;
+        for (int i = 0; i < 3; ++i) vb.ds[i] = ds[i];
+        if (prepare_vision_grid(gh, gw)) return -1;
+        HIPCK(hipMemcpyAsync((void*)vb.rgb, rgb, (size_t)width * height * 3, hipMemcpyHostToDevice, stream));
+        HIPCK(hipEventRecord(ev0, stream));
+        HIPCK(launch_vision(vw, vb, gh, gw, stream));
+        HIPCK(hipEventRecord(ev1, stream));
+        HIPCK(hipEventSynchronize(ev1));
+        float t = 0;
+        HIPCK(hipEventElapsedTime(&t, ev0, ev1));
+        if (ms) *ms = t;
+        n_vis = np / 4;
+        has_ds = true;
+        return 0;
     }
 
     // The persistent kernel needs all PERSIST_WGS workgroups (one per CU) resident at once.
@@ -714,7 +912,7 @@ void icua_engine_destroy(icua_engine* e) {
         if (g) (void)hipGraphExecDestroy(g);
     void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->pval,
                     e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
-                    e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_layers};
+                    e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_layers, e->d_vision, e->vbuf};
     e->free_pf();
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -728,13 +926,13 @@ int icua_engine_info(icua_engine* e, icua_info_t* out) {
     if (!e || !out) return fail("null argument");
     out->format = e->fmt;
     out->layers = e->layers;
+    out->vision = e->d_vision != nullptr;
     out->max_context = e->maxctx;
     out->max_pass = e->maxpass;
     out->max_steps = e->maxsteps;
     out->weight_bytes = (int64_t)e->weight_bytes;
     out->kv_bytes = (int64_t)e->layers * 2 * NKV * e->maxctx * HD * 2;
     out->persistent_decode = e->persist_ok ? 1 : 0;
-    out->reserved = 0;
     return 0;
 }
 
@@ -759,17 +957,8 @@ int icua_prepare_mrope(icua_engine* e, int vis_offset, int llm_h, int llm_w) {
 int icua_set_visual(icua_engine* e, const float* pooler, const float* const* deepstack, int n_vis) {
     if (!e || !pooler || n_vis <= 0) return fail("bad visual inputs");
     if (n_vis > e->maxctx) return fail("too many visual rows");
-    if (n_vis > e->n_vis) {
-        if (e->pooler) (void)hipFree(e->pooler);
-        for (auto& d : e->ds)
-            if (d) {
-                (void)hipFree(d);
-                d = nullptr;
-            }
-        e->pooler = nullptr;
-        HIPCK(hipMalloc(&e->pooler, sizeof(float) * (size_t)n_vis * H));
-        for (auto& d : e->ds) HIPCK(hipMalloc(&d, sizeof(float) * (size_t)n_vis * H));
-    }
+    if (e->ensure_visual_rows(n_vis)) return -1;
+    e->has_cached_vision = false;  // the rows no longer come from the last encoded frame
     HIPCK(hipMemcpy(e->pooler, pooler, sizeof(float) * (size_t)n_vis * H, hipMemcpyHostToDevice));
     e->has_ds = deepstack != nullptr;
     if (deepstack)
@@ -837,6 +1026,60 @@ int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, 
     e->timing.total_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     e->timing.generated_tokens = cnt;
     e->timing.vision_ms = 0;
+    return 0;
+}
+
+int icua_vision(icua_engine* e, const uint8_t* rgb, int width, int height) {
+    if (!e || !rgb) return fail("null argument");
+    double ms = 0;
+    if (e->vision(rgb, width, height, &ms)) return -1;
+    e->timing.vision_ms = ms;
+    e->has_cached_vision = false;
+    return 0;
+}
+
+// hashRGB (Engine.swift:684-693): FNV-1a over the frame's whole 8-byte words.
+static uint64_t hash_rgb(const uint8_t* p, size_t bytes) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i < bytes / 8; ++i) {
+        uint64_t w;
+        std::memcpy(&w, p + 8 * i, 8);
+        h ^= w;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+int icua_generate_vision(icua_engine* e, const uint8_t* rgb, int width, int height, const int32_t* tokens, int n,
+                         int max_new, int32_t* out_tokens, int* n_out) {
+    if (!e || !rgb || !tokens || !out_tokens || !n_out) return fail("null argument");
+    const auto t0 = std::chrono::steady_clock::now();
+    if (width <= 0 || height <= 0 || width % 32 || height % 32)
+        return fail("image sides must be positive multiples of 32");
+    // Vision delta cache (Engine.swift:707-716): an identical consecutive frame reuses the last
+    // encoder outputs.  The frame size is part of the key here.
+    const uint64_t hsh = hash_rgb(rgb, (size_t)width * height * 3);
+    const bool skip = (e->flags & ICUA_FLAG_VISION_DELTA_CACHE) && e->has_cached_vision && hsh == e->rgb_hash &&
+                      e->rgb_dims[0] == width && e->rgb_dims[1] == height;
+    double vms = 0;
+    if (!skip) {
+        e->has_cached_vision = false;
+        if (e->vision(rgb, width, height, &vms)) return -1;
+        e->rgb_hash = hsh;
+        e->rgb_dims[0] = width;
+        e->rgb_dims[1] = height;
+        e->has_cached_vision = true;
+    }
+    int vis_offset = -1;  // first <|image_pad|> (Engine.swift:718)
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] == IMAGE_PAD_ID) {
+            vis_offset = i;
+            break;
+        }
+    if (e->prepare_mrope(vis_offset, height / 32, width / 32)) return -1;
+    if (icua_generate(e, tokens, n, vis_offset, max_new, out_tokens, n_out)) return -1;
+    e->timing.vision_ms = vms;
+    e->timing.total_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return 0;
 }
 
@@ -989,8 +1232,16 @@ int icua_read_buffer(icua_engine* e, int which, void* dst, size_t bytes) {
         case ICUA_BUF_QKV: src = e->qkv; cap = sizeof(float) * MAXM * QKV; break;
         case ICUA_BUF_ATTN: src = e->attn; cap = sizeof(float) * MAXM * H; break;
         case ICUA_BUF_MLP: src = e->h; cap = sizeof(float) * MAXM * FF; break;
+        case ICUA_BUF_POOLER: src = e->pooler; cap = sizeof(float) * (size_t)e->n_vis * H; break;
+        case ICUA_BUF_DEEPSTACK0:
+        case ICUA_BUF_DEEPSTACK0 + 1:
+        case ICUA_BUF_DEEPSTACK0 + 2:
+            src = e->has_ds ? e->ds[which - ICUA_BUF_DEEPSTACK0] : nullptr;
+            cap = sizeof(float) * (size_t)e->n_vis * H;
+            break;
         default: return fail("unknown buffer");
     }
+    if (!src) return fail("buffer not set");
     if (bytes > cap) return fail("read past the buffer");
     HIPCK(hipStreamSynchronize(e->stream));
     HIPCK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));

@@ -146,4 +146,51 @@ hipError_t launch_dequant(int fmt, const uint8_t* w, const uint8_t* sb, int K, i
 hipError_t launch_quant(int fmt, const float* m, int64_t rows, int64_t cols, void* codes, void* sb, uint8_t* none,
                         hipStream_t s);
 
+// Vision tower (ModelFile.swift:31-45): dimensions, weights, work buffers.
+constexpr int VH = 1024, VFF = 4096, VNH = 16, VHD = 64, VQKV = 3072, VPATCH = 768, MH = 4096;
+constexpr int VLAYERS = 24, VPOS = 48, NPATCH_MAX = 1024;
+enum { VG_F32 = 0, VG_F32_ADD = 1, VG_F32_POS = 2, VG_GELU_TANH = 3, VG_GELU_ERF = 4, VG_QKV = 5 };
+struct VitGemmArgs {
+    const uint16_t* X;  // fp16 [M][K]
+    const uint16_t* W;  // fp16 [N][K]
+    const float* bias;  // [N]
+    float* outf;        // [M][N] float32 (VG_F32, VG_F32_ADD, VG_F32_POS)
+    uint16_t* outh;     // [M][N] fp16 (GELU modes)
+    const float* pos;   // [M][N] (VG_F32_POS)
+    const float* rope;  // [M][32][2] (VG_QKV)
+    uint16_t* q;        // [VNH][ld][VHD] fp16 (VG_QKV)
+    uint16_t* k;        // [VNH][ld][VHD]
+    uint16_t* vt;       // [VNH][VHD][ld], V transposed
+    int ld, M, N, K;
+};
+struct VitBlock {
+    const float *n1w, *n1b, *qkvb, *projb, *n2w, *n2b, *fc1b, *fc2b;
+    const uint16_t *qkvw, *projw, *fc1w, *fc2w;
+};
+struct VitMerger {
+    const float *nw, *nb, *fc1b, *fc2b;
+    const uint16_t *fc1w, *fc2w;
+};
+struct VitWeights {
+    const uint16_t* patch_w;
+    const float* patch_b;
+    VitBlock blk[VLAYERS];
+    VitMerger mg[4];  // DeepStack mergers 0-2, final merger 3
+};
+struct VitBuffers {
+    const uint8_t* rgb;  // [16 gh][16 gw][3]
+    uint16_t* patches;   // [NPATCH_MAX][VPATCH]
+    float* x;            // residual [NPATCH_MAX][VH]
+    uint16_t* xn;        // LayerNorm out [NPATCH_MAX][VH] (= [NPATCH_MAX / 4][MH])
+    uint16_t *q, *k, *vt;
+    uint16_t* attn;      // [NPATCH_MAX][VH]
+    uint16_t* h;         // [NPATCH_MAX][VFF]
+    const float* pos;    // interpolated position table [np][VH]
+    const float* rope;   // [np][32][2]
+    float* pooler;       // [np / 4][H]
+    float* ds[3];        // [np / 4][H]
+};
+// The whole tower for a gh x gw patch grid (even sides, at most NPATCH_MAX patches).
+hipError_t launch_vision(const VitWeights& w, const VitBuffers& b, int gh, int gw, hipStream_t s);
+
 }  // namespace icua

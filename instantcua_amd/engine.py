@@ -28,6 +28,7 @@ FLAG_GRAMMAR_PAIRS = 1
 FLAG_PREFIX_CACHE = 2
 FLAG_GRAPH_DECODE = 4
 FLAG_PASS_PREFILL = 8
+FLAG_VISION_DELTA_CACHE = 16
 
 EXPORTS = [
     "icua_last_error", "icua_engine_create", "icua_engine_create_from_memory", "icua_engine_destroy",
@@ -36,7 +37,7 @@ EXPORTS = [
     "icua_read_state", "icua_read_tokens", "icua_logits", "icua_timing", "icua_layer_step",
     "icua_read_kv", "icua_write_kv", "icua_read_buffer", "icua_dev_alloc", "icua_dev_free", "icua_memcpy_h2d",
     "icua_memcpy_d2h", "icua_device_sync", "icua_repack", "icua_gemv", "icua_gemv_bench", "icua_dequant",
-    "icua_quantize", "icua_quantize_bench",
+    "icua_quantize", "icua_quantize_bench", "icua_vision", "icua_generate_vision",
 ]
 
 
@@ -58,7 +59,7 @@ class _Timing(C.Structure):
 class _Info(C.Structure):
     _fields_ = [("format", C.c_int32), ("layers", C.c_int32), ("max_context", C.c_int32),
                 ("max_pass", C.c_int32), ("max_steps", C.c_int32), ("weight_bytes", C.c_int64),
-                ("kv_bytes", C.c_int64), ("persistent_decode", C.c_int32), ("reserved", C.c_int32)]
+                ("kv_bytes", C.c_int64), ("persistent_decode", C.c_int32), ("vision", C.c_int32)]
 
 
 _lib = None
@@ -86,6 +87,8 @@ def lib() -> C.CDLL:
         L.icua_decode_steps.argtypes = [vp, i32]
         L.icua_generate.argtypes = [vp, vp, i32, i32, i32, vp, C.POINTER(C.c_int)]
         L.icua_verify.argtypes = [vp, vp, i32, vp, vp]
+        L.icua_vision.argtypes = [vp, vp, i32, i32]
+        L.icua_generate_vision.argtypes = [vp, vp, i32, i32, vp, i32, i32, vp, C.POINTER(C.c_int)]
         L.icua_set_position.argtypes = [vp, i32, C.c_int32, i32, i32]
         L.icua_read_state.argtypes = [vp, C.POINTER(_State)]
         L.icua_read_tokens.argtypes = [vp, vp, i32]
@@ -209,6 +212,8 @@ class Engine:
         self.max_context = info.max_context
         self.max_pass = info.max_pass
         self.max_steps = info.max_steps
+        self.has_vision = bool(info.vision)
+        self._vis_rows = 0
         self.weight_bytes = info.weight_bytes
         self.kv_bytes = info.kv_bytes
         self.persistent_decode = bool(info.persistent_decode)
@@ -263,6 +268,15 @@ class Engine:
         self.set_flags((self._flags | FLAG_GRAPH_DECODE) if v else (self._flags & ~FLAG_GRAPH_DECODE))
 
     @property
+    def use_vision_delta_cache(self) -> bool:
+        """generate_vision skips the encoder on an identical consecutive frame."""
+        return bool(self._flags & FLAG_VISION_DELTA_CACHE)
+
+    @use_vision_delta_cache.setter
+    def use_vision_delta_cache(self, v: bool):
+        self.set_flags((self._flags | FLAG_VISION_DELTA_CACHE) if v else (self._flags & ~FLAG_VISION_DELTA_CACHE))
+
+    @property
     def pass_prefill(self) -> bool:
         """Prefill q4 prompts in passes of 8 rows instead of the matrix-core GEMMs."""
         return bool(self._flags & FLAG_PASS_PREFILL)
@@ -290,6 +304,45 @@ class Engine:
             keep.append(arr)
             ds_ptr = C.cast(arr, C.c_void_p)
         _check(lib().icua_set_visual(self._h, _p(pool), ds_ptr, pool.shape[0]))
+        self._vis_rows = pool.shape[0]
+
+    # -- vision tower ------------------------------------------------------------------------
+    @staticmethod
+    def _rgb(rgb: np.ndarray) -> np.ndarray:
+        img = np.ascontiguousarray(rgb, dtype=np.uint8)
+        if img.ndim != 3 or img.shape[2] != 3:
+            raise EngineError("rgb must be uint8 [height][width][3]")
+        return img
+
+    def vision(self, rgb: np.ndarray) -> None:
+        """encodeVision (Engine.swift:317-473): the frame's pooler and DeepStack rows become the
+        visual rows of the next prefill."""
+        img = self._rgb(rgb)
+        _check(lib().icua_vision(self._h, _p(img), img.shape[1], img.shape[0]))
+        self._vis_rows = (img.shape[0] // 32) * (img.shape[1] // 32)
+
+    def visual_rows(self):
+        """(pooler, [deepstack x 3]) float32 [n_vis][2048] currently held by the engine."""
+        n = self._vis_rows
+        pool = np.empty((n, H), dtype=np.float32)
+        _check(lib().icua_read_buffer(self._h, 4, _p(pool), pool.nbytes))
+        ds = []
+        for i in range(3):
+            d = np.empty((n, H), dtype=np.float32)
+            _check(lib().icua_read_buffer(self._h, 5 + i, _p(d), d.nbytes))
+            ds.append(d)
+        return pool, ds
+
+    def generate_vision(self, rgb: np.ndarray, tokens, max_new_tokens: int = 64) -> list:
+        """generateVision (Engine.swift:696-827) on an RGB8 frame [height][width][3]."""
+        img = self._rgb(rgb)
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(max(1, min(max_new_tokens, self.max_steps) + 1), dtype=np.int32)
+        n = C.c_int(0)
+        _check(lib().icua_generate_vision(self._h, _p(img), img.shape[1], img.shape[0], _p(toks), toks.size,
+                                          max_new_tokens, _p(out), C.byref(n)))
+        self._vis_rows = (img.shape[0] // 32) * (img.shape[1] // 32)
+        return [int(t) for t in out[:n.value]]
 
     def prefill(self, tokens, start_pos: int = 0, vis_offset: int = -1, max_new: int = 1,
                 write_logits: bool = False) -> int:

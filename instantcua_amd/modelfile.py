@@ -59,13 +59,31 @@ class Dims:
     eps = 1e-6
     vit_layers = 24
     num_deepstack = 3
+    # Vision encoder (ModelFile.swift:31-45).
+    vit_hidden = 1024
+    vit_ff = 4096
+    vit_heads = 16
+    vit_head_dim = 64
+    vit_qkv_rows = 3072
+    vit_patch = 16
+    vit_patch_dim = 768  # 3 x 16 x 16 (the temporal pair folded into the patch embedding)
+    vit_pos_grid = 48
+    deepstack_layers = (5, 11, 17)
+    merger_hidden = 4096
+    npatch_max = 1024
 
 
 class TensorID:
     """Tensor-table indices (ModelFile.swift:62-111)."""
 
+    vit_patch_w = 0  # [1024][768] f16
+    vit_patch_b = 1  # [1024] f32
+    vit_pos_emb = 2  # [2304][1024] f32
     vit_base = 3
     vit_per_layer = 12
+    v_norm1_w, v_norm1_b, v_qkv_w, v_qkv_b, v_proj_w, v_proj_b = 0, 1, 2, 3, 4, 5
+    v_norm2_w, v_norm2_b, v_fc1_w, v_fc1_b, v_fc2_w, v_fc2_b = 6, 7, 8, 9, 10, 11
+    m_norm_w, m_norm_b, m_fc1_w, m_fc1_b, m_fc2_w, m_fc2_b = 0, 1, 2, 3, 4, 5
     merger_base = vit_base + Dims.vit_layers * vit_per_layer  # 291
     merger_per_unit = 6
     llm_base = merger_base + (Dims.num_deepstack + 1) * merger_per_unit  # 315
@@ -82,6 +100,15 @@ class TensorID:
     wgu, wgu_sb = 8, 9
     wd, wd_sb = 10, 11
     count = llm_layer_base + Dims.layers * llm_per_layer  # 710
+
+    @staticmethod
+    def vit_layer(l: int, k: int) -> int:
+        return TensorID.vit_base + l * TensorID.vit_per_layer + k
+
+    @staticmethod
+    def merger(i: int, k: int) -> int:
+        """DeepStack mergers 0..2 and the final merger 3."""
+        return TensorID.merger_base + i * TensorID.merger_per_unit + k
 
     @staticmethod
     def llm_layer(l: int, k: int) -> int:

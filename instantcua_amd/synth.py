@@ -72,6 +72,60 @@ def model_tensor_sizes(fmt: int, n_layers: int) -> dict:
     return sizes
 
 
+def vision_tensor_specs():
+    """(slot, dtype, shape) of every vision-tower tensor (Convert.swift:97-152): fp16 matrices,
+    float32 biases, norms and the position table."""
+    VH, VF, MH = Dims.vit_hidden, Dims.vit_ff, Dims.merger_hidden
+    specs = [(TensorID.vit_patch_w, np.float16, (VH, Dims.vit_patch_dim)),
+             (TensorID.vit_patch_b, np.float32, (VH,)),
+             (TensorID.vit_pos_emb, np.float32, (Dims.vit_pos_grid ** 2, VH))]
+    for l in range(Dims.vit_layers):
+        V = lambda k: TensorID.vit_layer(l, k)
+        specs += [(V(TensorID.v_norm1_w), np.float32, (VH,)), (V(TensorID.v_norm1_b), np.float32, (VH,)),
+                  (V(TensorID.v_qkv_w), np.float16, (Dims.vit_qkv_rows, VH)),
+                  (V(TensorID.v_qkv_b), np.float32, (Dims.vit_qkv_rows,)),
+                  (V(TensorID.v_proj_w), np.float16, (VH, VH)), (V(TensorID.v_proj_b), np.float32, (VH,)),
+                  (V(TensorID.v_norm2_w), np.float32, (VH,)), (V(TensorID.v_norm2_b), np.float32, (VH,)),
+                  (V(TensorID.v_fc1_w), np.float16, (VF, VH)), (V(TensorID.v_fc1_b), np.float32, (VF,)),
+                  (V(TensorID.v_fc2_w), np.float16, (VH, VF)), (V(TensorID.v_fc2_b), np.float32, (VH,))]
+    for i in range(Dims.num_deepstack + 1):
+        M = lambda k: TensorID.merger(i, k)
+        nn = MH if i < Dims.num_deepstack else VH  # DeepStack mergers normalise 4096 columns
+        specs += [(M(TensorID.m_norm_w), np.float32, (nn,)), (M(TensorID.m_norm_b), np.float32, (nn,)),
+                  (M(TensorID.m_fc1_w), np.float16, (MH, MH)), (M(TensorID.m_fc1_b), np.float32, (MH,)),
+                  (M(TensorID.m_fc2_w), np.float16, (Dims.hidden, MH)),
+                  (M(TensorID.m_fc2_b), np.float32, (Dims.hidden,))]
+    return specs
+
+
+def _fill_vision(view, tag: str, zero_blocks: bool = False) -> None:
+    """Random vision weights: matrices fp16(N(0, 0.02)) (QKV 0.05, so that attention is peaked),
+    biases N(0, 0.02), norm weights 1 + 0.1 N(0, 1), norm biases 0.1 N(0, 1), position table
+    N(0, 0.2).  zero_blocks zeroes every block tensor (each block is then the identity)."""
+    norm_w = {TensorID.v_norm1_w, TensorID.v_norm2_w}
+    norm_b = {TensorID.v_norm1_b, TensorID.v_norm2_b}
+    for tid, dt, shape in vision_tensor_specs():
+        rng = _rng(tag + "-vision", 0, tid)
+        n = int(np.prod(shape))
+        in_block = TensorID.vit_base <= tid < TensorID.merger_base
+        k = (tid - TensorID.vit_base) % TensorID.vit_per_layer if in_block else \
+            (tid - TensorID.merger_base) % TensorID.merger_per_unit
+        if in_block and zero_blocks:
+            continue  # the image is zero-initialised
+        if in_block and k in norm_w or not in_block and tid >= TensorID.merger_base and k == TensorID.m_norm_w:
+            v = 1.0 + 0.1 * rng.standard_normal(n, dtype=np.float32)
+        elif in_block and k in norm_b or not in_block and tid >= TensorID.merger_base and k == TensorID.m_norm_b:
+            v = 0.1 * rng.standard_normal(n, dtype=np.float32)
+        elif tid == TensorID.vit_pos_emb:
+            v = 0.2 * rng.standard_normal(n, dtype=np.float32)
+        elif dt == np.float16:
+            sd = 0.05 if in_block and k == TensorID.v_qkv_w else 0.02
+            v = sd * rng.standard_normal(n, dtype=np.float32)
+        else:
+            v = 0.02 * rng.standard_normal(n, dtype=np.float32)
+        view(tid).view(dt)[:] = v.astype(dt)
+
+
 def _layout(sizes: dict):
     table = np.zeros((TensorID.count, 2), dtype="<u8")
     cursor = HEADER_SIZE
@@ -107,9 +161,14 @@ def _norm_weights(rng: np.random.Generator, n: int) -> np.ndarray:
     return (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
 
 
-def build_model_image(fmt: int, n_layers: int = Dims.layers, tag: str = "model") -> np.ndarray:
-    """Return a complete in-memory ``.icua`` image (uint8 array) of a synthetic decoder."""
+def build_model_image(fmt: int, n_layers: int = Dims.layers, tag: str = "model", vision: bool = False,
+                      zero_vision_blocks: bool = False) -> np.ndarray:
+    """Return a complete in-memory ``.icua`` image (uint8 array) of a synthetic decoder, with the
+    vision tower and its mergers when ``vision`` is set."""
     sizes = model_tensor_sizes(fmt, n_layers)
+    if vision:
+        for tid, dt, shape in vision_tensor_specs():
+            sizes[tid] = int(np.prod(shape)) * np.dtype(dt).itemsize
     table, total = _layout(sizes)
     img = np.zeros(total, dtype=np.uint8)
     hdr = np.array([MAGIC, VERSION, fmt, TensorID.count], dtype="<u4")
@@ -130,7 +189,17 @@ def build_model_image(fmt: int, n_layers: int = Dims.layers, tag: str = "model")
             view(L(slot)).view(np.float32)[:] = _norm_weights(_rng(tag, l, L(slot)), n)
         for wid, sid, rows, cols in _layer_mats():
             fill_matrix(fmt, rows, cols, view(L(wid)), view(L(sid)), _rng(tag, l, L(wid)))
+    if vision:
+        _fill_vision(view, tag, zero_vision_blocks)
     return img
+
+
+def random_rgb(gh: int, gw: int, tag: str, index: int = 0) -> np.ndarray:
+    """RGB8 image [16 gh][16 gw][3]: smooth gradients plus uniform noise."""
+    rng = _rng(tag, index, 13)
+    y, x = np.mgrid[0:16 * gh, 0:16 * gw].astype(np.float32)
+    base = np.stack([x / (16 * gw), y / (16 * gh), (x + y) / (16 * (gh + gw))], axis=-1) * 160.0
+    return np.clip(base + rng.uniform(0, 96, base.shape), 0, 255).astype(np.uint8)
 
 
 def save_image(img: np.ndarray, path: str) -> None:

@@ -133,6 +133,43 @@ int or_generate_commit(or_model* m, const int32_t* toks, int n, const float* poo
 void or_quant_q8(const float* m, int rows, int cols, int8_t* codes, uint16_t* scales);
 void or_quant_q4(const float* m, int rows, int cols, uint8_t* packed, uint16_t* sb);
 
+/* Vision encoder and mergers (oracle/vision.c; Sources/Engine/Engine.swift:189-246, 317-473;
+ * Shaders.swift:59-454; tools/reference/qwen3vl_ref.py:25-85, 165-216).  Dimensions from
+ * Sources/Engine/ModelFile.swift:31-45.  fp16 tensors are uint16_t bit patterns. */
+#define OR_VH 1024
+#define OR_VFF 4096
+#define OR_VNH 16
+#define OR_VHD 64
+#define OR_VQKV 3072
+#define OR_VPATCH 768
+#define OR_VLAYERS 24
+#define OR_VPOS 48
+#define OR_MH 4096
+#define OR_NPATCH_MAX 1024
+
+/* RGB8 [gh * 16][gw * 16][3] -> fp16 patches [gh * gw][768] in 2 x 2 merge-block order. */
+void or_vit_patchify(const uint8_t* rgb, int gh, int gw, uint16_t* out);
+/* Bilinear (align_corners) interpolation of the [48 * 48][1024] position table: [gh * gw][1024]. */
+void or_vit_pos_interp(const float* table, int gh, int gw, float* out);
+/* 2D RoPE table [gh * gw][32] of (cos, sin): row angles for j < 16, column angles after. */
+void or_vit_rope_table(int gh, int gw, float* out);
+/* LayerNorm (eps 1e-6) of rows of n floats to fp16. */
+void or_layernorm_f16(const float* x, const float* w, const float* b, int rows, int n, uint16_t* out);
+/* y[M][N] = X[M][K] W[N][K]^T + bias, fp16 operands, float32 result. */
+void or_linear_f16(const uint16_t* X, const uint16_t* W, const float* bias, int M, int N, int K, float* y);
+float or_gelu_tanh(float x);
+float or_gelu_erf(float x);
+/* Bidirectional attention: q, k, v fp16 [16][np][64] -> out fp16 [np][1024]. */
+void or_vit_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int np, uint16_t* out);
+/* The whole encoder over the vision tensors of an .icua image: pooler [np / 4][2048] and the three
+ * DeepStack outputs (entries may be NULL) [np / 4][2048], float32.  Returns 0, or -1 with
+ * or_vision_error() set. */
+int or_vision(const uint8_t* img, size_t len, const uint8_t* rgb, int gh, int gw, float* pooler,
+              float* const* deepstack);
+const char* or_vision_error(void);
+/* Block l of the tower on the float32 residual x [gh * gw][1024] in place (test tap). */
+int or_vit_block(const uint8_t* img, size_t len, int l, float* x, int gh, int gw);
+
 /* Threads used by the OpenMP regions (0 = library default). */
 void or_set_threads(int n);
 int or_get_threads(void);

@@ -67,6 +67,19 @@ def lib():
                                          C.c_int, C.c_int, C.c_int, C.c_int, _i32p]
         L.or_quant_q8.argtypes = [_f32p, C.c_int, C.c_int, C.c_void_p, _u16p]
         L.or_quant_q4.argtypes = [_f32p, C.c_int, C.c_int, _u8p, _u16p]
+        L.or_vit_patchify.argtypes = [_u8p, C.c_int, C.c_int, _u16p]
+        L.or_vit_pos_interp.argtypes = [_f32p, C.c_int, C.c_int, _f32p]
+        L.or_vit_rope_table.argtypes = [C.c_int, C.c_int, _f32p]
+        L.or_layernorm_f16.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, _u16p]
+        L.or_linear_f16.argtypes = [_u16p, _u16p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]
+        L.or_gelu_tanh.argtypes = [C.c_float]
+        L.or_gelu_tanh.restype = C.c_float
+        L.or_gelu_erf.argtypes = [C.c_float]
+        L.or_gelu_erf.restype = C.c_float
+        L.or_vit_attention.argtypes = [_u16p, _u16p, _u16p, C.c_int, _u16p]
+        L.or_vision.argtypes = [C.c_void_p, C.c_size_t, _u8p, C.c_int, C.c_int, _f32p, C.c_void_p]
+        L.or_vision_error.restype = C.c_char_p
+        L.or_vit_block.argtypes = [C.c_void_p, C.c_size_t, C.c_int, _f32p, C.c_int, C.c_int]
         L.or_set_threads.argtypes = [C.c_int]
         L.or_get_threads.restype = C.c_int
         _lib = L
@@ -246,3 +259,93 @@ class OracleModel:
         if rc:
             raise RuntimeError("oracle: " + lib().or_last_error().decode())
         return out, margins, first
+
+
+# ---------------------------------------------------------------------------------------------
+# Vision encoder (oracle/vision.c).  fp16 arrays travel as uint16 bit patterns.
+
+VH, VPATCH, VNH, VHD = 1024, 768, 16, 64
+
+
+def _u16(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint16) if a.dtype == np.float16 else np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def vit_patchify(rgb: np.ndarray) -> np.ndarray:
+    """RGB8 [16 gh][16 gw][3] -> fp16 patches [gh * gw][768] in 2 x 2 merge-block order."""
+    rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+    gh, gw = rgb.shape[0] // 16, rgb.shape[1] // 16
+    out = np.empty((gh * gw, VPATCH), dtype=np.uint16)
+    lib().or_vit_patchify(rgb.reshape(-1), gh, gw, out)
+    return out.view(np.float16)
+
+
+def vit_pos_interp(table: np.ndarray, gh: int, gw: int) -> np.ndarray:
+    out = np.empty((gh * gw, VH), dtype=np.float32)
+    lib().or_vit_pos_interp(np.ascontiguousarray(table, dtype=np.float32), gh, gw, out)
+    return out
+
+
+def vit_rope_table(gh: int, gw: int) -> np.ndarray:
+    out = np.empty((gh * gw, 32, 2), dtype=np.float32)
+    lib().or_vit_rope_table(gh, gw, out)
+    return out
+
+
+def layernorm_f16(x: np.ndarray, w: np.ndarray, b: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, n = x.shape
+    out = np.empty((rows, n), dtype=np.uint16)
+    lib().or_layernorm_f16(x, np.ascontiguousarray(w, dtype=np.float32), np.ascontiguousarray(b, dtype=np.float32),
+                           rows, n, out)
+    return out.view(np.float16)
+
+
+def linear_f16(x: np.ndarray, w: np.ndarray, bias: np.ndarray) -> np.ndarray:
+    x, w = _u16(x), _u16(w)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), dtype=np.float32)
+    lib().or_linear_f16(x, w, np.ascontiguousarray(bias, dtype=np.float32), M, N, K, y)
+    return y
+
+
+def gelu_tanh(x: float) -> float:
+    return lib().or_gelu_tanh(x)
+
+
+def gelu_erf(x: float) -> float:
+    return lib().or_gelu_erf(x)
+
+
+def vit_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """q, k, v fp16 [16][np][64] -> fp16 [np][1024]."""
+    np_ = q.shape[1]
+    out = np.empty((np_, VH), dtype=np.uint16)
+    lib().or_vit_attention(_u16(q).reshape(-1), _u16(k).reshape(-1), _u16(v).reshape(-1), np_, out)
+    return out.view(np.float16)
+
+
+def vision(image: np.ndarray, rgb: np.ndarray):
+    """The encoder over an .icua image's vision tensors: (pooler, [deepstack x 3]) float32
+    [np / 4][2048] each."""
+    rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+    gh, gw = rgb.shape[0] // 16, rgb.shape[1] // 16
+    nvis = gh * gw // 4
+    pooler = np.empty((nvis, H), dtype=np.float32)
+    ds = [np.empty((nvis, H), dtype=np.float32) for _ in range(3)]
+    arr = (C.c_void_p * 3)(*[d.ctypes.data for d in ds])
+    img = np.ascontiguousarray(image, dtype=np.uint8)
+    if lib().or_vision(img.ctypes.data_as(C.c_void_p), img.size, rgb.reshape(-1), gh, gw, pooler, arr) != 0:
+        raise RuntimeError(lib().or_vision_error().decode())
+    return pooler, ds
+
+
+def vit_block(image: np.ndarray, l: int, x: np.ndarray, gh: int, gw: int) -> np.ndarray:
+    """Block l of the tower on residual rows x [gh * gw][1024] (returns the updated rows)."""
+    out = np.array(x, dtype=np.float32, order="C")
+    img = np.ascontiguousarray(image, dtype=np.uint8)
+    if lib().or_vit_block(img.ctypes.data_as(C.c_void_p), img.size, l, out, gh, gw) != 0:
+        raise RuntimeError(lib().or_vision_error().decode())
+    return out
