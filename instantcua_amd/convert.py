@@ -9,9 +9,10 @@ Mirrors ``Converter`` of Sources/Engine/Convert.swift:
   with the reference's float32 arithmetic.
 * ``convert`` (Convert.swift:156-206): the language-backbone part of ``Converter.convert`` --
   embed_tokens, the final norm and, per layer, the four norm vectors and the fused q|k|v, o,
-  gate|up and down matrices, in the given weight format.  The vision encoder and its mergers
-  (Convert.swift:93-154) are not converted: the decoder does not read them, and their tensor
-  ids stay empty in the output.
+  gate|up and down matrices, in the given weight format.
+* ``vision_tensors`` (Convert.swift:93-154): the vision tower and its four mergers, when the
+  checkpoint holds them -- fp16 matrices, float32 biases, norms and position table, and the
+  patch embedding with its two temporal slices summed in float32 (the image is one frame).
 """
 from __future__ import annotations
 
@@ -127,6 +128,50 @@ def _emit(fmt: int, m: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return c, s
 
 
+def vision_tensors(st: "SafeTensors") -> Dict[int, np.ndarray]:
+    """The vision tower and mergers of Converter.convert (Convert.swift:93-154), by tensor id."""
+    VH, VF, MH = Dims.vit_hidden, Dims.vit_ff, Dims.merger_hidden
+    out: Dict[int, np.ndarray] = {}
+
+    def f32(name, n):
+        v = st.floats(name)[1]
+        if v.size != n:
+            raise ValueError(f"{name}: {v.size} values, expected {n}")
+        return np.ascontiguousarray(v, dtype=np.float32)
+
+    f16 = lambda name, n: f32(name, n).astype(np.float16)  # noqa: E731  Float16(x), nearest even
+    pw = f32("model.visual.patch_embed.proj.weight", VH * 3 * 2 * 256).reshape(VH, 3, 2, 256)
+    out[TensorID.vit_patch_w] = (pw[:, :, 0] + pw[:, :, 1]).astype(np.float16).reshape(-1)  # Convert.swift:97-112
+    out[TensorID.vit_patch_b] = f32("model.visual.patch_embed.proj.bias", VH)
+    out[TensorID.vit_pos_emb] = f32("model.visual.pos_embed.weight", Dims.vit_pos_grid ** 2 * VH)
+    for l in range(Dims.vit_layers):
+        p = f"model.visual.blocks.{l}."
+        V = lambda k: TensorID.vit_layer(l, k)  # noqa: E731
+        out[V(TensorID.v_norm1_w)] = f32(p + "norm1.weight", VH)
+        out[V(TensorID.v_norm1_b)] = f32(p + "norm1.bias", VH)
+        out[V(TensorID.v_qkv_w)] = f16(p + "attn.qkv.weight", Dims.vit_qkv_rows * VH)
+        out[V(TensorID.v_qkv_b)] = f32(p + "attn.qkv.bias", Dims.vit_qkv_rows)
+        out[V(TensorID.v_proj_w)] = f16(p + "attn.proj.weight", VH * VH)
+        out[V(TensorID.v_proj_b)] = f32(p + "attn.proj.bias", VH)
+        out[V(TensorID.v_norm2_w)] = f32(p + "norm2.weight", VH)
+        out[V(TensorID.v_norm2_b)] = f32(p + "norm2.bias", VH)
+        out[V(TensorID.v_fc1_w)] = f16(p + "mlp.linear_fc1.weight", VF * VH)
+        out[V(TensorID.v_fc1_b)] = f32(p + "mlp.linear_fc1.bias", VF)
+        out[V(TensorID.v_fc2_w)] = f16(p + "mlp.linear_fc2.weight", VH * VF)
+        out[V(TensorID.v_fc2_b)] = f32(p + "mlp.linear_fc2.bias", VH)
+    for i in range(Dims.num_deepstack + 1):
+        p = f"model.visual.deepstack_merger_list.{i}." if i < Dims.num_deepstack else "model.visual.merger."
+        nn = MH if i < Dims.num_deepstack else VH  # post-shuffle norm over 4096, final merger over 1024
+        M = lambda k: TensorID.merger(i, k)  # noqa: E731
+        out[M(TensorID.m_norm_w)] = f32(p + "norm.weight", nn)
+        out[M(TensorID.m_norm_b)] = f32(p + "norm.bias", nn)
+        out[M(TensorID.m_fc1_w)] = f16(p + "linear_fc1.weight", MH * MH)
+        out[M(TensorID.m_fc1_b)] = f32(p + "linear_fc1.bias", MH)
+        out[M(TensorID.m_fc2_w)] = f16(p + "linear_fc2.weight", Dims.hidden * MH)
+        out[M(TensorID.m_fc2_b)] = f32(p + "linear_fc2.bias", Dims.hidden)
+    return out
+
+
 def convert(hf_dir: str, output: str, fmt: int, layers: Optional[int] = None, log=print) -> int:
     """Converter.convert (Convert.swift:83-206) for the language backbone; returns the file size.
 
@@ -136,6 +181,9 @@ def convert(hf_dir: str, output: str, fmt: int, layers: Optional[int] = None, lo
     n_layers = Dims.layers if layers is None else int(layers)
     H, F, V = Dims.hidden, Dims.ff, Dims.vocab
     out: Dict[int, np.ndarray] = {}
+    if "model.visual.patch_embed.proj.weight" in st.entries:
+        out.update(vision_tensors(st))
+        log("vision encoder & mergers done")
 
     def f32(name):
         return st.floats(name)[1]

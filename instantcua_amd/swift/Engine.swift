@@ -33,6 +33,7 @@ public final class Engine {
     }
     public var usePrefixCache: Bool = true { didSet { applyFlags() } }
     public var useGrammarPairs: Bool = false { didSet { applyFlags() } }
+    public var useVisionDeltaCache: Bool = true { didSet { applyFlags() } }
 
     public struct Timing {
         public var visionMs = 0.0, prefillMs = 0.0, decodeMs = 0.0, totalMs = 0.0
@@ -65,6 +66,7 @@ public final class Engine {
         var f: UInt32 = 0
         if usePrefixCache { f |= UInt32(ICUA_FLAG_PREFIX_CACHE.rawValue) }
         if useGrammarPairs { f |= UInt32(ICUA_FLAG_GRAMMAR_PAIRS.rawValue) }
+        if useVisionDeltaCache { f |= UInt32(ICUA_FLAG_VISION_DELTA_CACHE.rawValue) }
         _ = icua_set_flags(handle, f)
     }
 
@@ -98,6 +100,19 @@ public final class Engine {
         var n: Int32 = 0
         let rc = tokens.withUnsafeBufferPointer { t in
             icua_generate(handle, t.baseAddress, Int32(tokens.count), Int32(visOffset), Int32(maxNewTokens), &out, &n)
+        }
+        return rc == 0 ? Array(out[0..<Int(n)]) : []
+    }
+
+    /// generateVision (Engine.swift:696-827) on an RGB8 frame [height][width][3]: vision tower
+    /// (skipped on an identical frame when useVisionDeltaCache), prefill, greedy decode.
+    public func generateVision(rgbBytes: UnsafeRawPointer, width: Int = 640, height: Int = 384,
+                               tokens: [Int32], maxNewTokens: Int = 64) -> [Int32] {
+        var out = [Int32](repeating: 0, count: max(maxNewTokens, 1) + 4)
+        var n: Int32 = 0
+        let rc = tokens.withUnsafeBufferPointer { t in
+            icua_generate_vision(handle, rgbBytes.assumingMemoryBound(to: UInt8.self), Int32(width), Int32(height),
+                                 t.baseAddress, Int32(tokens.count), Int32(maxNewTokens), &out, &n)
         }
         return rc == 0 ? Array(out[0..<Int(n)]) : []
     }
