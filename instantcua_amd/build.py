@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "libicua.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["engine.hip", "gemv.hip", "attention.hip", "misc.hip", "persist.hip", "prefill.hip", "quant.hip", "vision.hip"]
+SOURCES = ["engine.hip", "gemv.hip", "attention.hip", "misc.hip", "persist.hip", "prefill.hip", "quant.hip", "vision.hip", "tokenizer.cpp"]
 
 # Packed-FP32 instructions are disabled for every device pass (the host pass ignores the
 # feature with a warning).

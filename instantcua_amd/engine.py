@@ -38,6 +38,10 @@ EXPORTS = [
     "icua_read_kv", "icua_write_kv", "icua_read_buffer", "icua_dev_alloc", "icua_dev_free", "icua_memcpy_h2d",
     "icua_memcpy_d2h", "icua_device_sync", "icua_repack", "icua_gemv", "icua_gemv_bench", "icua_dequant",
     "icua_quantize", "icua_quantize_bench", "icua_vision", "icua_generate_vision",
+    # include/icua_tok.h
+    "icua_tok_last_error", "icua_tok_open", "icua_tok_close", "icua_tok_vocab_size", "icua_tok_special_id",
+    "icua_tok_encode", "icua_tok_encode_chat", "icua_tok_encode_vision_chat", "icua_tok_token_bytes",
+    "icua_tok_decode", "icua_tok_stream_new", "icua_tok_stream_free", "icua_tok_stream_push",
 ]
 
 

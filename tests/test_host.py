@@ -105,9 +105,11 @@ def test_bench_byte_model_matches_survey_figures():
 # C ABI library (no GPU needed)
 
 def _header_functions():
-    with open(os.path.join(ROOT, "include", "icua.h")) as f:
-        text = f.read()
-    return sorted(set(re.findall(r"\b(icua_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in ("icua.h", "icua_tok.h"):
+        with open(os.path.join(ROOT, "include", h)) as f:
+            names |= set(re.findall(r"\b(icua_[a-z0-9_]+)\s*\(", f.read()))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")
