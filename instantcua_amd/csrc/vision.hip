@@ -77,6 +77,19 @@ __global__ __launch_bounds__(256) void vit_layernorm_kernel(const float* __restr
     }
 }
 
+// Barrier for LDS filled by global-to-LDS loads: this wave waits until at most `pending` of its
+// vector-memory loads are outstanding (expcnt and lgkmcnt at their maximum), then all waves meet.
+// __syncthreads() would also drain every load in flight, which empties the load pipeline; the
+// empty asm statements keep the compiler from moving memory accesses across the barrier.
+template <int pending>
+__device__ __forceinline__ void dma_barrier() {
+    static_assert(pending >= 0 && pending <= 63, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((pending & 15) | (7 << 4) | (15 << 8) | ((pending >> 4) << 14));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
 }
@@ -85,84 +98,73 @@ __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + e
 // C[m][n] = sum_k X[m][k] W[n][k] over fp16 X [M][K] and W [N][K].  Workgroup tile BN x BM
 // (outputs x tokens), 4 waves in a WN x WM grid; each wave holds TN x TM 16 x 16 accumulators.
 // W rows are the A operand and X rows the B operand of v_mfma_f32_16x16x32_f16, so lane l
-// ends with C[m = l % 16][n = 4 (l / 16) + i], four consecutive outputs of one token.  K runs
-// in steps of 64 through double-buffered LDS tiles padded to 72 halves a row (the 16 rows a
-// fragment read touches fall in distinct banks).  Token rows past M read row M - 1 and are not
+// ends with C[m = l % 16][n = 4 (l / 16) + i], four consecutive outputs of one token.
+//
+// K runs in steps of 64 through a ring of S LDS stages filled by direct global-to-LDS loads
+// (global_load_lds_dwordx4, 16 bytes a lane), S - 1 steps ahead of the products.  A stage
+// holds 128-byte rows; the 16-byte chunk c of row r sits at chunk c ^ (r % 8), so the 16 rows
+// of a fragment read spread over the banks.  Token rows past M read row M - 1 and are not
 // stored.
-template <int BN, int BM, int WN, int WM, int MODE>
+template <int BN, int BM, int WN, int WM, int MODE, int S = 4>
 __global__ __launch_bounds__(256) void vit_gemm_kernel(VitGemmArgs g) {
 #pragma clang fp contract(off)
-    constexpr int TN = BN / WN / 16, TM = BM / WM / 16, BK = 64, LROW = BK + 8;
-    constexpr int WCH = BN * 8 / 256, XCH = BM * 8 / 256;  // 16-byte chunks per thread
-    static_assert(WN * WM == 4 && TN >= 1 && TM >= 1 && WCH >= 1 && XCH >= 1, "tile");
+    constexpr int TN = BN / WN / 16, TM = BM / WM / 16, BK = 64;
+    constexpr int WLOADS = (BN + BM) / 8;  // 1 KiB wave loads per stage (8 rows each)
+    constexpr int L = WLOADS / 4;          // per wave
+    static_assert(WN * WM == 4 && TN >= 1 && TM >= 1 && WLOADS % 4 == 0 && S >= 2 && (S - 2) * L <= 63, "tile");
     static_assert(MODE != VG_QKV || (BN == 64 && WN == 1), "the RoPE pairs (d, d + 32) of a head stay in one lane");
-    __shared__ __align__(16) uint16_t Ws[2][BN * LROW];
-    __shared__ __align__(16) uint16_t Xs[2][BM * LROW];
+    __shared__ __align__(1024) uint8_t ring[S][(BN + BM) * 128];
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, r16 = lane & 15, q4 = lane >> 4;
     const int wn = wave / WM, wm = wave % WM;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-    const int K = g.K;
-
-    // Register-staged tile loads (macros, not lambdas: arrays captured by reference stay in
-    // scratch memory).
-    uint4 wr[WCH], xr[XCH];
-#define VG_GLOAD(kt_)                                                               \
-    do {                                                                            \
-        const int k0_ = (kt_) * BK;                                                 \
-        _Pragma("unroll") for (int c = 0; c < WCH; ++c) {                            \
-            const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;      \
-            wr[c] = *(const uint4*)(g.W + (size_t)(n0 + row) * K + k0_ + col);      \
-        }                                                                           \
-        _Pragma("unroll") for (int c = 0; c < XCH; ++c) {                            \
-            const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;      \
-            const int m = min(m0 + row, g.M - 1);                                   \
-            xr[c] = *(const uint4*)(g.X + (size_t)m * K + k0_ + col);               \
-        }                                                                           \
-    } while (0)
-#define VG_LSTORE(buf_)                                                             \
-    do {                                                                            \
-        _Pragma("unroll") for (int c = 0; c < WCH; ++c) {                            \
-            const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;      \
-            *(uint4*)&Ws[buf_][row * LROW + col] = wr[c];                            \
-        }                                                                           \
-        _Pragma("unroll") for (int c = 0; c < XCH; ++c) {                            \
-            const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;      \
-            *(uint4*)&Xs[buf_][row * LROW + col] = xr[c];                            \
-        }                                                                           \
-    } while (0)
+    const int K = g.K, nk = K / BK;
+    // Lane l of wave load j (rows 8 j .. 8 j + 7 of the stage: W rows first, then X rows) lands at
+    // row 8 j + l / 8, chunk l % 8, and reads source chunk (l % 8) ^ (l / 8).
+    const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+    auto issue = [&](int kt) __attribute__((always_inline)) {
+        uint8_t* st = ring[kt % S];
+        const int k0 = kt * BK + 8 * lchunk;
+#pragma unroll
+        for (int u = 0; u < L; ++u) {
+            const int j = wave + 4 * u, row = 8 * j + lrow;
+            const uint16_t* src = row < BN ? g.W + (size_t)(n0 + row) * K + k0
+                                           : g.X + (size_t)min(m0 + row - BN, g.M - 1) * K + k0;
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(st + 1024 * j), 16, 0, 0);
+        }
+    };
+    auto frag = [&](const uint8_t* st, int row, int chunk) __attribute__((always_inline)) {
+        return *(const v8h*)(st + row * 128 + ((chunk ^ (row & 7)) << 4));
+    };
 
     f32x4 acc[TN][TM];
 #pragma unroll
     for (int a = 0; a < TN; ++a)
 #pragma unroll
         for (int b = 0; b < TM; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int nk = K / BK;
-    VG_GLOAD(0);
-    VG_LSTORE(0);
-    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < S - 1; ++p) issue(min(p, nk - 1));
     for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        VG_GLOAD(min(kt + 1, nk - 1));  // unconditional: a conditional keeps wr / xr in scratch
+        // This wave's loads of step kt have landed once at most (S - 2) * L newer ones are
+        // outstanding; after the barrier every wave's have, and the stage read in step kt - 1
+        // is free (its reads completed before each wave's products of that step).
+        dma_barrier<(S - 2) * L>();
+        issue(min(kt + S - 1, nk - 1));  // past the end: a repeat into a stage no one reads again
+        const uint8_t* st = ring[kt % S];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             v8h af[TN], bf[TM];
 #pragma unroll
-            for (int a = 0; a < TN; ++a)
-                af[a] = *(const v8h*)&Ws[buf][((wn * TN + a) * 16 + r16) * LROW + 32 * ks + 8 * q4];
+            for (int a = 0; a < TN; ++a) af[a] = frag(st, (wn * TN + a) * 16 + r16, 4 * ks + q4);
 #pragma unroll
-            for (int b = 0; b < TM; ++b)
-                bf[b] = *(const v8h*)&Xs[buf][((wm * TM + b) * 16 + r16) * LROW + 32 * ks + 8 * q4];
+            for (int b = 0; b < TM; ++b) bf[b] = frag(st, BN + (wm * TM + b) * 16 + r16, 4 * ks + q4);
 #pragma unroll
             for (int a = 0; a < TN; ++a)
 #pragma unroll
                 for (int b = 0; b < TM; ++b)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
         }
-        VG_LSTORE(buf ^ 1);  // the last one fills the idle buffer
-        __syncthreads();
     }
-#undef VG_GLOAD
-#undef VG_LSTORE
+    __builtin_amdgcn_s_waitcnt(0);  // no load is in flight when the workgroup ends
 
     const int N = g.N;
 #pragma unroll
@@ -239,19 +241,23 @@ __global__ __launch_bounds__(256) void vit_gemm_kernel(VitGemmArgs g) {
 }
 
 // Bidirectional attention of one head over all patches (k_vit_attn, Shaders.swift:294-395),
-// grid (ceil(np / 64), 16 heads).  Wave w owns queries 64 x + 16 w .. + 15, lane l query l % 16.
-// Per block of 64 keys: S^T = K . Q^T on v_mfma_f32_16x16x32_f16 (lane: keys 16 j + 4 (l / 16) + i
-// of sub-block j), scaled by 1/8; an online softmax per query column; O^T += V^T . P^T on
-// v_mfma_f32_16x16x16_f16 with the fp16 probabilities straight from the score registers and
-// V^T read from LDS.  Keys past np are masked (their cache rows hold finite values).
-__global__ __launch_bounds__(256) void vit_attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+// grid (ceil(np / 64), 16 heads), 8 waves.  Waves w and w + 4 own the same 16 queries,
+// 64 x + 16 (w % 4) .. + 15 (lane l: query l % 16), and split the key blocks in two halves, so the
+// serial chain of block loads is half as long.  Per block of 64 keys: S^T = K . Q^T on
+// v_mfma_f32_16x16x32_f16 (lane: keys 16 j + 4 (l / 16) + i of sub-block j), scaled by 1/8; an
+// online softmax per query column; O^T += V^T . P^T on v_mfma_f32_16x16x16_f16 with the fp16
+// probabilities straight from the score registers and V^T read from LDS.  The two halves'
+// (max, sum, O) are combined through LDS.  Keys past np are masked (their rows hold finite
+// values).
+__global__ __launch_bounds__(512) void vit_attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                             const uint16_t* __restrict__ vt, uint16_t* __restrict__ out,
                                                             int np, int ld) {
-    constexpr int ROW = 72;
-    __shared__ __align__(16) uint16_t Ks[2][64 * ROW];
-    __shared__ __align__(16) uint16_t Vs[2][64 * ROW];
-    const int h = blockIdx.y, tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, r16 = lane & 15, q4 = lane >> 4;
-    const int qt = blockIdx.x * 64 + wave * 16 + r16;
+    constexpr int ROW = 72, TILE = 64 * ROW;
+    __shared__ __align__(16) uint16_t lds[2][2][2][TILE];  // [key half][K, V^T][buffer]
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, r16 = lane & 15, q4 = lane >> 4;
+    const int grp = wave >> 2, gt = tid & 255;
+    const int h = blockIdx.y;
+    const int qt = blockIdx.x * 64 + (wave & 3) * 16 + r16;
     const uint16_t* qh = q + (size_t)h * ld * VHD;
     const uint16_t* kh = k + (size_t)h * ld * VHD;
     const uint16_t* vh = vt + (size_t)h * VHD * ld;
@@ -260,11 +266,12 @@ __global__ __launch_bounds__(256) void vit_attention_kernel(const uint16_t* __re
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) qf[ks] = *(const v8h*)(qh + (size_t)qc * VHD + 32 * ks + 8 * q4);
 
+    // Register-staged block loads by the 256 threads of a half (macros: see vit_gemm_kernel).
     uint4 kr[2], vr[2];
 #define VA_GLOAD(blk_)                                                              \
     do {                                                                            \
         _Pragma("unroll") for (int c = 0; c < 2; ++c) {                              \
-            const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;      \
+            const int idx = gt + 256 * c, row = idx >> 3, col = (idx & 7) * 8;       \
             kr[c] = *(const uint4*)(kh + (size_t)(64 * (blk_) + row) * VHD + col);   \
             vr[c] = *(const uint4*)(vh + (size_t)row * ld + 64 * (blk_) + col);      \
         }                                                                           \
@@ -272,89 +279,111 @@ __global__ __launch_bounds__(256) void vit_attention_kernel(const uint16_t* __re
 #define VA_LSTORE(buf_)                                                             \
     do {                                                                            \
         _Pragma("unroll") for (int c = 0; c < 2; ++c) {                              \
-            const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;      \
-            *(uint4*)&Ks[buf_][row * ROW + col] = kr[c];                             \
-            *(uint4*)&Vs[buf_][row * ROW + col] = vr[c];                             \
+            const int idx = gt + 256 * c, row = idx >> 3, col = (idx & 7) * 8;       \
+            *(uint4*)&lds[grp][0][buf_][row * ROW + col] = kr[c];                    \
+            *(uint4*)&lds[grp][1][buf_][row * ROW + col] = vr[c];                    \
         }                                                                           \
     } while (0)
 
-    const int nblk = (np + 63) / 64;
+    const int nblk = (np + 63) / 64, nh = (nblk + 1) / 2;
+    const int b0 = grp * nh, bend = min(nblk, b0 + nh);  // this half's blocks [b0, bend)
     float m_run = -__builtin_inff(), l_run = 0.f;
     f32x4 O[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    VA_GLOAD(0);
+    VA_GLOAD(min(b0, nblk - 1));
     VA_LSTORE(0);
     __syncthreads();
-    for (int blk = 0; blk < nblk; ++blk) {
-        const int buf = blk & 1;
-        VA_GLOAD(min(blk + 1, nblk - 1));
-        f32x4 S[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            S[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const v8h kf = *(const v8h*)&Ks[buf][(16 * j + r16) * ROW + 32 * ks + 8 * q4];
-                S[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], S[j], 0, 0, 0);
-            }
-        }
-        float mb = -__builtin_inff();
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = 64 * blk + 16 * j + 4 * q4 + i;
-                S[j][i] = key < np ? S[j][i] * 0.125f : -__builtin_inff();
-                mb = fmaxf(mb, S[j][i]);
-            }
-        mb = max_x4(mb);  // finite: key 64 blk < np
-        const float m_new = fmaxf(m_run, mb);
-        const float corr = expf(m_run - m_new);
-        float ls = 0.f;
-        v4h P[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = expf(S[j][i] - m_new);
-                ls += p;
-                P[j][i] = (_Float16)p;
-            }
-        l_run = l_run * corr + sum_x4(ls);
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) O[dt][i] *= corr;
+    for (int it = 0; it < nh; ++it) {
+        const int blk = b0 + it, buf = it & 1;
+        VA_GLOAD(min(blk + 1, nblk - 1));  // unconditional (a valid block either way)
+        if (blk < bend) {
+            const uint16_t* Ks = lds[grp][0][buf];
+            const uint16_t* Vs = lds[grp][1][buf];
+            f32x4 S[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const v4h vf = *(const v4h*)&Vs[buf][(16 * dt + r16) * ROW + 16 * j + 4 * q4];
-                O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, P[j], O[dt], 0, 0, 0);
+                S[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const v8h kf = *(const v8h*)&Ks[(16 * j + r16) * ROW + 32 * ks + 8 * q4];
+                    S[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], S[j], 0, 0, 0);
+                }
+            }
+            float mb = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = 64 * blk + 16 * j + 4 * q4 + i;
+                    S[j][i] = key < np ? S[j][i] * 0.125f : -__builtin_inff();
+                    mb = fmaxf(mb, S[j][i]);
+                }
+            mb = max_x4(mb);  // finite: key 64 blk < np
+            const float m_new = fmaxf(m_run, mb);
+            const float corr = expf(m_run - m_new);
+            float ls = 0.f;
+            v4h P[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = expf(S[j][i] - m_new);
+                    ls += p;
+                    P[j][i] = (_Float16)p;
+                }
+            l_run = l_run * corr + sum_x4(ls);
+            m_run = m_new;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[dt][i] *= corr;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const v4h vf = *(const v4h*)&Vs[(16 * dt + r16) * ROW + 16 * j + 4 * q4];
+                    O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, P[j], O[dt], 0, 0, 0);
+                }
             }
         }
-        VA_LSTORE(buf ^ 1);
+        VA_LSTORE(buf ^ 1);  // the last fills an idle buffer
         __syncthreads();
     }
 #undef VA_GLOAD
 #undef VA_LSTORE
-    if (qt < np) {
-        const float inv = 1.0f / l_run;
+    // Combine the halves: the second half's state goes through LDS (every tile read is done).
+    float* xo = (float*)&lds[0][0][0][0];  // [256 lanes][18]
+    if (grp == 1) {
+        float* d = xo + (size_t)gt * 18;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) d[4 * dt + i] = O[dt][i];
+        d[16] = m_run;
+        d[17] = l_run;
+    }
+    __syncthreads();
+    if (grp == 0 && qt < np) {
+        const float* d = xo + (size_t)gt * 18;
+        const float m1 = d[16], m = fmaxf(m_run, m1);
+        const float f0 = expf(m_run - m), f1 = expf(m1 - m);  // m is finite: the first half is never empty
+        const float inv = 1.0f / (l_run * f0 + d[17] * f1);
         uint16_t* dst = out + (size_t)qt * VH + h * VHD;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-            const uint32_t h0 = f2h(O[dt][0] * inv), h1 = f2h(O[dt][1] * inv);
-            const uint32_t h2 = f2h(O[dt][2] * inv), h3 = f2h(O[dt][3] * inv);
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (O[dt][i] * f0 + d[4 * dt + i] * f1) * inv;
+            const uint32_t h0 = f2h(o[0]), h1 = f2h(o[1]), h2 = f2h(o[2]), h3 = f2h(o[3]);
             *(uint2*)(dst + 16 * dt + 4 * q4) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
         }
     }
 }
 
-template <int BN, int BM, int WN, int WM, int MODE>
+template <int BN, int BM, int WN, int WM, int MODE, int S = 4>
 hipError_t gemm(const VitGemmArgs& g, hipStream_t s) {
     if (g.N % BN || g.K % 64 || g.M < 1) return hipErrorInvalidValue;
     const dim3 grid(g.N / BN, (g.M + BM - 1) / BM);
-    hipLaunchKernelGGL((vit_gemm_kernel<BN, BM, WN, WM, MODE>), grid, dim3(256), 0, s, g);
+    hipLaunchKernelGGL((vit_gemm_kernel<BN, BM, WN, WM, MODE, S>), grid, dim3(256), 0, s, g);
     return hipGetLastError();
 }
 
@@ -379,7 +408,7 @@ hipError_t merger(const VitMerger& mg, const uint16_t* xn, int nvis, uint16_t* h
     g.M = nvis;
     g.N = MH;
     g.K = MH;
-    VCK((gemm<64, 64, 2, 2, VG_GELU_ERF>(g, s)));
+    VCK((gemm<32, 64, 2, 2, VG_GELU_ERF>(g, s)));
     g = VitGemmArgs{};
     g.X = hbuf;
     g.W = mg.fc2w;
@@ -388,7 +417,7 @@ hipError_t merger(const VitMerger& mg, const uint16_t* xn, int nvis, uint16_t* h
     g.M = nvis;
     g.N = H;
     g.K = MH;
-    return gemm<32, 64, 2, 2, VG_F32>(g, s);
+    return gemm<32, 32, 2, 2, VG_F32>(g, s);
 }
 
 }  // namespace
@@ -407,7 +436,7 @@ hipError_t launch_vision(const VitWeights& w, const VitBuffers& b, int gh, int g
     g.M = np;
     g.N = VH;
     g.K = VPATCH;
-    VCK((gemm<64, 64, 2, 2, VG_F32_POS>(g, s)));
+    VCK((gemm<32, 64, 2, 2, VG_F32_POS>(g, s)));
     int ds = 0;
     for (int l = 0; l < VLAYERS; ++l) {
         const VitBlock& L = w.blk[l];
@@ -425,7 +454,7 @@ hipError_t launch_vision(const VitWeights& w, const VitBuffers& b, int gh, int g
         g.N = VQKV;
         g.K = VH;
         VCK((gemm<64, 64, 1, 4, VG_QKV>(g, s)));
-        hipLaunchKernelGGL(vit_attention_kernel, dim3((np + 63) / 64, VNH), dim3(256), 0, s, b.q, b.k, b.vt, b.attn, np,
+        hipLaunchKernelGGL(vit_attention_kernel, dim3((np + 63) / 64, VNH), dim3(512), 0, s, b.q, b.k, b.vt, b.attn, np,
                            NPATCH_MAX);
         VCK(hipGetLastError());
         g = VitGemmArgs{};
@@ -436,7 +465,7 @@ hipError_t launch_vision(const VitWeights& w, const VitBuffers& b, int gh, int g
         g.M = np;
         g.N = VH;
         g.K = VH;
-        VCK((gemm<64, 64, 2, 2, VG_F32_ADD>(g, s)));
+        VCK((gemm<32, 64, 2, 2, VG_F32_ADD>(g, s)));
         VCK(layernorm<VH>(b.x, L.n2w, L.n2b, b.xn, np, s));
         g = VitGemmArgs{};
         g.X = b.xn;
@@ -446,7 +475,7 @@ hipError_t launch_vision(const VitWeights& w, const VitBuffers& b, int gh, int g
         g.M = np;
         g.N = VFF;
         g.K = VH;
-        VCK((gemm<128, 64, 2, 2, VG_GELU_TANH>(g, s)));
+        VCK((gemm<128, 64, 2, 2, VG_GELU_TANH, 3>(g, s)));
         g = VitGemmArgs{};
         g.X = b.h;
         g.W = L.fc2w;
@@ -455,7 +484,7 @@ hipError_t launch_vision(const VitWeights& w, const VitBuffers& b, int gh, int g
         g.M = np;
         g.N = VH;
         g.K = VFF;
-        VCK((gemm<64, 64, 2, 2, VG_F32_ADD>(g, s)));
+        VCK((gemm<32, 64, 2, 2, VG_F32_ADD>(g, s)));
         if (l == 5 || l == 11 || l == 17) {
             // DeepStack merger: LayerNorm over each 2 x 2 block's 4096 values (Engine.swift:420-447).
             VCK(layernorm<MH>(b.x, w.mg[ds].nw, w.mg[ds].nb, b.xn, nvis, s));
