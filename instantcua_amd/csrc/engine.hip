@@ -117,6 +117,8 @@ struct icua_engine {
     float *attn = nullptr, *h = nullptr;
     uint16_t* kv = nullptr;
     int splits = 0;
+    float* kpart = nullptr;  // split-K partials of the down GEMV [3][MAXM][H]
+    int* kcnt = nullptr;     // its arrival counters [H / 16]
     int *counters = nullptr, *pidx = nullptr, *out_tokens = nullptr, *prompt = nullptr, *argmax_rows = nullptr;
     State* st = nullptr;
     float* pooler = nullptr;
@@ -215,6 +217,8 @@ struct icua_engine {
         a.y = x;
         a.ds = (has_ds && l < 3) ? ds[l] : nullptr;
         a.ds_row0 = row0;
+        a.kpart = kpart;
+        a.kcnt = kcnt;
         HIPCK(launch_gemv(fmt, GEMV_DOWN, a, mt, stream));
         return 0;
     }
@@ -396,6 +400,9 @@ struct icua_engine {
         HIPCK(hipMalloc(&rope, sizeof(float) * (size_t)maxctx * 128));
         splits = attention_splits(maxctx);
         HIPCK(hipMalloc(&part, sizeof(float) * (size_t)NKV * splits * MAXM * 2 * (HD + 2)));
+        HIPCK(hipMalloc(&kpart, sizeof(float) * 3 * MAXM * H));
+        HIPCK(hipMalloc(&kcnt, sizeof(int) * (H / 16)));
+        HIPCK(hipMemset(kcnt, 0, sizeof(int) * (H / 16)));
         HIPCK(hipMalloc(&counters, sizeof(int) * NKV));
         HIPCK(hipMemset(counters, 0, sizeof(int) * NKV));
         HIPCK(hipMalloc(&pval, sizeof(float) * MAXM * LMH_WAVES));
@@ -910,7 +917,7 @@ void icua_engine_destroy(icua_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     for (auto& g : e->graph)
         if (g) (void)hipGraphExecDestroy(g);
-    void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->pval,
+    void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->kpart, e->kcnt, e->pval,
                     e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
                     e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_layers, e->d_vision, e->vbuf};
     e->free_pf();

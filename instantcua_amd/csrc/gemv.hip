@@ -289,11 +289,18 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
     }
 
     const int r16 = lane % 16, lg = lane / 16;
-    for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
+    // K = 6144 residual GEMVs split along K: workgroup b takes segment b % NSEG of row block
+    // b / NSEG, and the last of a row block's workgroups to finish adds the partials in segment
+    // order (deterministic).  Every other GEMV walks whole row blocks.
+    constexpr bool SPLITK = (EPI == EPI_RESID && NSEG > 1);
+    const int seg_lo = SPLITK ? (int)(blockIdx.x % NSEG) : 0;
+    const int seg_hi = SPLITK ? seg_lo + 1 : NSEG;
+    const int rb_step = SPLITK ? nrb : (int)gridDim.x;
+    for (int rb = SPLITK ? (int)(blockIdx.x / NSEG) : (int)blockIdx.x; rb < nrb; rb += rb_step) {
         const int row = rb * 16 + r16;  // tiled row of this lane
         const uint8_t* wblk = a.w + (size_t)rb * NC * 1024;
         float acc[2] = {0.f, 0.f};
-        for (int seg = 0; seg < NSEG; ++seg) {
+        for (int seg = seg_lo; seg < seg_hi; ++seg) {
             // Weights of this wave's chunks, issued before the activation staging.
             uint4 wv[CPW];
 #pragma unroll
@@ -390,6 +397,39 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
             }
             __syncthreads();
         }
+        if constexpr (SPLITK) {
+            // Partials go out with device-scope stores (coherent across the XCDs' L2s) and are
+            // complete before the arrival is counted.
+            __shared__ int is_last;
+            if (wave == 0) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
+                    if (t < M)
+                        __hip_atomic_store(a.kpart + ((size_t)seg_lo * MAXM + t) * a.N + row, acc[j], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __builtin_amdgcn_s_waitcnt(0);
+            }
+            __syncthreads();
+            if (tid == 0)
+                is_last = __hip_atomic_fetch_add(a.kcnt + rb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == NSEG - 1;
+            __syncthreads();
+            if (!is_last) continue;
+            if (wave == 0) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
+                    float sum = 0.f;
+                    if (t < M)
+                        for (int sg = 0; sg < NSEG; ++sg)
+                            sum += __hip_atomic_load(a.kpart + ((size_t)sg * MAXM + t) * a.N + row, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                    acc[j] = sum;
+                }
+                if (lane == 0) __hip_atomic_store(a.kcnt + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
         if (wave == 0) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -472,9 +512,10 @@ static hipError_t gemv_fmt(GemvOp op, const GemvArgs& a, int mt, hipStream_t s) 
         case GEMV_GU:  // RMSNorm -> gate|up pairs -> SwiGLU
             return one ? launch_one<FMT, H, 4, 1, PRO_NORM, EPI_SWIGLU>(a, FF / 8, s)
                        : launch_one<FMT, H, 4, MAXM, PRO_NORM, EPI_SWIGLU>(a, FF / 8, s);
-        case GEMV_DOWN:  // SwiGLU output -> down rows, residual add
-            return one ? launch_one<FMT, FF, 4, 1, PRO_F32, EPI_RESID>(a, H / 16, s)
-                       : launch_one<FMT, FF, 4, MAXM, PRO_F32, EPI_RESID>(a, H / 16, s);
+        case GEMV_DOWN:  // SwiGLU output -> down rows, residual add; split along K in 3 segments
+            if (!a.kpart || !a.kcnt) return hipErrorInvalidValue;
+            return one ? launch_one<FMT, FF, 4, 1, PRO_F32, EPI_RESID>(a, H / 16 * (FF / SEG), s)
+                       : launch_one<FMT, FF, 4, MAXM, PRO_F32, EPI_RESID>(a, H / 16 * (FF / SEG), s);
         case GEMV_LMHEAD:  // final RMSNorm -> tied embedding rows -> argmax partials
             return one ? launch_one<FMT, H, 4, 1, PRO_NORM, EPI_ARGMAX>(a, LMH_WAVES, s)
                        : launch_one<FMT, H, 4, MAXM, PRO_NORM, EPI_ARGMAX>(a, LMH_WAVES, s);

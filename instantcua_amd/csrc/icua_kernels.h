@@ -35,6 +35,8 @@ struct GemvArgs {
     const State* st;
     int m_fixed;            // > 0: rows of the pass given by the host, else st->n
     int blocks;             // isolated GEMV launches: grid size
+    float* kpart;           // K = 6144 residual GEMV: per-segment partials [3][MAXM][N]
+    int* kcnt;              // and per-row-block arrival counters [N / 16], zero between launches
 };
 
 hipError_t launch_gemv(int fmt, GemvOp op, const GemvArgs& a, int mt, hipStream_t s);
