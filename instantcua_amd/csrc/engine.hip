@@ -117,6 +117,8 @@ struct icua_engine {
     float *attn = nullptr, *h = nullptr;
     uint16_t* kv = nullptr;
     int splits = 0;
+    uint8_t* apre = nullptr;  // pre-staged GEMV operands of multi-row passes
+    float* fxpre = nullptr;
     float* kpart = nullptr;  // split-K partials of the down GEMV [3][MAXM][H]
     int* kcnt = nullptr;     // its arrival counters [H / 16]
     int *counters = nullptr, *pidx = nullptr, *out_tokens = nullptr, *prompt = nullptr, *argmax_rows = nullptr;
@@ -166,6 +168,19 @@ struct icua_engine {
         return 0;
     }
 
+    // One GEMV of the pass.  Multi-row gate|up and lm_head passes stage their activation
+    // operands once in a separate launch first: their 768 / 1024 workgroups would otherwise each
+    // repeat the RMSNorm and the int8 slicing of every row, which makes them VALU-bound.  For the
+    // GEMVs of 128-256 workgroups the extra launch costs more than it saves.
+    int gemv(GemvOp op, GemvArgs& a, int mt) {
+        const bool pre = mt > 1 && (op == GEMV_GU || op == GEMV_LMHEAD);
+        a.apre = pre ? apre : nullptr;
+        a.fxpre = pre ? fxpre : nullptr;
+        if (pre) HIPCK(launch_gemv_prep(fmt, op, a, stream));
+        HIPCK(launch_gemv(fmt, op, a, mt, stream));
+        return 0;
+    }
+
     // encodeLLMLayer for the rows of the current pass (pos / n from the control block).
     int enqueue_layer(int l, int mt, int row0) {
         const LayerW& w = L[l];
@@ -179,7 +194,7 @@ struct icua_engine {
         a.x = x;
         a.norm_w = w.attn_norm;
         a.y = qkv;
-        HIPCK(launch_gemv(fmt, GEMV_QKV, a, mt, stream));
+        if (gemv(GEMV_QKV, a, mt)) return -1;
         // 2. q/k norm + M-RoPE + KV write + causal GQA attention.
         AttnArgs t{};
         t.qkv = qkv;
@@ -199,7 +214,7 @@ struct icua_engine {
         a.x = attn;
         a.norm_w = nullptr;
         a.y = x;
-        HIPCK(launch_gemv(fmt, GEMV_O, a, mt, stream));
+        if (gemv(GEMV_O, a, mt)) return -1;
         // 4. RMSNorm + gate|up + SwiGLU.
         a.w = w.wgu;
         a.sb = w.wgu_sb;
@@ -207,7 +222,7 @@ struct icua_engine {
         a.x = x;
         a.norm_w = w.mlp_norm;
         a.h = h;
-        HIPCK(launch_gemv(fmt, GEMV_GU, a, mt, stream));
+        if (gemv(GEMV_GU, a, mt)) return -1;
         // 5. Down projection + residual (+ DeepStack after layers 0-2 at visual rows).
         a.w = w.wd;
         a.sb = w.wd_sb;
@@ -219,7 +234,7 @@ struct icua_engine {
         a.ds_row0 = row0;
         a.kpart = kpart;
         a.kcnt = kcnt;
-        HIPCK(launch_gemv(fmt, GEMV_DOWN, a, mt, stream));
+        if (gemv(GEMV_DOWN, a, mt)) return -1;
         return 0;
     }
 
@@ -234,7 +249,7 @@ struct icua_engine {
         a.pval = pval;
         a.pidx = pidx;
         a.logits = logits;
-        HIPCK(launch_gemv(fmt, GEMV_LMHEAD, a, mt, stream));
+        if (gemv(GEMV_LMHEAD, a, mt)) return -1;
         CommitArgs c{};
         c.pval = pval;
         c.pidx = pidx;
@@ -400,6 +415,8 @@ struct icua_engine {
         HIPCK(hipMalloc(&rope, sizeof(float) * (size_t)maxctx * 128));
         splits = attention_splits(maxctx);
         HIPCK(hipMalloc(&part, sizeof(float) * (size_t)NKV * splits * MAXM * 2 * (HD + 2)));
+        HIPCK(hipMalloc(&apre, GEMV_PREP_BYTES));
+        HIPCK(hipMalloc(&fxpre, GEMV_PREP_FX_BYTES));
         HIPCK(hipMalloc(&kpart, sizeof(float) * 3 * MAXM * H));
         HIPCK(hipMalloc(&kcnt, sizeof(int) * (H / 16)));
         HIPCK(hipMemset(kcnt, 0, sizeof(int) * (H / 16)));
@@ -917,7 +934,7 @@ void icua_engine_destroy(icua_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     for (auto& g : e->graph)
         if (g) (void)hipGraphExecDestroy(g);
-    void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->kpart, e->kcnt, e->pval,
+    void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->kpart, e->kcnt, e->apre, e->fxpre, e->pval,
                     e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
                     e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_layers, e->d_vision, e->vbuf};
     e->free_pf();

@@ -76,16 +76,22 @@ struct Smem {
     }
 };
 
-// Stages the activation operands of segment `seg`, tokens [t0, t0 + TOK) of the pass, with NTHR
-// threads.  Each thread's units are loaded first (one memory round trip), then sliced.
-template <int FMT, int K, int PRO, int NTHR>
+// Stages the activation operands of columns [col0, col0 + COLS) of segment `seg`, tokens
+// [t0, t0 + TOK) of the pass, with NTHR threads, into the operand layout at Alds / fx (LDS, or
+// global memory for the pre-staged operands).  Each thread's units are loaded first (one memory
+// round trip), then sliced.
+// With FUSE (PRO_NORM, the whole row in one call, one unit per token per thread), the RMSNorm
+// scales come from the loaded values themselves: nscale is then LDS scratch of NTHR / 64 x MAXM
+// floats, and the call holds one workgroup barrier.
+template <int FMT, int K, int PRO, int NTHR, int COLS = SEG, bool FUSE = false>
 __device__ __forceinline__ void stage(const GemvArgs& a, int seg, int t0, int M, int row0, uint8_t* Alds, float* fx,
-                                      const float* nscale) {
+                                      const float* nscale, int col0 = 0) {
     constexpr int TOK = TileT<FMT>::TOK;
     constexpr int G = TileT<FMT>::G;
     constexpr int NG = SEG / G;
-    constexpr int NU = TOK * (SEG / 8) / NTHR;  // units per thread
-    static_assert(TOK * (SEG / 8) % NTHR == 0, "whole units per thread");
+    constexpr int NU = TOK * (COLS / 8) / NTHR;  // units per thread
+    static_assert(TOK * (COLS / 8) % NTHR == 0 && COLS % 64 == 0, "whole units per thread, whole groups");
+    static_assert(!FUSE || (PRO == PRO_NORM && COLS == K && NTHR == COLS / 8), "fused norm: unit j is token j's");
     const int tid = threadIdx.x;
     // One unit = 8 consecutive activations of one token; the units of a group sit in adjacent
     // lanes (G / 8 of them), so the group reductions are DPP steps.
@@ -93,8 +99,8 @@ __device__ __forceinline__ void stage(const GemvArgs& a, int seg, int t0, int M,
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
         const int u = tid + NTHR * j;
-        const int tl = u / (SEG / 8);
-        const int k0 = (u % (SEG / 8)) * 8;  // within the segment
+        const int tl = u / (COLS / 8);
+        const int k0 = col0 + (u % (COLS / 8)) * 8;  // within the segment
         const int t = t0 + tl;
         // Rows past the pass read row M - 1 and are zeroed: the loads stay unconditional, so the
         // compiler issues all of them before the first use.
@@ -104,15 +110,35 @@ __device__ __forceinline__ void stage(const GemvArgs& a, int seg, int t0, int M,
         vv[j][0] = in ? p0.x : 0.f; vv[j][1] = in ? p0.y : 0.f; vv[j][2] = in ? p0.z : 0.f; vv[j][3] = in ? p0.w : 0.f;
         vv[j][4] = in ? p1.x : 0.f; vv[j][5] = in ? p1.y : 0.f; vv[j][6] = in ? p1.z : 0.f; vv[j][7] = in ? p1.w : 0.f;
     }
+    float fsc[NU];
+    if constexpr (FUSE) {
+        float* red = (float*)nscale;
+        const int lane = tid % 64, wave = tid / 64;
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += vv[j][i] * vv[j][i];
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave * MAXM + j] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            float tot = 0.f;
+            for (int w = 0; w < NTHR / 64; ++w) tot += red[w * MAXM + j];
+            fsc[j] = 1.0f / sqrtf(tot / (float)K + EPS);
+        }
+    }
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
         const int u = tid + NTHR * j;
-        const int tl = u / (SEG / 8);
-        const int k0 = (u % (SEG / 8)) * 8;  // within the segment
+        const int tl = u / (COLS / 8);
+        const int k0 = col0 + (u % (COLS / 8)) * 8;  // within the segment
         const int t = t0 + tl;
         float* v = vv[j];
         if constexpr (PRO == PRO_NORM) {
-            const float sc = nscale[min(t, M - 1)];
+            const float sc = FUSE ? fsc[j] : nscale[min(t, M - 1)];
             const float* w = a.norm_w + seg * SEG + k0;
             const float4 w0 = ((const float4*)w)[0], w1 = ((const float4*)w)[1];
             v[0] = v[0] * sc * w0.x; v[1] = v[1] * sc * w0.y; v[2] = v[2] * sc * w0.z; v[3] = v[3] * sc * w0.w;
@@ -201,19 +227,9 @@ __device__ __forceinline__ void stage(const GemvArgs& a, int seg, int t0, int M,
     }
 }
 
-template <int FMT, int K, int KS, int MT, int PRO, int EPI>
-__global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
-    const State* st = a.st;
-    if (st->done) return;
-    using T = TileT<FMT>;
-    constexpr int NSEG = K / SEG;
-    constexpr int CPS = SEG / T::CHK;  // chunks per segment
-    constexpr int CPW = CPS / KS;      // chunks per wave per segment
-    static_assert(CPS % KS == 0, "chunks per segment must split evenly over the waves");
-    constexpr int NG = SEG / T::G;
-    constexpr int NC = K / T::CHK;  // chunks per row block
-
-    int M, row0;
+// Rows of the pass: M tokens from row row0 of the activations.
+template <int EPI, int MT>
+__device__ __forceinline__ void gemv_rows(const GemvArgs& a, const State* st, int& M, int& row0) {
     if (a.m_fixed > 0) {
         M = a.m_fixed;
         row0 = 0;
@@ -228,6 +244,75 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
         }
     }
     if (M > MT) M = MT;
+}
+
+// RMSNorm scale of every token over the full K (NTHR threads; red holds NTHR / 64 x MAXM
+// floats); the tokens' loads are issued together and reduced in one round.
+template <int K, int MT, int NTHR>
+__device__ __forceinline__ void norm_scales(const GemvArgs& a, int M, int row0, float* nscale, float* red) {
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    float ss[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) ss[t] = 0.f;
+#pragma unroll
+    for (int k = tid; k < K; k += NTHR) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {  // unconditional loads (row clamped), zero past the pass
+            const float v = a.x[(size_t)(row0 + min(t, M - 1)) * K + k];
+            ss[t] += t < M ? v * v : 0.f;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const float w = wave_sum(ss[t]);
+        if (lane == 0) red[wave * MAXM + t] = w;
+    }
+    __syncthreads();
+    if (tid < M) {
+        float tot = 0.f;
+        for (int w = 0; w < NTHR / 64; ++w) tot += red[w * MAXM + tid];
+        nscale[tid] = 1.0f / sqrtf(tot / (float)K + EPS);
+    }
+    __syncthreads();
+}
+
+// Pre-staging of a multi-row GEMV's activation operands, once per launch instead of once per
+// workgroup: workgroup (segment, pass, chunk of PREP_COLS columns) writes its part of the
+// operands and group factors in the LDS layout of gemv_kernel to a.apre [NSEG][NP][A_BYTES] and
+// a.fxpre [NSEG][NP][FX], RMSNorm (PRO_NORM) included.
+// One workgroup per (segment, pass) of SEG / 8 threads: every thread loads one unit of 8
+// activations of each token of the pass, once; RMSNorm takes its sums from those registers.
+template <int FMT, int K, int PRO, int EPI>
+__global__ __launch_bounds__(SEG / 8) void gemv_prep_kernel(GemvArgs a) {
+    const State* st = a.st;
+    if (st->done) return;
+    using T = TileT<FMT>;
+    constexpr int NSEG = K / SEG, NP = Smem<FMT>::passes(MAXM);
+    static_assert(PRO != PRO_NORM || NSEG == 1, "RMSNorm prologues take K = 2048");
+    int M, row0;
+    gemv_rows<EPI, MAXM>(a, st, M, row0);
+    const int p = blockIdx.x % NP, seg = blockIdx.x / NP;
+    if (p * T::TOK >= M) return;  // a pass the GEMV does not run
+    __shared__ float red[(SEG / 8 / 64) * MAXM];
+    stage<FMT, K, PRO, SEG / 8, SEG, PRO == PRO_NORM>(a, seg, p * T::TOK, M, row0,
+                                                      a.apre + (size_t)(seg * NP + p) * Smem<FMT>::A_BYTES,
+                                                      a.fxpre + (size_t)(seg * NP + p) * Smem<FMT>::FX, red);
+}
+
+template <int FMT, int K, int KS, int MT, int PRO, int EPI>
+__global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
+    const State* st = a.st;
+    if (st->done) return;
+    using T = TileT<FMT>;
+    constexpr int NSEG = K / SEG;
+    constexpr int CPS = SEG / T::CHK;  // chunks per segment
+    constexpr int CPW = CPS / KS;      // chunks per wave per segment
+    static_assert(CPS % KS == 0, "chunks per segment must split evenly over the waves");
+    constexpr int NG = SEG / T::G;
+    constexpr int NC = K / T::CHK;  // chunks per row block
+
+    int M, row0;
+    gemv_rows<EPI, MT>(a, st, M, row0);
     const int npass = (M + T::TOK - 1) / T::TOK;
     constexpr int NP = Smem<FMT>::passes(MT);
 
@@ -240,37 +325,33 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
 
-    // RMSNorm scale of every token over the full K, once per workgroup; the tokens' loads are
-    // issued together and reduced in one round.
+    // Operands pre-staged by gemv_prep_kernel (multi-row passes): copied into LDS, no RMSNorm or
+    // slicing here.
+    const bool pre = MT > 1 && a.apre != nullptr;
     if constexpr (PRO == PRO_NORM) {
-        float ss[MT];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) ss[t] = 0.f;
-#pragma unroll
-        for (int k = tid; k < K; k += KS * 64) {
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {  // unconditional loads (row clamped), zero past the pass
-                const float v = a.x[(size_t)(row0 + min(t, M - 1)) * K + k];
-                ss[t] += t < M ? v * v : 0.f;
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const float w = wave_sum(ss[t]);
-            if (lane == 0) red[wave * MAXM + t] = w;
-        }
-        __syncthreads();
-        if (tid < M) {
-            float tot = 0.f;
-            for (int w = 0; w < KS; ++w) tot += red[w * MAXM + tid];
-            nscale[tid] = 1.0f / sqrtf(tot / (float)K + EPS);
-        }
-        __syncthreads();
+        if (!pre) norm_scales<K, MT, KS * 64>(a, M, row0, nscale, red);
     }
 
     // Activation operands of every pass, staged once per segment (once per launch when K fits
     // one segment).
     auto stage_all = [&](int seg) {
+        if (pre) {
+            // 1 KiB wave loads straight into LDS: the passes' operands, then their group factors.
+            constexpr int AW = Smem<FMT>::A_BYTES / 1024, FW = (FMT == FMT_F16) ? 0 : Smem<FMT>::FX * 4 / 1024;
+            for (int p = 0; p < npass; ++p) {
+                const uint8_t* src = a.apre + (size_t)(seg * NP + p) * Smem<FMT>::A_BYTES;
+                const uint8_t* fsrc = (const uint8_t*)(a.fxpre + (size_t)(seg * NP + p) * Smem<FMT>::FX);
+                for (int w = wave; w < AW + FW; w += KS) {
+                    const uint8_t* g = w < AW ? src + w * 1024 : fsrc + (w - AW) * 1024;
+                    uint8_t* l = w < AW ? Alds + p * Smem<FMT>::A_BYTES + w * 1024
+                                        : (uint8_t*)(fx + p * Smem<FMT>::FX) + (w - AW) * 1024;
+                    __builtin_amdgcn_global_load_lds(g + lane * 16, (__attribute__((address_space(3))) void*)l, 16, 0,
+                                                     0);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed (the barrier after covers all)
+            return;
+        }
         for (int p = 0; p < npass; ++p)
             stage<FMT, K, PRO, KS * 64>(a, seg, p * T::TOK, M, row0, Alds + p * Smem<FMT>::A_BYTES,
                                         fx + p * Smem<FMT>::FX, nscale);
@@ -525,6 +606,35 @@ static hipError_t gemv_fmt(GemvOp op, const GemvArgs& a, int mt, hipStream_t s) 
         case GEMV_PLAIN_K6144:
             return one ? launch_one<FMT, FF, 4, 1, PRO_F32, EPI_STORE>(a, a.blocks, s)
                        : launch_one<FMT, FF, 4, MAXM, PRO_F32, EPI_STORE>(a, a.blocks, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int FMT, int K, int PRO, int EPI>
+static hipError_t launch_prep_one(const GemvArgs& a, hipStream_t s) {
+    constexpr int NB = (K / SEG) * Smem<FMT>::passes(MAXM);
+    hipLaunchKernelGGL((gemv_prep_kernel<FMT, K, PRO, EPI>), dim3(NB), dim3(SEG / 8), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t prep_fmt(GemvOp op, const GemvArgs& a, hipStream_t s) {
+    switch (op) {
+        case GEMV_QKV: return launch_prep_one<FMT, H, PRO_NORM, EPI_STORE>(a, s);
+        case GEMV_O: return launch_prep_one<FMT, H, PRO_F32, EPI_RESID>(a, s);
+        case GEMV_GU: return launch_prep_one<FMT, H, PRO_NORM, EPI_SWIGLU>(a, s);
+        case GEMV_DOWN: return launch_prep_one<FMT, FF, PRO_F32, EPI_RESID>(a, s);
+        case GEMV_LMHEAD: return launch_prep_one<FMT, H, PRO_NORM, EPI_ARGMAX>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemv_prep(int fmt, GemvOp op, const GemvArgs& a, hipStream_t s) {
+    if (!a.apre || !a.fxpre) return hipErrorInvalidValue;
+    switch (fmt) {
+        case FMT_Q4: return prep_fmt<FMT_Q4>(op, a, s);
+        case FMT_Q8: return prep_fmt<FMT_Q8>(op, a, s);
+        case FMT_F16: return prep_fmt<FMT_F16>(op, a, s);
     }
     return hipErrorInvalidValue;
 }

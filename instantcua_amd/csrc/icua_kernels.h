@@ -37,9 +37,15 @@ struct GemvArgs {
     int blocks;             // isolated GEMV launches: grid size
     float* kpart;           // K = 6144 residual GEMV: per-segment partials [3][MAXM][N]
     int* kcnt;              // and per-row-block arrival counters [N / 16], zero between launches
+    uint8_t* apre;          // multi-row passes: operands pre-staged by launch_gemv_prep (or null)
+    float* fxpre;           // and their group factors
 };
 
 hipError_t launch_gemv(int fmt, GemvOp op, const GemvArgs& a, int mt, hipStream_t s);
+// Stages the activation operands of a multi-row (MAXM) GEMV of the same arguments into a.apre /
+// a.fxpre (GEMV_PREP_BYTES / GEMV_PREP_FX_BYTES), for the GEMV launched next on the stream.
+hipError_t launch_gemv_prep(int fmt, GemvOp op, const GemvArgs& a, hipStream_t s);
+constexpr size_t GEMV_PREP_BYTES = 3 * 2 * 65536, GEMV_PREP_FX_BYTES = 3 * 2 * 1024 * 4;
 
 // Repacks a row-major .icua matrix (codes + scales) into the GEMV tile layout.  gu_interleave
 // reorders the fused gate|up rows so that tiled block b holds gate units 8b..8b+7 and then the
