@@ -293,23 +293,40 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
     VA_GLOAD(0);
 
     // Query columns: normalised, rotated, scaled rows split into fp16 hi + lo; zero past the pass.
+    // The wave's four columns load their rows, norm weights and rotations together (rows past the
+    // pass read the last row and are zeroed), so the prologue is one memory round trip.
     const float qscale = 1.0f / sqrtf((float)HD);
-    for (int c = wave; c < 16; c += ATT_THREADS / WAVE) {
-        const int t = c >> 1, hh = c & 1;
-        float x0 = 0.f, x1 = 0.f;
-        if (t < M) {
-            const float* src = a.qkv + (size_t)t * QKV + (2 * g + hh) * HD;
-            x0 = src[lane];
-            x1 = src[lane + 64];
-            norm_rope_pair(x0, x1, a.q_norm, a.rope + (size_t)(pos + t) * 128, lane);
-            x0 *= qscale;
-            x1 *= qscale;
+    {
+        constexpr int NCW = 16 / (ATT_THREADS / WAVE);  // columns per wave
+        float x0[NCW], x1[NCW], c0[NCW], s0[NCW];
+        const float w0 = a.q_norm[lane], w1 = a.q_norm[lane + 64];
+#pragma unroll
+        for (int i = 0; i < NCW; ++i) {
+            const int c = wave + (ATT_THREADS / WAVE) * i, t = c >> 1, hh = c & 1, tc = min(t, M - 1);
+            const float* src = a.qkv + (size_t)tc * QKV + (2 * g + hh) * HD;
+            x0[i] = src[lane];
+            x1[i] = src[lane + 64];
+            const float* cs = a.rope + (size_t)(pos + tc) * 128;
+            c0[i] = cs[2 * lane];
+            s0[i] = cs[2 * lane + 1];
         }
-        const f16 h0 = (f16)x0, h1 = (f16)x1;
-        Qh[c * VA_QROW + lane] = __builtin_bit_cast(uint16_t, h0);
-        Qh[c * VA_QROW + lane + 64] = __builtin_bit_cast(uint16_t, h1);
-        Ql[c * VA_QROW + lane] = __builtin_bit_cast(uint16_t, (f16)(x0 - (float)h0));
-        Ql[c * VA_QROW + lane + 64] = __builtin_bit_cast(uint16_t, (f16)(x1 - (float)h1));
+#pragma unroll
+        for (int i = 0; i < NCW; ++i) {
+            const int c = wave + (ATT_THREADS / WAVE) * i, t = c >> 1;
+            float y0 = x0[i], y1 = x1[i];
+            const float ss = wave_sum(y0 * y0 + y1 * y1);
+            const float scale = 1.0f / sqrtf(ss / (float)HD + EPS);
+            y0 = y0 * scale * w0;
+            y1 = y1 * scale * w1;
+            const float r0 = y0 * c0[i] - y1 * s0[i], r1 = y1 * c0[i] + y0 * s0[i];
+            y0 = t < M ? r0 * qscale : 0.f;
+            y1 = t < M ? r1 * qscale : 0.f;
+            const f16 h0 = (f16)y0, h1 = (f16)y1;
+            Qh[c * VA_QROW + lane] = __builtin_bit_cast(uint16_t, h0);
+            Qh[c * VA_QROW + lane + 64] = __builtin_bit_cast(uint16_t, h1);
+            Ql[c * VA_QROW + lane] = __builtin_bit_cast(uint16_t, (f16)(y0 - (float)h0));
+            Ql[c * VA_QROW + lane + 64] = __builtin_bit_cast(uint16_t, (f16)(y1 - (float)h1));
+        }
     }
     if (tail) {
         // The pass's new rows: per-head RMSNorm + RoPE on K, fp16 K/V into the cache and into
