@@ -173,6 +173,25 @@ def test_verify_eight_drafts(oracle_mod, q4_small):
 
 
 @pytest.mark.parametrize("fmt", [WeightFormat.Q4, WeightFormat.Q8])
+def test_verify_is_deterministic_across_replays(fmt):
+    """Repeated verify passes at one position give bit-identical logits: the down GEMV's split-K
+    partials are summed in a fixed order by the last arriving workgroup, its arrival counters
+    reset themselves for the next replay, and the pre-staged gate|up / lm_head operands are
+    rewritten by each pass.  Drafts of 8, 5 and 1 rows, interleaved, also exercise partial
+    passes of the staged operands."""
+    img = synth.build_model_image(fmt, n_layers=2, tag=f"det-{fmt}")
+    toks = synth.random_tokens(21, "det")
+    drafts = [synth.random_tokens(m, "det-draft", m) for m in (8, 5, 1)]
+    with Engine(image=img, max_context=128, max_steps=16) as e:
+        e.prefill(toks, max_new=4)
+        first = [e.verify(d, want_logits=True)[1] for d in drafts]
+        for rep in range(3):
+            for d, ref in zip(drafts, first):
+                lg = e.verify(d, want_logits=True)[1]
+                assert np.array_equal(lg.view(np.uint32), ref.view(np.uint32)), (rep, len(d))
+
+
+@pytest.mark.parametrize("fmt", [WeightFormat.Q4, WeightFormat.Q8])
 def test_layer_stages(oracle_mod, fmt):
     """Stage-by-stage parity of one layer pass (3 rows over 29 prior slots): raw QKV rows,
     attention output, SwiGLU output and the residual."""
