@@ -132,16 +132,22 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     const int tm = tile / TN, tn = tile % TN;
 
     __shared__ uint4 Bs[2][8][4][64];   // fp16 codes: [buffer][row block][k-step][lane]
-    __shared__ float2 SBs[2][2][128];   // (scale, bias): [buffer][group of the step][row]
+    // Per-step words: [buffer][0..255] fp16 (scale, bias) of group 2 c + i / 128, row i % 128;
+    // [buffer][256 + 32 b + 16 g + t] float group sum of group 2 c + g, token 16 b + t of the tile.
+    __shared__ __attribute__((aligned(16))) uint32_t Vs[2][512];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;
     const int tb0 = tm * 8 + 2 * (wave & 3), rb0 = 4 * (wave >> 2);
     const uint16_t* xa = a.xa + (size_t)tb0 * NKS * 1024 + lane * 8;   // token block tb0 (+ NKS * 1024 for tb0 + 1)
-    const float* xsp = a.xs + ((size_t)tb0 * NG) * 16 + 4 * q;
     // Staging: thread t unpacks nibble lane t % 64 of row block t / 64.
     const int srb = tid >> 6;
     const uint8_t* wsrc = a.w + (size_t)(tn * 8 + srb) * NC * 1024 + lane * 16;
-    const uint32_t* sbsrc = (const uint32_t*)a.sb + (size_t)(tn * 128 + (tid & 127)) * NG + ((tid >> 7) & 1);
+    // Thread t < 256 loads the (scale, bias) word of its row, t >= 256 one group sum: one
+    // unconditional 4-byte load per step (stride 2 words or 32 floats per step).
+    const int vj = tid & 255;
+    const uint32_t* vsrc = tid < 256 ? (const uint32_t*)a.sb + (size_t)(tn * 128 + (vj & 127)) * NG + (vj >> 7)
+                                     : (const uint32_t*)a.xs + ((size_t)(tm * 8 + (vj >> 5)) * NG + ((vj >> 4) & 1)) * 16 + (vj & 15);
+    const int vstride = tid < 256 ? 2 : 32;
 
     f32x4 acc[2][4];
 #pragma unroll
@@ -150,11 +156,10 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         for (int r = 0; r < 4; ++r) acc[i][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Activation operands of one 64-group (two k-steps), prefetched one group ahead.
-    uint4 Ac[2][2][2], An[2][2][2];  // [token block][k-step of the group][hi, lo]
-    float4 Xc[2], Xn[2];             // [token block]: group sums of tokens 4 q .. 4 q + 3
+    uint4 Ae[2][2][2], Ao[2][2][2];  // [token block][k-step of the group][hi, lo]
     uint4 Wn;
-    uint32_t SBn = 0;
-    auto aload = [&](int g, uint4(&A)[2][2][2], float4(&X)[2]) {
+    uint32_t Vn;
+    auto aload = [&](int g, uint4(&A)[2][2][2]) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -162,12 +167,11 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                 for (int hl = 0; hl < 2; ++hl)
                     A[i][kk][hl] = *(const uint4*)(xa + (size_t)i * NKS * 1024 + ((size_t)(2 * g + kk) * 2 + hl) * 512);
-            X[i] = *(const float4*)(xsp + ((size_t)i * NG + g) * 16);
         }
     };
     auto wload = [&](int c) {
         Wn = *(const uint4*)(wsrc + (size_t)c * 1024);
-        if (tid < 256) SBn = sbsrc[2 * c];
+        Vn = vsrc[(size_t)c * vstride];
     };
     // Nibble lane L (row L % 16, 16-K slot L / 16 of each group) -> fp16 lanes (L % 16) + 16 (2 (slot % 2) + h)
     // of k-step 2 gg + slot / 2, h = 0 for K 0..7 of the slot, 1 for K 8..15.
@@ -193,13 +197,10 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                 Bs[b][srb][2 * gg + (slot >> 1)][r + 16 * (2 * (slot & 1) + h)] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
-        if (tid < 256) {
-            const f16x2 sb2 = as_h2(SBn);
-            SBs[b][tid >> 7][tid & 127] = make_float2((float)sb2.x, (float)sb2.y);
-        }
+        Vs[b][tid] = Vn;
     };
     // One 64-group: the wave's 8 B fragments first, then 4 x 2 accumulator chains of 4 MFMAs.
-    auto group = [&](int b, int gg) {
+    auto group = [&](int b, int gg, const uint4(&Ac)[2][2][2]) {
         v8h Bf[4][2];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -207,7 +208,13 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
             for (int kk = 0; kk < 2; ++kk) Bf[r][kk] = __builtin_bit_cast(v8h, Bs[b][rb0 + r][2 * gg + kk][lane]);
         float2 sb[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sb[r] = SBs[b][gg][(rb0 + r) * 16 + r16];
+        for (int r = 0; r < 4; ++r) {
+            const f16x2 sb2 = as_h2(Vs[b][gg * 128 + (rb0 + r) * 16 + r16]);
+            sb[r] = make_float2((float)sb2.x, (float)sb2.y);
+        }
+        f32x4 xg[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) xg[i] = *(const f32x4*)&Vs[b][256 + (2 * (wave & 3) + i) * 32 + gg * 16 + 4 * q];
         f32x4 C[4][2];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -227,24 +234,14 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const float xg[4] = {Xc[i].x, Xc[i].y, Xc[i].z, Xc[i].w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], fmaf(sb[r].y, xg[e], acc[i][r][e]));
+                for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], fmaf(sb[r].y, xg[i][e], acc[i][r][e]));
             }
-    };
-    auto advance = [&]() {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                Ac[i][kk][0] = An[i][kk][0];
-                Ac[i][kk][1] = An[i][kk][1];
-            }
-            Xc[i] = Xn[i];
-        }
     };
 
-    aload(0, Ac, Xc);
+    // Even groups use Ae, odd groups Ao: each set is reloaded right after its group, so no
+    // register copy waits on an outstanding load.
+    aload(0, Ae);
     wload(0);
     lstore(0);
     __syncthreads();
@@ -252,13 +249,11 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         const int b = c & 1;
         // The next step's codes (the last step reloads step 0 into the idle buffer: no branch).
         wload(c + 1 < NC ? c + 1 : 0);
-        aload(2 * c + 1, An, Xn);
-        group(b, 0);
-        advance();
-        aload(2 * c + 2 < NG ? 2 * c + 2 : 0, An, Xn);
-        group(b, 1);
+        aload(2 * c + 1, Ao);
+        group(b, 0, Ae);
+        aload(2 * c + 2 < NG ? 2 * c + 2 : 0, Ae);
+        group(b, 1, Ao);
         lstore(b ^ 1);
-        advance();
         __syncthreads();
     }
 
