@@ -30,7 +30,9 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 // Activation operands.  XA: [Mpad / 16][K / 32][2 (hi, lo)][64 lanes][8 halves], lane l
 // holding token 16 tb + l % 16, K = 32 ks + 8 (l / 16) + 0..7.  XS: [Mpad / 16][K / 64][16]
 // group sums of hi + lo.  TS: [Mpad] row scales 2^(E_t - 14).  One workgroup per token row
-// (rows >= M are zero).
+// (rows >= M are zero).  A row writes 16-byte pieces of lines that the 16 rows of its token
+// block share, so rows are dealt to the 8 XCDs (workgroup i runs on XCD i % 8) in contiguous
+// ranges: the lines are completed in one L2 rather than written back in parts from eight.
 
 template <int K, bool NORM>
 __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ src, const float* __restrict__ norm_w,
@@ -38,7 +40,8 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
                                                       float* __restrict__ ts) {
     constexpr int NU = K / 8 / 256;  // units of 8 activations per thread
     constexpr int NG = K / 64, NKS = K / 32;
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int t = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);  // gridDim.x % 8 == 0
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
     __shared__ float red[8];
     float v[NU][8];
 #pragma unroll
