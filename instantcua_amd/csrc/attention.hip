@@ -532,8 +532,9 @@ hipError_t launch_attention(const AttnArgs& a, int mt, int splits, hipStream_t s
         hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(ATT_THREADS), 0, s, a);
         hipLaunchKernelGGL(attention_merge_kernel<1>, dim3(NKV, 2), dim3(ATT_THREADS), 0, s, a, splits, ATT_CH);
     } else {
-        // splits - 1 prior splits of 64 slots cover the cache: so do ceil((splits - 1) / 4) of 256.
-        const int vs = (splits - 1 + 3) / 4 + 1;
+        // splits - 1 prior splits of ATT_CH slots cover the cache: so do ceil((splits - 1) / R) of VA_CH.
+        constexpr int R = VA_CH / ATT_CH;
+        const int vs = (splits - 1 + R - 1) / R + 1;
         hipLaunchKernelGGL(attention_mfma_kernel, dim3(vs, NKV), dim3(ATT_THREADS), 0, s, a);
         hipLaunchKernelGGL(attention_merge_kernel<MAXM>, dim3(NKV, 2 * MAXM), dim3(ATT_THREADS), 0, s, a, vs, VA_CH);
     }

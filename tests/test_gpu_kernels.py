@@ -34,16 +34,15 @@ def test_dequant_bit_exact(oracle_mod, fmt):
     assert np.array_equal(out.to_array(np.float32, (N, K)).view(np.uint32), ref.view(np.uint32))
 
 
-# The isolated GEMV shapes (K x N): fused QKV, O, gate+up, down, lm_head.
+# The isolated GEMV shapes (K x N): fused QKV, O, gate+up, down, lm_head, at 1, 3 and 8 rows;
+# the lm_head shape at one row only (its multi-row passes run in the decoder and verify tests).
 SHAPES = [(2048, 4096), (2048, 2048), (2048, 12288), (6144, 2048), (2048, 151936)]
+GEMV_CASES = [(K, N, m) for K, N in SHAPES for m in (1, 3, 8) if N != 151936 or m == 1]
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("K,N", SHAPES)
-@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("K,N,m", GEMV_CASES)
 def test_gemv_parity(oracle_mod, fmt, K, N, m):
-    if N == 151936 and m != 1:
-        pytest.skip("lm_head-sized multi-row case covered by the decoder tests")
     mat = synth.make_matrix(fmt, N, K, tag="gemv", index=fmt)
     x = synth.fp16_normal((m, K), "gemvx", m).astype(np.float32)  # fp16 N(0,1) activations
     ref = oracle_mod.gemv(fmt, mat.codes, mat.sb, N, K, x)
