@@ -223,6 +223,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a) {
 // contributes exactly nothing.
 constexpr int VA_CH = 4 * ATT_CH;                          // prior slots per split
 constexpr int VA_KROW = 136, VA_VROW = 72, VA_QROW = 136;  // padded LDS rows (halves)
+// Column (halves) of key `key` in V^T row `row`: 4-key chunks XOR-swizzled by (row / 8) % 8, so
+// the staging writes (lane l of a half-wave: rows 4 l + j, one chunk) and the P.V reads (16
+// rows, one chunk) each cover all 32 banks.
+__device__ __forceinline__ int va_vcol(int row, int key) { return 4 * ((key >> 2) ^ ((row >> 3) & 7)) + (key & 3); }
 
 __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a) {
     typedef _Float16 v4h __attribute__((ext_vector_type(4)));
@@ -286,7 +290,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
                 uint32_t e[4];                                                                        \
                 _Pragma("unroll") for (int i = 0; i < 4; ++i)                                         \
                     e[i] = ((j < 2 ? vr[h][i].x : vr[h][i].y) >> (16 * (j & 1))) & 0xFFFFu;           \
-                *(uint2*)(Vt_ + (d0_ + j) * VA_VROW + k0_) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16)); \
+                *(uint2*)(Vt_ + (d0_ + j) * VA_VROW + va_vcol(d0_ + j, k0_)) =                        \
+                    make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));                             \
             }                                                                                         \
         }                                                                                             \
     } while (0)
@@ -353,8 +358,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
             }
             Ks[t * VA_KROW + lane] = hk0;
             Ks[t * VA_KROW + lane + 64] = hk1;
-            Vt[lane * VA_VROW + t] = hv0;
-            Vt[(lane + 64) * VA_VROW + t] = hv1;
+            Vt[lane * VA_VROW + va_vcol(lane, t)] = hv0;
+            Vt[(lane + 64) * VA_VROW + va_vcol(lane + 64, t)] = hv1;
         }
     } else {
         VA_LSTORE(0);
@@ -410,7 +415,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
         }
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-            const v4h vf = *(const v4h*)(Vt + (16 * dt + r16) * VA_VROW + kt + 4 * q4);
+            const v4h vf = *(const v4h*)(Vt + (16 * dt + r16) * VA_VROW + va_vcol(16 * dt + r16, kt + 4 * q4));
 #pragma unroll
             for (int i = 0; i < 4; ++i) O[dt][i] *= corr;
             O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, Ph, O[dt], 0, 0, 0);
