@@ -343,8 +343,6 @@ __global__ __launch_bounds__(256) void pf_qk_kernel(PfQkArgs a) {
 constexpr int PA_KB = 64;     // keys per block
 constexpr int PA_KROW = 136;  // halves per K row in LDS (128 + 8 pad)
 constexpr int PA_VROW = 68;   // halves per V^T row in LDS (64 keys + 4 pad)
-// V^T row d holds its 4-key chunk c at chunk c ^ ((d >> 4) & 3): the staging writes (lane l of a
-// half-wave: rows 4 l + j) then cover all 32 banks, and the P.V reads (16 rows, one chunk) too.
 constexpr int PA_BUF = PA_KB * PA_KROW + HD * PA_VROW;  // halves per buffer
 constexpr size_t PA_LDS = 2 * PA_BUF * 2;
 
@@ -405,8 +403,7 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
             uint32_t e[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) e[i] = ((j < 2 ? vr[i].x : vr[i].y) >> (16 * (j & 1))) & 0xFFFFu;
-            const int d = d0 + j;
-            *(uint2*)(Vt + d * PA_VROW + 4 * ((k0 >> 2) ^ ((d >> 4) & 3))) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+            *(uint2*)(Vt + (d0 + j) * PA_VROW + k0) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
         }
     };
 
@@ -477,7 +474,7 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
                 }
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt) {
-                    const uint16_t* vp = Vt + (dt * 16 + r16) * PA_VROW + 32 * c + 4 * (q ^ (dt & 3));
+                    const uint16_t* vp = Vt + (dt * 16 + r16) * PA_VROW + 32 * c + 4 * q;
                     const v4h va = *(const v4h*)vp, vb = *(const v4h*)(vp + 16);
                     const v8h vf = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
                     O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Ph, O[dt], 0, 0, 0);
