@@ -253,7 +253,9 @@ __global__ __launch_bounds__(512) void vit_attention_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ vt, uint16_t* __restrict__ out,
                                                             int np, int ld) {
     constexpr int ROW = 72, TILE = 64 * ROW;
-    __shared__ __align__(16) uint16_t lds[2][2][2][TILE];  // [key half][K, V^T][buffer]
+    // [key half][K, V^T][buffer].  V^T rows with (row / 8) odd hold their 4-key chunks pairwise
+    // swapped (chunk c at c ^ 1): the P.V reads of 16 rows x one chunk then cover all 32 banks.
+    __shared__ __align__(16) uint16_t lds[2][2][2][TILE];
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, r16 = lane & 15, q4 = lane >> 4;
     const int grp = wave >> 2, gt = tid & 255;
     const int h = blockIdx.y;
@@ -281,7 +283,8 @@ __global__ __launch_bounds__(512) void vit_attention_kernel(const uint16_t* __re
         _Pragma("unroll") for (int c = 0; c < 2; ++c) {                              \
             const int idx = gt + 256 * c, row = idx >> 3, col = (idx & 7) * 8;       \
             *(uint4*)&lds[grp][0][buf_][row * ROW + col] = kr[c];                    \
-            *(uint4*)&lds[grp][1][buf_][row * ROW + col] = vr[c];                    \
+            const uint4 vv_ = ((row >> 3) & 1) ? make_uint4(vr[c].z, vr[c].w, vr[c].x, vr[c].y) : vr[c]; \
+            *(uint4*)&lds[grp][1][buf_][row * ROW + col] = vv_;                      \
         }                                                                           \
     } while (0)
 
@@ -340,7 +343,7 @@ __global__ __launch_bounds__(512) void vit_attention_kernel(const uint16_t* __re
                 for (int i = 0; i < 4; ++i) O[dt][i] *= corr;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const v4h vf = *(const v4h*)&Vs[(16 * dt + r16) * ROW + 16 * j + 4 * q4];
+                    const v4h vf = *(const v4h*)&Vs[(16 * dt + r16) * ROW + 4 * ((4 * j + q4) ^ (r16 >> 3))];
                     O[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, P[j], O[dt], 0, 0, 0);
                 }
             }
