@@ -371,6 +371,8 @@ def main():
         e.set_position(PREFILL, int(vp.tokens[-1]), 1, W + K + 1)
         prefill_ms = float("nan")
     else:
+        # One untimed prefill first: the first launch of each kernel loads its code object.
+        e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=W + K + 1)
         t1 = time.perf_counter()
         e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=W + K + 1)
         prefill_wall = time.perf_counter() - t1
