@@ -10,37 +10,45 @@ namespace icua {
 __global__ __launch_bounds__(1024) void commit_kernel(CommitArgs a) {
     State* st = a.st;
     if (st->done) return;
-    __shared__ float rv[16];
-    __shared__ int ri[16];
-    __shared__ int tok_s[2];
+    __shared__ float rv[MAXM][16];
+    __shared__ int ri[MAXM][16];
+    __shared__ int tok_s[MAXM];
     __shared__ int halt;
     const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     const int n = st->n;
     const bool all_rows = (st->logits_rows == n);
     const int r_first = all_rows ? 0 : n - 1;
-    int tok_last = 0;
-    for (int r = r_first; r < n; ++r) {
-        float best = -__builtin_inff();
-        int bi = 0x7fffffff;
+    const int nr = max(min(n - r_first, MAXM), 0);  // rows reduced: n, or the last one
+    // All rows' partials are loaded together (row indices clamped into the buffer; rows past
+    // nr are reduced and discarded), then reduced per row with one barrier.
+    float best[MAXM];
+    int bi[MAXM];
+#pragma unroll
+    for (int j = 0; j < MAXM; ++j) {
+        const int r = min(max(r_first + min(j, nr - 1), 0), MAXM - 1);
+        best[j] = -__builtin_inff();
+        bi[j] = 0x7fffffff;
         for (int i = tid; i < LMH_WAVES; i += 1024)
-            argmax_merge(best, bi, a.pval[(size_t)r * LMH_WAVES + i], a.pidx[(size_t)r * LMH_WAVES + i]);
-        wave_argmax(best, bi);
+            argmax_merge(best[j], bi[j], a.pval[(size_t)r * LMH_WAVES + i], a.pidx[(size_t)r * LMH_WAVES + i]);
+    }
+#pragma unroll
+    for (int j = 0; j < MAXM; ++j) {
+        wave_argmax(best[j], bi[j]);
         if (lane == 0) {
-            rv[wave] = best;
-            ri[wave] = bi;
+            rv[j][wave] = best[j];
+            ri[j][wave] = bi[j];
         }
-        __syncthreads();
-        if (tid == 0) {
-            float b2 = rv[0];
-            int i2 = ri[0];
-            for (int w = 1; w < 16; ++w) argmax_merge(b2, i2, rv[w], ri[w]);
-            tok_s[0] = i2;
-            if (a.argmax_rows) a.argmax_rows[r] = i2;
-        }
-        __syncthreads();
-        tok_last = tok_s[0];
     }
     __syncthreads();
+    if (tid < nr) {
+        float b2 = rv[tid][0];
+        int i2 = ri[tid][0];
+        for (int w = 1; w < 16; ++w) argmax_merge(b2, i2, rv[tid][w], ri[tid][w]);
+        tok_s[tid] = i2;
+        if (a.argmax_rows) a.argmax_rows[r_first + tid] = i2;
+    }
+    __syncthreads();
+    const int tok_last = nr > 0 ? tok_s[nr - 1] : 0;
     if (a.verify_only) return;  // speculative verify: per-row argmax only, state untouched
     if (tid == 0) {
         halt = st->step >= st->maxsteps;  // nothing may be written past out_tokens[maxsteps + 1]
