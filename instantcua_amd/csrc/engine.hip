@@ -130,6 +130,7 @@ struct icua_engine {
     hipGraphExec_t graph[2] = {nullptr, nullptr};
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     icua_timing_t timing{};
+    // Prefix cache key: the tokens whose K/V rows occupy slots 0..size-1 (empty: no valid prefix).
     std::vector<int32_t> cached_prefix;
     int mrope_key[3] = {-999, 0, 0};
     int last_logits_rows = 0;
@@ -680,8 +681,14 @@ struct icua_engine {
         return 0;
     }
 
+    // Any write of K/V rows below the cached prefix's end invalidates the prefix cache.
+    void kv_written_from(int slot0) {
+        if (slot0 < (int)cached_prefix.size()) cached_prefix.clear();
+    }
+
     int prepare_mrope(int vis_offset, int llm_h, int llm_w) {
         if (vis_offset >= 0 && (llm_h <= 0 || llm_w <= 0)) return fail("bad visual grid");
+        if (vis_offset < 0) vis_offset = -1, llm_h = llm_w = 1;  // one key for every text-only table
         if (mrope_key[0] == vis_offset && mrope_key[1] == llm_h && mrope_key[2] == llm_w) return 0;
         std::vector<float> tab;
         mrope_table(maxctx, vis_offset, llm_h, llm_w, tab);
@@ -808,6 +815,7 @@ struct icua_engine {
             if (tokens[i] < 0 || tokens[i] >= VOCAB) return fail("token id out of range");
         if (vis_offset >= n) return fail("vis_offset beyond the prompt");
         if (vis_offset >= 0 && n_vis <= 0) return fail("visual rows requested but no visual embeddings set");
+        kv_written_from(start_pos);
         HIPCK(hipMemcpyAsync(prompt, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, stream));
         State s{};
         s.pos = start_pos;
@@ -1010,18 +1018,29 @@ int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, 
                   int* n_out) {
     if (!e || !tokens || !out_tokens || !n_out) return fail("null argument");
     const auto t0 = std::chrono::steady_clock::now();
-    // System-prompt KV prefix cache (Engine.swift:719-735).
-    bool hit = false;
-    if ((e->flags & ICUA_FLAG_PREFIX_CACHE) && vis_offset > 0) {
-        std::vector<int32_t> prefix(tokens, tokens + vis_offset);
-        hit = (prefix == e->cached_prefix);
-        e->cached_prefix = prefix;
+    if (n <= 0) return fail("empty prompt");
+    if (vis_offset >= n) return fail("vis_offset beyond the prompt");
+    if (vis_offset < 0) {
+        // Text only: the positions are 1-D whatever table an earlier call prepared.
+        if (e->prepare_mrope(-1, 1, 1)) return -1;
+    } else {
+        // Visual rows: the table must be the one of this image (icua_prepare_mrope, or
+        // icua_generate_vision which prepares it from the frame).
+        if (e->mrope_key[0] != vis_offset || e->mrope_key[1] * e->mrope_key[2] != e->n_vis)
+            return fail("the M-RoPE table was not prepared for this image: call icua_prepare_mrope(vis_offset, "
+                        "llm_h, llm_w) with llm_h * llm_w visual rows first");
     }
+    // System-prompt KV prefix cache (Engine.swift:719-735).  The key names the tokens whose K/V
+    // rows the cache holds; it is set only after a prefill that wrote them succeeded.
+    const bool use_cache = (e->flags & ICUA_FLAG_PREFIX_CACHE) && vis_offset > 0;
+    const bool hit = use_cache && (int)e->cached_prefix.size() == vis_offset &&
+                     std::equal(e->cached_prefix.begin(), e->cached_prefix.end(), tokens);
     const int start = hit ? vis_offset : 0;
     const int active = n - start;
     const int active_vis = vis_offset >= 0 ? vis_offset - start : -1;
     max_new = std::max(1, std::min(max_new, e->maxsteps));
     if (e->prefill(tokens + start, active, start, active_vis, max_new, 0)) return -1;
+    if (use_cache && !hit) e->cached_prefix.assign(tokens, tokens + vis_offset);
     double dec_ms = 0;
     int submitted = 1;
     while (submitted < max_new) {  // batches of 8 steps (Engine.swift:771-792)
@@ -1148,6 +1167,7 @@ int icua_set_position(icua_engine* e, int pos, int32_t next_token, int step, int
     if (pos < 0 || pos >= e->maxctx) return fail("position out of range");
     if (next_token < 0 || next_token >= VOCAB) return fail("token out of range");
     if (step < 0 || step >= std::max(1, std::min(max_steps, e->maxsteps))) return fail("step out of range");
+    e->kv_written_from(pos);  // the next step writes K/V at slot pos
     State s;
     if (e->read_state(s)) return -1;
     s.pos = pos;
@@ -1227,6 +1247,7 @@ static int kv_copy(icua_engine* e, int layer, int kind, int slot0, int nslots, v
     if (!e || !host) return fail("null argument");
     if (layer < 0 || layer >= e->layers || kind < 0 || kind > 1) return fail("bad layer/kind");
     if (slot0 < 0 || nslots < 0 || slot0 + nslots > e->maxctx) return fail("slots out of range");
+    if (to_dev && nslots > 0) e->kv_written_from(slot0);
     for (int g = 0; g < NKV; ++g) {
         uint16_t* dev = e->kv_ptr(layer, kind) + ((size_t)g * e->maxctx + slot0) * HD;
         uint16_t* hp = (uint16_t*)host + (size_t)g * nslots * HD;

@@ -137,3 +137,64 @@ def test_generate_timing_record(q4_small):
     assert len(out) == 16 and t["generated_tokens"] == 16 and t["prefill_tokens"] == 12
     assert t["prefill_ms"] > 0 and t["decode_ms"] > 0 and t["vision_ms"] == 0
     assert t["total_ms"] >= t["decode_ms"]
+
+
+def test_prefix_cache_survives_failed_calls_and_text_prompts(oracle_mod, q4_small):
+    """The prefix key names only K/V rows the cache holds: a call that fails validation leaves it
+    alone, a text prompt (which rewrites slots 0..) clears it, and every output still equals the
+    oracle's."""
+    from instantcua_amd.engine import EngineError
+
+    vp1 = synth.visual_prompt(30, vis_offset=5, llm_h=2, llm_w=4, tag="pfx5")
+    vp2 = synth.visual_prompt(30, vis_offset=5, llm_h=2, llm_w=4, tag="pfx6")
+    text = synth.random_tokens(20, "pfx-text")
+    steps = 6
+    pool1 = vp1.pooler.astype(np.float32)
+    om = oracle_mod.OracleModel(q4_small, 64)
+    om.prepare_mrope(vp1.vis_offset, vp1.llm_h, vp1.llm_w)
+    ref_vis, m_vis, lg_vis = om.generate(vp1.tokens, steps, pooler=pool1, vis_offset=vp1.vis_offset)
+    om.prepare_mrope(-1, 1, 1)
+    ref_txt, m_txt, lg_txt = om.generate(text, steps)
+    with Engine(image=q4_small, max_context=64, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.use_prefix_cache = True
+        e.prepare_mrope(vp1.vis_offset, vp1.llm_h, vp1.llm_w)
+        e.set_visual(pool1, None)
+        a = e.generate(vp1.tokens, vis_offset=vp1.vis_offset, max_new_tokens=steps)
+        assert e.last_timing["prefill_tokens"] == 30
+        bad = vp2.tokens.copy()
+        bad[-1] = Dims.vocab  # out of range: rejected before any K/V row is written
+        with pytest.raises(EngineError, match="out of range"):
+            e.generate(bad, vis_offset=vp2.vis_offset, max_new_tokens=steps)
+        with pytest.raises(EngineError, match="vis_offset"):
+            e.generate(vp1.tokens[:4], vis_offset=vp1.vis_offset, max_new_tokens=steps)
+        b = e.generate(vp1.tokens, vis_offset=vp1.vis_offset, max_new_tokens=steps)
+        assert e.last_timing["prefill_tokens"] == 30 - 5  # hit: the failed calls kept the key
+        t = e.generate(text, max_new_tokens=steps)  # text-only: rewrites slots 0..19
+        e.prepare_mrope(vp1.vis_offset, vp1.llm_h, vp1.llm_w)
+        c = e.generate(vp1.tokens, vis_offset=vp1.vis_offset, max_new_tokens=steps)
+        assert e.last_timing["prefill_tokens"] == 30  # miss: the text prompt cleared the key
+    for got in (a, b, c):
+        compare_greedy(np.array(got), ref_vis, m_vis, lg_vis.max() * np.ones(steps))
+    compare_greedy(np.array(t), ref_txt, m_txt, lg_txt.max() * np.ones(steps))
+
+
+def test_text_generate_after_a_visual_table(oracle_mod, q4_small):
+    """generate() on a text prompt builds the 1-D table itself, whatever grid an earlier call
+    prepared; a visual prompt without a table for its offset is refused."""
+    from instantcua_amd.engine import EngineError
+
+    vp = synth.visual_prompt(30, vis_offset=5, llm_h=2, llm_w=4, tag="pfx7")
+    text = synth.random_tokens(24, "pfx-text2")
+    steps = 6
+    om = oracle_mod.OracleModel(q4_small, 64)
+    ref, margins, lg = om.generate(text, steps)
+    with Engine(image=q4_small, max_context=64, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
+        e.set_visual(vp.pooler.astype(np.float32), None)
+        e.generate(vp.tokens, vis_offset=vp.vis_offset, max_new_tokens=steps)
+        got = e.generate(text, max_new_tokens=steps)
+        with pytest.raises(EngineError, match="M-RoPE table"):
+            e.generate(vp.tokens, vis_offset=vp.vis_offset + 1, max_new_tokens=steps)
+    compare_greedy(np.array(got), ref, margins, lg.max() * np.ones(steps))

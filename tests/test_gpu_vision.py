@@ -101,3 +101,19 @@ def test_vision_errors(vimg):
         assert not e.has_vision
         with pytest.raises(EngineError, match="no vision tower"):
             e.vision(np.zeros((64, 64, 3), np.uint8))
+
+
+def test_text_generate_after_generate_vision(oracle_mod, vimg):
+    """A text prompt after generate_vision on the same engine decodes with 1-D positions."""
+    gh, gw = 4, 8
+    rgb = synth.random_rgb(gh, gw, "vis-then-text")
+    toks, _ = _prompt(gh * gw // 4, "vis-then-text")
+    text = synth.random_tokens(20, "vis-then-text2")
+    steps = 6
+    om = oracle_mod.OracleModel(vimg, 64)
+    ref, margins, first = om.generate(text, steps)
+    with Engine(image=vimg, max_context=64, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.generate_vision(rgb, toks, max_new_tokens=steps)
+        got = e.generate(text, max_new_tokens=steps)
+    compare_greedy(got, ref, margins, first.max() * np.ones(steps))
