@@ -192,6 +192,14 @@ int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0
  *                least-squares refit (quantizeQ4Raw / quantGroup, Convert.swift:243-320).
  * cols must be a multiple of the group size.  All pointers are device buffers. */
 int icua_quantize(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb);
+/* icua_quantize without any device allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  The q4 quantiser's per-group scratch (one byte per 64-weight group) is a
+ * static device array of 8 MiB per GPU, so rows * cols / 64 must not exceed 8,388,608 (larger
+ * matrices fail with an error; icua_quantize takes any size).  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (other host threads, other streams) race.  Each call
+ * rewrites every byte it reads, so nothing carries over from an earlier call. */
+int icua_quantize_noalloc(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb);
 /* Times `iters` back-to-back icua_quantize launches on the same buffers; *avg_us per call (HIP
  * events on the launch stream). */
 int icua_quantize_bench(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb, int iters,

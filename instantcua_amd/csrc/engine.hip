@@ -1407,6 +1407,21 @@ int icua_quantize(int fmt, const float* d_m, int rows, int cols, void* d_codes, 
     return 0;
 }
 
+int icua_quantize_noalloc(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb) {
+    if (quant_check(fmt, d_m, rows, cols, d_codes, d_sb)) return -1;
+    uint8_t* none = nullptr;
+    if (fmt == FMT_Q4) {
+        const int64_t groups = (int64_t)rows * (cols / 64);
+        if (groups > QUANT_SCRATCH_GROUPS)
+            return fail("quantize_noalloc: " + std::to_string(groups) + " q4 groups exceed the static scratch of " +
+                        std::to_string(QUANT_SCRATCH_GROUPS) + " groups (use icua_quantize)");
+        HIPCK(quant_scratch(&none));
+    }
+    HIPCK(launch_quant(fmt, d_m, rows, cols, d_codes, d_sb, none, nullptr));
+    HIPCK(hipDeviceSynchronize());
+    return 0;
+}
+
 int icua_quantize_bench(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb, int iters,
                         double* avg_us) {
     if (quant_check(fmt, d_m, rows, cols, d_codes, d_sb)) return -1;

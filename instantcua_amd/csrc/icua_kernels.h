@@ -153,6 +153,11 @@ hipError_t launch_dequant(int fmt, const uint8_t* w, const uint8_t* sb, int K, i
 // + fp16 scales, or q4 packed codes + fp16 (scale, bias); `none` is a scratch byte per q4 group.
 hipError_t launch_quant(int fmt, const float* m, int64_t rows, int64_t cols, void* codes, void* sb, uint8_t* none,
                         hipStream_t s);
+// Device address, on the current device, of the quantiser's static scratch: one `none` byte per
+// q4 group for up to QUANT_SCRATCH_GROUPS groups.  Looked up once per device.
+constexpr int64_t QUANT_SCRATCH_GROUPS = (int64_t)8 << 20;
+constexpr int QUANT_MAX_DEVICES = 64;
+hipError_t quant_scratch(uint8_t** out);
 
 // Vision tower (ModelFile.swift:31-45): dimensions, weights, work buffers.
 constexpr int VH = 1024, VFF = 4096, VNH = 16, VHD = 64, VQKV = 3072, VPATCH = 768, MH = 4096;

@@ -12,6 +12,8 @@
 // overwrites, so it is not run.  When no candidate is accepted (every fp16 scale rounds to 0) the
 // reference leaves the codes of the chunk's previous group in its code array; a second kernel
 // copies them, so the output bytes match as well (the dequantised values are 0 either way).
+#include <mutex>
+
 #include "icua_device.h"
 #include "icua_kernels.h"
 
@@ -173,6 +175,32 @@ __global__ __launch_bounds__(QT) void quant_q4_carry_kernel(int64_t ngroups, int
 }
 
 }  // namespace
+
+// Static scratch of the allocation-free quantiser entry point: the q4 kernel's per-group "no
+// candidate accepted" byte, for up to QUANT_SCRATCH_GROUPS 64-weight groups (8 MiB, 512 M
+// weights: every matrix of the decoder, the 151936 x 2048 embedding included).  Each GPU the
+// library runs on holds its own copy for the life of the process.  Host code never names the
+// array: it passes the device address that hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint8_t scratch[QUANT_SCRATCH_GROUPS];
+
+hipError_t quant_scratch(uint8_t** out) {
+    // One lookup per device, with that device current (the caller's), kept for later calls.
+    static std::mutex mu;
+    static uint8_t* ptrs[QUANT_MAX_DEVICES] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= QUANT_MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        ptrs[dev] = (uint8_t*)p;
+    }
+    *out = ptrs[dev];
+    return hipSuccess;
+}
 
 hipError_t launch_quant(int fmt, const float* m, int64_t rows, int64_t cols, void* codes, void* sb, uint8_t* none,
                         hipStream_t s) {

@@ -37,7 +37,7 @@ EXPORTS = [
     "icua_read_state", "icua_read_tokens", "icua_logits", "icua_timing", "icua_layer_step",
     "icua_read_kv", "icua_write_kv", "icua_read_buffer", "icua_dev_alloc", "icua_dev_free", "icua_memcpy_h2d",
     "icua_memcpy_d2h", "icua_device_sync", "icua_repack", "icua_gemv", "icua_gemv_bench", "icua_dequant",
-    "icua_quantize", "icua_quantize_bench", "icua_vision", "icua_generate_vision",
+    "icua_quantize", "icua_quantize_noalloc", "icua_quantize_bench", "icua_vision", "icua_generate_vision",
     # include/icua_tok.h
     "icua_tok_last_error", "icua_tok_open", "icua_tok_close", "icua_tok_vocab_size", "icua_tok_special_id",
     "icua_tok_encode", "icua_tok_encode_chat", "icua_tok_encode_vision_chat", "icua_tok_token_bytes",
@@ -111,6 +111,7 @@ def lib() -> C.CDLL:
         L.icua_dequant.argtypes = [i32, vp, vp, i32, i32, i32, vp, i32]
         L.icua_repack.argtypes = [i32, vp, vp, i32, i32, vp, vp]
         L.icua_quantize.argtypes = [i32, vp, i32, i32, vp, vp]
+        L.icua_quantize_noalloc.argtypes = [i32, vp, i32, i32, vp, vp]
         L.icua_quantize_bench.argtypes = [i32, vp, i32, i32, vp, vp, i32, C.POINTER(C.c_double)]
         _lib = L
     return _lib

@@ -140,3 +140,10 @@ def test_create_errors_without_gpu_work(libicua, tmp_path):
         img = np.zeros(mf.HEADER_SIZE, np.uint8)
         img[:16] = np.array([mf.MAGIC, 1, 2, 5], dtype="<u4").view(np.uint8)
         eng.Engine(image=img)
+
+
+def test_noalloc_quantize_rejects_matrices_beyond_its_scratch(libicua):
+    """The size check runs before any device work: 8,388,608 q4 groups is the static limit."""
+    fake = C.c_void_p(256)  # never dereferenced: the call fails on the size first
+    rc = libicua.icua_quantize_noalloc(2, fake, 262145, 2048, fake, fake)
+    assert rc != 0 and b"exceed the static scratch of 8388608 groups" in libicua.icua_last_error()
