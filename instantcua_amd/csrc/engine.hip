@@ -134,9 +134,8 @@ struct icua_engine {
     std::vector<int32_t> cached_prefix;
     int mrope_key[3] = {-999, 0, 0};
     int last_logits_rows = 0;
-    // Persistent decode kernel: counter block, device copy of the layer table, availability.
+    // Persistent decode kernel: counter block and availability.
     unsigned* psync = nullptr;
-    LayerPtrs* d_layers = nullptr;
     bool persist_ok = false;
     // Matrix-core prefill buffers for chunks of up to pf_cap rows (allocated on first use).
     int pf_cap = 0;
@@ -639,14 +638,6 @@ struct icua_engine {
         HIPCK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         if (!coop || cus < PERSIST_WGS) return 0;
         HIPCK(hipMalloc(&psync, persistent_sync_bytes()));
-        std::vector<LayerPtrs> lp(layers);
-        for (int l = 0; l < layers; ++l) {
-            const LayerW& w = L[l];
-            lp[l] = LayerPtrs{w.attn_norm, w.q_norm, w.k_norm, w.mlp_norm, w.wqkv, w.wqkv_sb,
-                              w.wo,        w.wo_sb,  w.wgu,    w.wgu_sb,   w.wd,   w.wd_sb};
-        }
-        HIPCK(hipMalloc(&d_layers, sizeof(LayerPtrs) * layers));
-        HIPCK(hipMemcpy(d_layers, lp.data(), sizeof(LayerPtrs) * layers, hipMemcpyHostToDevice));
         persist_ok = true;
         return 0;
     }
@@ -655,7 +646,11 @@ struct icua_engine {
 
     int enqueue_persistent(int k) {
         PersistArgs a{};
-        a.layers = d_layers;
+        for (int l = 0; l < layers; ++l) {
+            const LayerW& w = L[l];
+            a.layers[l] = LayerPtrs{w.attn_norm, w.q_norm, w.k_norm, w.mlp_norm, w.wqkv, w.wqkv_sb,
+                                    w.wo,        w.wo_sb,  w.wgu,    w.wgu_sb,   w.wd,   w.wd_sb};
+        }
         a.nlayers = layers;
         a.nsteps = k;
         a.maxctx = maxctx;
@@ -944,7 +939,7 @@ void icua_engine_destroy(icua_engine* e) {
         if (g) (void)hipGraphExecDestroy(g);
     void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->kpart, e->kcnt, e->apre, e->fxpre, e->pval,
                     e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
-                    e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_layers, e->d_vision, e->vbuf};
+                    e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_vision, e->vbuf};
     e->free_pf();
     for (void* b : bufs)
         if (b) (void)hipFree(b);

@@ -18,7 +18,10 @@ struct LayerPtrs {
 };
 
 struct PersistArgs {
-    const LayerPtrs* layers;  // device array [nlayers]
+    // Per-layer tensor pointers, held in the kernel arguments so that the kernel reads them with
+    // scalar loads: a vector load of a pointer would make the wave wait for every weight tile it
+    // has in flight before the address can be formed.
+    LayerPtrs layers[MAX_LAYERS];
     int nlayers;
     int nsteps;               // decode steps to run (stops early at a stop condition)
     int maxctx;               // cache capacity (row stride of the K/V cache)

@@ -223,11 +223,10 @@ constexpr int A_BYTES = 18432;
 // Down half-block of a workgroup in LDS: 1 KiB chunks (q4 24, q8 48), then the 16 rows' scales
 // in four per-wave parts of 16 x 48 B (q4: 12 (scale, bias) pairs, q8: 24 scales per row).
 constexpr int WD_CODES = (FFH / 64) * 1024, WD_SB = 16 * MW * 48;
-static_assert(((VOCAB / 16 + NWG - 1) / NWG) * WAVES * 16 * 4 <= WD_CODES + WD_SB, "lm_head partial sums fit S.wdb");
+static_assert(((VOCAB / 16 + NWG - 1) / NWG) * WAVES * 16 * 4 <= WD_CODES + WD_SB, "lm_head partial sums fit the down block buffer");
 
 struct Shared {
     uint8_t A[A_BYTES];       // activation operands; the merger's fp32 partials during the merge
-    uint8_t wdb[WD_CODES + WD_SB];  // q4 down half-block (streamed in before down); lm_head partial sums
     uint32_t zero[4];         // operand rows 3..15 of every tile (16 zero bytes)
     float fx[192 * 2];        // per-group (2^(e-21), sum X * 2^(e-21))
     float red[3 * MW * 64];   // math-wave partial sums (up to 3 blocks)
@@ -487,10 +486,10 @@ struct WB {
     }
 };
 
-// Down half-block `half` of row block rb straight into S.wdb (math wave mw requests the chunks
+// Down half-block `half` of row block rb straight into wdb (math wave mw requests the chunks
 // and the scale columns it multiplies later, so each wave reads back only its own requests).
 template <int FMT>
-__device__ __forceinline__ void wd_request(Shared& S, const uint8_t* wd, const uint8_t* wd_sb, int rb, int half,
+__device__ __forceinline__ void wd_request(uint8_t* wdb, const uint8_t* wd, const uint8_t* wd_sb, int rb, int half,
                                            int mw, int lane) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int NC = FF / CHK, CWD = FFH / CHK / MW;  // chunks per row block, per wave
@@ -498,22 +497,22 @@ __device__ __forceinline__ void wd_request(Shared& S, const uint8_t* wd, const u
 #pragma unroll
     for (int i = 0; i < CWD; ++i) {
         const int c = mw * CWD + i;
-        lds_dma16(blk + (size_t)c * 1024 + lane * 16, S.wdb + c * 1024);
+        lds_dma16(blk + (size_t)c * 1024 + lane * 16, wdb + c * 1024);
     }
     // Scales (FF / 16 bytes per row in both formats): rows 16 rb + r, bytes 192 half + 48 mw ..
     // + 47 -> 16 x 48 B at WD_CODES + 768 mw; lane j < 48 carries row j / 3, 16 B part j % 3.
     if (lane < 48)
         lds_dma16(wd_sb + (size_t)(16 * rb + lane / 3) * (FF / 16) + 192 * half + 48 * mw + 16 * (lane % 3),
-                  S.wdb + WD_CODES + mw * 768);
+                  wdb + WD_CODES + mw * 768);
 }
 
-// The math wave's share of the down half-block from S.wdb (after its requests have landed), in
+// The math wave's share of the down half-block from wdb (after its requests have landed), in
 // batches of chunks.
 template <int FMT>
-__device__ __forceinline__ float wd_mac_lds(const Shared& S, int mw, int lane) {
+__device__ __forceinline__ float wd_mac_lds(const Shared& S, const uint8_t* wdb, int mw, int lane) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CWD = FFH / CHK / MW, NB = batch_of(CWD);
-    const uint8_t* sbr = S.wdb + WD_CODES + mw * 768 + 48 * (lane & 15);
+    const uint8_t* sbr = wdb + WD_CODES + mw * 768 + 48 * (lane & 15);
     float part[CWD];
 #pragma unroll
     for (int b = 0; b < CWD; b += NB) {
@@ -521,7 +520,7 @@ __device__ __forceinline__ float wd_mac_lds(const Shared& S, int mw, int lane) {
         uint2 sbv[NB];
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            wv[i] = *(const uint4*)(S.wdb + (mw * CWD + b + i) * 1024 + lane * 16);
+            wv[i] = *(const uint4*)(wdb + (mw * CWD + b + i) * 1024 + lane * 16);
             if constexpr (FMT == FMT_Q4)
                 sbv[i] = *(const uint2*)(sbr + 8 * (b + i));
             else
@@ -620,7 +619,7 @@ __device__ uint64_t g_trace[NWG][MAX_LAYERS + 1][32];
 // and the exchange waves' poll buffers side by side.  Both copies execute the same sequence of
 // workgroup barriers (s_barrier counts waves, not call sites), so they stay in lockstep.
 template <int FMT, bool MATH>
-__device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int w, int pos, int stp) {
+__device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
     constexpr int NRB = VOCAB / 16;     // lm_head row blocks
@@ -1015,7 +1014,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             }
             // This layer's down half-block streams into LDS while the gate|up input is awaited
             // and during gate|up (the math waves would otherwise idle at the next barrier).
-            if (math) wd_request<FMT>(S, P.wd, P.wd_sb, w % (NWG / 2), w / (NWG / 2), mw, lane);
+            if (math) wd_request<FMT>(wdb, P.wd, P.wd_sb, w % (NWG / 2), w / (NWG / 2), mw, lane);
 
             // ---------------- RMSNorm + gate|up + SwiGLU: blocks 3w .. 3w + 2 --------------
             {
@@ -1075,7 +1074,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
                     __builtin_amdgcn_s_waitcnt(0);
                     __atomic_signal_fence(__ATOMIC_SEQ_CST);
                     PK_TRACE(l, 23);
-                    yd = wd_mac_lds<FMT>(S, mw, lane);
+                    yd = wd_mac_lds<FMT>(S, wdb, mw, lane);
                     PK_TRACE(l, 24);
                 }
                 const float y = reduce_math<MATH>(S, yd);
@@ -1113,7 +1112,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
             if (__syncthreads_or(!ok)) return;
             PK_TRACE_X(L, 1);
             stage_c<FMT, H, MATH>(S, S.vec, true);
-            float* plm = (float*)S.wdb;  // [LM_BLOCKS][WAVES][16] partial sums
+            float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
             for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
 #pragma unroll
                 for (int k = 0; k < LM_DEPTH; ++k) {
@@ -1211,6 +1210,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, int
 template <int FMT>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     __shared__ Shared S;
+    // The LDS-DMA destination (down half-block; lm_head partial sums later) is an object of its
+    // own, so that LDS accesses to S need not wait for the DMA's completion.
+    __shared__ __align__(16) uint8_t wdb[WD_CODES + WD_SB];
     const int w = blockIdx.x;
     if (my_tid() < 4) S.zero[my_tid()] = 0u;
     // Control block and the embedding of the first token (written before this launch).
@@ -1219,9 +1221,9 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     for (int i = my_tid(); i < H; i += THREADS) S.emb[i] = a.x[i];
     if (my_tid() < 16 && w < H / 16) S.xown[my_tid()] = a.x[w * 16 + my_tid()];
     if (wave_id() < MW)
-        decode_loop<FMT, true>(a, S, w, st->pos, st->step);
+        decode_loop<FMT, true>(a, S, wdb, w, st->pos, st->step);
     else
-        decode_loop<FMT, false>(a, S, w, st->pos, st->step);
+        decode_loop<FMT, false>(a, S, wdb, w, st->pos, st->step);
 }
 
 }  // namespace pk
