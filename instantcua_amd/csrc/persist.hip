@@ -245,136 +245,148 @@ struct Shared {
 
 // ------------------------------------------------------------------------------------------
 // Staging by the whole workgroup: units of 4 consecutive activations (u = tid + THREADS * j <
-// K / 4) -> optional RMSNorm with S.nw -> 22-bit slices -> compact A operands (rows 0, 1, 2 of a
-// group's tile: the hi, mid, lo slices; rows 3..15 read S.zero).  A group is 16 (q4) or 8 (q8)
-// consecutive lanes, so its maximum and sum are DPP row reductions.  When K / 4 is not a
-// multiple of THREADS the last unit row is held by the first waves only (whole waves, so whole
-// groups).
-
-template <int FMT, int K, bool MATH>
+// K / 4), each multiplied by its RMSNorm weight S.nw when `normed`, become exact integers of the
+// group's fixed point (|v| < 2^22, the group maximum's exponent e mapped to bit 21) and are cut
+// into three int8 slices: the compact A operands (rows 0, 1, 2 of a group's tile: hi, mid, lo;
+// rows 3..15 read S.zero) and the group factors (2^(e-21), sum of the integers * 2^(e-21)).  A
+// group is 16 (q4) or 8 (q8) consecutive lanes, so its maximum and sum are DPP row reductions.
+//
+// The RMS factor 1/sqrt(mean(v^2) + eps) of a normed input is a scalar of the whole vector, so it
+// is not applied here: each wave leaves its sum of v^2 in S.misc[40 + wave] and the stage's
+// epilogue multiplies its sums by norm_scale().  The integer conversion is one fma with the
+// magic constant 1.5 * 2^23 (round to nearest even, as rint); the slices are the bytes of
+// (v + 0x808080) ^ 0x808080, which three byte permutes gather into the hi / mid / lo rows.  When
+// K / 4 is not a multiple of THREADS the last unit row is held by the first waves only (whole
+// waves, so whole groups).
+template <int FMT, int K>
 __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed) {
     constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
     constexpr int TILE = (FMT == FMT_Q4) ? 192 : 96;
+    constexpr int SLOT = (FMT == FMT_Q4) ? 16 : 8;  // bytes of a K-slot row
     constexpr int NU = (K / 4 + THREADS - 1) / THREADS;
+    constexpr uint32_t MAGIC = 0x4B400000u;        // 1.5 * 2^23
     static_assert((K / 4) % 64 == 0, "units of whole waves");
     const int tid = my_tid(), lane = tid % 64, wave = wave_id();
-    auto has = [&](int j) { return (K / 4) % THREADS == 0 || tid + THREADS * j < K / 4; };
-    float v[NU][4];
+    float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
-        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (has(j)) a = ((const float4*)src)[tid + THREADS * j];
-        v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
-    }
-    if (normed) {
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < NU; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) ss += v[j][i] * v[j][i];
-        ss = wave_sum(ss);
-        if (lane == 0) S.misc[40 + wave] = ss;
-        __syncthreads();
-        const float tot = ((S.misc[40] + S.misc[41]) + (S.misc[42] + S.misc[43])) +
-                          ((S.misc[44] + S.misc[45]) + (S.misc[46] + S.misc[47]));
-        const float scale = 1.0f / sqrtf(tot / (float)K + EPS);
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            if (!has(j)) continue;
-            const float4 wn = ((const float4*)S.nw)[tid + THREADS * j];
-            v[j][0] = v[j][0] * scale * wn.x;
-            v[j][1] = v[j][1] * scale * wn.y;
-            v[j][2] = v[j][2] * scale * wn.z;
-            v[j][3] = v[j][3] * scale * wn.w;
+        const int u = tid + THREADS * j;
+        if ((K / 4) % THREADS != 0 && u >= K / 4) continue;
+        const float4 a4 = ((const float4*)src)[u];
+        float v[4] = {a4.x, a4.y, a4.z, a4.w};
+        if (normed) {
+            const float4 wn = ((const float4*)S.nw)[u];
+            ss = fmaf(v[0], v[0], ss);
+            ss = fmaf(v[1], v[1], ss);
+            ss = fmaf(v[2], v[2], ss);
+            ss = fmaf(v[3], v[3], ss);
+            v[0] *= wn.x;
+            v[1] *= wn.y;
+            v[2] *= wn.z;
+            v[3] *= wn.w;
         }
-    }
-#pragma unroll
-    for (int j = 0; j < NU; ++j) {
-        if (!has(j)) continue;
-        const int k0 = (tid + THREADS * j) * 4;
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
+        const float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
         int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
         bits = max(bits, dpp_i<DPP_XOR1>(bits));
         bits = max(bits, dpp_i<DPP_XOR2>(bits));
         bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
         if constexpr (G == 64) bits = max(bits, dpp_i<DPP_MIRROR>(bits));
-        int e = ((bits >> 23) & 0xFF) - 127;
-        if (bits == 0) e = -100;  // all-zero group: X = 0 for any exponent
-        const int sh = 21 - e;
+        // e: exponent of the group maximum, clamped so that 2^(21 - e) and 2^(e - 21) are normal
+        // (an all-zero group gives X = 0 with any e).
+        const int e = min(max(((bits >> 23) & 0xFF) - 127, -100), 126);
+        const float p = as_f32((uint32_t)(148 - e) << 23);  // 2^(21 - e)
+        uint32_t t[4];
         int xs = 0;
-        uint32_t p0 = 0, p1 = 0, p2 = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int xv = (int)rintf(ldexpf(v[j][i], sh));
-            xs += xv;
-            const int lo = (int)(int8_t)(xv & 0xFF);
-            const int r1 = (xv - lo) >> 8;
-            const int mid = (int)(int8_t)(r1 & 0xFF);
-            const int hi = (r1 - mid) >> 8;
-            p0 |= (uint32_t)(lo & 0xFF) << (8 * i);
-            p1 |= (uint32_t)(mid & 0xFF) << (8 * i);
-            p2 |= (uint32_t)(hi & 0xFF) << (8 * i);
+            const uint32_t f = as_u32(__builtin_fmaf(v[i], p, as_f32(MAGIC)));  // MAGIC + rint(v 2^(21-e))
+            xs += (int)(f - MAGIC);
+            t[i] = (f + 0x408080u) ^ 0x808080u;  // bytes: lo, mid, hi slices as int8
         }
+        const uint32_t p01 = __builtin_amdgcn_perm(t[1], t[0], 0x05010400u);  // l0 l1 m0 m1
+        const uint32_t p23 = __builtin_amdgcn_perm(t[3], t[2], 0x05010400u);  // l2 l3 m2 m3
+        const uint32_t q01 = __builtin_amdgcn_perm(t[1], t[0], 0x0C0C0602u);  // h0 h1
+        const uint32_t q23 = __builtin_amdgcn_perm(t[3], t[2], 0x0C0C0602u);  // h2 h3
+        const uint32_t lo = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+        const uint32_t mid = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
+        const uint32_t hi = __builtin_amdgcn_perm(q23, q01, 0x05040100u);
         xs += dpp_i<DPP_XOR1>(xs);
         xs += dpp_i<DPP_XOR2>(xs);
         xs += dpp_i<DPP_HALF_MIRROR>(xs);
         if constexpr (G == 64) xs += dpp_i<DPP_MIRROR>(xs);
-        const int gl = k0 / G, kk = k0 % G;
+        const int k0 = u * 4, gl = k0 / G, kk = k0 % G;
         uint8_t* A = S.A + gl * TILE;
-        constexpr int SLOT = (FMT == FMT_Q4) ? 16 : 8;  // bytes of a K-slot row
         const int q = kk / SLOT, j0 = kk % SLOT;
-        *(uint32_t*)(A + (3 * q + 0) * SLOT + j0) = p2;
-        *(uint32_t*)(A + (3 * q + 1) * SLOT + j0) = p1;
-        *(uint32_t*)(A + (3 * q + 2) * SLOT + j0) = p0;
+        *(uint32_t*)(A + (3 * q + 0) * SLOT + j0) = hi;
+        *(uint32_t*)(A + (3 * q + 1) * SLOT + j0) = mid;
+        *(uint32_t*)(A + (3 * q + 2) * SLOT + j0) = lo;
         if (kk == 0) {
-            const float f = ldexpf(1.0f, -sh);
+            const float f = as_f32((uint32_t)(106 + e) << 23);  // 2^(e - 21)
             S.fx[gl * 2] = f;
             S.fx[gl * 2 + 1] = (float)xs * f;
         }
     }
+    if (normed) {
+        ss = wave_sum(ss);
+        if (lane == 0) S.misc[40 + wave] = ss;
+    }
     __syncthreads();
 }
 
-// One 1 KiB chunk of a 16-row block against the staged operands, in phases so that a batch of
-// chunks issues all of its LDS reads before the first multiply: ops_load reads the chunk's two
-// operand tiles (row lane % 16 of K-slot lane / 16: rows 0-2 are the slices, rows 3-15 read the
-// zero block) and group factors; ops_mfma forms the integer sums, ops_scale the lane's partial.
+// RMS factor of the last normed staging of a K-vector: 1/sqrt(mean(v^2) + eps) from the eight
+// waves' sums (valid after the staging's barrier, until the next normed staging).
+template <int K>
+__device__ __forceinline__ float norm_scale(const Shared& S) {
+    const float tot = ((S.misc[40] + S.misc[41]) + (S.misc[42] + S.misc[43])) +
+                      ((S.misc[44] + S.misc[45]) + (S.misc[46] + S.misc[47]));
+    return 1.0f / sqrtf(tot / (float)K + EPS);
+}
+
+// Two 1 KiB chunks (c, c + 1) of a 16-row block against the staged operands: a quad of four
+// quantisation groups (q4: 2 x 64 K per chunk; q8: 2 x 32 K).  The four multiplies of a quad
+// accumulate into one result: group j's operand tile puts its three slices in rows 4j .. 4j + 2
+// and zeros elsewhere, so lanes 16j .. 16j + 15 end with group j's (hi, mid, lo) sums of weight
+// rows 0-15, and one group scaling serves all four groups.  quad_load reads the four operand
+// tiles (lane (r, q): slice r % 4 of K-slot q of group r / 4 when r % 4 < 3, else the zero
+// block) and the factors (2^(e-21), sum X 2^(e-21)) of the lane's group j = lane / 16.
 template <int FMT>
-struct ChunkOps {
-    v4i A[2];     // q4: operand tiles of groups 2c, 2c + 1 (q8 uses the low 8 bytes)
-    float f[4];   // (2^(e-21), sum X 2^(e-21)) of both groups
+struct QuadOps {
+    v4i A[4];  // operand tile of group position j (q8 uses the low 8 bytes)
+    float f, fX;
 };
 
 template <int FMT>
-__device__ __forceinline__ ChunkOps<FMT> ops_load(const Shared& S, int c, int lane) {
-    ChunkOps<FMT> o;
-    const int r = lane & 15, q = lane >> 4;
+__device__ __forceinline__ QuadOps<FMT> quad_load(const Shared& S, int c, int lane) {
+    QuadOps<FMT> o;
+    const int r = lane & 15, q = lane >> 4, sl = r & 3, jr = r >> 2;
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const int gl = 2 * c + hh;
+    for (int j = 0; j < 4; ++j) {
+        const int gl = 2 * c + j;  // groups 2c, 2c + 1 (chunk c), 2c + 2, 2c + 3 (chunk c + 1)
+        const bool on = jr == j && sl < 3;
         if constexpr (FMT == FMT_Q4) {
-            const uint8_t* ap = r < 3 ? S.A + gl * 192 + (3 * q + r) * 16 : (const uint8_t*)S.zero;
-            o.A[hh] = *(const v4i*)ap;
+            const uint8_t* ap = on ? S.A + gl * 192 + (3 * q + sl) * 16 : (const uint8_t*)S.zero;
+            o.A[j] = *(const v4i*)ap;
         } else {
-            const uint8_t* ap = r < 3 ? S.A + gl * 96 + (3 * q + r) * 8 : (const uint8_t*)S.zero;
+            const uint8_t* ap = on ? S.A + gl * 96 + (3 * q + sl) * 8 : (const uint8_t*)S.zero;
             const long v = *(const long*)ap;
-            o.A[hh] = v4i{(int)(uint32_t)v, (int)(uint32_t)((uint64_t)v >> 32), 0, 0};
+            o.A[j] = v4i{(int)(uint32_t)v, (int)(uint32_t)((uint64_t)v >> 32), 0, 0};
         }
-        const float2 fx = *(const float2*)(S.fx + gl * 2);
-        o.f[2 * hh] = fx.x;
-        o.f[2 * hh + 1] = fx.y;
     }
+    const float2 fx = *(const float2*)(S.fx + (2 * c + q) * 2);
+    o.f = fx.x;
+    o.fX = fx.y;
     return o;
 }
 
-// Integer partial sums of both groups of a chunk (q4: v_mfma_i32_16x16x64_i8, q8: 16x16x32).
+// Integer sums of a quad against weight chunks w0 (groups j = 0, 1) and w1 (j = 2, 3):
+// v_mfma_i32_16x16x64_i8 (q4) / 16x16x32 (q8), accumulated.
 template <int FMT>
-__device__ __forceinline__ void ops_mfma(const ChunkOps<FMT>& o, uint4 wv, v4i (&C)[2]) {
-    const v4i zero = {0, 0, 0, 0};
+__device__ __forceinline__ v4i quad_mfma(const QuadOps<FMT>& o, uint4 w0, uint4 w1) {
+    v4i C = {0, 0, 0, 0};
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
+    for (int j = 0; j < 4; ++j) {
+        const uint4 wv = j < 2 ? w0 : w1;
+        const int hh = j & 1;
         if constexpr (FMT == FMT_Q4) {
             const uint32_t d0 = hh ? wv.z : wv.x, d1 = hh ? wv.w : wv.y;
             v4i B;
@@ -382,109 +394,86 @@ __device__ __forceinline__ void ops_mfma(const ChunkOps<FMT>& o, uint4 wv, v4i (
             B[1] = (int)((d0 >> 4) & 0x0F0F0F0Fu);
             B[2] = (int)(d1 & 0x0F0F0F0Fu);
             B[3] = (int)((d1 >> 4) & 0x0F0F0F0Fu);
-            C[hh] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[hh], B, zero, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.A[j], B, C, 0, 0, 0);
         } else {
             const long B = (long)(hh ? ((uint64_t)wv.w << 32 | wv.z) : ((uint64_t)wv.y << 32 | wv.x));
-            const long A = (long)((uint64_t)(uint32_t)o.A[hh][0] | ((uint64_t)(uint32_t)o.A[hh][1] << 32));
-            C[hh] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+            const long A = (long)((uint64_t)(uint32_t)o.A[j][0] | ((uint64_t)(uint32_t)o.A[j][1] << 32));
+            C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C, 0, 0, 0);
         }
     }
+    return C;
 }
 
-// Group scaling of a chunk's integer sums: the lane's partial (lanes 0-15 hold rows 0-15).
+// Group scaling of a quad's sums into the lane's partial: Sv = 65536 hi + (256 mid + lo) (the
+// bracket exact in int32), then acc += s (f Sv) + b (f X) with the fp16 scale / bias word `sq` of
+// the lane's group (q8: the scale in the low half) read by mixed-precision fmas.
 template <int FMT>
-__device__ __forceinline__ float ops_scale(const ChunkOps<FMT>& o, const v4i (&C)[2], uint2 sbv) {
-    float acc = 0.f;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const float Sv = fmaf((float)C[hh][0], 65536.f, fmaf((float)C[hh][1], 256.f, (float)C[hh][2]));
-        if constexpr (FMT == FMT_Q4) {
-            const f16x2 sb2 = as_h2(hh ? sbv.y : sbv.x);
-            // The two groups' terms are independent; they meet in one add.
-            acc += fmaf((float)sb2.x * o.f[2 * hh], Sv, (float)sb2.y * o.f[2 * hh + 1]);
-        } else {
-            const f16x2 s2 = as_h2(sbv.x);
-            acc += (hh ? (float)s2.y : (float)s2.x) * o.f[2 * hh] * Sv;
-        }
-    }
+__device__ __forceinline__ float quad_scale(const QuadOps<FMT>& o, v4i C, uint32_t sq, float acc) {
+    const float Sv = fmaf((float)C[0], 65536.f, (float)(C[1] * 256 + C[2]));
+    const f16x2 sb2 = as_h2(sq);
+    acc = fmaf((float)sb2.x, o.f * Sv, acc);
+    if constexpr (FMT == FMT_Q4) acc = fmaf((float)sb2.y, o.fX, acc);
     return acc;
 }
 
-// Pairwise sum of N values (fixed order).
-template <int N>
-__device__ __forceinline__ float tree_sum(float (&v)[N]) {
-#pragma unroll
-    for (int w = 1; w < N; w *= 2)
-#pragma unroll
-        for (int i = 0; i + w < N; i += 2 * w) v[i] += v[i + w];
-    return v[0];
-}
+// Sum of a lane's partial with the three other lanes of its weight row (l, l ^ 16, l ^ 32,
+// l ^ 48): lanes 0-15 then hold the row totals.
+__device__ __forceinline__ float quad_rows(float v) { return sum_x4(v); }
 
-// Chunks c0 + i (i < N) against weights wv / sbv: all LDS reads, then all multiplies, then the
-// group scaling (no multiply result is consumed right after its issue).  Partials into part[i].
-template <int FMT, int N>
-__device__ __forceinline__ void mac_batch(const Shared& S, const uint4* wv, const uint2* sbv, int c0, int lane,
-                                          float* part) {
-    ChunkOps<FMT> o[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) o[i] = ops_load<FMT>(S, c0 + i, lane);
-    v4i C[N][2];
-#pragma unroll
-    for (int i = 0; i < N; ++i) ops_mfma<FMT>(o[i], wv[i], C[i]);
-#pragma unroll
-    for (int i = 0; i < N; ++i) part[i] = ops_scale<FMT>(o[i], C[i], sbv[i]);
-}
-
-// Scales of chunk c of tiled row `row`: q4 chunk = 128 K (two half2 (scale, bias) of 64-K
-// groups), q8 chunk = 64 K (two half scales of 32-K groups).
+// The scale word of the lane's group in a quad: row `row`, group 2c + lane / 16 (q4: the
+// (scale, bias) half2; q8: the scale).
 template <int FMT>
-__device__ __forceinline__ uint2 load_sb(const uint8_t* sb, int row, int K, int c) {
+__device__ __forceinline__ uint32_t load_sq(const uint8_t* sb, int row, int K, int c, int lane) {
     if constexpr (FMT == FMT_Q4)
-        return *(const uint2*)(sb + ((size_t)row * (K / 64) + 2 * c) * 4);
+        return *(const uint32_t*)(sb + ((size_t)row * (K / 64) + 2 * c + (lane >> 4)) * 4);
     else
-        return make_uint2(*(const uint32_t*)(sb + ((size_t)row * (K / 32) + 2 * c) * 2), 0u);
+        return (uint32_t) * (const uint16_t*)(sb + ((size_t)row * (K / 32) + 2 * c + (lane >> 4)) * 2);
 }
 
-// Chunks per batch of a wave's CW chunks (at most 4).
-constexpr int batch_of(int cw) { return cw <= 4 ? cw : cw % 4 == 0 ? 4 : cw % 3 == 0 ? 3 : 2; }
-
-// This math wave's share (chunks c0 + mw * CW .. c0 + mw * CW + CW - 1) of 16-row block rb; the
-// staged operands start at chunk c0.
+// This math wave's share (chunks mw * CW .. mw * CW + CW - 1, CW even) of 16-row block rb.
 template <int FMT, int CW>
 struct WB {
+    static_assert(CW % 2 == 0, "whole quads");
     uint4 wv[CW];
-    uint2 sb[CW];
-    __device__ __forceinline__ void load(const uint8_t* w, const uint8_t* sbp, int rb, int K, int mw, int lane,
-                                         int c0 = 0) {
+    uint32_t sq[CW / 2];
+    __device__ __forceinline__ void load(const uint8_t* w, const uint8_t* sbp, int rb, int K, int mw, int lane) {
         constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
         const int cpb = K / CHK;
         const uint8_t* blk = w + (size_t)rb * cpb * 1024;
 #pragma unroll
-        for (int i = 0; i < CW; ++i) {
-            const int c = c0 + mw * CW + i;
-            wv[i] = ((const uint4*)(blk + (size_t)c * 1024))[lane];
-            sb[i] = load_sb<FMT>(sbp, rb * 16 + lane % 16, K, c);
-        }
+        for (int i = 0; i < CW; ++i) wv[i] = ((const uint4*)(blk + (size_t)(mw * CW + i) * 1024))[lane];
+#pragma unroll
+        for (int p = 0; p < CW / 2; ++p) sq[p] = load_sq<FMT>(sbp, rb * 16 + (lane & 15), K, mw * CW + 2 * p, lane);
     }
     // Ends the live range of the tile's registers (no instruction): a tile loaded under a
     // condition is otherwise kept alive across every path where the condition is false.
     __device__ __forceinline__ void forget() {
 #pragma unroll
-        for (int i = 0; i < CW; ++i) {
-            asm volatile("" : "=v"(wv[i].x), "=v"(wv[i].y), "=v"(wv[i].z), "=v"(wv[i].w));
-            asm volatile("" : "=v"(sb[i].x), "=v"(sb[i].y));
-        }
-    }
-    // Batches of chunks issue their LDS reads together; partials summed pairwise.
-    __device__ __forceinline__ float mac(const Shared& S, int mw, int lane) const {
-        constexpr int NB = batch_of(CW);
-        static_assert(CW % NB == 0, "chunk batches");
-        float part[CW];
+        for (int i = 0; i < CW; ++i) asm volatile("" : "=v"(wv[i].x), "=v"(wv[i].y), "=v"(wv[i].z), "=v"(wv[i].w));
 #pragma unroll
-        for (int b = 0; b < CW; b += NB) mac_batch<FMT, NB>(S, wv + b, sb + b, mw * CW + b, lane, part + b);
-        return tree_sum<CW>(part);
+        for (int p = 0; p < CW / 2; ++p) asm volatile("" : "=v"(sq[p]));
     }
 };
+
+// NB blocks' shares (the same chunks of NB row blocks) against the staged operands: each quad's
+// operand tiles are read from LDS once for all blocks.  acc[b] is block b's total of this wave in
+// lanes 0-15.
+template <int FMT, int CW, int NB>
+__device__ __forceinline__ void mac_blocks(const Shared& S, const WB<FMT, CW>* wb, int mw, int lane, float (&acc)[NB]) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+#pragma unroll
+    for (int p = 0; p < CW / 2; ++p) {
+        const QuadOps<FMT> o = quad_load<FMT>(S, mw * CW + 2 * p, lane);
+        v4i C[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) C[b] = quad_mfma<FMT>(o, wb[b].wv[2 * p], wb[b].wv[2 * p + 1]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] = quad_scale<FMT>(o, C[b], wb[b].sq[p], acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = quad_rows(acc[b]);
+}
 
 // Down half-block `half` of row block rb straight into wdb (math wave mw requests the chunks
 // and the scale columns it multiplies later, so each wave reads back only its own requests).
@@ -506,33 +495,31 @@ __device__ __forceinline__ void wd_request(uint8_t* wdb, const uint8_t* wd, cons
                   wdb + WD_CODES + mw * 768);
 }
 
-// The math wave's share of the down half-block from wdb (after its requests have landed), in
-// batches of chunks.
+// The math wave's share of the down half-block from wdb (after its requests have landed), a
+// quad (two chunks) at a time; the total in lanes 0-15.  The wave's scale columns in LDS are
+// 16 rows x 48 B: (scale, bias) words of its 12 q4 groups, or the scales of its 24 q8 groups.
 template <int FMT>
 __device__ __forceinline__ float wd_mac_lds(const Shared& S, const uint8_t* wdb, int mw, int lane) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
-    constexpr int CWD = FFH / CHK / MW, NB = batch_of(CWD);
+    constexpr int CWD = FFH / CHK / MW;
+    static_assert(CWD % 2 == 0, "whole quads");
     const uint8_t* sbr = wdb + WD_CODES + mw * 768 + 48 * (lane & 15);
-    float part[CWD];
+    float acc = 0.f;
 #pragma unroll
-    for (int b = 0; b < CWD; b += NB) {
-        uint4 wv[NB];
-        uint2 sbv[NB];
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            wv[i] = *(const uint4*)(wdb + (mw * CWD + b + i) * 1024 + lane * 16);
-            if constexpr (FMT == FMT_Q4)
-                sbv[i] = *(const uint2*)(sbr + 8 * (b + i));
-            else
-                sbv[i] = make_uint2(*(const uint32_t*)(sbr + 4 * (b + i)), 0u);
-        }
-        mac_batch<FMT, NB>(S, wv, sbv, mw * CWD + b, lane, part + b);
+    for (int p = 0; p < CWD / 2; ++p) {
+        const uint4 w0 = *(const uint4*)(wdb + (mw * CWD + 2 * p) * 1024 + lane * 16);
+        const uint4 w1 = *(const uint4*)(wdb + (mw * CWD + 2 * p + 1) * 1024 + lane * 16);
+        const int gq = 4 * p + (lane >> 4);  // the lane's group among the wave's
+        const uint32_t sq = FMT == FMT_Q4 ? *(const uint32_t*)(sbr + 4 * gq) : (uint32_t) * (const uint16_t*)(sbr + 2 * gq);
+        const QuadOps<FMT> o = quad_load<FMT>(S, mw * CWD + 2 * p, lane);
+        acc = quad_scale<FMT>(o, quad_mfma<FMT>(o, w0, w1), sq, acc);
     }
-    return tree_sum<CWD>(part);
+    return quad_rows(acc);
 }
 
 // Sum of the math waves' per-lane partials (whole-workgroup call); the total is valid in math
-// wave 0 (lanes 0-15 meaningful).
+// wave 0 (lanes 0-15 meaningful).  One barrier: S.red is next written after the barriers of a
+// later stage, so wave 0's reads need no second one.
 template <bool MATH>
 __device__ __forceinline__ float reduce_math(Shared& S, float acc) {
     const int tid = my_tid(), lane = tid % 64, wave = wave_id();
@@ -540,11 +527,10 @@ __device__ __forceinline__ float reduce_math(Shared& S, float acc) {
     __syncthreads();
     float s = 0.f;
     if (wave == 0) s = (S.red[lane] + S.red[64 + lane]) + (S.red[128 + lane] + S.red[192 + lane]);
-    __syncthreads();
     return s;
 }
 
-// reduce_math for N <= 3 blocks at once (one pair of barriers).
+// reduce_math for N <= 3 blocks at once (one barrier).
 template <bool MATH, int N>
 __device__ __forceinline__ void reduce_math_n(Shared& S, const float (&acc)[N], float (&out)[N]) {
     static_assert(N <= 3, "S.red holds three blocks");
@@ -561,7 +547,6 @@ __device__ __forceinline__ void reduce_math_n(Shared& S, const float (&acc)[N], 
             out[j] = (r[lane] + r[64 + lane]) + (r[128 + lane] + r[192 + lane]);
         }
     }
-    __syncthreads();
 }
 
 __device__ __forceinline__ void norm_rope(float& a, float& b, float w0, float w1, float c, float sn) {
@@ -709,14 +694,14 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             if (__syncthreads_or(!ok_in)) return;
             PK_TRACE_X(l, 1);
             if (qkv_wg) {
-                stage_c<FMT, H, MATH>(S, l == 0 ? S.emb : S.vec, true);
+                stage_c<FMT, H>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[2] = {0.f, 0.f}, y[2] = {0.f, 0.f};
-                if (math) {
-                    acc[0] = wx[0].mac(S, mw, lane);
-                    acc[1] = wx[1].mac(S, mw, lane);
-                }
+                if (math) mac_blocks<FMT, CW2, 2>(S, wx, mw, lane, acc);
                 reduce_math_n<MATH, 2>(S, acc, y);
                 if (wave == 0) {  // rows 2i, 2i + 1 of a block in packet i (even lanes)
+                    const float rs = norm_scale<H>(S);
+                    y[0] *= rs;
+                    y[1] *= rs;
                     const float n0 = __shfl_xor(y[0], 1), n1 = __shfl_xor(y[1], 1);
                     if (lane < 16 && !(lane & 1)) {
                         st64(ll + QKVP + (w - NWG / 2) * 8 + lane / 2, pack2(y[0], n0, r + 1));
@@ -1000,8 +985,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             }
             if (w < H / 16) {
                 PK_TRACE_X(l, 7);
-                stage_c<FMT, H, MATH>(S, S.vec, false);
-                const float y = reduce_math<MATH>(S, math ? wx[0].mac(S, mw, lane) : 0.f);
+                stage_c<FMT, H>(S, S.vec, false);
+                float acc1[1] = {0.f};
+                if (math) mac_blocks<FMT, CW2, 1>(S, wx, mw, lane, acc1);
+                const float y = reduce_math<MATH>(S, acc1[0]);
                 if (wave == 0) {  // the owner keeps the residual as published (even rows rounded)
                     const float xn = lane < 16 ? (S.xown[lane] + S.xhi[lane]) + y : 0.f;
                     const float xo = __shfl_xor(xn, 1);
@@ -1028,19 +1015,18 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 }
                 if (__syncthreads_or(!ok)) return;
                 PK_TRACE_X(l, 9);
-                stage_c<FMT, H, MATH>(S, S.vec, true);
+                stage_c<FMT, H>(S, S.vec, true);
                 PK_TRACE(l, 13);
                 float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
-                if (math) {
-#pragma unroll
-                    for (int j = 0; j < 3; ++j) acc[j] = wgu[j].mac(S, mw, lane);
-                }
+                if (math) mac_blocks<FMT, CW2, 3>(S, wgu, mw, lane, acc);
                 reduce_math_n<MATH, 3>(S, acc, y);
                 PK_TRACE(l, 14);
                 if (wave == 0) {
+                    const float rs = norm_scale<H>(S);
 #pragma unroll
                     for (int j = 0; j < 3; ++j) {
                         // Block 3w + j: gate units 8 (3w + j) + 0..7 in lanes 0-7, their up rows in 8-15.
+                        y[j] *= rs;
                         const float up = __shfl_xor(y[j], 8);
                         const float hv = (y[j] / (1.f + expf(-y[j]))) * up, hn = __shfl_xor(hv, 1);
                         if (lane < 8 && !(lane & 1)) st64(ll + HP + (3 * w + j) * 4 + lane / 2, pack2(hv, hn, r + 1));
@@ -1065,7 +1051,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 }
                 if (__syncthreads_or(!ok)) return;
                 PK_TRACE_X(l, 11);
-                stage_c<FMT, FFH, MATH>(S, S.vec, false);
+                stage_c<FMT, FFH>(S, S.vec, false);
                 PK_TRACE(l, 18);
                 float yd = 0.f;
                 if (math) {
@@ -1111,14 +1097,22 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
             if (__syncthreads_or(!ok)) return;
             PK_TRACE_X(L, 1);
-            stage_c<FMT, H, MATH>(S, S.vec, true);
+            stage_c<FMT, H>(S, S.vec, true);
             float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
+            QuadOps<FMT> lq[CW8 / 2];  // this wave's operand quads, the same for every block
+#pragma unroll
+            for (int p = 0; p < CW8 / 2; ++p) lq[p] = quad_load<FMT>(S, wave * CW8 + 2 * p, lane);
             for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
 #pragma unroll
                 for (int k = 0; k < LM_DEPTH; ++k) {
                     const int kb = k0 + k, rb = w + kb * NWG;
                     if (rb < NRB) {
-                        const float y = wl[k].mac(S, wave, lane);
+                        float y = 0.f;
+#pragma unroll
+                        for (int p = 0; p < CW8 / 2; ++p)
+                            y = quad_scale<FMT>(lq[p], quad_mfma<FMT>(lq[p], wl[k].wv[2 * p], wl[k].wv[2 * p + 1]),
+                                                wl[k].sq[p], y);
+                        y = quad_rows(y);
                         if (lane < 16) plm[(kb * WAVES + wave) * 16 + lane] = y;
                         if (rb + LM_DEPTH * NWG < NRB) wl[k].load(a.E, a.Esb, rb + LM_DEPTH * NWG, H, wave, lane);
                     }
@@ -1127,6 +1121,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             __syncthreads();
             float best = -__builtin_inff();
             int besti = 0x7fffffff;
+            const float rs = norm_scale<H>(S);
             for (int e = tid; e < LM_BLOCKS * 16; e += THREADS) {  // (block, row) pairs
                 const int kb = e / 16, rw = e % 16;
                 if (w + kb * NWG < NRB) {
@@ -1134,7 +1129,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     float y = 0.f;
 #pragma unroll
                     for (int wv = 0; wv < WAVES; ++wv) y += pp[wv * 16];
-                    argmax_merge(best, besti, y, (w + kb * NWG) * 16 + rw);
+                    argmax_merge(best, besti, y * rs, (w + kb * NWG) * 16 + rw);
                 }
             }
             wave_argmax(best, besti);
