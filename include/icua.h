@@ -34,6 +34,7 @@ enum {
     ICUA_FLAG_GRAPH_DECODE = 4,  /* decode through the per-kernel HIP graph instead of the persistent kernel */
     ICUA_FLAG_PASS_PREFILL = 8,  /* prefill q4 prompts in passes of 8 rows instead of the matrix-core GEMMs */
     ICUA_FLAG_VISION_DELTA_CACHE = 16, /* icua_generate_vision skips the encoder on an identical frame (Engine.swift:707-716) */
+    ICUA_FLAG_FIRST_LOGITS = 32, /* icua_generate(_vision) keep the first token's logits for icua_logits (writeFirstLogits, Engine.swift:697) */
 };
 
 /* Decode control block, first twelve fields as `State` (Shaders.swift:41-54). */
@@ -53,6 +54,8 @@ typedef struct {
     int64_t weight_bytes, kv_bytes;
     int32_t persistent_decode; /* 1 if icua_decode_steps can use the persistent kernel on this device */
     int32_t vision; /* 1 if the model file holds the vision tower and its mergers */
+    int32_t last_decode_persistent; /* 1 if the last icua_decode_steps call ran as the persistent kernel */
+    int32_t visual_rows; /* rows of the pooler / DeepStack buffers (ICUA_BUF_POOLER, ...), 0 if unset */
 } icua_info_t;
 
 /* Last error message of the calling thread ("" if none). */
@@ -93,10 +96,11 @@ int icua_prefill(icua_engine* e, const int32_t* tokens, int n, int start_pos, in
                  int write_logits);
 
 /* k x Engine.encodeDecodeStep (Engine.swift:675-681), GPU-resident with token feedback on the
- * device; returns after completion.  Steps after a stop are no-ops.  q4 / q8 models without
- * grammar pairs run all k steps in one persistent cooperative kernel (one workgroup per CU);
- * otherwise, or with ICUA_FLAG_GRAPH_DECODE, each step replays a captured HIP graph of the
- * per-stage kernels.  Both paths compute the same arithmetic. */
+ * device; returns after completion.  Steps after a stop are no-ops.  q4 / q8 models run all k
+ * steps in one persistent cooperative kernel (one workgroup per CU), where a forced grammar pair
+ * takes two single-row steps (the first of them commits nothing); f16 models, or
+ * ICUA_FLAG_GRAPH_DECODE, replay a captured HIP graph of the per-stage kernels per step, where a
+ * forced pair is one two-row pass.  Both paths compute the same arithmetic. */
 int icua_decode_steps(icua_engine* e, int k);
 
 /* Engine.generateVision (Engine.swift:696-827) minus the vision encoder: prefill + greedy decode

@@ -134,8 +134,9 @@ struct icua_engine {
     std::vector<int32_t> cached_prefix;
     int mrope_key[3] = {-999, 0, 0};
     int last_logits_rows = 0;
-    // Persistent decode kernel: counter block and availability.
+    // Persistent decode kernel: counter block and availability; whether the last decode call used it.
     unsigned* psync = nullptr;
+    bool last_persistent = false;
     bool persist_ok = false;
     // Matrix-core prefill buffers for chunks of up to pf_cap rows (allocated on first use).
     int pf_cap = 0;
@@ -642,7 +643,7 @@ struct icua_engine {
         return 0;
     }
 
-    bool use_persistent() const { return persist_ok && !(flags & (ICUA_FLAG_GRAMMAR_PAIRS | ICUA_FLAG_GRAPH_DECODE)); }
+    bool use_persistent() const { return persist_ok && !(flags & ICUA_FLAG_GRAPH_DECODE); }
 
     int enqueue_persistent(int k) {
         PersistArgs a{};
@@ -868,11 +869,12 @@ struct icua_engine {
     int decode_steps(int k, double* ms_out) {
         if (k < 0) return fail("negative step count");
         bool persistent = use_persistent();
-        if (persistent) {  // single-row passes only (a grammar pair pass takes the graph path)
+        if (persistent) {  // single-row passes, or a pending forced pair (run as two rows)
             State s;
             if (read_state(s)) return -1;
-            if (s.n != 1 || (s.flags & STATE_FLAG_GRAMMAR)) persistent = false;
+            if (s.n < 1 || s.n > 2 || (s.n == 2 && !(s.flags & STATE_FLAG_GRAMMAR))) persistent = false;
         }
+        last_persistent = persistent;
         const int mt = decode_mt();
         if (!persistent && ensure_graph(mt)) return -1;
         HIPCK(hipEventRecord(ev0, stream));
@@ -960,6 +962,8 @@ int icua_engine_info(icua_engine* e, icua_info_t* out) {
     out->weight_bytes = (int64_t)e->weight_bytes;
     out->kv_bytes = (int64_t)e->layers * 2 * NKV * e->maxctx * HD * 2;
     out->persistent_decode = e->persist_ok ? 1 : 0;
+    out->last_decode_persistent = e->last_persistent ? 1 : 0;
+    out->visual_rows = e->n_vis;
     return 0;
 }
 
@@ -1034,23 +1038,25 @@ int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, 
     const int active = n - start;
     const int active_vis = vis_offset >= 0 ? vis_offset - start : -1;
     max_new = std::max(1, std::min(max_new, e->maxsteps));
-    if (e->prefill(tokens + start, active, start, active_vis, max_new, 0)) return -1;
+    if (e->prefill(tokens + start, active, start, active_vis, max_new, (e->flags & ICUA_FLAG_FIRST_LOGITS) ? 1 : 0))
+        return -1;
     if (use_cache && !hit) e->cached_prefix.assign(tokens, tokens + vis_offset);
     double dec_ms = 0;
-    int submitted = 1;
-    while (submitted < max_new) {  // batches of 8 steps (Engine.swift:771-792)
-        // The persistent kernel stops on the device at EOS: no host round trip per batch.
-        const int count = e->use_persistent() ? max_new - submitted : std::min(8, max_new - submitted);
+    State s;
+    if (e->read_state(s)) return -1;
+    while (!s.done && s.step < s.maxsteps) {
+        // Batches of 8 passes on the graph path (Engine.swift:771-792).  The persistent kernel
+        // runs to the stop on the device (EOS, ')', the step limit): a forced pair takes one step
+        // more than the tokens it commits, so twice the remaining tokens bound its steps.
+        const int left = s.maxsteps - s.step;
+        const int count = e->use_persistent() ? 2 * left + 1 : std::min(8, left);
+        const int step0 = s.step, pos0 = s.pos;
         double ms = 0;
         if (e->decode_steps(count, &ms)) return -1;
         dec_ms += ms;
-        submitted += count;
-        State s;
         if (e->read_state(s)) return -1;
-        if (s.done) break;
+        if (!s.done && s.step == step0 && s.pos == pos0) return fail("decode made no progress");
     }
-    State s;
-    if (e->read_state(s)) return -1;
     std::vector<int32_t> toks(std::max(s.step, 1));
     HIPCK(hipMemcpy(toks.data(), e->out_tokens, sizeof(int32_t) * s.step, hipMemcpyDeviceToHost));
     int cnt = 0;

@@ -604,7 +604,8 @@ __device__ uint64_t g_trace[NWG][MAX_LAYERS + 1][32];
 // and the exchange waves' poll buffers side by side.  Both copies execute the same sequence of
 // workgroup barriers (s_barrier counts waves, not call sites), so they stay in lockstep.
 template <int FMT, bool MATH>
-__device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp) {
+__device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp,
+                                            bool pair) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
     constexpr int NRB = VOCAB / 16;     // lm_head row blocks
@@ -615,6 +616,14 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     unsigned* err = (unsigned*)a.ll + ERRW;
     State* st = a.st;
     const int maxsteps = st->maxsteps, eos0 = st->eos0, eos1 = st->eos1, maxctx = st->maxctx;
+    const bool grammar = (st->flags & STATE_FLAG_GRAMMAR) != 0;
+    // A forced pair (grammar pairs, Shaders.swift:1537-1561) is the reference's two-token pass:
+    // here it runs as two single-row steps.  `skip` marks a step whose token is the first of a
+    // pair: its logits are not used, and the forced token `pend` (already committed) follows at
+    // the next slot.  A launch that starts with a pair (n = 2) reads the forced token back from
+    // the token list.
+    bool skip = pair;
+    int pend = pair ? a.out_tokens[stp - 1] : -1;
     const int L = a.nlayers;
     float nreg[8];  // math threads: norm weights of the next normed stage (8 each)
     if (MATH) load_norm8(nreg, a.layers[0].attn_norm + my_tid() * 8);
@@ -1077,6 +1086,28 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             }
         }
 
+        if (skip) {
+            // ---------------- first token of a forced pair: no lm_head, no commit -------------
+            const int tid = my_tid();
+            skip = false;
+            pos += 1;
+            const int tok = pend;
+            pend = -1;
+            if (w == 0 && tid == 0) {
+                st->pos = pos;
+                st->n = 1;
+                st->vis_offset = -1;
+                st->logits_rows = 0;
+            }
+            for (int i = tid; i < H; i += THREADS) S.emb[i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)tok, i, H);
+            __syncthreads();
+            if (tid < 16 && w < H / 16) S.xown[tid] = S.emb[w * 16 + tid];
+            if (w == 0 && step == a.nsteps - 1)
+                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row for the host
+            if (MATH) load_norm8(nreg, a.layers[0].attn_norm + tid * 8);  // for the next step
+            continue;
+        }
+
         // ---------------- final RMSNorm + lm_head + per-workgroup argmax ---------------------
         {
             const int tid = my_tid(), lane = tid % 64, wave = wave_id();
@@ -1179,12 +1210,26 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 if (w == 0 && tid == 0) a.out_tokens[stp] = tok;
                 stp += 1;
                 pos += 1;
-                stop = bad || tok == eos0 || tok == eos1 || stp >= maxsteps || pos + 2 > maxctx;
+                stop = bad || tok == eos0 || tok == eos1 || (grammar && tok == 8) || stp >= maxsteps ||
+                       pos + 2 > maxctx;
+                // Grammar pairs: after a first-step action token, or after 11, the next token is
+                // forced (7, or 220 after 11); it is committed now and fed after `tok`.
+                if (!stop && grammar &&
+                    ((stp == 1 && (tok == 3678 || tok == 7241 || tok == 12476 || tok == 10855 || tok == 11862 ||
+                                   tok == 1339 || tok == 1472 || tok == 24769)) ||
+                     tok == 11)) {
+                    const int forced = tok == 11 ? 220 : 7;
+                    if (w == 0 && tid == 0) a.out_tokens[stp] = forced;
+                    stp += 1;
+                    pend = forced;
+                    skip = true;
+                    stop = stp >= maxsteps;  // the pair's pass would start at the step limit
+                }
             }
             if (w == 0 && tid == 0) {
                 st->pos = pos;
                 st->step = stp;
-                st->n = 1;
+                st->n = (skip && !stop) ? 2 : 1;
                 st->vis_offset = -1;
                 st->logits_rows = 0;
                 if (stop) st->done = 1;
@@ -1195,8 +1240,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             for (int i = tid; i < H; i += THREADS) S.emb[i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)tok, i, H);
             __syncthreads();
             if (tid < 16 && w < H / 16) S.xown[tid] = S.emb[w * 16 + tid];
-            if (w == 0 && step == a.nsteps - 1)
-                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row for the host
+            if (w == 0 && step == a.nsteps - 1) {
+                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row(s) for the host
+                if (skip)
+                    for (int i = tid; i < H; i += THREADS) a.x[H + i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)pend, i, H);
+            }
             PK_TRACE(L, 4);
         }
     }
@@ -1212,13 +1260,14 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     if (my_tid() < 4) S.zero[my_tid()] = 0u;
     // Control block and the embedding of the first token (written before this launch).
     const State* st = a.st;
-    if (st->done || st->n != 1) return;  // single-row passes only (checked by the host too)
+    if (st->done || st->n < 1 || st->n > 2) return;  // a single row, or a forced pair (checked by the host too)
+    const bool pair = st->n == 2;
     for (int i = my_tid(); i < H; i += THREADS) S.emb[i] = a.x[i];
     if (my_tid() < 16 && w < H / 16) S.xown[my_tid()] = a.x[w * 16 + my_tid()];
     if (wave_id() < MW)
-        decode_loop<FMT, true>(a, S, wdb, w, st->pos, st->step);
+        decode_loop<FMT, true>(a, S, wdb, w, st->pos, st->step, pair);
     else
-        decode_loop<FMT, false>(a, S, wdb, w, st->pos, st->step);
+        decode_loop<FMT, false>(a, S, wdb, w, st->pos, st->step, pair);
 }
 
 }  // namespace pk

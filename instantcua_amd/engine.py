@@ -29,6 +29,7 @@ FLAG_PREFIX_CACHE = 2
 FLAG_GRAPH_DECODE = 4
 FLAG_PASS_PREFILL = 8
 FLAG_VISION_DELTA_CACHE = 16
+FLAG_FIRST_LOGITS = 32
 
 EXPORTS = [
     "icua_last_error", "icua_engine_create", "icua_engine_create_from_memory", "icua_engine_destroy",
@@ -63,7 +64,8 @@ class _Timing(C.Structure):
 class _Info(C.Structure):
     _fields_ = [("format", C.c_int32), ("layers", C.c_int32), ("max_context", C.c_int32),
                 ("max_pass", C.c_int32), ("max_steps", C.c_int32), ("weight_bytes", C.c_int64),
-                ("kv_bytes", C.c_int64), ("persistent_decode", C.c_int32), ("vision", C.c_int32)]
+                ("kv_bytes", C.c_int64), ("persistent_decode", C.c_int32), ("vision", C.c_int32),
+                ("last_decode_persistent", C.c_int32), ("visual_rows", C.c_int32)]
 
 
 _lib = None
@@ -196,7 +198,8 @@ class Engine:
     """Drop-in mirror of ``Engine`` (Sources/Engine/Engine.swift:5)."""
 
     def __init__(self, model_path: Optional[str] = None, image: Optional[np.ndarray] = None,
-                 max_context: int = 2048, max_pass: int = 512, max_steps: int = 256, flags: int = 0):
+                 max_context: int = 2048, max_pass: int = 512, max_steps: int = 256,
+                 flags: int = FLAG_GRAMMAR_PAIRS):
         h = C.c_void_p()
         if model_path is not None:
             _check(lib().icua_engine_create(model_path.encode(), max_context, max_pass, max_steps, flags,
@@ -222,6 +225,13 @@ class Engine:
         self.weight_bytes = info.weight_bytes
         self.kv_bytes = info.kv_bytes
         self.persistent_decode = bool(info.persistent_decode)
+
+    @property
+    def last_decode_persistent(self) -> bool:
+        """Whether the last decode_steps call ran as the persistent kernel."""
+        info = _Info()
+        _check(lib().icua_engine_info(self._h, C.byref(info)))
+        return bool(info.last_decode_persistent)
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -328,7 +338,9 @@ class Engine:
 
     def visual_rows(self):
         """(pooler, [deepstack x 3]) float32 [n_vis][2048] currently held by the engine."""
-        n = self._vis_rows
+        info = _Info()
+        _check(lib().icua_engine_info(self._h, C.byref(info)))
+        n = info.visual_rows
         pool = np.empty((n, H), dtype=np.float32)
         _check(lib().icua_read_buffer(self._h, 4, _p(pool), pool.nbytes))
         ds = []
@@ -338,14 +350,25 @@ class Engine:
             ds.append(d)
         return pool, ds
 
-    def generate_vision(self, rgb: np.ndarray, tokens, max_new_tokens: int = 64) -> list:
-        """generateVision (Engine.swift:696-827) on an RGB8 frame [height][width][3]."""
+    def _with_first_logits(self, on: bool, fn):
+        """Runs fn with FLAG_FIRST_LOGITS set as `on` (writeFirstLogits), restoring the flags."""
+        saved = self._flags
+        self.set_flags((saved | FLAG_FIRST_LOGITS) if on else (saved & ~FLAG_FIRST_LOGITS))
+        try:
+            return fn()
+        finally:
+            self.set_flags(saved)
+
+    def generate_vision(self, rgb: np.ndarray, tokens, max_new_tokens: int = 64,
+                        write_first_logits: bool = False) -> list:
+        """generateVision (Engine.swift:696-827) on an RGB8 frame [height][width][3];
+        write_first_logits keeps the first token's logits for logits()."""
         img = self._rgb(rgb)
         toks = np.ascontiguousarray(tokens, dtype=np.int32)
         out = np.empty(max(1, min(max_new_tokens, self.max_steps) + 1), dtype=np.int32)
         n = C.c_int(0)
-        _check(lib().icua_generate_vision(self._h, _p(img), img.shape[1], img.shape[0], _p(toks), toks.size,
-                                          max_new_tokens, _p(out), C.byref(n)))
+        self._with_first_logits(write_first_logits, lambda: _check(lib().icua_generate_vision(
+            self._h, _p(img), img.shape[1], img.shape[0], _p(toks), toks.size, max_new_tokens, _p(out), C.byref(n))))
         self._vis_rows = (img.shape[0] // 32) * (img.shape[1] // 32)
         return [int(t) for t in out[:n.value]]
 
@@ -358,12 +381,13 @@ class Engine:
     def decode_steps(self, k: int) -> None:
         _check(lib().icua_decode_steps(self._h, k))
 
-    def generate(self, tokens, vis_offset: int = -1, max_new_tokens: int = 64) -> list:
+    def generate(self, tokens, vis_offset: int = -1, max_new_tokens: int = 64,
+                 write_first_logits: bool = False) -> list:
         toks = np.ascontiguousarray(tokens, dtype=np.int32)
         out = np.empty(max(max_new_tokens, 1) + 4, dtype=np.int32)
         n_out = C.c_int()
-        _check(lib().icua_generate(self._h, _p(toks), toks.size, vis_offset, max_new_tokens, _p(out),
-                                   C.byref(n_out)))
+        self._with_first_logits(write_first_logits, lambda: _check(lib().icua_generate(
+            self._h, _p(toks), toks.size, vis_offset, max_new_tokens, _p(out), C.byref(n_out))))
         return [int(t) for t in out[:n_out.value]]
 
     def verify(self, draft, want_logits: bool = False):

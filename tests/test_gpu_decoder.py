@@ -51,7 +51,7 @@ def test_single_layer_q8_step(oracle_mod):
     ref_k = om.kv(0, 0)[:, pos].copy()
     ref_v = om.kv(0, 1)[:, pos].copy()
 
-    with Engine(image=img, max_context=1024) as e:
+    with Engine(flags=0, image=img, max_context=1024) as e:
         e.write_kv(0, 0, 0, kc)
         e.write_kv(0, 1, 0, vc)
         got = e.layer_step(0, x, pos)
@@ -75,7 +75,7 @@ def test_multi_row_layer_q4(oracle_mod, q4_small, n):
     om.kv(1, 0)[:, :pos] = kc
     om.kv(1, 1)[:, :pos] = vc
     ref = om.layer(1, x, pos)
-    with Engine(image=q4_small, max_context=256) as e:
+    with Engine(flags=0, image=q4_small, max_context=256) as e:
         e.write_kv(1, 0, 0, kc)
         e.write_kv(1, 1, 0, vc)
         got = e.layer_step(1, x, pos)
@@ -91,7 +91,7 @@ def test_greedy_decode_small(oracle_mod, q4_small, q8_small, fmt_name):
     steps = 32
     om = oracle_mod.OracleModel(img, 256)
     ref_toks, margins, ref_first = om.generate(toks, steps)
-    with Engine(image=img, max_context=256, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=256, max_steps=steps) as e:
         e.eos = (-1, -1)
         first = e.prefill(toks, max_new=steps, write_logits=True)
         lg = e.logits(1)[0]
@@ -110,7 +110,7 @@ def test_generate_api_matches_oracle(oracle_mod, q4_small):
     toks = synth.random_tokens(13, "gen-api")
     om = oracle_mod.OracleModel(q4_small, 128)
     ref, margins, first = om.generate(toks, 16)
-    with Engine(image=q4_small, max_context=128, max_steps=64) as e:
+    with Engine(flags=0, image=q4_small, max_context=128, max_steps=64) as e:
         e.eos = (-1, -1)
         out = e.generate(toks, max_new_tokens=16)
         t = e.last_timing
@@ -121,7 +121,7 @@ def test_generate_api_matches_oracle(oracle_mod, q4_small):
 
 def test_eos_stops_generation(q4_small):
     toks = synth.random_tokens(9, "eos")
-    with Engine(image=q4_small, max_context=128, max_steps=64) as e:
+    with Engine(flags=0, image=q4_small, max_context=128, max_steps=64) as e:
         e.eos = (-1, -1)
         free = e.generate(toks, max_new_tokens=12)
         stop_tok = free[3]
@@ -140,7 +140,7 @@ def test_visual_prefill_deepstack(oracle_mod, q4_small):
     om = oracle_mod.OracleModel(q4_small, 128)
     om.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
     ref, margins, first = om.generate(vp.tokens, steps, pooler=pooler, vis_offset=vp.vis_offset, deepstack=ds)
-    with Engine(image=q4_small, max_context=128, max_steps=steps) as e:
+    with Engine(flags=0, image=q4_small, max_context=128, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
         e.set_visual(pooler, ds)
@@ -158,7 +158,7 @@ def test_verify_eight_drafts(oracle_mod, q4_small):
     om = oracle_mod.OracleModel(q4_small, 128)
     om.run_pass(toks, 0, logits_rows=1)
     ref_lg = om.run_pass(draft, len(toks), logits_rows=8)
-    with Engine(image=q4_small, max_context=128, max_steps=16) as e:
+    with Engine(flags=0, image=q4_small, max_context=128, max_steps=16) as e:
         e.prefill(toks, max_new=4)
         st0 = e.state()
         am, lg = e.verify(draft, want_logits=True)
@@ -182,7 +182,7 @@ def test_verify_is_deterministic_across_replays(fmt):
     img = synth.build_model_image(fmt, n_layers=2, tag=f"det-{fmt}")
     toks = synth.random_tokens(21, "det")
     drafts = [synth.random_tokens(m, "det-draft", m) for m in (8, 5, 1)]
-    with Engine(image=img, max_context=128, max_steps=16) as e:
+    with Engine(flags=0, image=img, max_context=128, max_steps=16) as e:
         e.prefill(toks, max_new=4)
         first = [e.verify(d, want_logits=True)[1] for d in drafts]
         for rep in range(3):
@@ -204,7 +204,7 @@ def test_layer_stages(oracle_mod, fmt):
     om.kv(0, 0)[:, :pos] = kc
     om.kv(0, 1)[:, :pos] = vc
     ref_x, ref_qkv, ref_att, ref_act = om.layer_taps(0, x, pos)
-    with Engine(image=img, max_context=64) as e:
+    with Engine(flags=0, image=img, max_context=64) as e:
         e.write_kv(0, 0, 0, kc)
         e.write_kv(0, 1, 0, vc)
         got_x = e.layer_step(0, x, pos)

@@ -52,6 +52,12 @@ def _kv_bound_ok(got, ref, rel=2e-3):
 
 
 def _check(e, fx, steps, label):
+    # The engine runs with grammar pairs on (the reference's setting).  The oracle's sequence
+    # holds no token that fires a rule (")" = 8, 11, a first-step action), so it is also the
+    # sequence under the rules.
+    g = fx["greedy"]
+    assert e.grammar_pairs and not ((g == 8) | (g == 11)).any()
+    assert int(g[0]) not in (3678, 7241, 12476, 10855, 11862, 1339, 1472, 24769)
     lg = e.logits(1)[0]
     e.decode_steps(steps - 1)
     st = e.state()
@@ -86,6 +92,7 @@ def test_text_context_1024_prefill_256_greedy(model28):
         assert e.persistent_decode
         e.prefill(toks, max_new=steps, write_logits=True)
         _check(e, fx, steps, "config 3")
+        assert e.last_decode_persistent
 
 
 def test_vision_context_4096_prefill_128_greedy(model28):
@@ -102,6 +109,7 @@ def test_vision_context_4096_prefill_128_greedy(model28):
         e.set_visual(vp.pooler.astype(np.float32), [d.astype(np.float32) for d in vp.deepstack])
         e.prefill(vp.tokens, vis_offset=vp.vis_offset, max_new=steps, write_logits=True)
         _check(e, fx, steps, "config 4")
+        assert e.last_decode_persistent
 
 
 def test_prefill_chunk_of_4096_rows_matches_the_oracle(oracle_mod):
@@ -113,7 +121,7 @@ def test_prefill_chunk_of_4096_rows_matches_the_oracle(oracle_mod):
     om = oracle_mod.OracleModel(img, 4096 + steps + 8)
     ref, margins, first = om.generate(toks, steps)
     slots = [0, 1, 63, 64, 2047, 4000, 4095]
-    with Engine(image=img, max_context=4096 + steps + 8, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=4096 + steps + 8, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.prefill(toks, max_new=steps, write_logits=True)
         lg = e.logits(1)[0]

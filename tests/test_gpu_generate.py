@@ -52,13 +52,43 @@ def test_grammar_pairs_match_the_oracle(oracle_mod, grammar_base, scales, seed, 
         assert ref[-1] == 8 and len(ref) < steps, ref
     else:
         assert sum(a == 11 and b == 220 for a, b in zip(ref, ref[1:])) >= 3, ref
-    with Engine(image=img, max_context=128, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=128, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.grammar_pairs = True
         got = e.generate(toks, max_new_tokens=steps)
         st = e.state()
+        assert e.last_decode_persistent  # the reference's normal setting stays on the fast path
+        e.graph_decode = True
+        got_graph = e.generate(toks, max_new_tokens=steps)
+        assert not e.last_decode_persistent
     assert got == ref, (got, ref)
+    assert got_graph == ref, (got_graph, ref)
     assert st["done"] == 1 and st["step"] == len(ref)
+
+
+@pytest.mark.parametrize("split", [1, 2, 3])
+def test_grammar_pairs_across_decode_calls(oracle_mod, grammar_base, split):
+    """A forced pair left pending at the end of a decode call (state n = 2) continues in the next
+    call: decode in calls of `split` steps and compare with the oracle's loop."""
+    img = scale_embedding_rows(grammar_base, {11: 8, 3678: 8, 8: 3})
+    toks = synth.random_tokens(9, "gram", 3)
+    steps = 16
+    om = oracle_mod.OracleModel(img, 128)
+    ref = [int(t) for t in om.generate_commit(toks, steps, grammar=True)]
+    assert any(a == 11 and b == 220 for a, b in zip(ref, ref[1:])), ref
+    with Engine(flags=0, image=img, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.grammar_pairs = True
+        e.prefill(toks, max_new=steps)
+        for _ in range(4 * steps):
+            st = e.state()
+            if st["done"]:
+                break
+            e.decode_steps(split)
+            assert e.last_decode_persistent
+        st = e.state()
+        got = [int(t) for t in e.tokens(st["step"])]
+    assert got == ref, (got, ref)
 
 
 def test_without_grammar_pairs_no_token_is_forced(oracle_mod, grammar_base):
@@ -69,7 +99,7 @@ def test_without_grammar_pairs_no_token_is_forced(oracle_mod, grammar_base):
     om = oracle_mod.OracleModel(img, 128)
     ref = [int(t) for t in om.generate_commit(toks, steps, grammar=False)]
     assert ref[0] == 3678 and ref[1] != 7
-    with Engine(image=img, max_context=128, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=128, max_steps=steps) as e:
         e.eos = (-1, -1)
         got = e.generate(toks, max_new_tokens=steps)
     assert got == ref
@@ -88,7 +118,7 @@ def test_prefix_cache_reuses_the_system_prompt(oracle_mod, q4_small):
     vp2.tokens[:6] = vp1.tokens[:6]
     steps = 10
     ds2 = [d.astype(np.float32) for d in vp2.deepstack]
-    with Engine(image=q4_small, max_context=128, max_steps=steps) as e:
+    with Engine(flags=0, image=q4_small, max_context=128, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.use_prefix_cache = True
         e.prepare_mrope(vp1.vis_offset, vp1.llm_h, vp1.llm_w)
@@ -101,7 +131,7 @@ def test_prefix_cache_reuses_the_system_prompt(oracle_mod, q4_small):
         t2 = e.last_timing
     assert len(first) == steps and t1["prefill_tokens"] == 40
     assert t2["prefill_tokens"] == 44 - 6, t2
-    with Engine(image=q4_small, max_context=128, max_steps=steps) as e:
+    with Engine(flags=0, image=q4_small, max_context=128, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.prepare_mrope(vp2.vis_offset, vp2.llm_h, vp2.llm_w)
         e.set_visual(vp2.pooler.astype(np.float32), ds2)
@@ -118,7 +148,7 @@ def test_prefix_cache_reuses_the_system_prompt(oracle_mod, q4_small):
 def test_prefix_cache_misses_on_a_new_prefix(q4_small):
     vp1 = synth.visual_prompt(30, vis_offset=4, llm_h=2, llm_w=4, tag="pfx3")
     vp2 = synth.visual_prompt(30, vis_offset=4, llm_h=2, llm_w=4, tag="pfx4")
-    with Engine(image=q4_small, max_context=64, max_steps=4) as e:
+    with Engine(flags=0, image=q4_small, max_context=64, max_steps=4) as e:
         e.eos = (-1, -1)
         e.use_prefix_cache = True
         for vp, want in ((vp1, 30), (vp2, 30), (vp2, 26)):
@@ -130,7 +160,7 @@ def test_prefix_cache_misses_on_a_new_prefix(q4_small):
 
 def test_generate_timing_record(q4_small):
     toks = synth.random_tokens(12, "timing")
-    with Engine(image=q4_small, max_context=64, max_steps=16) as e:
+    with Engine(flags=0, image=q4_small, max_context=64, max_steps=16) as e:
         e.eos = (-1, -1)
         out = e.generate(toks, max_new_tokens=16)
         t = e.last_timing
@@ -155,7 +185,7 @@ def test_prefix_cache_survives_failed_calls_and_text_prompts(oracle_mod, q4_smal
     ref_vis, m_vis, lg_vis = om.generate(vp1.tokens, steps, pooler=pool1, vis_offset=vp1.vis_offset)
     om.prepare_mrope(-1, 1, 1)
     ref_txt, m_txt, lg_txt = om.generate(text, steps)
-    with Engine(image=q4_small, max_context=64, max_steps=steps) as e:
+    with Engine(flags=0, image=q4_small, max_context=64, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.use_prefix_cache = True
         e.prepare_mrope(vp1.vis_offset, vp1.llm_h, vp1.llm_w)
@@ -189,7 +219,7 @@ def test_text_generate_after_a_visual_table(oracle_mod, q4_small):
     steps = 6
     om = oracle_mod.OracleModel(q4_small, 64)
     ref, margins, lg = om.generate(text, steps)
-    with Engine(image=q4_small, max_context=64, max_steps=steps) as e:
+    with Engine(flags=0, image=q4_small, max_context=64, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
         e.set_visual(vp.pooler.astype(np.float32), None)

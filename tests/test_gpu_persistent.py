@@ -54,7 +54,7 @@ def _random_cache(pos, tag):
 
 
 def test_persistent_path_is_available(images):
-    with Engine(image=images["q4"], max_context=128) as e:
+    with Engine(flags=0, image=images["q4"], max_context=128) as e:
         assert e.persistent_decode, "the persistent decode kernel did not initialise on this device"
         assert not e.graph_decode
 
@@ -72,7 +72,7 @@ def test_long_context_decode(oracle_mod, images, fmt_name, pos):
     for (l, k), arr in cache.items():
         om.kv(l, k)[:, :pos] = arr
     ref, margins, tops = _oracle_greedy(om, tok0, pos, steps)
-    with Engine(image=img, max_context=maxctx, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=maxctx, max_steps=steps) as e:
         e.eos = (-1, -1)
         for (l, k), arr in cache.items():
             e.write_kv(l, k, 0, arr)
@@ -102,7 +102,7 @@ def test_persistent_matches_graph_path(oracle_mod, images, fmt_name):
     out = {}
     nrows = len(toks) + steps - 1
     for graph in (False, True):
-        with Engine(image=img, max_context=256, max_steps=steps) as e:
+        with Engine(flags=0, image=img, max_context=256, max_steps=steps) as e:
             e.eos = (-1, -1)
             e.graph_decode = graph
             e.prefill(toks, max_new=steps)
@@ -130,7 +130,7 @@ def test_context_limit_stop_matches_graph_path(images):
     toks = synth.random_tokens(10, "ctx-stop")
     states = []
     for graph in (False, True):
-        with Engine(image=images["q4"], max_context=24, max_steps=64) as e:
+        with Engine(flags=0, image=images["q4"], max_context=24, max_steps=64) as e:
             e.eos = (-1, -1)
             e.graph_decode = graph
             e.prefill(toks, max_new=8)

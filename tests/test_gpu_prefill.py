@@ -38,7 +38,7 @@ def test_prefill_matches_oracle(oracle_mod, q4_small, n):
     steps = 6
     om = oracle_mod.OracleModel(q4_small, n + 16)
     ref, margins, first = om.generate(toks, steps)
-    with Engine(image=q4_small, max_context=n + 16, max_steps=steps) as e:
+    with Engine(flags=0, image=q4_small, max_context=n + 16, max_steps=steps) as e:
         e.eos = (-1, -1)
         assert not e.pass_prefill
         tok0 = e.prefill(toks, max_new=steps, write_logits=True)
@@ -61,7 +61,7 @@ def test_prefill_continuation_at_offset(oracle_mod, q4_small):
     toks = synth.random_tokens(500, "pf-offset")
     om = oracle_mod.OracleModel(q4_small, 512)
     ref_lg = om.run_pass(toks, 0, logits_rows=1)[0]
-    with Engine(image=q4_small, max_context=512, max_steps=8) as e:
+    with Engine(flags=0, image=q4_small, max_context=512, max_steps=8) as e:
         e.eos = (-1, -1)
         e.prefill(toks[:200], max_new=2)
         e.prefill(toks[200:], start_pos=200, max_new=2, write_logits=True)
@@ -83,7 +83,7 @@ def test_visual_prefill_matches_oracle(oracle_mod, q4_small):
     om = oracle_mod.OracleModel(q4_small, 320)
     om.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
     ref, margins, first = om.generate(vp.tokens, steps, pooler=pooler, vis_offset=vp.vis_offset, deepstack=ds)
-    with Engine(image=q4_small, max_context=320, max_steps=steps) as e:
+    with Engine(flags=0, image=q4_small, max_context=320, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
         e.set_visual(pooler, ds)
@@ -104,7 +104,7 @@ def test_two_chunks_match_pass_path(q4_small):
     toks = synth.random_tokens(n, "pf-chunks")
     out = {}
     for passes in (False, True):
-        with Engine(image=q4_small, max_context=n + 8, max_steps=4) as e:
+        with Engine(flags=0, image=q4_small, max_context=n + 8, max_steps=4) as e:
             e.eos = (-1, -1)
             e.pass_prefill = passes
             tok0 = e.prefill(toks, max_new=2, write_logits=True)

@@ -136,7 +136,7 @@ def test_converted_model_matches_oracle(oracle_mod, hf_dir, fmt):
     steps = 12
     om = oracle_mod.OracleModel(img, 64)
     ref, margins, first = om.generate(toks, steps)
-    with Engine(image=img, max_context=64, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=64, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.prefill(toks, max_new=steps)
         e.decode_steps(steps - 1)

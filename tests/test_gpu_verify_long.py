@@ -26,7 +26,7 @@ def test_verify_q8_28_layers_8192_context(oracle_mod):
     img = synth.build_model_image(WeightFormat.Q8, n_layers=layers, tag="verify-q8")
     draft = synth.random_tokens(m, "verify-q8-draft")
     om = oracle_mod.OracleModel(img, ctx + m + 8)
-    with Engine(image=img, max_context=ctx + m + 8, max_steps=8) as e:
+    with Engine(flags=0, image=img, max_context=ctx + m + 8, max_steps=8) as e:
         for l in range(layers):
             for kind in (0, 1):
                 rows = synth.fp16_normal((NKV, ctx, HD), f"verify-q8-kv{kind}", l)
@@ -62,7 +62,7 @@ def test_greedy_256_steps(oracle_mod, fmt_name):
     steps = 256
     om = oracle_mod.OracleModel(img, 64 + steps + 8)
     ref, margins, first = om.generate(toks, steps)
-    with Engine(image=img, max_context=64 + steps + 8, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=64 + steps + 8, max_steps=steps) as e:
         e.eos = (-1, -1)
         assert e.persistent_decode
         e.prefill(toks, max_new=steps)

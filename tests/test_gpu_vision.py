@@ -33,7 +33,7 @@ def rel(got, ref):
 def test_tower_matches_oracle(oracle_mod, vimg, gh, gw):
     rgb = synth.random_rgb(gh, gw, "tower", 100 * gh + gw)
     ref_p, ref_ds = oracle_mod.vision(vimg, rgb)
-    with Engine(image=vimg, max_context=64, max_steps=4) as e:
+    with Engine(flags=0, image=vimg, max_context=64, max_steps=4) as e:
         assert e.has_vision
         e.vision(rgb)
         assert e.last_timing["vision_ms"] > 0
@@ -60,10 +60,15 @@ def test_generate_vision_matches_oracle(oracle_mod, vimg):
     om = oracle_mod.OracleModel(vimg, 128)
     om.prepare_mrope(vis_offset, gh // 2, gw // 2)
     ref, margins, first = om.generate(toks, steps, pooler=ref_p, vis_offset=vis_offset, deepstack=ref_ds)
-    with Engine(image=vimg, max_context=128, max_steps=steps) as e:
+    with Engine(flags=0, image=vimg, max_context=128, max_steps=steps) as e:
         e.eos = (-1, -1)
-        got = e.generate_vision(rgb, toks, max_new_tokens=steps)
+        got = e.generate_vision(rgb, toks, max_new_tokens=steps, write_first_logits=True)
         t = e.last_timing
+        lg = e.logits(1)[0]  # writeFirstLogits (Engine.swift:697): the golden command's first logits
+        p, ds = e.visual_rows()  # poolerBuf / deepstackBufs after the call
+    err = float(np.abs(lg - first).max() / np.abs(first).max())
+    assert err < 1e-2, err
+    assert rel(p, ref_p) < TOL and max(rel(d, r) for d, r in zip(ds, ref_ds)) < TOL
     assert t["vision_ms"] > 0 and t["prefill_tokens"] == toks.size and t["generated_tokens"] == steps
     assert t["total_ms"] >= t["vision_ms"] + t["decode_ms"]
     n, note = compare_greedy(got, ref, margins, first.max() * np.ones(steps))
@@ -74,7 +79,7 @@ def test_vision_delta_cache(vimg):
     gh, gw = 4, 6
     rgb = synth.random_rgb(gh, gw, "delta")
     toks, _ = _prompt(gh * gw // 4, "delta")
-    with Engine(image=vimg, max_context=64, max_steps=4) as e:
+    with Engine(flags=0, image=vimg, max_context=64, max_steps=4) as e:
         e.eos = (-1, -1)
         e.use_vision_delta_cache = True
         a = e.generate_vision(rgb, toks, 4)
@@ -91,13 +96,13 @@ def test_vision_delta_cache(vimg):
 
 
 def test_vision_errors(vimg):
-    with Engine(image=vimg, max_context=64, max_steps=4) as e:
+    with Engine(flags=0, image=vimg, max_context=64, max_steps=4) as e:
         with pytest.raises(EngineError, match="multiples of 32"):
             e.vision(np.zeros((48, 64, 3), np.uint8))
         with pytest.raises(EngineError, match="1024 patches"):
             e.vision(np.zeros((32 * 17, 32 * 16, 3), np.uint8))
     img = synth.build_model_image(WeightFormat.Q4, n_layers=1, tag="q4-novision")
-    with Engine(image=img, max_context=64, max_steps=4) as e:
+    with Engine(flags=0, image=img, max_context=64, max_steps=4) as e:
         assert not e.has_vision
         with pytest.raises(EngineError, match="no vision tower"):
             e.vision(np.zeros((64, 64, 3), np.uint8))
@@ -112,7 +117,7 @@ def test_text_generate_after_generate_vision(oracle_mod, vimg):
     steps = 6
     om = oracle_mod.OracleModel(vimg, 64)
     ref, margins, first = om.generate(text, steps)
-    with Engine(image=vimg, max_context=64, max_steps=steps) as e:
+    with Engine(flags=0, image=vimg, max_context=64, max_steps=steps) as e:
         e.eos = (-1, -1)
         e.generate_vision(rgb, toks, max_new_tokens=steps)
         got = e.generate(text, max_new_tokens=steps)

@@ -139,7 +139,7 @@ def test_create_errors_without_gpu_work(libicua, tmp_path):
     with pytest.raises(eng.EngineError, match="tensor table mismatch|not an instantcua"):
         img = np.zeros(mf.HEADER_SIZE, np.uint8)
         img[:16] = np.array([mf.MAGIC, 1, 2, 5], dtype="<u4").view(np.uint8)
-        eng.Engine(image=img)
+        eng.Engine(flags=0, image=img)
 
 
 def test_noalloc_quantize_rejects_matrices_beyond_its_scratch(libicua):
