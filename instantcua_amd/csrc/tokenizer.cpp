@@ -1,20 +1,27 @@
 // Qwen2 byte-level BPE tokenizer on the host (Sources/Tokenizer/Tokenizer.swift:36-462,
-// Core.swift:1-559): NFC normalisation, the Qwen2 split pattern as a hand-written scanner, BPE by
-// merge rank, added tokens matched on the raw text, lossy UTF-8 decoding, a streaming detokenizer,
-// and the Qwen3-VL chat templates.  It reads the file written by instantcua_amd/tokenizer.py
-// (`compile`), which holds the vocabulary as raw bytes, the merges with their result ids, the
-// added tokens and the Unicode tables (property classes, canonical combining classes, full
-// canonical decompositions and primary compositions).
+// Core.swift:1-559): NFC normalisation, the tokenizer.json Split pattern, BPE by merge rank,
+// added tokens matched on the raw text, lossy UTF-8 decoding, a streaming detokenizer, and the
+// Qwen3-VL chat templates.
 //
-// Split pattern (Tokenizer.swift qwen2SplitRegex), leftmost-first at every position:
-//   A1 (?i:'s|'t|'re|'ve|'m|'ll|'d)   A2 [^\r\n\p{L}\p{N}]?\p{L}+   A3 \p{N}
-//   A4 ' '?[^\s\p{L}\p{N}]+[\r\n]*     A5 \s*[\r\n]+   A6 \s+(?!\S)   A7 \s+
+// It reads the file written by instantcua_amd/tokenizer.py (`compile`): a directory of tagged
+// sections (the vocabulary as raw bytes, the merges with their result ids, the added tokens, the
+// split program and its character-class bitmaps, canonical combining classes, canonical
+// decompositions and primary compositions).
+//
+// Pre-tokenizer: the Split pattern is not hand-coded here.  instantcua_amd/split_pattern.py
+// lowers the regex of tokenizer.json to a program of six instructions (MATCH, CLASS, SPLIT, JMP,
+// AHEAD, NOT_AHEAD; a SPLIT carries the class of the code points that can begin its preferred
+// branch, so alternatives that cannot match are skipped without backtracking) with every character class as a two-stage bitmap over the code points;
+// `Splitter` runs it by backtracking with a visited set over (instruction, position), which keeps
+// Oniguruma's leftmost-first result and bounds the work of one match attempt by
+// (program length x bytes explored).
 #include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "icua_tok.h"
@@ -27,19 +34,17 @@ int tok_fail(const std::string& m) {
     return -1;
 }
 
-// Property word of a code point: class in bits 0-2, contraction flags, combining class in 8-15.
-enum : uint16_t { C_L = 0, C_N = 1, C_O = 2, C_WS = 3, C_SP = 4, C_NL = 5 };
-constexpr uint16_t F_C1 = 1 << 4;  // s t m d (case-insensitive): one-letter contractions
-constexpr uint16_t F_RV = 1 << 5;  // r v: 're 've
-constexpr uint16_t F_E = 1 << 6;   // e
-constexpr uint16_t F_LL = 1 << 7;  // l: 'll
+constexpr uint32_t FILE_MAGIC = 0x32544349u;  // "ICT2"
+constexpr uint32_t FILE_VERSION = 2;
+constexpr uint32_t STAGE1 = 0x110000 >> 8;  // 256-code-point blocks in a two-stage table
 
-constexpr uint32_t MAGIC = 0x31544349u;  // "ICT1"
-
-struct Header {
-    uint32_t magic, version, n_total, n_merges, n_specials, n_blocks, n_decomp, n_comp;
-    uint64_t off_tok_off, off_tok_bytes, off_byte_tok, off_merges, off_specials, off_spec_bytes, off_uni1, off_uni2,
-        off_decomp_keys, off_decomp_vals, off_decomp_data, off_comp_keys, off_comp_vals, size;
+struct FileHead {
+    uint32_t magic, version, n_sections, reserved;
+};
+struct SectionEntry {
+    char tag[4];
+    uint32_t elem_size;
+    uint64_t offset, count;
 };
 
 uint32_t decode_cp(const uint8_t* p, size_t i, size_t n, int* len) {
@@ -74,34 +79,116 @@ void append_utf8(uint32_t c, std::string& out) {
     }
 }
 
+// The split program (instantcua_amd/split_pattern.py).
+enum : int32_t { OP_MATCH = 0, OP_CLASS = 1, OP_SPLIT = 2, OP_JMP = 3, OP_AHEAD = 4, OP_NOT_AHEAD = 5 };
+struct Insn {
+    int32_t op, a, b, guard;
+};
+
+// Per-call state of the matcher: the visited set of one attempt (bit (p - start) * n_code + pc,
+// cleared after the attempt up to the highest word it touched) and the backtracking stack.
+struct MatchScratch {
+    std::vector<uint64_t> seen;
+    std::vector<std::pair<int32_t, size_t>> stack;
+};
+
+struct Splitter {
+    const Insn* code = nullptr;
+    uint32_t n_code = 0, n_classes = 0;
+    const uint16_t* stage1 = nullptr;  // [n_classes][STAGE1] -> block
+    const uint8_t* blocks = nullptr;   // 32 bytes (256 bits, LSB first) per block
+    std::vector<uint64_t> ascii;       // [n_classes][2]: the classes on code points below 128
+
+    bool member(int32_t k, uint32_t cp) const {
+        if (cp < 128) return (ascii[2 * (size_t)k + (cp >> 6)] >> (cp & 63)) & 1;
+        if (cp >= 0x110000) return false;
+        const uint8_t* b = blocks + 32 * (size_t)stage1[(size_t)k * STAGE1 + (cp >> 8)];
+        return (b[(cp & 255) >> 3] >> (cp & 7)) & 1;
+    }
+
+    // End of the leftmost-first match that starts at byte `start`, or `start` when there is none
+    // (the compiler rejects patterns that match the empty string).
+    size_t match(const uint8_t* s, size_t start, size_t n, MatchScratch& sc) const {
+        size_t top = 0, end = start;
+        bool found = false;
+        sc.stack.clear();
+        sc.stack.emplace_back(0, start);
+        while (!found && !sc.stack.empty()) {
+            int32_t pc = sc.stack.back().first;
+            size_t p = sc.stack.back().second;
+            sc.stack.pop_back();
+            for (;;) {
+                const size_t bit = (p - start) * n_code + (size_t)pc, w = bit >> 6;
+                if (w >= sc.seen.size()) sc.seen.resize(std::max(w + 1, 2 * sc.seen.size()), 0);
+                const uint64_t m = 1ull << (bit & 63);
+                if (sc.seen[w] & m) break;  // explored before from here, without a match
+                sc.seen[w] |= m;
+                top = std::max(top, w);
+                const Insn& in = code[pc];
+                if (in.op == OP_MATCH) {
+                    end = p;
+                    found = true;
+                    break;
+                }
+                if (in.op == OP_SPLIT) {
+                    int len;
+                    if (in.guard >= 0 && (p >= n || !member(in.guard, decode_cp(s, p, n, &len)))) {
+                        pc = in.b;  // no match can begin through a here
+                    } else {
+                        sc.stack.emplace_back(in.b, p);
+                        pc = in.a;
+                    }
+                    continue;
+                }
+                if (in.op == OP_JMP) {
+                    pc = in.a;
+                    continue;
+                }
+                int len = 0;
+                const bool inside = p < n && member(in.a, decode_cp(s, p, n, &len));
+                if (in.op == OP_CLASS) {
+                    if (!inside) break;
+                    p += len;
+                } else if (inside != (in.op == OP_AHEAD)) {
+                    break;
+                }
+                ++pc;
+            }
+        }
+        std::fill(sc.seen.begin(), sc.seen.begin() + (std::ptrdiff_t)top + 1, 0ull);
+        return end;
+    }
+};
+
 }  // namespace
 
 struct icua_tok {
     std::vector<uint8_t> file;
-    const Header* h = nullptr;
+    uint32_t n_total = 0, n_merges = 0, n_specials = 0, n_decomp = 0, n_comp = 0;
+    size_t n_tok_bytes = 0, n_spec_bytes = 0;
     const uint32_t* tok_off = nullptr;
     const uint8_t* tok_bytes = nullptr;
     const int32_t* byte_tok = nullptr;
     const uint32_t* specials = nullptr;  // (id, offset, len)
     const uint8_t* spec_bytes = nullptr;
-    const uint16_t *uni1 = nullptr, *uni2 = nullptr;
+    const uint16_t* ccc_stage1 = nullptr;
+    const uint8_t* ccc_blocks = nullptr;  // 256 classes per block
     const uint32_t *decomp_keys = nullptr, *decomp_vals = nullptr, *decomp_data = nullptr;
     const uint64_t* comp_keys = nullptr;
     const uint32_t* comp_vals = nullptr;
+    Splitter split;
     std::unordered_map<uint64_t, uint64_t> merge;  // (left << 32 | right) -> (rank << 32 | result id)
     int32_t im_start = -1, im_end = -1, end_of_text = -1;
 
-    uint16_t prop(uint32_t c) const {
-        if (c >= 0x110000) return C_O;
-        return uni2[(size_t)uni1[c >> 8] * 256 + (c & 0xFF)];
+    uint16_t ccc(uint32_t c) const {
+        if (c >= 0x110000) return 0;
+        return ccc_blocks[(size_t)ccc_stage1[c >> 8] * 256 + (c & 255)];
     }
-    int cls_at(const uint8_t* p, size_t i, size_t n, int* len) const { return prop(decode_cp(p, i, n, len)) & 7; }
-    uint16_t ccc(uint32_t c) const { return prop(c) >> 8; }
 
     // --- NFC (UAX #15: full canonical decomposition, canonical ordering, composition) ---------
     void decompose(uint32_t c, std::vector<uint32_t>& out) const {
-        const uint32_t* k = std::lower_bound(decomp_keys, decomp_keys + h->n_decomp, c);
-        if (k != decomp_keys + h->n_decomp && *k == c) {
+        const uint32_t* k = std::lower_bound(decomp_keys, decomp_keys + n_decomp, c);
+        if (k != decomp_keys + n_decomp && *k == c) {
             const uint32_t v = decomp_vals[k - decomp_keys];
             for (uint32_t j = 0; j < (v & 31); ++j) out.push_back(decomp_data[(v >> 5) + j]);
         } else {
@@ -110,8 +197,8 @@ struct icua_tok {
     }
     uint32_t compose(uint32_t a, uint32_t b) const {
         const uint64_t key = (uint64_t)a << 21 | b;
-        const uint64_t* k = std::lower_bound(comp_keys, comp_keys + h->n_comp, key);
-        return (k != comp_keys + h->n_comp && *k == key) ? comp_vals[k - comp_keys] : 0;
+        const uint64_t* k = std::lower_bound(comp_keys, comp_keys + n_comp, key);
+        return (k != comp_keys + n_comp && *k == key) ? comp_vals[k - comp_keys] : 0;
     }
     void nfc(const uint8_t* p, size_t n, std::string& out) const {
         std::vector<uint32_t> d;
@@ -155,84 +242,6 @@ struct icua_tok {
         for (uint32_t c : r) append_utf8(c, out);
     }
 
-    // --- pre-tokenizer --------------------------------------------------------------------
-    size_t scan_class(const uint8_t* p, size_t j, size_t n, int cls) const {
-        while (j < n) {
-            int l;
-            if (cls_at(p, j, n, &l) != cls) return j;
-            j += l;
-        }
-        return j;
-    }
-    static size_t scan_nl(const uint8_t* p, size_t j, size_t n) {
-        while (j < n && (p[j] == '\n' || p[j] == '\r')) ++j;
-        return j;
-    }
-    // A5 / A6 / A7 on the whitespace run starting at i.
-    size_t ws_run(const uint8_t* p, size_t i, size_t n) const {
-        size_t j = i, last_start = i;
-        long last_nl = -1;
-        while (j < n) {
-            int l;
-            const int c = cls_at(p, j, n, &l);
-            if (c < C_WS) break;
-            if (c == C_NL) last_nl = (long)j;
-            last_start = j;
-            j += l;
-        }
-        if (last_nl >= 0) return (size_t)last_nl + 1;  // A5: through the last CR / LF
-        if (j == n) return n;                          // A6: the run ends the text
-        if (last_start > i) return last_start;         // A6: all but the run's last character
-        return j;                                      // A7: one whitespace character
-    }
-    // A1 after an apostrophe at k - 1: end of the contraction, or 0.
-    size_t contraction(const uint8_t* p, size_t k, size_t n) const {
-        if (k >= n) return 0;
-        int l1;
-        const uint16_t p1 = prop(decode_cp(p, k, n, &l1));
-        if (p1 & F_C1) return k + l1;
-        if (p1 & (F_RV | F_LL)) {
-            const size_t k2 = k + l1;
-            if (k2 >= n) return 0;
-            int l2;
-            const uint16_t p2 = prop(decode_cp(p, k2, n, &l2));
-            if (((p1 & F_RV) && (p2 & F_E)) || ((p1 & F_LL) && (p2 & F_LL))) return k2 + l2;
-        }
-        return 0;
-    }
-    size_t piece_end(const uint8_t* p, size_t i, size_t n) const {
-        int l;
-        const int c = cls_at(p, i, n, &l);
-        const size_t nx = i + l;
-        if (c == C_L) return scan_class(p, nx, n, C_L);  // A2, no prefix
-        if (c == C_N) return nx;                          // A3
-        if (c == C_O) {
-            if (p[i] == '\'') {
-                const size_t k = contraction(p, i + 1, n);
-                if (k) return k;  // A1
-            }
-            if (nx >= n) return nx;
-            int ln;
-            const int cn = cls_at(p, nx, n, &ln);
-            if (cn == C_L) return scan_class(p, nx + ln, n, C_L);  // A2: prefix + letters
-            return scan_nl(p, scan_class(p, nx, n, C_O), n);       // A4
-        }
-        if (c == C_SP) {
-            if (nx >= n) return n;
-            int ln;
-            const int cn = cls_at(p, nx, n, &ln);
-            if (cn == C_L) return scan_class(p, nx + ln, n, C_L);                 // A2: " word"
-            if (cn == C_O) return scan_nl(p, scan_class(p, nx + ln, n, C_O), n);  // A4: " +="
-            return ws_run(p, i, n);
-        }
-        if (c == C_WS) {
-            if (nx >= n) return n;
-            int ln;
-            if (cls_at(p, nx, n, &ln) == C_L) return scan_class(p, nx + ln, n, C_L);  // A2: "\tword"
-            return ws_run(p, i, n);
-        }
-        return ws_run(p, i, n);  // CR / LF
-    }
 
     // --- BPE --------------------------------------------------------------------------------
     // Merges the adjacent pair of lowest rank, leftmost first, until none applies.
@@ -264,12 +273,23 @@ struct icua_tok {
         }
         out.insert(out.end(), sym.begin(), sym.end());
     }
+    // Split's "isolated" behaviour: every match is a piece and so is every gap between matches.
     void encode_segment(const uint8_t* p, size_t n, std::vector<int32_t>& out) const {
+        MatchScratch sc;
+        size_t gap = 0;
         for (size_t i = 0; i < n;) {
-            const size_t j = piece_end(p, i, n);
-            bpe(p + i, j - i, out);
-            i = j;
+            const size_t e = split.match(p, i, n, sc);
+            if (e > i) {
+                if (gap < i) bpe(p + gap, i - gap, out);
+                bpe(p + i, e - i, out);
+                i = gap = e;
+            } else {
+                int len;
+                decode_cp(p, i, n, &len);
+                i += len;
+            }
         }
+        if (gap < n) bpe(p + gap, n - gap, out);
     }
     void encode_text(const uint8_t* p, size_t n, std::vector<int32_t>& out) const {
         bool ascii = true;
@@ -286,7 +306,7 @@ struct icua_tok {
     int match_special(const uint8_t* p, size_t q, size_t n) const {
         int best = -1;
         uint32_t best_len = 0;
-        for (uint32_t k = 0; k < h->n_specials; ++k) {
+        for (uint32_t k = 0; k < n_specials; ++k) {
             const uint32_t len = specials[3 * k + 2];
             if (len <= best_len || len > n - q) continue;
             if (memcmp(spec_bytes + specials[3 * k + 1], p + q, len) == 0) {
@@ -317,7 +337,7 @@ struct icua_tok {
     }
     int32_t special_id(const char* s) const {
         const size_t n = strlen(s);
-        for (uint32_t k = 0; k < h->n_specials; ++k)
+        for (uint32_t k = 0; k < n_specials; ++k)
             if (specials[3 * k + 2] == n && memcmp(spec_bytes + specials[3 * k + 1], s, n) == 0)
                 return (int32_t)specials[3 * k];
         return -1;
@@ -405,64 +425,119 @@ int icua_tok_open(const char* path, icua_tok** out) {
     *out = nullptr;
     FILE* f = fopen(path, "rb");
     if (!f) return tok_fail(std::string("cannot open ") + path);
-    auto* t = new icua_tok();
+    std::vector<uint8_t> file;
     fseek(f, 0, SEEK_END);
     const long len = ftell(f);
     fseek(f, 0, SEEK_SET);
-    t->file.resize(len > 0 ? (size_t)len : 0);
-    const size_t got = len > 0 ? fread(t->file.data(), 1, (size_t)len, f) : 0;
+    file.resize(len > 0 ? (size_t)len : 0);
+    const size_t got = len > 0 ? fread(file.data(), 1, (size_t)len, f) : 0;
     fclose(f);
-    if (len < (long)sizeof(Header) || got != (size_t)len) {
-        delete t;
-        return tok_fail("truncated tokenizer file");
-    }
-    const Header* h = (const Header*)t->file.data();
-    if (h->magic != MAGIC || h->version != 1 || h->size != (uint64_t)len) {
-        delete t;
-        return tok_fail("not a compiled tokenizer file (magic, version or size)");
-    }
-    const uint64_t sec[][2] = {{h->off_tok_off, 4ull * (h->n_total + 1)},
-                               {h->off_byte_tok, 4ull * 256},
-                               {h->off_merges, 12ull * h->n_merges},
-                               {h->off_specials, 12ull * h->n_specials},
-                               {h->off_uni1, 2ull * 4352},
-                               {h->off_uni2, 512ull * h->n_blocks},
-                               {h->off_decomp_keys, 4ull * h->n_decomp},
-                               {h->off_decomp_vals, 4ull * h->n_decomp},
-                               {h->off_comp_keys, 8ull * h->n_comp},
-                               {h->off_comp_vals, 4ull * h->n_comp}};
-    for (const auto& s : sec)
-        if (s[0] % 8 || s[0] + s[1] > (uint64_t)len) {
-            delete t;
-            return tok_fail("tokenizer file section out of range");
+    if (len < (long)sizeof(FileHead) || got != (size_t)len) return tok_fail("truncated tokenizer file");
+    const FileHead* head = (const FileHead*)file.data();
+    if (head->magic != FILE_MAGIC || head->version != FILE_VERSION)
+        return tok_fail("not a compiled tokenizer file of version 2 (magic or version)");
+    const size_t size = file.size();
+    if (head->n_sections > 64 || sizeof(FileHead) + head->n_sections * sizeof(SectionEntry) > size)
+        return tok_fail("tokenizer file: bad section directory");
+    const SectionEntry* dir = (const SectionEntry*)(file.data() + sizeof(FileHead));
+    // Finds a section by tag and checks its element size and extent; count < 0 is any count.
+    std::string err;
+    auto section = [&](const char* tag, uint32_t elem, int64_t count, uint64_t* n) -> const uint8_t* {
+        for (uint32_t k = 0; k < head->n_sections; ++k) {
+            const SectionEntry& e = dir[k];
+            if (memcmp(e.tag, tag, 4) != 0) continue;
+            const bool fits = e.elem_size == elem && e.offset % 8 == 0 && e.offset <= size &&
+                              e.count <= (size - e.offset) / elem && (count < 0 || e.count == (uint64_t)count);
+            if (!fits) {
+                if (err.empty()) err = std::string("tokenizer file: section ") + tag + " has a bad size";
+                return nullptr;
+            }
+            if (n) *n = e.count;
+            return file.data() + e.offset;
         }
-    const uint8_t* b = t->file.data();
-    t->h = h;
-    t->tok_off = (const uint32_t*)(b + h->off_tok_off);
-    t->tok_bytes = b + h->off_tok_bytes;
-    t->byte_tok = (const int32_t*)(b + h->off_byte_tok);
-    t->specials = (const uint32_t*)(b + h->off_specials);
-    t->spec_bytes = b + h->off_spec_bytes;
-    t->uni1 = (const uint16_t*)(b + h->off_uni1);
-    t->uni2 = (const uint16_t*)(b + h->off_uni2);
-    t->decomp_keys = (const uint32_t*)(b + h->off_decomp_keys);
-    t->decomp_vals = (const uint32_t*)(b + h->off_decomp_vals);
-    t->decomp_data = (const uint32_t*)(b + h->off_decomp_data);
-    t->comp_keys = (const uint64_t*)(b + h->off_comp_keys);
-    t->comp_vals = (const uint32_t*)(b + h->off_comp_vals);
-    if (t->tok_off[h->n_total] > h->off_spec_bytes - h->off_tok_bytes) {
+        if (err.empty()) err = std::string("tokenizer file: section ") + tag + " is missing";
+        return nullptr;
+    };
+    auto* t = new icua_tok();
+    uint64_t n_off = 0, n_tok_bytes = 0, n_merges = 0, n_specials = 0, n_spec_bytes = 0, n_code = 0, n_stage1 = 0,
+             n_blocks = 0, n_ccc_blocks = 0, n_dk = 0, n_dv = 0, n_dd = 0, n_ck = 0, n_cv = 0;
+    t->tok_off = (const uint32_t*)section("TOFF", 4, -1, &n_off);
+    t->tok_bytes = section("TBYT", 1, -1, &n_tok_bytes);
+    t->byte_tok = (const int32_t*)section("BYTK", 4, 256, nullptr);
+    const uint32_t* merges = (const uint32_t*)section("MRGE", 12, -1, &n_merges);
+    t->specials = (const uint32_t*)section("SPEC", 12, -1, &n_specials);
+    t->spec_bytes = section("SBYT", 1, -1, &n_spec_bytes);
+    t->split.code = (const Insn*)section("PROG", 16, -1, &n_code);
+    t->split.stage1 = (const uint16_t*)section("CIDX", 2, -1, &n_stage1);
+    t->split.blocks = section("CBIT", 32, -1, &n_blocks);
+    t->ccc_stage1 = (const uint16_t*)section("CCCI", 2, STAGE1, nullptr);
+    t->ccc_blocks = section("CCCD", 256, -1, &n_ccc_blocks);
+    t->decomp_keys = (const uint32_t*)section("DKEY", 4, -1, &n_dk);
+    t->decomp_vals = (const uint32_t*)section("DVAL", 4, -1, &n_dv);
+    t->decomp_data = (const uint32_t*)section("DDAT", 4, -1, &n_dd);
+    t->comp_keys = (const uint64_t*)section("CKEY", 8, -1, &n_ck);
+    t->comp_vals = (const uint32_t*)section("CVAL", 4, -1, &n_cv);
+    auto bad = [&](const std::string& m) {
         delete t;
-        return tok_fail("token bytes out of range");
+        return tok_fail(err.empty() ? "tokenizer file: " + m : err);
+    };
+    if (!err.empty()) return bad("");
+    if (n_off < 1 || n_off - 1 > (uint64_t)INT32_MAX || n_dk != n_dv || n_ck != n_cv || n_code < 1 ||
+        n_code > 4096 || n_stage1 % STAGE1 != 0 || n_blocks > 0x10000 || n_merges > UINT32_MAX ||
+        n_specials > UINT32_MAX)
+        return bad("inconsistent section counts");
+    t->n_total = (uint32_t)(n_off - 1);
+    t->n_merges = (uint32_t)n_merges;
+    t->n_specials = (uint32_t)n_specials;
+    t->n_decomp = (uint32_t)n_dk;
+    t->n_comp = (uint32_t)n_ck;
+    t->n_tok_bytes = n_tok_bytes;
+    t->n_spec_bytes = n_spec_bytes;
+    for (uint32_t i = 0; i < t->n_total; ++i)
+        if (t->tok_off[i] > t->tok_off[i + 1]) return bad("token offsets out of order");
+    if (t->tok_off[t->n_total] > n_tok_bytes) return bad("token bytes out of range");
+    for (int b = 0; b < 256; ++b)
+        if (t->byte_tok[b] < 0 || (uint32_t)t->byte_tok[b] >= t->n_total) return bad("byte token out of range");
+    for (uint64_t r = 0; r < n_merges; ++r)
+        for (int j = 0; j < 3; ++j)
+            if (merges[3 * r + j] >= t->n_total) return bad("merge names a token outside the vocabulary");
+    for (uint64_t k = 0; k < n_specials; ++k) {
+        const uint32_t* s = t->specials + 3 * k;
+        if (s[0] >= t->n_total || s[1] > n_spec_bytes || s[2] > n_spec_bytes - s[1])
+            return bad("added token out of range");
     }
-    for (uint32_t k = 0; k < 4352; ++k)
-        if (t->uni1[k] >= h->n_blocks) {
-            delete t;
-            return tok_fail("bad Unicode table");
+    // The program: every jump lands inside it, every class exists, and it ends in MATCH.
+    Splitter& sp = t->split;
+    sp.n_code = (uint32_t)n_code;
+    sp.n_classes = (uint32_t)(n_stage1 / STAGE1);
+    for (uint32_t pc = 0; pc < sp.n_code; ++pc) {
+        const Insn& in = sp.code[pc];
+        const bool jumps_ok = in.a >= 0 && (uint32_t)in.a < sp.n_code && in.b >= 0 && (uint32_t)in.b < sp.n_code;
+        const bool class_ok = in.a >= 0 && (uint32_t)in.a < sp.n_classes;
+        const bool guard_ok =
+            in.guard == -1 || (in.op == OP_SPLIT && in.guard >= 0 && (uint32_t)in.guard < sp.n_classes);
+        const bool op_ok = in.op == OP_MATCH || ((in.op == OP_SPLIT || in.op == OP_JMP) && jumps_ok) ||
+                           ((in.op == OP_CLASS || in.op == OP_AHEAD || in.op == OP_NOT_AHEAD) && class_ok);
+        const bool ok = guard_ok && op_ok;
+        if (!ok) return bad("bad split program instruction " + std::to_string(pc));
+    }
+    if (sp.code[sp.n_code - 1].op != OP_MATCH) return bad("split program does not end in MATCH");
+    for (uint64_t k = 0; k < n_stage1; ++k)
+        if (sp.stage1[k] >= n_blocks) return bad("class bitmap index out of range");
+    for (uint32_t k = 0; k < STAGE1; ++k)
+        if (t->ccc_stage1[k] >= n_ccc_blocks) return bad("combining-class index out of range");
+    for (uint64_t k = 0; k < n_dk; ++k)
+        if ((t->decomp_vals[k] >> 5) + (t->decomp_vals[k] & 31) > n_dd) return bad("decomposition out of range");
+    sp.ascii.assign(2 * (size_t)sp.n_classes, 0);
+    for (uint32_t k = 0; k < sp.n_classes; ++k)
+        for (uint32_t cp = 0; cp < 128; ++cp) {
+            const uint8_t* b = sp.blocks + 32 * (size_t)sp.stage1[(size_t)k * STAGE1];
+            if ((b[cp >> 3] >> (cp & 7)) & 1) sp.ascii[2 * k + (cp >> 6)] |= 1ull << (cp & 63);
         }
-    const uint32_t* m = (const uint32_t*)(b + h->off_merges);
-    t->merge.reserve(h->n_merges * 2);
-    for (uint32_t r = 0; r < h->n_merges; ++r)
-        t->merge.emplace((uint64_t)m[3 * r] << 32 | m[3 * r + 1], (uint64_t)r << 32 | m[3 * r + 2]);
+    t->merge.reserve(n_merges * 2);
+    for (uint32_t r = 0; r < n_merges; ++r)
+        t->merge.emplace((uint64_t)merges[3 * r] << 32 | merges[3 * r + 1], (uint64_t)r << 32 | merges[3 * r + 2]);
+    t->file.swap(file);  // the pointers stay valid: swap keeps the buffer
     t->im_start = t->special_id("<|im_start|>");
     t->im_end = t->special_id("<|im_end|>");
     t->end_of_text = t->special_id("<|endoftext|>");
@@ -472,7 +547,7 @@ int icua_tok_open(const char* path, icua_tok** out) {
 
 void icua_tok_close(icua_tok* t) { delete t; }
 
-int icua_tok_vocab_size(const icua_tok* t) { return t ? (int)t->h->n_total : -1; }
+int icua_tok_vocab_size(const icua_tok* t) { return t ? (int)t->n_total : -1; }
 
 int32_t icua_tok_special_id(const icua_tok* t, const char* content) {
     return (t && content) ? t->special_id(content) : -1;
@@ -523,7 +598,7 @@ int icua_tok_encode_vision_chat(const icua_tok* t, const char* system, size_t sl
 
 int icua_tok_token_bytes(const icua_tok* t, int32_t id, const uint8_t** bytes, size_t* len) {
     if (!t || !bytes || !len) return tok_fail("null argument");
-    if (id < 0 || (uint32_t)id >= t->h->n_total) {
+    if (id < 0 || (uint32_t)id >= t->n_total) {
         *bytes = nullptr;
         *len = 0;
         return 0;
@@ -537,7 +612,7 @@ int icua_tok_decode(const icua_tok* t, const int32_t* ids, size_t n, char* out, 
     if (!t || (!ids && n) || !n_out) return tok_fail("null argument");
     std::string raw, s;
     for (size_t i = 0; i < n; ++i) {
-        if (ids[i] < 0 || (uint32_t)ids[i] >= t->h->n_total) continue;
+        if (ids[i] < 0 || (uint32_t)ids[i] >= t->n_total) continue;
         raw.append((const char*)t->tok_bytes + t->tok_off[ids[i]], t->tok_off[ids[i] + 1] - t->tok_off[ids[i]]);
     }
     lossy_utf8((const uint8_t*)raw.data(), raw.size(), s, true);
@@ -560,7 +635,7 @@ int icua_tok_stream_push(const icua_tok* t, icua_tok_stream* s, int32_t id, int 
                          size_t* n_out) {
     if (!t || !s || !n_out || (!out && cap)) return tok_fail("null argument");
     const size_t before = s->pending.size();
-    if (id >= 0 && (uint32_t)id < t->h->n_total)
+    if (id >= 0 && (uint32_t)id < t->n_total)
         s->pending.append((const char*)t->tok_bytes + t->tok_off[id], t->tok_off[id + 1] - t->tok_off[id]);
     std::string txt;
     const size_t used = lossy_utf8((const uint8_t*)s->pending.data(), s->pending.size(), txt, final != 0);

@@ -1,16 +1,34 @@
 """Qwen2 tokenizer: compile step (Python) and the native tokenizer of ``libicua.so`` (ctypes).
 
-``compile`` mirrors ``Tokenizer.compile(tokenizerJSON:output:)`` (Sources/Tokenizer/
-Compile.swift:20-258): it checks that a Hugging Face ``tokenizer.json`` is the Qwen2 pipeline
-(Compile.swift:260-291), decodes the byte-level alphabet back to raw bytes, and writes one
-binary file (layout below) that the native tokenizer reads:
+``compile`` takes the place of ``Tokenizer.compile(tokenizerJSON:output:)`` (Sources/Tokenizer/
+Compile.swift:20-258).  It checks a Hugging Face ``tokenizer.json`` against ``REQUIREMENTS`` (the
+pipeline the native tokenizer runs: NFC, one regex Split, byte-level BPE), decodes the
+byte-level alphabet back to raw bytes, compiles the Split regex (``split_pattern``) and writes one
+file of tagged sections that ``icua_tok_open`` reads:
 
-* the vocabulary and added tokens as raw bytes, the token id of every single byte;
-* every merge as (left id, right id, result id) in rank order;
-* the added tokens (id, content), matched leftmost-longest on the raw text;
-* the Unicode tables: a two-stage property table (split-pattern class, contraction letters,
-  canonical combining class), full canonical decompositions and primary compositions, from
-  Python's ``unicodedata``.
+====  =====  ===========================================================================
+tag   elem   contents
+====  =====  ===========================================================================
+TOFF  u32    byte offset of every token in TBYT, n_tokens + 1 entries
+TBYT  u8     the tokens' raw bytes (vocabulary and added tokens)
+BYTK  i32    the token of every single byte, 256 entries
+MRGE  3xu32  merges in rank order: (left id, right id, result id)
+SPEC  3xu32  added tokens: (id, offset in SBYT, length), matched leftmost-longest
+SBYT  u8     the added tokens' bytes
+PROG  4xi32  the split program (op, a, b, guard)
+CIDX  u16    per class, the block of each 256-code-point range (classes x 4352)
+CBIT  32xu8  256-bit membership blocks, LSB first
+CCCI  u16    the block of each 256-code-point range of the canonical combining classes
+CCCD  256xu8 combining-class blocks
+DKEY  u32    code points with a canonical decomposition, ascending
+DVAL  u32    offset << 5 | length of each decomposition in DDAT
+DDAT  u32    full canonical decompositions
+CKEY  u64    first << 21 | second of every primary composition, ascending
+CVAL  u32    the composed code point
+====  =====  ===========================================================================
+
+The file starts with (magic, version, number of sections, 0) as u32, then one 24-byte entry per
+section (tag, element size u32, offset u64, element count u64); sections are 64-byte aligned.
 
 ``Tokenizer`` and ``TextStream`` mirror the reference's ``Tokenizer`` and ``TextStream``
 (Tokenizer.swift:36-462) over ``include/icua_tok.h``.
@@ -26,17 +44,13 @@ from typing import List, Tuple
 import numpy as np
 
 from . import engine as eng
+from .split_pattern import PatternError, SplitProgram
 
+# The Split regex of the Qwen2 / Qwen3 tokenizer.json.
 QWEN2_SPLIT = (r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}| ?[^\s\p{L}\p{N}]+[\r\n]*|"
                r"\s*[\r\n]+|\s+(?!\S)|\s+")
-MAGIC, VERSION = 0x31544349, 1
+FILE_MAGIC, FILE_VERSION = 0x32544349, 2
 VISION_START, VISION_END, IMAGE_PAD = 151652, 151653, 151655
-
-# Unicode White_Space (PropList.txt): the characters \s matches.
-WHITE_SPACE = set(range(0x09, 0x0E)) | {0x20, 0x85, 0xA0, 0x1680, 0x2028, 0x2029, 0x202F, 0x205F, 0x3000} \
-    | set(range(0x2000, 0x200B))
-C_L, C_N, C_O, C_WS, C_SP, C_NL = 0, 1, 2, 3, 4, 5
-F_C1, F_RV, F_E, F_LL = 1 << 4, 1 << 5, 1 << 6, 1 << 7
 
 
 class TokenizerError(RuntimeError):
@@ -56,68 +70,93 @@ def bytes_to_unicode() -> dict:
     return {b: chr(c) for b, c in zip(bs, cs)}
 
 
+_MISSING = object()
+
+
+def _lookup(root, path: str):
+    """Value at a dotted path ("pre_tokenizer.pretokenizers.0.type"), or _MISSING."""
+    node = root
+    for key in path.split("."):
+        if isinstance(node, list) and key.isdigit() and int(key) < len(node):
+            node = node[int(key)]
+        elif isinstance(node, dict) and key in node:
+            node = node[key]
+        else:
+            return _MISSING
+    return node
+
+
+def _is(*allowed):
+    return lambda v: v in allowed
+
+
+def _absent_or(*allowed):
+    return lambda v: v is _MISSING or v in allowed
+
+
+# What the native tokenizer runs, as (path in tokenizer.json, test of the value found there, the
+# requirement in words).  The reference accepts the same pipeline (Compile.swift:260-291); here
+# the Split regex may be any pattern split_pattern compiles, not only the Qwen2 one.
+REQUIREMENTS = (
+    ("normalizer.type", _is("NFC"), "NFC normalisation"),
+    ("pre_tokenizer.type", _is("Sequence"), "a Sequence pre-tokenizer"),
+    ("pre_tokenizer.pretokenizers", lambda v: isinstance(v, list) and len(v) == 2, "exactly two pre-tokenizers"),
+    ("pre_tokenizer.pretokenizers.0.type", _is("Split"), "a Split first"),
+    ("pre_tokenizer.pretokenizers.0.behavior", _is("Isolated"), "Split behaviour Isolated"),
+    ("pre_tokenizer.pretokenizers.0.invert", _absent_or(False), "a Split that is not inverted"),
+    ("pre_tokenizer.pretokenizers.0.pattern",
+     lambda v: isinstance(v, dict) and len(v) == 1 and ("Regex" in v or "String" in v), "a Regex or String pattern"),
+    ("pre_tokenizer.pretokenizers.1.type", _is("ByteLevel"), "a ByteLevel second"),
+    ("pre_tokenizer.pretokenizers.1.add_prefix_space", _absent_or(False), "ByteLevel without a prefix space"),
+    ("pre_tokenizer.pretokenizers.1.use_regex", _is(False), "ByteLevel without its own regex"),
+    ("model.type", _is("BPE"), "a BPE model"),
+    ("model.dropout", _absent_or(None), "no BPE dropout"),
+    ("model.byte_fallback", _absent_or(False, None), "no byte fallback"),
+    ("model.continuing_subword_prefix", _absent_or(None, ""), "no continuing-subword prefix"),
+    ("model.end_of_word_suffix", _absent_or(None, ""), "no end-of-word suffix"),
+    ("model.ignore_merges", _absent_or(False, None), "merges always applied"),
+    ("model.vocab", lambda v: isinstance(v, dict), "a vocabulary"),
+    ("model.merges", lambda v: isinstance(v, list), "a merge list"),
+    ("decoder.type", _absent_or("ByteLevel"), "a ByteLevel decoder"),
+)
+
+
 def check_pipeline(root: dict) -> None:
-    """The Qwen2 pipeline, the only one the tokenizer implements (Compile.swift:260-291)."""
-    def no(what):
-        raise TokenizerError(f"unsupported tokenizer.json: {what}")
-    norm = root.get("normalizer") or {}
-    if norm.get("type") != "NFC":
-        no("normalizer must be NFC")
-    pre = root.get("pre_tokenizer") or {}
-    lst = pre.get("pretokenizers") or []
-    if pre.get("type") != "Sequence" or len(lst) != 2:
-        no("pre_tokenizer must be Sequence[Split, ByteLevel]")
-    sp, bl = lst
-    if sp.get("type") != "Split" or (sp.get("pattern") or {}).get("Regex") != QWEN2_SPLIT \
-            or sp.get("behavior") != "Isolated" or sp.get("invert", False):
-        no("Split must be the Qwen2 pattern with behavior Isolated")
-    if bl.get("type") != "ByteLevel" or bl.get("add_prefix_space", False) or bl.get("use_regex", True):
-        no("ByteLevel pre-tokenizer must have add_prefix_space=false, use_regex=false")
-    model = root.get("model") or {}
-    if model.get("type") != "BPE":
-        no("model must be BPE")
-    if model.get("dropout") is not None:
-        no("BPE dropout")
-    if model.get("byte_fallback"):
-        no("byte_fallback")
-    if model.get("continuing_subword_prefix") or model.get("end_of_word_suffix"):
-        no("subword prefix / suffix")
-    if model.get("ignore_merges"):
-        no("ignore_merges")
-    dec = root.get("decoder")
-    if dec is not None and dec.get("type") != "ByteLevel":
-        no("decoder must be ByteLevel")
+    """Raise TokenizerError naming every requirement the tokenizer.json does not meet."""
+    unmet = []
+    for path, ok, want in REQUIREMENTS:
+        v = _lookup(root, path)
+        if not ok(v):
+            found = "absent" if v is _MISSING else json.dumps(v)[:60]
+            unmet.append(f"{path} is {found}; needed: {want}")
+    if unmet:
+        raise TokenizerError("tokenizer.json describes a pipeline this tokenizer does not run:\n  "
+                             + "\n  ".join(unmet))
 
 
-_UNICODE = None
+def split_program(root: dict) -> SplitProgram:
+    pat = root["pre_tokenizer"]["pretokenizers"][0]["pattern"]
+    regex = pat["Regex"] if "Regex" in pat else "".join("\\" + c if not c.isalnum() else c for c in pat["String"])
+    try:
+        return SplitProgram(regex)
+    except PatternError as e:
+        raise TokenizerError(f"pre_tokenizer.pretokenizers.0.pattern: {e}") from e
 
 
-def unicode_tables():
-    """(uni1 u16[4352], uni2 u16[blocks * 256], decomposition keys / values / data, composition
-    keys / values) from the interpreter's unicodedata."""
-    global _UNICODE
-    if _UNICODE is not None:
-        return _UNICODE
-    fold = {"s": F_C1, "t": F_C1, "m": F_C1, "d": F_C1, "r": F_RV, "v": F_RV, "e": F_E, "l": F_LL}
-    prop = np.zeros(0x110000, dtype=np.uint16)
+_NFC = None
+
+
+def nfc_tables():
+    """Canonical combining classes as a two-stage table (CCCI u16[4352], CCCD u8[blocks, 256]) and
+    the canonical decompositions / primary compositions, from the interpreter's unicodedata."""
+    global _NFC
+    if _NFC is not None:
+        return _NFC
+    ccc = np.zeros(0x110000, dtype=np.uint8)
     dkeys, dvals, ddata, comp = [], [], [], {}
     for cp in range(0x110000):
         ch = chr(cp)
-        cat = unicodedata.category(ch)
-        if cp in (0x0A, 0x0D):
-            c = C_NL
-        elif cp == 0x20:
-            c = C_SP
-        elif cp in WHITE_SPACE:
-            c = C_WS
-        elif cat[0] == "L":
-            c = C_L
-        elif cat[0] == "N":
-            c = C_N
-        else:
-            c = C_O
-        f = fold.get(ch.casefold(), 0) if cat[0] == "L" else 0
-        prop[cp] = c | f | (unicodedata.combining(ch) << 8)
+        ccc[cp] = unicodedata.combining(ch)
         if 0xD800 <= cp <= 0xDFFF:
             continue
         nfd = unicodedata.normalize("NFD", ch)
@@ -137,15 +176,31 @@ def unicode_tables():
             comp[(0x1100 + l) << 21 | (0x1161 + v)] = lv
             for t in range(1, 28):
                 comp[lv << 21 | (0x11A7 + t)] = lv + t
-    blocks, uni1 = {}, np.zeros(4352, dtype=np.uint16)
-    for b in range(4352):
-        key = prop[b * 256:(b + 1) * 256].tobytes()
-        uni1[b] = blocks.setdefault(key, len(blocks))
-    uni2 = np.frombuffer(b"".join(sorted(blocks, key=blocks.get)), dtype=np.uint16)
+    blocks, index = np.unique(ccc.reshape(4352, 256), axis=0, return_inverse=True)
     ck = np.array(sorted(comp), dtype=np.uint64)
-    _UNICODE = (uni1, uni2, np.array(dkeys, np.uint32), np.array(dvals, np.uint32), np.array(ddata, np.uint32),
-                ck, np.array([comp[int(k)] for k in ck], np.uint32))
-    return _UNICODE
+    _NFC = (index.reshape(4352).astype(np.uint16), np.ascontiguousarray(blocks, dtype=np.uint8),
+            np.array(dkeys, np.uint32), np.array(dvals, np.uint32), np.array(ddata, np.uint32),
+            ck, np.array([comp[int(k)] for k in ck], np.uint32))
+    return _NFC
+
+
+def _write_sections(path: str, sections) -> int:
+    """sections: [(tag, element size, array or bytes)] -> file; returns its size."""
+    head = struct.calcsize("<4I") + struct.calcsize("<4sIQQ") * len(sections)
+    entries, cur = [], (head + 63) // 64 * 64
+    for tag, elem, data in sections:
+        raw = data.tobytes() if isinstance(data, np.ndarray) else bytes(data)
+        assert len(raw) % elem == 0, tag
+        entries.append((tag, elem, cur, len(raw) // elem, raw))
+        cur = (cur + len(raw) + 63) // 64 * 64
+    buf = bytearray(cur)
+    struct.pack_into("<4I", buf, 0, FILE_MAGIC, FILE_VERSION, len(sections), 0)
+    for k, (tag, elem, off, count, raw) in enumerate(entries):
+        struct.pack_into("<4sIQQ", buf, 16 + 24 * k, tag.encode(), elem, off, count)
+        buf[off:off + len(raw)] = raw
+    with open(path, "wb") as f:
+        f.write(buf)
+    return cur
 
 
 def compile(tokenizer_json: str, output: str) -> int:  # noqa: A001  (mirrors Tokenizer.compile)
@@ -153,10 +208,9 @@ def compile(tokenizer_json: str, output: str) -> int:  # noqa: A001  (mirrors To
     with open(tokenizer_json, encoding="utf-8") as f:
         root = json.load(f)
     check_pipeline(root)
+    prog = split_program(root)
     model = root["model"]
-    vocab, merges = model.get("vocab"), model.get("merges")
-    if not isinstance(vocab, dict) or merges is None:
-        raise TokenizerError("model.vocab / model.merges missing")
+    vocab, merges = model["vocab"], model["merges"]
     b2u = bytes_to_unicode()
     u2b = {c: b for b, c in b2u.items()}
     added = [(int(a["id"]), a["content"].encode("utf-8")) for a in root.get("added_tokens") or []]
@@ -169,7 +223,10 @@ def compile(tokenizer_json: str, output: str) -> int:  # noqa: A001  (mirrors To
             raise TokenizerError(f"vocab entry {s!r} is not in the byte-level alphabet") from e
     for i, content in added:
         tok[i] = content
-    byte_tok = np.array([vocab[b2u[b]] for b in range(256)], dtype=np.int32)
+    try:
+        byte_tok = np.array([vocab[b2u[b]] for b in range(256)], dtype=np.int32)
+    except KeyError as e:
+        raise TokenizerError(f"the vocabulary lacks the single byte {e}") from e
     mtab = np.zeros((len(merges), 3), dtype=np.uint32)
     for r, m in enumerate(merges):
         a, b = m.split(" ", 1) if isinstance(m, str) else m
@@ -178,30 +235,18 @@ def compile(tokenizer_json: str, output: str) -> int:  # noqa: A001  (mirrors To
         mtab[r] = (vocab[a], vocab[b], vocab[a + b])
     tok_off = np.zeros(n_total + 1, dtype=np.uint32)
     tok_off[1:] = np.cumsum([len(t) for t in tok])
-    tok_bytes = b"".join(tok)
     spec_tab = np.zeros((len(added), 3), dtype=np.uint32)
     spec_bytes = b""
     for k, (i, content) in enumerate(added):
         spec_tab[k] = (i, len(spec_bytes), len(content))
         spec_bytes += content
-    uni1, uni2, dk, dv, dd, ck, cv = unicode_tables()
-
-    sections = [tok_off.tobytes(), tok_bytes, byte_tok.tobytes(), mtab.tobytes(), spec_tab.tobytes(), spec_bytes,
-                uni1.tobytes(), uni2.tobytes(), dk.tobytes(), dv.tobytes(), dd.tobytes(), ck.tobytes(), cv.tobytes()]
-    hdr_fmt = "<8I14Q"
-    offs, cur = [], (struct.calcsize(hdr_fmt) + 63) // 64 * 64
-    for sec in sections:
-        offs.append(cur)
-        cur = (cur + len(sec) + 63) // 64 * 64
-    header = struct.pack(hdr_fmt, MAGIC, VERSION, n_total, len(merges), len(added), uni2.size // 256, dk.size, ck.size,
-                         *offs, cur)
-    buf = bytearray(cur)
-    buf[:len(header)] = header
-    for o, sec in zip(offs, sections):
-        buf[o:o + len(sec)] = sec
-    with open(output, "wb") as f:
-        f.write(buf)
-    return cur
+    cidx, cbits = prog.tables()
+    ccci, cccd, dk, dv, dd, ck, cv = nfc_tables()
+    return _write_sections(output, [
+        ("TOFF", 4, tok_off), ("TBYT", 1, b"".join(tok)), ("BYTK", 4, byte_tok), ("MRGE", 12, mtab),
+        ("SPEC", 12, spec_tab), ("SBYT", 1, spec_bytes), ("PROG", 16, prog.code), ("CIDX", 2, cidx),
+        ("CBIT", 32, cbits), ("CCCI", 2, ccci), ("CCCD", 256, cccd), ("DKEY", 4, dk), ("DVAL", 4, dv),
+        ("DDAT", 4, dd), ("CKEY", 8, ck), ("CVAL", 4, cv)])
 
 
 _bound = False
@@ -256,8 +301,9 @@ class Tokenizer:
     def __del__(self):
         self.close()
 
-    def _ids(self, fn, *args) -> List[int]:
-        cap = 256
+    def _ids(self, fn, *args, cap: int = 256) -> List[int]:
+        """Every token holds at least one byte of the text (an added token too), so a buffer of the
+        input's length plus the template's tokens is enough the first time."""
         while True:
             out = np.empty(cap, dtype=np.int32)
             n = C.c_size_t(0)
@@ -271,22 +317,22 @@ class Tokenizer:
     def encode(self, text: str) -> List[int]:
         """Plain text: added tokens are not matched (Tokenizer.swift:153)."""
         b = text.encode("utf-8")
-        return self._ids(_lib().icua_tok_encode, b, len(b), 0)
+        return self._ids(_lib().icua_tok_encode, b, len(b), 0, cap=len(b) + 1)
 
     def encode_with_specials(self, text: str) -> List[int]:
         """Added tokens matched leftmost-longest on the raw text, like HF encode (159)."""
         b = text.encode("utf-8")
-        return self._ids(_lib().icua_tok_encode, b, len(b), 1)
+        return self._ids(_lib().icua_tok_encode, b, len(b), 1, cap=len(b) + 1)
 
     def encode_chat(self, system: str, user: str) -> List[int]:
         s, u = system.encode("utf-8"), user.encode("utf-8")
-        return self._ids(_lib().icua_tok_encode_chat, s, len(s), u, len(u))
+        return self._ids(_lib().icua_tok_encode_chat, s, len(s), u, len(u), cap=len(s) + len(u) + 64)
 
     def encode_vision_chat(self, system: str, user: str, num_image_tokens: int) -> Tuple[List[int], int]:
         """(tokens, index of the first image pad) (Tokenizer.swift:192-204)."""
         s, u = system.encode("utf-8"), user.encode("utf-8")
         off = C.c_int(0)
-        cap = 256 + num_image_tokens
+        cap = len(s) + len(u) + 64 + num_image_tokens
         while True:
             out = np.empty(cap, dtype=np.int32)
             n = C.c_size_t(0)

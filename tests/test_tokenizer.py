@@ -33,11 +33,20 @@ PALETTE = list("abcXYZ éèÅ日本語한국ΩЖ0123456789٣²Ⅻ.,;:!?'\"()[]{}
      "'ll", "'LL", "'re", "'VE", "'d", "'m", "'t", "'x", "🙂", "​", "­"]
 
 
-def _train(vocab_size, seed):
+# Split patterns of other byte-level BPE tokenizers (GPT-2's, and the one of Llama 3 / GPT-4 with
+# digit runs of at most three), plus constructs the compiler supports beyond them.
+GPT2_SPLIT = r"""'s|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+|\s+(?!\S)|\s+"""
+LLAMA3_SPLIT = (r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}{1,3}| ?[^\s\p{L}\p{N}]+[\r\n]*|"
+                r"\s*[\r\n]+|\s+(?!\S)|\s+")
+EXTRA_SPLITS = [r"\p{Lu}?\p{Ll}+|\d{2,}?|[\x{4e00}-\x{9fff}]|(?i:[a-c]+x)|\S", r"[\p{L}\p{M}]+(?=\s)|\P{L}|.",
+                r"(?:ab|a)+?c|\P{L}+|\p{^N}"]
+
+
+def _train(vocab_size, seed, pattern=None):
     tok = tokenizers.Tokenizer(models.BPE())
     tok.normalizer = normalizers.NFC()
     tok.pre_tokenizer = pre_tokenizers.Sequence([
-        pre_tokenizers.Split(Regex(itok.QWEN2_SPLIT), behavior="isolated"),
+        pre_tokenizers.Split(Regex(pattern or itok.QWEN2_SPLIT), behavior="isolated"),
         pre_tokenizers.ByteLevel(add_prefix_space=False, use_regex=False)])
     tok.decoder = decoders.ByteLevel()
     rng = random.Random(seed)
@@ -50,7 +59,8 @@ def _train(vocab_size, seed):
     return tokenizers.Tokenizer.from_str(tok.to_str())
 
 
-@pytest.fixture(scope="module", params=[(700, 1), (3000, 2)], ids=["v700", "v3000"])
+@pytest.fixture(scope="module", params=[(700, 1), (3000, 2), (700, 3, LLAMA3_SPLIT)],
+                ids=["v700", "v3000", "llama3-split"])
 def pair(request, tmp_path_factory):
     hf = _train(*request.param)
     d = tmp_path_factory.mktemp("tok")
@@ -152,3 +162,133 @@ def test_invalid_utf8_is_rejected(pair):
     L = itok._lib()
     assert L.icua_tok_encode(ours._h, b"\xff\xfe", 2, 0, None, 0, C.byref(n)) == -1
     assert b"UTF-8" in L.icua_tok_last_error()
+
+
+# --- the split program against HF's Split -----------------------------------------------------
+
+def _run_program(prog, text, start):
+    """End (code-point index) of the leftmost-first match of a compiled split program at start, or
+    -1: a plain backtracking interpreter of the instruction set of split_pattern, written from its
+    table, with no memo and no guards (so it also checks that both only skip dead paths)."""
+    from instantcua_amd import split_pattern as sp
+    stack = [(0, start)]
+    while stack:
+        pc, p = stack.pop()
+        while True:
+            op, a, b, _ = (int(x) for x in prog.code[pc])
+            if op == sp.MATCH:
+                return p
+            if op == sp.SPLIT:
+                stack.append((b, p))
+                pc = a
+                continue
+            if op == sp.JMP:
+                pc = a
+                continue
+            inside = p < len(text) and bool(prog.classes[a, ord(text[p])])
+            if op == sp.CLASS:
+                if not inside:
+                    break
+                p += 1
+            elif inside != (op == sp.AHEAD):
+                break
+            pc += 1
+    return -1
+
+
+def _program_split(prog, text):
+    out, gap, i = [], 0, 0
+    while i < len(text):
+        e = _run_program(prog, text, i)
+        if e > i:
+            out += [text[gap:i]] if gap < i else []
+            out.append(text[i:e])
+            i = gap = e
+        else:
+            i += 1
+    return out + ([text[gap:]] if gap < len(text) else [])
+
+
+ALL_SPLITS = [itok.QWEN2_SPLIT, GPT2_SPLIT, LLAMA3_SPLIT] + EXTRA_SPLITS
+
+
+@pytest.fixture(scope="module")
+def programs():
+    from instantcua_amd.split_pattern import SplitProgram
+    return [(SplitProgram(p), pre_tokenizers.Split(Regex(p), behavior="isolated")) for p in ALL_SPLITS]
+
+
+def test_split_program_matches_hf_split(programs):
+    rng = random.Random(11)
+    texts = SAMPLES + ["".join(rng.choice(PALETTE) for _ in range(rng.randrange(1, 30))) for _ in range(300)] + \
+        ["abcabx ABX aBcX abababc 12345 1 x", "ſ 'ſ 'ſt 'K 'k", "aaab ab abc ababc", "日本 語x  \u000b\u000c\u001c"]
+    for prog, hf_split in programs:
+        for t in texts:
+            want = [piece for piece, _ in hf_split.pre_tokenize_str(t)]
+            assert _program_split(prog, t) == want, (prog.pattern, t)
+
+
+@pytest.mark.parametrize("pattern,why", [
+    (r"a|", "empty"), (r"x*", "empty"), (r"(?=a)", "empty"), (r"^a", "anchor"), (r"a$", "anchor"),
+    (r"(a)\1", "escape"), (r"a++", "possessive"), (r"(?<=a)b", "group"), (r"\p{Foo}", "property"),
+    (r"[[a]]", "nested"), (r"[a&&b]", "intersection"), (r"(?!ab)c", "lookahead"), (r"(a", "missing"),
+    (r"a)", "unbalanced"), (r"*a", "repeat"), (r"a{3,2}", "max < min"), (r"\w+", "escape"), (r"(?=a)+b", "repeated"),
+])
+def test_split_patterns_outside_the_compiler_are_refused(pattern, why):
+    from instantcua_amd.split_pattern import PatternError, SplitProgram
+    with pytest.raises(PatternError, match=why):
+        SplitProgram(pattern)
+
+
+def test_pipeline_report_names_every_unmet_requirement(tmp_path, pair):
+    hf, _ = pair
+    root = json.loads(hf.to_str())
+    root["pre_tokenizer"]["pretokenizers"][1]["add_prefix_space"] = True
+    root["model"]["dropout"] = 0.1
+    root["decoder"] = {"type": "Metaspace"}
+    with pytest.raises(itok.TokenizerError) as e:
+        itok.check_pipeline(root)
+    msg = str(e.value)
+    for path in ("pretokenizers.1.add_prefix_space", "model.dropout", "decoder.type"):
+        assert path in msg
+    assert "normalizer" not in msg
+    root = json.loads(hf.to_str())
+    root["pre_tokenizer"]["pretokenizers"][0]["pattern"] = {"Regex": r"\s*"}
+    p = tmp_path / "empty.json"
+    p.write_text(json.dumps(root))
+    with pytest.raises(itok.TokenizerError, match="empty string"):
+        itok.compile(str(p), str(tmp_path / "x.ict"))
+
+
+def test_corrupt_compiled_files_are_refused(tmp_path, pair):
+    import struct
+    hf, _ = pair
+    js, good = tmp_path / "t.json", tmp_path / "t.ict"
+    hf.save(str(js))
+    itok.compile(str(js), str(good))
+    raw = bytearray(good.read_bytes())
+    n_sec = struct.unpack_from("<I", raw, 8)[0]
+    entries = {struct.unpack_from("<4s", raw, 16 + 24 * k)[0].decode(): struct.unpack_from("<IQQ", raw, 20 + 24 * k)
+               for k in range(n_sec)}
+
+    def refused(buf, what):
+        p = tmp_path / "bad.ict"
+        p.write_bytes(bytes(buf))
+        with pytest.raises(itok.TokenizerError, match=what):
+            itok.Tokenizer(str(p))
+
+    refused(raw[:len(raw) // 2], "section")
+    _, off, count = entries["PROG"]
+    bad = bytearray(raw)
+    struct.pack_into("<i", bad, off + 16 * 0 + 4, count + 5)  # SPLIT target past the end
+    refused(bad, "split program")
+    bad = bytearray(raw)
+    struct.pack_into("<i", bad, off + 16 * (count - 1), 1)  # last instruction no longer MATCH
+    refused(bad, "split program|instruction")
+    _, off, _ = entries["MRGE"]
+    bad = bytearray(raw)
+    struct.pack_into("<I", bad, off, 10 ** 8)
+    refused(bad, "merge")
+    bad = bytearray(raw)
+    struct.pack_into("<I", bad, 4, 1)
+    refused(bad, "version")
