@@ -101,7 +101,74 @@ def cpu_baseline(img, ctx, seconds=10.0):
     threads = oracle.get_threads()
     om.close()
     return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "precision": "fp64 accumulation over fp32 storage (the oracle's arithmetic; an fp32 port would be faster)",
             "sample": f"{n} decode steps of the 28-layer q4 decoder at {ctx}-token context (oracle, fp64 accumulation)"}
+
+
+def cpu_rows(budget_s=6.0):
+    """The oracle on the host for the single-layer q8 decode step (512 cache rows) and for the q4
+    GEMV shapes of the sweep (fp64 accumulation, all host threads)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    oracle.build()
+    rows = []
+    img = synth.build_model_image(WeightFormat.Q8, n_layers=1, tag="cpu-layer-q8")
+    om = oracle.OracleModel(img, 520)
+    for kind in (0, 1):
+        om.kv(0, kind)[:, :512] = synth.fp16_normal((Dims.kv_heads, 512, Dims.head_dim), f"cpu-layer-kv{kind}", 0)
+    x = synth.fp16_normal((1, Dims.hidden), "cpu-layer-x").astype(np.float32)
+    om.layer(0, x.copy(), 512)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s / 3 and n < 200:
+        om.layer(0, x.copy(), 512)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    om.close()
+    rows.append({"config": "one q8 decoder layer, one decode step over 512 fp16 cache rows", "ms": round(dt * 1e3, 3),
+                 "steps_s": round(1 / dt, 1)})
+    for K, N in GEMV_SHAPES:
+        m = synth.make_matrix(WeightFormat.Q4, N, K, tag="cpu-gemv")
+        xv = synth.fp16_normal((1, K), "cpu-gemv-x").astype(np.float32)
+        oracle.gemv(WeightFormat.Q4, m.codes, m.sb, N, K, xv)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s / 10 and n < 50:
+            oracle.gemv(WeightFormat.Q4, m.codes, m.sb, N, K, xv)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        nbytes = m.codes.nbytes + m.sb.nbytes
+        rows.append({"config": f"q4 GEMV {K}x{N}", "us": round(dt * 1e6, 1), "GB_s": round(nbytes / dt / 1e9, 2)})
+    return {"cores": oracle.get_threads(), "kind": "port", "precision": "fp64 accumulation", "rows": rows}
+
+
+def run_text_context(img, steps=256):
+    """The 1024-token text workload: prefill of 1024 random ids, then steps - 1 greedy decode steps
+    (one launch of the persistent kernel), the tokens checked against the oracle fixture."""
+    toks = synth.random_tokens(1024, "c3-prompt")
+    e = eng.Engine(flags=0, image=img, max_context=toks.size + steps + 8, max_steps=steps)
+    e.eos = (-1, -1)
+    e.prefill(toks, max_new=steps)  # loads the code objects
+    e.prefill(toks, max_new=steps)
+    prefill_ms = e.last_timing["prefill_ms"]
+    e.decode_steps(steps - 1)
+    dec_ms = e.last_timing["decode_ms"]
+    got = e.tokens(steps)
+    persistent = e.last_decode_persistent
+    e.close()
+    launch_bytes = sum(weight_bytes_per_token() + kv_bytes_per_token(toks.size + i + 1) for i in range(steps - 1))
+    out = {"workload": "28-layer q4 decoder, 1024-token text prefill + 255 greedy decode steps",
+           "prefill_tok_s": round(toks.size / (prefill_ms / 1e3), 1), "prefill_ms": round(prefill_ms, 3),
+           "decode_tok_s": round((steps - 1) / (dec_ms / 1e3), 1), "decode_us_per_token": round(dec_ms * 1e3 / (steps - 1), 1),
+           "decode_roofline_frac": round(launch_bytes / (dec_ms * 1e-3) / HBM_PEAK, 4), "persistent": persistent}
+    fx = os.path.join(ROOT, "tests", "golden", "oracle_c3_28layer.npz")
+    if os.path.exists(fx):
+        with np.load(fx, allow_pickle=False) as z:
+            ref = z["greedy"]
+        same = int(np.argmax(np.concatenate([got != ref, [True]])))
+        out["greedy_identical_to_oracle_fixture"] = f"{same}/{steps}"
+    log(f"text context: prefill {out['prefill_tok_s']:.0f} tok/s, decode {out['decode_tok_s']:.0f} tok/s "
+        f"({out['decode_roofline_frac']:.3f} of roofline)")
+    return out
 
 
 # Speculative verify workload: 8 random drafts over 8192 cache rows of a 28-layer q8 decoder.
@@ -389,6 +456,11 @@ def main():
     dec_ms = e.last_timing["decode_ms"]
     st = e.state()
     assert st["step"] == 1 + W + K, st
+    # Grammar pairs (the reference engine's default) are on for the timed launch; forced pairs
+    # follow token 11 and the first-step actions.
+    grammar = e.grammar_pairs
+    timed = e.tokens(1 + W + K)[1 + W:]
+    forced_pairs = int(np.sum(timed[:-1] == 11))
     ms_per_step = dec_ms / K
     value = K / (dec_ms / 1e3)
     # Algorithmic bytes of the timed launch: every step streams all weights once plus the K/V
@@ -402,7 +474,9 @@ def main():
     g = gemv_roofline()
     e.close()
 
+    text = run_text_context(img)
     cpu = None if args.no_cpu else cpu_baseline(img, PREFILL)
+    rows = None if args.no_cpu else cpu_rows()
 
     out = {
         "metric": "decode tok/s @bs1 (q4 2B VL decoder, 4k ctx)",
@@ -420,7 +494,7 @@ def main():
         "config": {"workload": "28-layer q4 g64 decoder, 4096-token vision-context prefill "
                                "(16 text + 32x32 visual + 3056 text, DeepStack), greedy decode",
                    "prefill_tokens": PREFILL, "context_at_timing": [PREFILL + W, PREFILL + W + K],
-                   "batch": 1},
+                   "batch": 1, "grammar_pairs": grammar, "forced_pairs_in_timed_steps": forced_pairs},
         "decode_roofline_frac": round(achieved / HBM_PEAK, 4),
         "decode_bytes_per_token": int(bytes_tok),
         "prefill_tok_s": None if args.no_prefill else round(PREFILL / (prefill_ms / 1e3), 1),
@@ -438,6 +512,8 @@ def main():
                           "GB_s": round(g["bytes"] / (g["us"] * 1e-6) / 1e9, 1),
                           "frac": round(g["bytes"] / (g["us"] * 1e-6) / HBM_PEAK, 4)},
         "cpu_baseline": cpu,
+        "cpu_rows": rows,
+        "text_context_1024": text,
     }
     print(json.dumps(out))
 

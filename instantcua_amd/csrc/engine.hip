@@ -1328,7 +1328,7 @@ static int gemv_setup(int fmt, int N, int K, int m, GemvArgs& a, GemvOp& op) {
     a.m_fixed = m;
     a.N = N;
     op = (K == H) ? GEMV_PLAIN : GEMV_PLAIN_K6144;
-    a.blocks = std::max(1, std::min(N / 16, 4096));
+    a.blocks = std::max(1, std::min(N / 16, 1024));  // four workgroups per CU, row blocks strided
     return 0;
 }
 
@@ -1342,15 +1342,25 @@ int icua_repack(int fmt, const void* d_codes, const void* d_sb, int N, int K, vo
     return 0;
 }
 
+// One-token q4 / q8 GEMVs take the streaming kernel (the lm_head stage's schedule); f16 and
+// multi-token ones the general kernel.
+static bool use_stream(int fmt, int N, int m) {
+    return m == 1 && (fmt == FMT_Q4 || fmt == FMT_Q8) && N / 16 <= 160 * 256;
+}
+
 int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const float* d_x, int m, float* d_y) {
     GemvArgs a;
     GemvOp op;
     if (gemv_setup(fmt, N, K, m, a, op)) return -1;
-    a.w = (const uint8_t*)d_codes;
-    a.sb = (const uint8_t*)d_sb;
-    a.x = d_x;
-    a.y = d_y;
-    HIPCK(launch_gemv(fmt, op, a, m == 1 ? 1 : MAXM, nullptr));
+    if (use_stream(fmt, N, m)) {
+        HIPCK(launch_gemv_stream(fmt, (const uint8_t*)d_codes, (const uint8_t*)d_sb, d_x, d_y, N, K, nullptr));
+    } else {
+        a.w = (const uint8_t*)d_codes;
+        a.sb = (const uint8_t*)d_sb;
+        a.x = d_x;
+        a.y = d_y;
+        HIPCK(launch_gemv(fmt, op, a, m == 1 ? 1 : MAXM, nullptr));
+    }
     HIPCK(hipDeviceSynchronize());
     return 0;
 }
@@ -1366,16 +1376,15 @@ int icua_gemv_bench(int fmt, const void* const* d_codes, const void* const* d_sb
     hipEvent_t e0, e1;
     HIPCK(hipEventCreate(&e0));
     HIPCK(hipEventCreate(&e1));
-    // warm-up
-    a.w = (const uint8_t*)d_codes[0];
-    a.sb = (const uint8_t*)d_sb[0];
-    HIPCK(launch_gemv(fmt, op, a, 1, nullptr));
-    HIPCK(hipEventRecord(e0, nullptr));
-    for (int i = 0; i < iters; ++i) {
+    const bool stream = use_stream(fmt, N, 1);
+    auto launch = [&](int i) {
         a.w = (const uint8_t*)d_codes[i % ncopies];
         a.sb = (const uint8_t*)d_sb[i % ncopies];
-        HIPCK(launch_gemv(fmt, op, a, 1, nullptr));
-    }
+        return stream ? launch_gemv_stream(fmt, a.w, a.sb, d_x, d_y, N, K, nullptr) : launch_gemv(fmt, op, a, 1, nullptr);
+    };
+    HIPCK(launch(0));  // warm-up
+    HIPCK(hipEventRecord(e0, nullptr));
+    for (int i = 0; i < iters; ++i) HIPCK(launch(i));
     HIPCK(hipEventRecord(e1, nullptr));
     HIPCK(hipEventSynchronize(e1));
     float ms = 0;

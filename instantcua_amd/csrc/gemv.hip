@@ -377,177 +377,201 @@ __global__ __launch_bounds__(KS * 64) void gemv_kernel(GemvArgs a) {
     const int seg_lo = SPLITK ? (int)(blockIdx.x % NSEG) : 0;
     const int seg_hi = SPLITK ? seg_lo + 1 : NSEG;
     const int rb_step = SPLITK ? nrb : (int)gridDim.x;
-    for (int rb = SPLITK ? (int)(blockIdx.x / NSEG) : (int)blockIdx.x; rb < nrb; rb += rb_step) {
-        const int row = rb * 16 + r16;  // tiled row of this lane
-        const uint8_t* wblk = a.w + (size_t)rb * NC * 1024;
-        float acc[2] = {0.f, 0.f};
-        for (int seg = seg_lo; seg < seg_hi; ++seg) {
-            // Weights of this wave's chunks, issued before the activation staging.
-            uint4 wv[CPW];
+    // This wave's chunks of row block b, segment seg: the weight codes and the lane's row scales.
+    auto load_w = [&](int b, int seg, uint4 (&wv)[CPW], uint2 (&sbv)[CPW]) {
+        const uint8_t* wblk = a.w + (size_t)b * NC * 1024;
+        const int row = b * 16 + r16;
 #pragma unroll
-            for (int i = 0; i < CPW; ++i) {
-                const int c = seg * CPS + wave * CPW + i;
-                wv[i] = ((const uint4*)(wblk + (size_t)c * 1024))[lane];
-            }
-            uint2 sbv[CPW];
+        for (int i = 0; i < CPW; ++i) {
+            const int c = seg * CPS + wave * CPW + i;
+            wv[i] = ((const uint4*)(wblk + (size_t)c * 1024))[lane];
+        }
 #pragma unroll
-            for (int i = 0; i < CPW; ++i) {
-                const int c = seg * CPS + wave * CPW + i;
-                if constexpr (FMT == FMT_Q4)
-                    sbv[i] = *(const uint2*)(a.sb + ((size_t)row * (K / 64) + 2 * c) * 4);
-                else if constexpr (FMT == FMT_Q8)
-                    sbv[i] = make_uint2(*(const uint32_t*)(a.sb + ((size_t)row * (K / 32) + 2 * c) * 2), 0u);
-                else
-                    sbv[i] = make_uint2(0u, 0u);
-            }
-            if (!stage_once || !staged) {
-                if (!stage_once) __syncthreads();
-                stage_all(seg);
-                __syncthreads();
-                staged = true;
-            }
-            for (int p = 0; p < npass; ++p) {
-                const uint8_t* Ap = Alds + p * Smem<FMT>::A_BYTES;
-                const float* fxp = fx + p * Smem<FMT>::FX;
-                float pacc = 0.f, pacc2 = 0.f;
-#pragma unroll
-                for (int i = 0; i < CPW; ++i) {
-                    const int cs = wave * CPW + i;  // chunk within the segment
-                    if constexpr (FMT == FMT_Q4) {
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh) {
-                            const uint32_t d0 = hh ? wv[i].z : wv[i].x;
-                            const uint32_t d1 = hh ? wv[i].w : wv[i].y;
-                            v4i B;
-                            B[0] = (int)(d0 & 0x0F0F0F0Fu);
-                            B[1] = (int)((d0 >> 4) & 0x0F0F0F0Fu);
-                            B[2] = (int)(d1 & 0x0F0F0F0Fu);
-                            B[3] = (int)((d1 >> 4) & 0x0F0F0F0Fu);
-                            const int gl = 2 * cs + hh;
-                            const v4i A = *(const v4i*)(Ap + gl * 1024 + lane * 16);
-                            const v4i zero = {0, 0, 0, 0};
-                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero, 0, 0, 0);
-                            const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
-                            const f16x2 sb2 = as_h2(hh ? sbv[i].y : sbv[i].x);
-                            const float f = fxp[(lg * NG + gl) * 2], X = fxp[(lg * NG + gl) * 2 + 1];
-                            pacc = fmaf((float)sb2.x * f, S, fmaf((float)sb2.y, X, pacc));
+        for (int i = 0; i < CPW; ++i) {
+            const int c = seg * CPS + wave * CPW + i;
+            if constexpr (FMT == FMT_Q4)
+                sbv[i] = *(const uint2*)(a.sb + ((size_t)row * (K / 64) + 2 * c) * 4);
+            else if constexpr (FMT == FMT_Q8)
+                sbv[i] = make_uint2(*(const uint32_t*)(a.sb + ((size_t)row * (K / 32) + 2 * c) * 2), 0u);
+            else
+                sbv[i] = make_uint2(0u, 0u);
+        }
+    };
+    // With K in one segment and int8 codes (4 KiB of a block per wave) the next row block's
+    // weights are requested before this one's matrix-core work (two blocks in flight per wave);
+    // the last block re-requests itself.  f16 blocks (16 KiB per wave) would spill.
+    constexpr bool prefetch = stage_once && FMT != FMT_F16;
+    // One row block: this wave's weights are in wv / sbv; with K in one segment the next block's
+    // are requested into wn / sn before the matrix-core work.  The two buffers swap roles from one
+    // block to the next (the loop below is unrolled by two), so no register copy waits on them.
+    auto row_block = [&](int rb, uint4 (&wv)[CPW], uint2 (&sbv)[CPW], uint4 (&wn)[CPW], uint2 (&sn)[CPW]) {
+            const int row = rb * 16 + r16;  // tiled row of this lane
+            float acc[2] = {0.f, 0.f};
+            for (int seg = seg_lo; seg < seg_hi; ++seg) {
+                // Weights of this wave's chunks, issued before the activation staging.
+                if (!prefetch || !staged) load_w(rb, seg, wv, sbv);
+                if (!stage_once || !staged) {
+                    if (!stage_once) __syncthreads();
+                    stage_all(seg);
+                    __syncthreads();
+                    staged = true;
+                }
+                if constexpr (prefetch) load_w(min(rb + rb_step, nrb - 1), seg, wn, sn);
+                for (int p = 0; p < npass; ++p) {
+                    const uint8_t* Ap = Alds + p * Smem<FMT>::A_BYTES;
+                    const float* fxp = fx + p * Smem<FMT>::FX;
+                    float pacc = 0.f, pacc2 = 0.f;
+    #pragma unroll
+                    for (int i = 0; i < CPW; ++i) {
+                        const int cs = wave * CPW + i;  // chunk within the segment
+                        if constexpr (FMT == FMT_Q4) {
+    #pragma unroll
+                            for (int hh = 0; hh < 2; ++hh) {
+                                const uint32_t d0 = hh ? wv[i].z : wv[i].x;
+                                const uint32_t d1 = hh ? wv[i].w : wv[i].y;
+                                v4i B;
+                                B[0] = (int)(d0 & 0x0F0F0F0Fu);
+                                B[1] = (int)((d0 >> 4) & 0x0F0F0F0Fu);
+                                B[2] = (int)(d1 & 0x0F0F0F0Fu);
+                                B[3] = (int)((d1 >> 4) & 0x0F0F0F0Fu);
+                                const int gl = 2 * cs + hh;
+                                const v4i A = *(const v4i*)(Ap + gl * 1024 + lane * 16);
+                                const v4i zero = {0, 0, 0, 0};
+                                const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, zero, 0, 0, 0);
+                                const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
+                                const f16x2 sb2 = as_h2(hh ? sbv[i].y : sbv[i].x);
+                                const float f = fxp[(lg * NG + gl) * 2], X = fxp[(lg * NG + gl) * 2 + 1];
+                                pacc = fmaf((float)sb2.x * f, S, fmaf((float)sb2.y, X, pacc));
+                            }
+                        } else if constexpr (FMT == FMT_Q8) {
+    #pragma unroll
+                            for (int hh = 0; hh < 2; ++hh) {
+                                const long B = (long)(hh ? ((uint64_t)wv[i].w << 32 | wv[i].z)
+                                                         : ((uint64_t)wv[i].y << 32 | wv[i].x));
+                                const int gl = 2 * cs + hh;
+                                const long A = *(const long*)(Ap + gl * 512 + lane * 8);
+                                const v4i zero = {0, 0, 0, 0};
+                                const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+                                const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
+                                const f16x2 s2 = as_h2(sbv[i].x);
+                                const float s = hh ? (float)s2.y : (float)s2.x;
+                                pacc = fmaf(s * fxp[(lg * NG + gl) * 2], S, pacc);
+                            }
+                        } else {
+                            const v8h B = __builtin_bit_cast(v8h, wv[i]);
+                            const v8h A = *(const v8h*)(Ap + cs * 1024 + lane * 16);
+                            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                            const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, zero, 0, 0, 0);
+                            pacc += C[0] + C[1];
+                            pacc2 += C[2] + C[3];
                         }
-                    } else if constexpr (FMT == FMT_Q8) {
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh) {
-                            const long B = (long)(hh ? ((uint64_t)wv[i].w << 32 | wv[i].z)
-                                                     : ((uint64_t)wv[i].y << 32 | wv[i].x));
-                            const int gl = 2 * cs + hh;
-                            const long A = *(const long*)(Ap + gl * 512 + lane * 8);
-                            const v4i zero = {0, 0, 0, 0};
-                            const v4i C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
-                            const float S = fmaf((float)C[0], 65536.f, fmaf((float)C[1], 256.f, (float)C[2]));
-                            const f16x2 s2 = as_h2(sbv[i].x);
-                            const float s = hh ? (float)s2.y : (float)s2.x;
-                            pacc = fmaf(s * fxp[(lg * NG + gl) * 2], S, pacc);
-                        }
+                    }
+                    if constexpr (FMT == FMT_F16) {
+                        acc[0] += pacc;
+                        acc[1] += pacc2;
                     } else {
-                        const v8h B = __builtin_bit_cast(v8h, wv[i]);
-                        const v8h A = *(const v8h*)(Ap + cs * 1024 + lane * 16);
-                        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-                        const f32x4 C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, zero, 0, 0, 0);
-                        pacc += C[0] + C[1];
-                        pacc2 += C[2] + C[3];
+                        acc[p] += pacc;  // pass p covers tokens 4 p .. 4 p + 3
                     }
                 }
-                if constexpr (FMT == FMT_F16) {
-                    acc[0] += pacc;
-                    acc[1] += pacc2;
-                } else {
-                    acc[p] += pacc;  // pass p covers tokens 4 p .. 4 p + 3
+            }
+            // Cross-wave reduction in a fixed order.
+            if constexpr (KS > 1) {
+                part[(wave * 2 + 0) * 64 + lane] = acc[0];
+                part[(wave * 2 + 1) * 64 + lane] = acc[1];
+                __syncthreads();
+                if (wave == 0) {
+    #pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        float s = part[j * 64 + lane];
+                        for (int w = 1; w < KS; ++w) s += part[(w * 2 + j) * 64 + lane];
+                        acc[j] = s;
+                    }
+                }
+                __syncthreads();
+            }
+            if constexpr (SPLITK) {
+                // Partials go out with device-scope stores (coherent across the XCDs' L2s) and are
+                // complete before the arrival is counted.
+                __shared__ int is_last;
+                if (wave == 0) {
+    #pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
+                        if (t < M)
+                            __hip_atomic_store(a.kpart + ((size_t)seg_lo * MAXM + t) * a.N + row, acc[j], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    __builtin_amdgcn_s_waitcnt(0);
+                }
+                __syncthreads();
+                if (tid == 0)
+                    is_last = __hip_atomic_fetch_add(a.kcnt + rb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == NSEG - 1;
+                __syncthreads();
+                if (!is_last) return;
+                if (wave == 0) {
+    #pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
+                        float sum = 0.f;
+                        if (t < M)
+                            for (int sg = 0; sg < NSEG; ++sg)
+                                sum += __hip_atomic_load(a.kpart + ((size_t)sg * MAXM + t) * a.N + row, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                        acc[j] = sum;
+                    }
+                    if (lane == 0) __hip_atomic_store(a.kcnt + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
-        }
-        // Cross-wave reduction in a fixed order.
-        if constexpr (KS > 1) {
-            part[(wave * 2 + 0) * 64 + lane] = acc[0];
-            part[(wave * 2 + 1) * 64 + lane] = acc[1];
-            __syncthreads();
             if (wave == 0) {
-#pragma unroll
+    #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    float s = part[j * 64 + lane];
-                    for (int w = 1; w < KS; ++w) s += part[(w * 2 + j) * 64 + lane];
-                    acc[j] = s;
-                }
-            }
-            __syncthreads();
-        }
-        if constexpr (SPLITK) {
-            // Partials go out with device-scope stores (coherent across the XCDs' L2s) and are
-            // complete before the arrival is counted.
-            __shared__ int is_last;
-            if (wave == 0) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                    // int8 formats: acc[j] is token 4 j + lg; f16: token 2 lg + j.
                     const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
-                    if (t < M)
-                        __hip_atomic_store(a.kpart + ((size_t)seg_lo * MAXM + t) * a.N + row, acc[j], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
-                __builtin_amdgcn_s_waitcnt(0);
-            }
-            __syncthreads();
-            if (tid == 0)
-                is_last = __hip_atomic_fetch_add(a.kcnt + rb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == NSEG - 1;
-            __syncthreads();
-            if (!is_last) continue;
-            if (wave == 0) {
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
-                    float sum = 0.f;
-                    if (t < M)
-                        for (int sg = 0; sg < NSEG; ++sg)
-                            sum += __hip_atomic_load(a.kpart + ((size_t)sg * MAXM + t) * a.N + row, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-                    acc[j] = sum;
-                }
-                if (lane == 0) __hip_atomic_store(a.kcnt + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        if (wave == 0) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                // int8 formats: acc[j] is token 4 j + lg; f16: token 2 lg + j.
-                const int t = (FMT == FMT_F16) ? 2 * lg + j : 4 * j + lg;
-                const bool valid = t < M;
-                const float y = acc[j];
-                if constexpr (EPI == EPI_STORE) {
-                    if (valid) a.y[(size_t)(row0 + t) * a.N + row] = y;
-                } else if constexpr (EPI == EPI_RESID) {
-                    if (valid) {
-                        float* xo = a.y + (size_t)(row0 + t) * a.N + row;
-                        float v = *xo + y;
-                        if (a.ds) {  // DeepStack residual of a visual row (Shaders.swift:696-707)
-                            const int vrow = a.ds_row0 + t - st->vis_offset;
-                            if (st->vis_offset >= 0 && vrow >= 0 && vrow < st->n_vis)
-                                v = v + a.ds[(size_t)vrow * H + row];
+                    const bool valid = t < M;
+                    const float y = acc[j];
+                    if constexpr (EPI == EPI_STORE) {
+                        if (valid) a.y[(size_t)(row0 + t) * a.N + row] = y;
+                    } else if constexpr (EPI == EPI_RESID) {
+                        if (valid) {
+                            float* xo = a.y + (size_t)(row0 + t) * a.N + row;
+                            float v = *xo + y;
+                            if (a.ds) {  // DeepStack residual of a visual row (Shaders.swift:696-707)
+                                const int vrow = a.ds_row0 + t - st->vis_offset;
+                                if (st->vis_offset >= 0 && vrow >= 0 && vrow < st->n_vis)
+                                    v = v + a.ds[(size_t)vrow * H + row];
+                            }
+                            *xo = v;
                         }
-                        *xo = v;
-                    }
-                } else if constexpr (EPI == EPI_SWIGLU) {
-                    // Block rb: gate units 8 rb .. 8 rb + 7 in columns 0-7, matching up rows in 8-15.
-                    const float up = __shfl_xor(y, 8);
-                    if (valid && r16 < 8) {
-                        const float g = y;
-                        a.h[(size_t)(row0 + t) * FF + rb * 8 + r16] = (g / (1.f + expf(-g))) * up;
-                    }
-                } else {  // EPI_ARGMAX: tiled rows are the vocabulary ids
-                    if (valid) {
-                        if (a.logits && st->logits_rows > 0) a.logits[(size_t)t * VOCAB + row] = y;
-#pragma unroll
-                        for (int tt = 0; tt < MT; ++tt)
-                            if (tt == t) argmax_merge(best_v[tt], best_i[tt], y, row);
+                    } else if constexpr (EPI == EPI_SWIGLU) {
+                        // Block rb: gate units 8 rb .. 8 rb + 7 in columns 0-7, matching up rows in 8-15.
+                        const float up = __shfl_xor(y, 8);
+                        if (valid && r16 < 8) {
+                            const float g = y;
+                            a.h[(size_t)(row0 + t) * FF + rb * 8 + r16] = (g / (1.f + expf(-g))) * up;
+                        }
+                    } else {  // EPI_ARGMAX: tiled rows are the vocabulary ids
+                        if (valid) {
+                            if (a.logits && st->logits_rows > 0) a.logits[(size_t)t * VOCAB + row] = y;
+    #pragma unroll
+                            for (int tt = 0; tt < MT; ++tt)
+                                if (tt == t) argmax_merge(best_v[tt], best_i[tt], y, row);
+                        }
                     }
                 }
             }
+    
+    };
+    uint4 wa[CPW], wb[CPW];
+    uint2 sa[CPW], sb2[CPW];
+    const int rb0 = SPLITK ? (int)(blockIdx.x / NSEG) : (int)blockIdx.x;
+    if constexpr (prefetch) {
+        for (int rb = rb0; rb < nrb; rb += 2 * rb_step) {
+            row_block(rb, wa, sa, wb, sb2);
+            if (rb + rb_step >= nrb) break;
+            row_block(rb + rb_step, wb, sb2, wa, sa);
         }
+    } else {
+        for (int rb = rb0; rb < nrb; rb += rb_step) row_block(rb, wa, sa, wb, sb2);
     }
     if constexpr (EPI == EPI_ARGMAX) {
         if (wave == 0) {

@@ -37,6 +37,10 @@ struct PersistArgs {
 };
 
 hipError_t launch_persistent(int fmt, const PersistArgs& a, hipStream_t s);
+// One-token GEMV y[N] = W x (W tiled, q4 or q8, K = 2048 or 6144) on the lm_head stage's
+// streaming schedule; hipErrorInvalidValue for other shapes or more than 160 x 256 row blocks.
+hipError_t launch_gemv_stream(int fmt, const uint8_t* w, const uint8_t* sb, const float* x, float* y, int N, int K,
+                              hipStream_t s);
 // Size of the packet area the workgroups exchange data through (zeroed before every launch), and
 // the index (in 32-bit words) of its error flag: non-zero after a launch means a wait timed out.
 size_t persistent_sync_bytes();

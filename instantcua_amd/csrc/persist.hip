@@ -1250,6 +1250,59 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// Isolated one-token GEMV y = W x (W tiled by icua_repack, K = 2048 or 6144) on the schedule of
+// the lm_head stage above: one 512-thread workgroup per CU streams 16-row blocks wg, wg + G, ...
+// All eight waves split K (CW chunks each; each quad's operand tiles are read from LDS once for
+// every block), DEPTH blocks are in flight per wave, and the per-block partial sums of the waves
+// wait in LDS for one reduction at the end.  Every lane does useful work: the four groups of a
+// quad accumulate into one matrix-core result (lanes 16j.. hold group j's sums).
+constexpr int GS_MAX_BLOCKS = 160;  // row blocks per workgroup (part[] below)
+template <int FMT, int K>
+__global__ __launch_bounds__(THREADS, 1) void gemv_stream_kernel(const uint8_t* w, const uint8_t* sb, const float* x,
+                                                                  float* y, int nrb) {
+    constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
+    constexpr int CW = K / CHK / WAVES;  // chunks per wave: q4 2 / 6, q8 4 / 12
+    constexpr int DEPTH = CW <= 2 ? 4 : CW <= 6 ? 2 : 1;
+    __shared__ Shared S;
+    __shared__ float part[GS_MAX_BLOCKS * WAVES * 16];
+    const int wg = blockIdx.x, G = gridDim.x, tid = my_tid(), lane = tid % 64, wave = wave_id();
+    const int nb = (nrb - wg + G - 1) / G;  // blocks of this workgroup (the host keeps wg < nrb)
+    if (tid < 4) S.zero[tid] = 0u;
+    WB<FMT, CW> wl[DEPTH];
+#pragma unroll
+    for (int k = 0; k < DEPTH; ++k) wl[k].load(w, sb, min(wg + k * G, nrb - 1), K, wave, lane);
+    stage_c<FMT, K>(S, x, false);
+    QuadOps<FMT> lq[CW / 2];
+#pragma unroll
+    for (int p = 0; p < CW / 2; ++p) lq[p] = quad_load<FMT>(S, wave * CW + 2 * p, lane);
+    for (int k0 = 0; k0 < nb; k0 += DEPTH) {
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) {
+            const int kb = k0 + k;
+            if (kb < nb) {
+                float v = 0.f;
+#pragma unroll
+                for (int p = 0; p < CW / 2; ++p)
+                    v = quad_scale<FMT>(lq[p], quad_mfma<FMT>(lq[p], wl[k].wv[2 * p], wl[k].wv[2 * p + 1]), wl[k].sq[p],
+                                        v);
+                v = quad_rows(v);
+                if (lane < 16) part[(kb * WAVES + wave) * 16 + lane] = v;
+                if (kb + DEPTH < nb) wl[k].load(w, sb, wg + (kb + DEPTH) * G, K, wave, lane);
+            }
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < nb * 16; e += THREADS) {
+        const int kb = e / 16, r = e % 16;
+        const float* pp = part + kb * WAVES * 16 + r;
+        float v = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < WAVES; ++wv) v += pp[wv * 16];
+        y[(size_t)(wg + kb * G) * 16 + r] = v;
+    }
+}
+
 template <int FMT>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     __shared__ Shared S;
@@ -1281,6 +1334,19 @@ hipError_t launch_persistent(int fmt, const PersistArgs& a, hipStream_t s) {
         return hipLaunchCooperativeKernel((const void*)pk::decode_kernel<FMT_Q8>, dim3(pk::NWG), dim3(pk::THREADS),
                                           args, 0, s);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_stream(int fmt, const uint8_t* w, const uint8_t* sb, const float* x, float* y, int N, int K,
+                              hipStream_t s) {
+    if (N <= 0 || N % 16 || (K != H && K != FF) || (fmt != FMT_Q4 && fmt != FMT_Q8)) return hipErrorInvalidValue;
+    const int nrb = N / 16, G = nrb < pk::NWG ? nrb : pk::NWG;
+    if (nrb > pk::GS_MAX_BLOCKS * G) return hipErrorInvalidValue;
+    const void* k = fmt == FMT_Q4 ? (K == H ? (const void*)pk::gemv_stream_kernel<FMT_Q4, H>
+                                            : (const void*)pk::gemv_stream_kernel<FMT_Q4, FF>)
+                                  : (K == H ? (const void*)pk::gemv_stream_kernel<FMT_Q8, H>
+                                            : (const void*)pk::gemv_stream_kernel<FMT_Q8, FF>);
+    void* args[] = {(void*)&w, (void*)&sb, (void*)&x, (void*)&y, (void*)&nrb};
+    return hipLaunchKernel(k, dim3(G), dim3(pk::THREADS), args, 0, s);
 }
 
 #ifdef ICUA_PERSIST_TRACE
