@@ -161,6 +161,22 @@ def _norm_weights(rng: np.random.Generator, n: int) -> np.ndarray:
     return (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
 
 
+def tensor_view(img: np.ndarray, tid: int) -> np.ndarray:
+    """Writable uint8 view of tensor `tid` of an in-memory ``.icua`` image."""
+    table = img[16:16 + TensorID.count * 16].view("<u8").reshape(TensorID.count, 2)
+    off, n = int(table[tid, 0]), int(table[tid, 1])
+    return img[off:off + n]
+
+
+def copy_embedding_row(img: np.ndarray, src: int, dst: int) -> None:
+    """Gives token dst the codes and scales of token src in the tied embedding, so the lm_head
+    logits of the two are bit-identical (an exact argmax tie)."""
+    codes = tensor_view(img, TensorID.embed).reshape(Dims.vocab, -1)
+    sb = tensor_view(img, TensorID.embed_sb).reshape(Dims.vocab, -1)
+    codes[dst] = codes[src]
+    sb[dst] = sb[src]
+
+
 def build_model_image(fmt: int, n_layers: int = Dims.layers, tag: str = "model", vision: bool = False,
                       zero_vision_blocks: bool = False) -> np.ndarray:
     """Return a complete in-memory ``.icua`` image (uint8 array) of a synthetic decoder, with the

@@ -122,3 +122,36 @@ def test_text_generate_after_generate_vision(oracle_mod, vimg):
         e.generate_vision(rgb, toks, max_new_tokens=steps)
         got = e.generate(text, max_new_tokens=steps)
     compare_greedy(got, ref, margins, first.max() * np.ones(steps))
+
+
+def test_tower_matches_oracle_at_the_default_frame(vimg):
+    """The reference's default 640 x 384 frame (24 x 40 patches: 960 patches in 15 whole 64-patch
+    tiles, 240 visual rows) against tests/golden/oracle_vision_24x40.npz (make_golden_vision.py):
+    every 15th row of the pooler and of each DeepStack set within TOL of the set's largest
+    magnitude, and for every row the sum within 1e-3 of sqrt(2048 x sum of squares) and the sum
+    of squares within 1e-2 relative."""
+    import hashlib
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "oracle_vision_24x40.npz")
+    with np.load(path, allow_pickle=False) as z:
+        fx = {k: z[k] for k in z.files}
+    gh, gw = (int(v) for v in fx["grid"])
+    assert hashlib.sha256(vimg.tobytes()).digest() == fx["image_sha256"].tobytes()
+    rgb = synth.random_rgb(gh, gw, "tower-24x40")
+    assert hashlib.sha256(np.ascontiguousarray(rgb).tobytes()).digest() == fx["rgb_sha256"].tobytes()
+    with Engine(flags=0, image=vimg, max_context=64, max_steps=4) as e:
+        e.vision(rgb)
+        p, ds = e.visual_rows()
+    sets = np.stack([p] + list(ds)).astype(np.float32)
+    assert sets.shape == (4, gh * gw // 4, 2048)
+    for i, name in enumerate(["pooler", "deepstack 0", "deepstack 1", "deepstack 2"]):
+        got = sets[i][fx["rows"]]
+        ref = fx["row_values"][i].astype(np.float32)
+        err = float(np.abs(got - ref).max() / fx["max_abs"][i])
+        s_err = float((np.abs(sets[i].sum(axis=1, dtype=np.float64) - fx["row_sum"][i])
+                       / np.sqrt(2048.0 * fx["row_sumsq"][i])).max())
+        q_err = float((np.abs((sets[i].astype(np.float64) ** 2).sum(axis=1) - fx["row_sumsq"][i])
+                       / fx["row_sumsq"][i]).max())
+        print(f"24x40 {name}: sampled rows {err:.2e}, row sums {s_err:.2e}, row sums of squares {q_err:.2e}")
+        assert err < TOL and s_err < 1e-3 and q_err < 1e-2, (name, err, s_err, q_err)

@@ -383,3 +383,39 @@ def test_commit_loop_grammar_pairs_replay_as_explicit_passes(oracle_mod):
         fired |= {"stop )"} if out[-1] == 8 else set()
         fired |= {"action"} if out[:2] == [3678, 7] else set()
     assert fired >= {"pair 11", "stop )"}, fired  # the scaled rows make the rules fire
+
+
+# ------------------------------------------------------------------------------------------
+# Greedy argmax ties (Shaders.swift:1514-1536: the lower token id wins an equal logit)
+
+def tie_models(oracle_mod, steps=6):
+    """A 2-layer q4 model, its greedy run, and for tie steps k = 0 and k = 3 a copy of the image
+    in which a lower id u takes the embedding row of the step's winner t (so logit u == logit t
+    at every step): (image, prompt, plain greedy, [(k, t, u, image_k)])."""
+    img = synth.build_model_image(WeightFormat.Q4, n_layers=2, tag="argmax-tie")
+    toks = synth.random_tokens(16, "argmax-tie-prompt")
+    om = oracle_mod.OracleModel(img, 64)
+    ref, _, _ = om.generate(toks, steps)
+    om.close()
+    cases = []
+    for k in (0, 3):
+        t = int(ref[k])
+        assert t not in ref[:k].tolist(), "pick a step whose winner is new (no earlier tie)"
+        used = set(toks.tolist()) | set(ref[:k + 1].tolist())
+        u = next(i for i in range(t - 1, -1, -1) if i not in used)
+        img_k = img.copy()
+        synth.copy_embedding_row(img_k, t, u)
+        cases.append((k, t, u, img_k))
+    return img, toks, ref, cases
+
+
+def test_argmax_tie_takes_the_lower_id(oracle_mod):
+    _, toks, ref, cases = tie_models(oracle_mod)
+    for k, t, u, img_k in cases:
+        om = oracle_mod.OracleModel(img_k, 64)
+        got, _, first = om.generate(toks, len(ref))
+        om.close()
+        if k == 0:
+            assert first[u] == first[t] and first[u] == first.max()
+        assert np.array_equal(got[:k], ref[:k]), (k, got, ref)
+        assert int(got[k]) == u, (k, t, u, got)
