@@ -743,7 +743,7 @@ struct icua_engine {
         g.sb = w.wqkv_sb;
         g.N = QKV;
         g.y = pqkv;
-        HIPCK(launch_pf_gemm(H, EPI_STORE, g, stream));
+        HIPCK(launch_pf_gemm(fmt, H, EPI_STORE, g, stream));
         // 2. q/k norm + M-RoPE + KV write, causal flash attention.
         PfQkArgs qa{pqkv, w.q_norm, w.k_norm, rope, kv_ptr(l, 0), kv_ptr(l, 1), pqh, pql, M, p0, maxctx};
         HIPCK(launch_pf_qk(qa, stream));
@@ -755,14 +755,14 @@ struct icua_engine {
         g.sb = w.wo_sb;
         g.N = H;
         g.y = px;
-        HIPCK(launch_pf_gemm(H, EPI_RESID, g, stream));
+        HIPCK(launch_pf_gemm(fmt, H, EPI_RESID, g, stream));
         // 4. RMSNorm + gate|up + SwiGLU.
         HIPCK(launch_pf_prep(H, 1, px, w.mlp_norm, M, Mpad, pxa, pxs, pts, stream));
         g.w = w.wgu;
         g.sb = w.wgu_sb;
         g.N = GU;
         g.h = ph;
-        HIPCK(launch_pf_gemm(H, EPI_SWIGLU, g, stream));
+        HIPCK(launch_pf_gemm(fmt, H, EPI_SWIGLU, g, stream));
         // 5. Down projection + residual (+ DeepStack after layers 0-2 at visual rows).
         HIPCK(launch_pf_prep(FF, 0, ph, nullptr, M, Mpad, pxa, pxs, pts, stream));
         g.w = w.wd;
@@ -770,7 +770,7 @@ struct icua_engine {
         g.N = H;
         g.y = px;
         g.ds = (has_ds && l < 3) ? ds[l] : nullptr;
-        HIPCK(launch_pf_gemm(FF, EPI_RESID, g, stream));
+        HIPCK(launch_pf_gemm(fmt, FF, EPI_RESID, g, stream));
         return 0;
     }
 
@@ -801,7 +801,7 @@ struct icua_engine {
         return enqueue_head(MAXM, 0);
     }
 
-    bool use_pf(int n) const { return fmt == 2 && n > MAXM && !(flags & ICUA_FLAG_PASS_PREFILL); }
+    bool use_pf(int n) const { return n > MAXM && !(flags & ICUA_FLAG_PASS_PREFILL); }
 
     int prefill(const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new, int write_logits) {
         if (n <= 0) return fail("empty prompt");

@@ -110,7 +110,7 @@ struct PfGemmArgs {
     const float* xs;        // group sums
     const float* ts;        // row scales
     const uint8_t* w;       // codes in 16-row MFMA tiles (launch_repack)
-    const uint8_t* sb;      // half2 (scale, bias) [N][K / 64], tiled row order
+    const uint8_t* sb;      // q4 half2 (scale, bias) [N][K / 64]; q8 half scales [N][K / 32]
     int N, M, Mpad;
     float* y;               // EPI_STORE: y [M][N]; EPI_RESID: residual x [M][N] (+=)
     float* h;               // EPI_SWIGLU: [M][FF]
@@ -118,8 +118,9 @@ struct PfGemmArgs {
     int row0;               // prompt row of pass row 0
     int vis_offset, n_vis;
 };
-// epi: EPI_STORE / EPI_RESID / EPI_SWIGLU; K = 2048 (any epilogue) or 6144 (EPI_RESID).
-hipError_t launch_pf_gemm(int K, int epi, const PfGemmArgs& a, hipStream_t s);
+// fmt: FMT_Q4 / FMT_Q8 / FMT_F16 (sb unused for f16); epi: EPI_STORE / EPI_RESID / EPI_SWIGLU;
+// K = 2048 (any epilogue) or 6144 (EPI_RESID).
+hipError_t launch_pf_gemm(int fmt, int K, int epi, const PfGemmArgs& a, hipStream_t s);
 
 struct PfQkArgs {
     const float* qkv;       // raw fused QKV rows [M][QKV]

@@ -1,16 +1,18 @@
-// Many-token prefill on the matrix cores, gfx950 (q4 weights).
+// Many-token prefill on the matrix cores, gfx950 (q4, q8 and f16 weights).
 //
 // Replaces the reference's multi-token path (Shaders.swift:676-1216: k_rmsnorm_rows_h,
 // llm_gemm_tile, k_g3_*, k_qk_norm_rope, k_prefill_attn) for prompts longer than one GEMV pass;
 // math per tools/reference/qwen3vl_ref.py:243-292 (fp32 activations, fp16 KV cache).
 //
-// Projections.  y[t][r] = sum_g (s_rg sum_{k in g} q_rk x_tk + b_rg sum_{k in g} x_tk).  A prep
+// Projections.  q4: y[t][r] = sum_g (s_rg sum_{k in g} q_rk x_tk + b_rg sum_{k in g} x_tk) over
+// 64-groups; q8: y[t][r] = sum_g s_rg sum_{k in g} q_rk x_tk over 32-groups; f16: y = W x.  A prep
 // kernel scales every activation row by a power of two that puts its largest |x| in
 // [2^14, 2^15) and splits it into fp16 hi + lo parts (x'' = hi + lo to ~22 bits; the scaling
 // keeps every part that matters far above the fp16 subnormal range).  The GEMM runs
-// v_mfma_f32_16x16x32_f16 on (hi, lo) x the integer codes, which are exact in fp16, so each
-// 64-group's sum C_g = sum_k q_k x''_k comes out of one accumulator chain; the group
-// epilogue is acc += s C_g + b X_g (X_g = sum_k x''_k), and the row scale 2^(E_t - 14) is
+// v_mfma_f32_16x16x32_f16 on (hi, lo) x the weights as fp16 B operands: the q4 and q8 integer
+// codes are exact in fp16, so each group's sum C_g = sum_k q_k x''_k comes out of one
+// accumulator chain; the group epilogue is acc += s C_g + b X_g (q4, X_g = sum_k x''_k) or
+// acc += s C_g (q8), f16 weights accumulate directly, and the row scale 2^(E_t - 14) is
 // applied once at the end.
 //
 // Attention.  Causal GQA flash attention on v_mfma_f32_16x16x32_f16: scores are computed
@@ -117,17 +119,19 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------
-// q4 GEMM: a workgroup of 8 waves computes 128 tokens x 128 weight rows; wave w owns token
-// blocks 8 tm + 2 (w % 4), + 1 (32 tokens) against row blocks 4 (w / 4) .. + 3 (64 rows), two
-// waves per SIMD.  Each 128-K step, the code chunks of the 8 row blocks are unpacked once into
-// fp16 B operands in LDS (double-buffered) and shared by the waves; the waves' activation
-// operands stream from global memory straight into registers one 64-group ahead.  Tiles are
-// numbered token-tile-major and dealt to the 8 XCDs in contiguous ranges, so the workgroups of
-// one XCD share token tiles in its L2.
+// GEMM: a workgroup of 8 waves computes 128 tokens x 128 weight rows; wave w owns token blocks
+// 8 tm + 2 (w % 4), + 1 (32 tokens) against row blocks 4 (w / 4) .. + 3 (64 rows), two waves
+// per SIMD.  Each 128-K step, the weight chunks of the 8 row blocks (q4 one 1 KiB chunk, q8
+// two, f16 four) become fp16 B operands in LDS once (double-buffered) and are shared by the
+// waves; the waves' activation operands stream from global memory straight into registers one
+// 64-K half-step ahead.  Tiles are numbered token-tile-major and dealt to the 8 XCDs in
+// contiguous ranges, so the workgroups of one XCD share token tiles in its L2.
 
-template <int K, int EPI>
+template <int FMT, int K, int EPI>
 __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     constexpr int NG = K / 64, NKS = K / 32, NC = K / 128;
+    constexpr int CPS = FMT == FMT_Q4 ? 1 : FMT == FMT_Q8 ? 2 : 4;  // 1 KiB chunks per 128-K step
+    constexpr int NCH = NC * CPS;                                      // chunks per row block
     const int TN = a.N / 128, TM = a.Mpad / 128, T = TM * TN;
     const int per = (T + 7) / 8;
     const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
@@ -144,13 +148,16 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     const uint16_t* xa = a.xa + (size_t)tb0 * NKS * 1024 + lane * 8;   // token block tb0 (+ NKS * 1024 for tb0 + 1)
     // Staging: thread t unpacks nibble lane t % 64 of row block t / 64.
     const int srb = tid >> 6;
-    const uint8_t* wsrc = a.w + (size_t)(tn * 8 + srb) * NC * 1024 + lane * 16;
-    // Thread t < 256 loads the (scale, bias) word of its row, t >= 256 one group sum: one
-    // unconditional 4-byte load per step (stride 2 words or 32 floats per step).
+    const uint8_t* wsrc = a.w + (size_t)(tn * 8 + srb) * NCH * 1024 + lane * 16;
+    // Thread t < 256 loads one scale word of its row, t >= 256 one group sum: one unconditional
+    // 4-byte load per step (stride 2 words or 32 floats per step).  q4: the (scale, bias) half2
+    // of 64-group 2 c + t / 128; q8: the scales of 32-groups 4 c + 2 (t / 128), + 1 (the same
+    // word offsets: a q8 row holds K / 64 words of scale pairs).  f16 weights have no scales.
     const int vj = tid & 255;
     const uint32_t* vsrc = tid < 256 ? (const uint32_t*)a.sb + (size_t)(tn * 128 + (vj & 127)) * NG + (vj >> 7)
                                      : (const uint32_t*)a.xs + ((size_t)(tm * 8 + (vj >> 5)) * NG + ((vj >> 4) & 1)) * 16 + (vj & 15);
     const int vstride = tid < 256 ? 2 : 32;
+    const bool vload = FMT != FMT_F16 || tid >= 256;
 
     f32x4 acc[2][4];
 #pragma unroll
@@ -160,8 +167,8 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 
     // Activation operands of one 64-group (two k-steps), prefetched one group ahead.
     uint4 Ae[2][2][2], Ao[2][2][2];  // [token block][k-step of the group][hi, lo]
-    uint4 Wn;
-    uint32_t Vn;
+    uint4 Wn[CPS];
+    uint32_t Vn = 0;
     auto aload = [&](int g, uint4(&A)[2][2][2]) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -173,14 +180,47 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         }
     };
     auto wload = [&](int c) {
-        Wn = *(const uint4*)(wsrc + (size_t)c * 1024);
-        Vn = vsrc[(size_t)c * vstride];
+#pragma unroll
+        for (int j = 0; j < CPS; ++j) Wn[j] = *(const uint4*)(wsrc + (size_t)(c * CPS + j) * 1024);
+        if (vload) Vn = vsrc[(size_t)c * vstride];
     };
     // Nibble lane L (row L % 16, 16-K slot L / 16 of each group) -> fp16 lanes (L % 16) + 16 (2 (slot % 2) + h)
     // of k-step 2 gg + slot / 2, h = 0 for K 0..7 of the slot, 1 for K 8..15.
     auto lstore = [&](int b) {
+        if constexpr (FMT == FMT_F16) {
+            // f16 chunk j is k-step j, already in the B-operand lane layout.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Bs[b][srb][j][lane] = Wn[j];
+            Vs[b][tid] = Vn;
+            return;
+        } else if constexpr (FMT == FMT_Q8) {
+            // q8 chunk j: bytes 0-7 of a lane are k-step 2 j (K-slot lane / 16 of row lane % 16),
+            // bytes 8-15 k-step 2 j + 1, the B-operand lane layout; a signed byte b spread into a
+            // 16-bit lane, xor 0x80 and or'ed into 0x6400, is the fp16 value 1152 + b, and one
+            // packed fp16 subtraction leaves b exactly.
+            const f16x2 k1152 = {(f16)1152.f, (f16)1152.f};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t dd[4] = {Wn[j].x, Wn[j].y, Wn[j].z, Wn[j].w};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t o[4];
+#pragma unroll
+                    for (int w2 = 0; w2 < 2; ++w2) {
+                        const uint32_t d = dd[2 * h + w2];
+                        const uint32_t s0 = __builtin_amdgcn_perm(d, d, 0x0C010C00u);  // b0, b1
+                        const uint32_t s1 = __builtin_amdgcn_perm(d, d, 0x0C030C02u);  // b2, b3
+                        o[2 * w2] = h2_bits(as_h2((s0 ^ 0x00800080u) | 0x64006400u) - k1152);
+                        o[2 * w2 + 1] = h2_bits(as_h2((s1 ^ 0x00800080u) | 0x64006400u) - k1152);
+                    }
+                    Bs[b][srb][2 * j + h][lane] = make_uint4(o[0], o[1], o[2], o[3]);
+                }
+            }
+            Vs[b][tid] = Vn;
+            return;
+        }
         const int r = lane & 15, slot = lane >> 4;
-        const uint32_t dd[4] = {Wn.x, Wn.y, Wn.z, Wn.w};
+        const uint32_t dd[4] = {Wn[0].x, Wn[0].y, Wn[0].z, Wn[0].w};
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
 #pragma unroll
@@ -213,7 +253,33 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const f16x2 sb2 = as_h2(Vs[b][gg * 128 + (rb0 + r) * 16 + r16]);
-            sb[r] = make_float2((float)sb2.x, (float)sb2.y);
+            sb[r] = make_float2((float)sb2.x, (float)sb2.y);  // q4 (scale, bias); q8 the two 32-groups' scales
+        }
+        if constexpr (FMT == FMT_Q8) {
+            // Two 32-groups, one k-step each.
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                f32x4 C[4][2];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+                            C[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, Ac[i][kk][hl]),
+                                                                             Bf[r][kk], C[r][i], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(kk ? sb[r].y : sb[r].x, C[r][i][e], acc[i][r][e]);
+            }
+            return;
         }
         f32x4 xg[2];
 #pragma unroll
@@ -238,7 +304,12 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], fmaf(sb[r].y, xg[i][e], acc[i][r][e]));
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (FMT == FMT_F16)
+                        acc[i][r][e] += C[r][i][e];
+                    else
+                        acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], fmaf(sb[r].y, xg[i][e], acc[i][r][e]));
+                }
             }
     };
 
@@ -512,21 +583,31 @@ hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w
     return hipGetLastError();
 }
 
-hipError_t launch_pf_gemm(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
-    if (a.M < 1 || a.Mpad < a.M || a.Mpad % 128 || a.N % 128) return hipErrorInvalidValue;
-    const int T = (a.Mpad / 128) * (a.N / 128);
-    const int grid = 8 * ((T + 7) / 8);
+template <int FMT>
+static hipError_t pf_gemm_fmt(int K, int epi, const PfGemmArgs& a, int grid, hipStream_t s) {
     if (K == H && epi == EPI_STORE)
-        hipLaunchKernelGGL((pf_gemm_kernel<H, EPI_STORE>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_STORE>), dim3(grid), dim3(512), 0, s, a);
     else if (K == H && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<H, EPI_RESID>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_RESID>), dim3(grid), dim3(512), 0, s, a);
     else if (K == H && epi == EPI_SWIGLU)
-        hipLaunchKernelGGL((pf_gemm_kernel<H, EPI_SWIGLU>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_SWIGLU>), dim3(grid), dim3(512), 0, s, a);
     else if (K == FF && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<FF, EPI_RESID>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, FF, EPI_RESID>), dim3(grid), dim3(512), 0, s, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+hipError_t launch_pf_gemm(int fmt, int K, int epi, const PfGemmArgs& a, hipStream_t s) {
+    if (a.M < 1 || a.Mpad < a.M || a.Mpad % 128 || a.N % 128) return hipErrorInvalidValue;
+    const int T = (a.Mpad / 128) * (a.N / 128);
+    const int grid = 8 * ((T + 7) / 8);
+    switch (fmt) {
+        case FMT_Q4: return pf_gemm_fmt<FMT_Q4>(K, epi, a, grid, s);
+        case FMT_Q8: return pf_gemm_fmt<FMT_Q8>(K, epi, a, grid, s);
+        case FMT_F16: return pf_gemm_fmt<FMT_F16>(K, epi, a, grid, s);
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_pf_qk(const PfQkArgs& a, hipStream_t s) {

@@ -1,5 +1,5 @@
-"""GPU parity of the matrix-core prefill (int8-sliced GEMMs, flash attention, chunking) against
-the oracle and against the 8-row pass path, through the C ABI."""
+"""GPU parity of the matrix-core prefill (fp16 hi/lo GEMMs over q4 / q8 / f16 weights, flash
+attention, chunking) against the oracle and against the 8-row pass path, through the C ABI."""
 import numpy as np
 import pytest
 
@@ -18,6 +18,16 @@ def q4_small():
     return synth.build_model_image(WeightFormat.Q4, n_layers=LAYERS, tag="q4-small")
 
 
+_IMAGES = {}
+
+
+def small_image(fmt):
+    """The 2-layer model of each weight format (q4 group 64, q8 group 32, f16)."""
+    if fmt not in _IMAGES:
+        _IMAGES[fmt] = synth.build_model_image(fmt, n_layers=LAYERS, tag=f"fmt{fmt}-small")
+    return _IMAGES[fmt]
+
+
 def _kv_close(got_rows, ref_rows, layer):
     # Layer 0's K/V come from one projection of the embedding: fp32-level differences only
     # flip fp16 rounding boundaries, or move a value near zero (RoPE cancellation) by a few of
@@ -30,15 +40,17 @@ def _kv_close(got_rows, ref_rows, layer):
         fp16_close(got_rows, ref_rows, max_ulp=2, row_tol=2e-3, frac_over_1ulp=5e-2)
 
 
+@pytest.mark.parametrize("fmt", [WeightFormat.Q4, WeightFormat.Q8, WeightFormat.F16], ids=["q4", "q8", "f16"])
 @pytest.mark.parametrize("n", [9, 130, 400])
-def test_prefill_matches_oracle(oracle_mod, q4_small, n):
-    """Prompts of one partial 16-row block up to several 128-row tiles: first logits, every
-    prompt K/V row of both layers and the greedy continuation."""
+def test_prefill_matches_oracle(oracle_mod, q4_small, n, fmt):
+    """Prompts of one partial 16-row block up to several 128-row tiles, for each weight format:
+    first logits, every prompt K/V row of both layers and the greedy continuation."""
+    img = q4_small if fmt == WeightFormat.Q4 else small_image(fmt)
     toks = synth.random_tokens(n, f"pf-oracle-{n}")
     steps = 6
-    om = oracle_mod.OracleModel(q4_small, n + 16)
+    om = oracle_mod.OracleModel(img, n + 16)
     ref, margins, first = om.generate(toks, steps)
-    with Engine(flags=0, image=q4_small, max_context=n + 16, max_steps=steps) as e:
+    with Engine(flags=0, image=img, max_context=n + 16, max_steps=steps) as e:
         e.eos = (-1, -1)
         assert not e.pass_prefill
         tok0 = e.prefill(toks, max_new=steps, write_logits=True)
@@ -53,7 +65,8 @@ def test_prefill_matches_oracle(oracle_mod, q4_small, n):
     for (l, k), rows in kv.items():
         _kv_close(rows, om.kv(l, k)[:, :n], l)
     cnt, note = compare_greedy(got, ref, margins, first.max() * np.ones(steps))
-    print(f"n {n}: {cnt}/{steps} identical ({note}); prefill {t['prefill_ms']:.2f} ms")
+    print(f"fmt {fmt} n {n}: logits rel err {rel_err(lg, first):.3g}; {cnt}/{steps} identical ({note}); "
+          f"prefill {t['prefill_ms']:.2f} ms")
 
 
 def test_prefill_continuation_at_offset(oracle_mod, q4_small):
