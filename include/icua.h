@@ -176,8 +176,9 @@ int icua_device_sync(void);
  * K in {2048, 6144}, N % 16 == 0. */
 int icua_repack(int fmt, const void* d_codes, const void* d_sb, int N, int K, void* d_tiled_codes, void* d_tiled_sb);
 /* y[m][N] = W[N][K] . x[m][K]: W repacked by icua_repack, x fp32, y fp32; K in {2048, 6144},
- * N % 16 == 0, m <= 8.  The dot64_row GEMV family of Shaders.swift:480-595.  One-token q4 / q8
- * products (N <= 655360) run on the streaming schedule of the decode kernel's lm_head stage. */
+ * N % 16 == 0, m <= 8.  The dot64_row GEMV family of Shaders.swift:480-595.  q4 / q8 products
+ * run on a streaming schedule, one workgroup per CU (one token: N <= 655360; 2-8 tokens: codes
+ * under 2 GiB). */
 int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, const float* d_x, int m, float* d_y);
 /* Times `iters` launches of icua_gemv (m = 1) cycling over `ncopies` weight copies; *avg_us per
  * launch (HIP events on the launch stream). */

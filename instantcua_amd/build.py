@@ -22,7 +22,7 @@ TRACE_LIB = os.path.join(HERE, "libicua_trace.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["engine.hip", "gemv.hip", "attention.hip", "misc.hip", "persist.hip", "prefill.hip", "quant.hip", "vision.hip", "tokenizer.cpp"]
+SOURCES = ["engine.hip", "gemv.hip", "gemv8.hip", "attention.hip", "misc.hip", "persist.hip", "prefill.hip", "quant.hip", "vision.hip", "tokenizer.cpp"]
 
 # Packed-FP32 instructions are disabled for every device pass (the host pass ignores the
 # feature with a warning).

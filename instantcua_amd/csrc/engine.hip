@@ -169,11 +169,15 @@ struct icua_engine {
         return 0;
     }
 
-    // One GEMV of the pass.  Multi-row gate|up and lm_head passes stage their activation
-    // operands once in a separate launch first: their 768 / 1024 workgroups would otherwise each
-    // repeat the RMSNorm and the int8 slicing of every row, which makes them VALU-bound.  For the
-    // GEMVs of 128-256 workgroups the extra launch costs more than it saves.
+    // One GEMV of the pass.  Multi-row q4 / q8 passes run the streaming kernel (the rows
+    // staged once per workgroup, one workgroup per CU).  Multi-row f16 gate|up and lm_head passes
+    // stage their activation operands once in a separate launch first: their 768 / 1024
+    // workgroups would otherwise each repeat the RMSNorm and the slicing of every row.
     int gemv(GemvOp op, GemvArgs& a, int mt) {
+        if (mt > 1 && gemv8_supports(fmt, op, a.N)) {
+            HIPCK(launch_gemv8(fmt, op, a, stream));
+            return 0;
+        }
         const bool pre = mt > 1 && (op == GEMV_GU || op == GEMV_LMHEAD);
         a.apre = pre ? apre : nullptr;
         a.fxpre = pre ? fxpre : nullptr;
@@ -410,6 +414,11 @@ struct icua_engine {
         HIPCK(hipMalloc(&qkv, sizeof(float) * MAXM * QKV));
         HIPCK(hipMalloc(&attn, sizeof(float) * MAXM * H));
         HIPCK(hipMalloc(&h, sizeof(float) * MAXM * FF));
+        // The multi-row GEMVs stage every row of these buffers (only the pass's rows are
+        // written): rows no pass has written yet hold zeros.
+        HIPCK(hipMemset(x, 0, sizeof(float) * MAXM * H));
+        HIPCK(hipMemset(attn, 0, sizeof(float) * MAXM * H));
+        HIPCK(hipMemset(h, 0, sizeof(float) * MAXM * FF));
         const size_t kvn = (size_t)layers * 2 * NKV * maxctx * HD;
         HIPCK(hipMalloc(&kv, kvn * 2));
         HIPCK(hipMemset(kv, 0, kvn * 2));
@@ -1342,8 +1351,8 @@ int icua_repack(int fmt, const void* d_codes, const void* d_sb, int N, int K, vo
     return 0;
 }
 
-// One-token q4 / q8 GEMVs take the streaming kernel (the lm_head stage's schedule); f16 and
-// multi-token ones the general kernel.
+// One-token q4 / q8 GEMVs take the streaming kernel (the lm_head stage's schedule), multi-token
+// ones its 8-row form (gemv8.hip); f16 the general kernel.
 static bool use_stream(int fmt, int N, int m) {
     return m == 1 && (fmt == FMT_Q4 || fmt == FMT_Q8) && N / 16 <= 160 * 256;
 }
@@ -1354,6 +1363,12 @@ int icua_gemv(int fmt, const void* d_codes, const void* d_sb, int N, int K, cons
     if (gemv_setup(fmt, N, K, m, a, op)) return -1;
     if (use_stream(fmt, N, m)) {
         HIPCK(launch_gemv_stream(fmt, (const uint8_t*)d_codes, (const uint8_t*)d_sb, d_x, d_y, N, K, nullptr));
+    } else if (m > 1 && gemv8_supports(fmt, op, N)) {
+        a.w = (const uint8_t*)d_codes;
+        a.sb = (const uint8_t*)d_sb;
+        a.x = d_x;
+        a.y = d_y;
+        HIPCK(launch_gemv8(fmt, op, a, nullptr));
     } else {
         a.w = (const uint8_t*)d_codes;
         a.sb = (const uint8_t*)d_sb;

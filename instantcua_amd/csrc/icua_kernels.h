@@ -23,7 +23,7 @@ struct GemvArgs {
     const uint8_t* w;       // codes in 16-row MFMA tiles (launch_repack)
     const uint8_t* sb;      // q4: half2 (scale, bias) [N][K/64]; q8: half [N][K/32] (tiled row order)
     int N;                  // output rows
-    const float* x;         // fp32 activations [M][K]
+    const float* x;         // fp32 activations [M][K] (MAXM rows when m_fixed == 0)
     const float* norm_w;    // PRO_NORM weights [K]
     float* y;               // EPI_STORE: y [M][N]; EPI_RESID: residual x [M][N] (+=)
     float* h;               // EPI_SWIGLU: [M][FF]
@@ -42,6 +42,10 @@ struct GemvArgs {
 };
 
 hipError_t launch_gemv(int fmt, GemvOp op, const GemvArgs& a, int mt, hipStream_t s);
+// Multi-token (MAXM-row) q4 / q8 GEMVs on the streaming schedule (gemv8.hip): the pass's rows
+// staged once per workgroup; every op of launch_gemv, K = 6144 for up to 1024 row blocks.
+bool gemv8_supports(int fmt, GemvOp op, int N);
+hipError_t launch_gemv8(int fmt, GemvOp op, const GemvArgs& a, hipStream_t s);
 // Stages the activation operands of a multi-row (MAXM) GEMV of the same arguments into a.apre /
 // a.fxpre (GEMV_PREP_BYTES / GEMV_PREP_FX_BYTES), for the GEMV launched next on the stream.
 hipError_t launch_gemv_prep(int fmt, GemvOp op, const GemvArgs& a, hipStream_t s);

@@ -66,7 +66,14 @@ def test_single_layer_q8_step(oracle_mod):
 
 @pytest.mark.parametrize("n", [1, 5, 8])
 def test_multi_row_layer_q4(oracle_mod, q4_small, n):
-    """A pass of n rows through layer 1 with a causal tail over 37 prior rows."""
+    """A pass of n rows through layer 1 with a causal tail over 37 prior rows.
+
+    The fused q|k|v rows, before any fp16 rounding, are held to 1e-6 of their largest magnitude.
+    The pass's own K/V rows are then rounded to fp16 in the cache: a value within 1e-7 of a
+    rounding boundary lands on the other side about as often on either path (one fp16 ulp,
+    ~5e-4 of the value), and the attention over those rows carries that into the layer output.
+    So the output is held to 2e-4 of its largest magnitude (still 50 times finer than the stated
+    1e-2), and the cache rows to one ulp."""
     pos = 37
     kc = synth.fp16_normal((NKV, pos, HD), "mr-k", n)
     vc = synth.fp16_normal((NKV, pos, HD), "mr-v", n)
@@ -74,14 +81,19 @@ def test_multi_row_layer_q4(oracle_mod, q4_small, n):
     om = oracle_mod.OracleModel(q4_small, 256)
     om.kv(1, 0)[:, :pos] = kc
     om.kv(1, 1)[:, :pos] = vc
-    ref = om.layer(1, x, pos)
+    ref, ref_qkv, _, _ = om.layer_taps(1, x, pos)
     with Engine(flags=0, image=q4_small, max_context=256) as e:
         e.write_kv(1, 0, 0, kc)
         e.write_kv(1, 1, 0, vc)
         got = e.layer_step(1, x, pos)
+        qkv = e.read_buffer("qkv")[:n]
         gk = e.read_kv(1, 0, pos, n)
-    assert rel_err(got, ref) < 2e-5, rel_err(got, ref)
+        gv = e.read_kv(1, 1, pos, n)
+    assert rel_err(qkv, ref_qkv) < 1e-6, rel_err(qkv, ref_qkv)
     _fp16_close(gk, om.kv(1, 0)[:, pos:pos + n])
+    _fp16_close(gv, om.kv(1, 1)[:, pos:pos + n])
+    print(f"n {n}: q|k|v rel err {rel_err(qkv, ref_qkv):.3g}, layer output {rel_err(got, ref):.3g}")
+    assert rel_err(got, ref) < 2e-4, rel_err(got, ref)
 
 
 @pytest.mark.parametrize("fmt_name", ["q4", "q8"])
@@ -194,7 +206,12 @@ def test_verify_is_deterministic_across_replays(fmt):
 @pytest.mark.parametrize("fmt", [WeightFormat.Q4, WeightFormat.Q8])
 def test_layer_stages(oracle_mod, fmt):
     """Stage-by-stage parity of one layer pass (3 rows over 29 prior slots): raw QKV rows,
-    attention output, SwiGLU output and the residual."""
+    the pass's K/V cache rows, attention output, SwiGLU output and the residual.
+
+    The QKV rows are compared before any rounding (2e-6 of their largest magnitude).  The stages
+    after them see the pass's K/V rows rounded to fp16, where a value within 1e-7 of a rounding
+    boundary may land on the other side (one ulp, ~5e-4 of the value; the cache rows are checked
+    to that bound), so they are held to 1e-4, still 100 times finer than the stated 1e-2."""
     img = synth.build_model_image(fmt, n_layers=1, tag=f"stages{fmt}")
     pos, n = 29, 3
     kc = synth.fp16_normal((NKV, pos, HD), "st-k")
@@ -211,6 +228,10 @@ def test_layer_stages(oracle_mod, fmt):
         qkv = e.read_buffer("qkv", n)
         att = e.read_buffer("attn", n)
         act = e.read_buffer("mlp", n)
+        gk = e.read_kv(0, 0, pos, n)
+        gv = e.read_kv(0, 1, pos, n)
+    _fp16_close(gk, om.kv(0, 0)[:, pos:pos + n])
+    _fp16_close(gv, om.kv(0, 1)[:, pos:pos + n])
     errs = {
         "qkv": rel_err(qkv, ref_qkv),
         "attn": rel_err(att, ref_att),
@@ -219,6 +240,6 @@ def test_layer_stages(oracle_mod, fmt):
     }
     print(fmt, {k: f"{v:.3g}" for k, v in errs.items()})
     assert errs["qkv"] < 2e-6
-    assert errs["attn"] < 1e-5
-    assert errs["mlp"] < 1e-5
-    assert errs["x"] < 1e-5
+    assert errs["attn"] < 1e-4
+    assert errs["mlp"] < 1e-4
+    assert errs["x"] < 1e-4
