@@ -260,8 +260,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
     const uint16_t* kbase = a.kc + (size_t)g * maxctx * HD;
     const uint16_t* vbase = a.vc + (size_t)g * maxctx * HD;
 
-    // Prior keys of block b: K row tid / 4, dims 32 (tid % 4) .. + 31; V keys 4 (tid / 32) + i
-    // (+ 32), dims 4 (tid % 32) .. + 3, transposed in registers.  Two register sets: block b + 2
+    // Prior keys of block b: K rows 16 wave + 4 i + lane / 16, dims 8 (lane % 16) .. + 7 (each
+    // load instruction reads four whole rows, 1 KiB contiguous); V keys 4 (tid / 32) + i (+ 32),
+    // dims 4 (tid % 32) .. + 3, transposed in registers.  Two register sets: block b + 2
     // is requested while block b + 1 waits in registers and block b is in LDS.  Buffer loads over
     // this group's cache rows: rows past the split are cache rows too (finite; their scores are
     // masked and their weights are 0), rows past the cache and blocks past the split read zeros
@@ -277,9 +278,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
 #define VA_GLOAD(set_, b_)                                                                            \
     do {                                                                                              \
         const bool in_ = (b_) < nblk;                                                                 \
-        const uint32_t kb_ = in_ ? (uint32_t)(((lrow0 + 64 * (b_) + (tid >> 2)) * HD + 32 * (tid & 3)) * 2) : 0x80000000u; \
+        const uint32_t kb_ = in_ ? (uint32_t)(((lrow0 + 64 * (b_) + 16 * wave + (lane >> 4)) * HD + 8 * (lane & 15)) * 2) : 0x80000000u; \
         _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                 \
-            kr[set_][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kb_ + 16 * i, 0, 0)); \
+            kr[set_][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kb_ + 4 * i * HD * 2, 0, 0)); \
         const uint32_t vb_ = in_ ? (uint32_t)(((lrow0 + 64 * (b_) + 4 * (tid >> 5)) * HD + 4 * (tid & 31)) * 2) : 0x80000000u; \
         _Pragma("unroll") for (int h = 0; h < 2; ++h)                                                 \
             _Pragma("unroll") for (int i = 0; i < 4; ++i)                                             \
@@ -290,8 +291,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_mfma_kernel(AttnArgs a)
     do {                                                                                              \
         uint16_t* Ks_ = (uint16_t*)(kv_lds + (buf_) * BUF);                                           \
         uint16_t* Vt_ = (uint16_t*)(kv_lds + (buf_) * BUF + KS_BYTES);                                \
-        uint4* kd_ = (uint4*)(Ks_ + (tid >> 2) * VA_KROW + 32 * (tid & 3));                           \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) kd_[i] = kr[set_][i];                           \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                 \
+            *(uint4*)(Ks_ + (16 * wave + 4 * i + (lane >> 4)) * VA_KROW + 8 * (lane & 15)) = kr[set_][i]; \
         const int d0_ = 4 * (tid & 31);                                                               \
         _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                               \
             const int k0_ = 32 * h + 4 * (tid >> 5);                                                  \
