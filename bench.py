@@ -231,7 +231,7 @@ def run_verify(K, W):
         "metric": "speculative verify passes/s (q8 28-layer decoder, 8 drafts, 8192 ctx)",
         "value": round(1.0 / dt, 2), "unit": "passes/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q8 weights, int codes x fp activations, fp32 accumulate, fp16 KV",
+        "dtype": "q8 weights as exact fp16 codes x fp16 hi+lo activation parts, fp32 accumulate, fp16 KV",
         "data": "synthetic (seeded random-init q8 weights, fp16 N(0,1) cache rows, random draft ids)",
         "config": {"workload": "28-layer q8 g32 decoder, one pass of 8 draft tokens over 8192 cache rows",
                    "context": VERIFY_CTX, "drafts": VERIFY_M},
