@@ -96,6 +96,34 @@ def test_multi_row_layer_q4(oracle_mod, q4_small, n):
     assert rel_err(got, ref) < 2e-4, rel_err(got, ref)
 
 
+@pytest.mark.parametrize("pos,n", [(0, 8), (64, 3), (1000, 8), (4500, 8)])
+def test_multi_row_attention_positions(oracle_mod, q4_small, pos, n):
+    """Multi-row passes at cache positions that exercise the matrix-core attention's split
+    layout: no prior rows (every prior split empty), one whole 64-row block, 16 blocks with a
+    partial last one, and 71 blocks dealt to 63 splits (some take two, the last block partial).
+    Bounds as in test_multi_row_layer_q4."""
+    kc = synth.fp16_normal((NKV, pos, HD), "ap-k", pos)
+    vc = synth.fp16_normal((NKV, pos, HD), "ap-v", pos)
+    x = synth.fp16_normal((n, Dims.hidden), "ap-x", pos).astype(np.float32)
+    om = oracle_mod.OracleModel(q4_small, pos + 16)
+    om.kv(1, 0)[:, :pos] = kc
+    om.kv(1, 1)[:, :pos] = vc
+    ref, ref_qkv, _, _ = om.layer_taps(1, x, pos)
+    with Engine(flags=0, image=q4_small, max_context=pos + 16) as e:
+        if pos:
+            e.write_kv(1, 0, 0, kc)
+            e.write_kv(1, 1, 0, vc)
+        got = e.layer_step(1, x, pos)
+        qkv = e.read_buffer("qkv")[:n]
+        gk = e.read_kv(1, 0, pos, n)
+        gv = e.read_kv(1, 1, pos, n)
+    assert rel_err(qkv, ref_qkv) < 1e-6, rel_err(qkv, ref_qkv)
+    _fp16_close(gk, om.kv(1, 0)[:, pos:pos + n])
+    _fp16_close(gv, om.kv(1, 1)[:, pos:pos + n])
+    print(f"pos {pos} n {n}: layer output rel err {rel_err(got, ref):.3g}")
+    assert rel_err(got, ref) < 2e-4, rel_err(got, ref)
+
+
 @pytest.mark.parametrize("fmt_name", ["q4", "q8"])
 def test_greedy_decode_small(oracle_mod, q4_small, q8_small, fmt_name):
     img = q4_small if fmt_name == "q4" else q8_small
