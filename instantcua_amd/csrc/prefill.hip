@@ -11,9 +11,9 @@
 // keeps every part that matters far above the fp16 subnormal range).  The GEMM runs
 // v_mfma_f32_16x16x32_f16 on (hi, lo) x the weights as fp16 B operands: the q4 and q8 integer
 // codes are exact in fp16, so each group's sum C_g = sum_k q_k x''_k comes out of one
-// accumulator chain; the group epilogue is acc += s C_g + b X_g (q4, X_g = sum_k x''_k) or
-// acc += s C_g (q8), f16 weights accumulate directly, and the row scale 2^(E_t - 14) is
-// applied once at the end.
+// accumulator chain; the group epilogue is acc += s C_g (q4 and q8: the q4 bias term
+// sum_g b_g X_g, X_g = sum_k x''_k, runs on the matrix cores once per tile before the loop),
+// f16 weights accumulate directly, and the row scale 2^(E_t - 14) is applied once at the end.
 //
 // Attention.  Causal GQA flash attention on v_mfma_f32_16x16x32_f16: scores are computed
 // transposed (S^T = K Q^T) so that the probabilities come out of the accumulator already in
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     const uint32_t* vsrc = tid < 256 ? (const uint32_t*)a.sb + (size_t)(tn * 128 + (vj & 127)) * NG + (vj >> 7)
                                      : (const uint32_t*)a.xs + ((size_t)(tm * 8 + (vj >> 5)) * NG + ((vj >> 4) & 1)) * 16 + (vj & 15);
     const int vstride = tid < 256 ? 2 : 32;
-    const bool vload = FMT != FMT_F16 || tid >= 256;
+    const bool vload = FMT != FMT_F16 && tid < 256;  // (the group sums of the upper half go unused)
 
     f32x4 acc[2][4];
 #pragma unroll
@@ -281,9 +281,6 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
             }
             return;
         }
-        f32x4 xg[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) xg[i] = *(const f32x4*)&Vs[b][256 + (2 * (wave & 3) + i) * 32 + gg * 16 + 4 * q];
         f32x4 C[4][2];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -307,8 +304,8 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (FMT == FMT_F16)
                         acc[i][r][e] += C[r][i][e];
-                    else
-                        acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], fmaf(sb[r].y, xg[i][e], acc[i][r][e]));
+                    else  // q4: the bias term sum_g b_g X_g went in before the loop
+                        acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], acc[i][r][e]);
                 }
             }
     };
@@ -317,6 +314,45 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     // register copy waits on an outstanding load.
     aload(0, Ae);
     wload(0);
+    if constexpr (FMT == FMT_Q4) {
+        // The q4 bias term sum_g b_g X_g of every output, on the matrix cores before the loop:
+        // per 32 groups, A = the token block's group sums X (scaled by 2^-8 into fp16 range,
+        // hi + lo parts) and B = the rows' fp16 biases, exact.  The loop's group epilogue is then
+        // one fma per output (acc += s C_g).
+#pragma unroll 1
+        for (int cg = 0; cg < NG / 32; ++cg) {
+            v8h Xh[2], Xl[2], Bb[4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float* xp = a.xs + ((size_t)(tb0 + i) * NG + 32 * cg + 8 * q) * 16 + r16;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float x = xp[16 * j] * 0.00390625f;  // 2^-8: a group sum of 64 values below 2^15
+                    const f16 hx = (f16)x;
+                    Xh[i][j] = hx;
+                    Xl[i][j] = (f16)(x - (float)hx);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint4* bp = (const uint4*)((const uint32_t*)a.sb + (size_t)(tn * 128 + (rb0 + r) * 16 + r16) * NG + 32 * cg + 8 * q);
+                const uint4 w0 = bp[0], w1 = bp[1];
+                const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) Bb[r][j] = as_h2(wv[j]).y;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    f32x4 B = f32x4{0.f, 0.f, 0.f, 0.f};
+                    B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xh[i], Bb[r], B, 0, 0, 0);
+                    B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xl[i], Bb[r], B, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(256.f, B[e], acc[i][r][e]);
+                }
+        }
+    }
     lstore(0);
     __syncthreads();
     for (int c = 0; c < NC; ++c) {
