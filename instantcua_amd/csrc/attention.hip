@@ -211,11 +211,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a) {
 
 }
 
-// Multi-row passes (verify, short prompts) on the matrix cores.  Grid (NKV, NS), NS <= 64: the
-// prior slots' 64-slot blocks are dealt evenly to splits 0 .. NS - 2 (two or three blocks each
-// at 8192 slots, double-buffered through LDS) and split NS - 1 takes the pass's new rows; with
-// 80 KiB of LDS and 184 registers two workgroups share a CU, so the 8 x 64 grid runs in one
-// round with two waves per SIMD, and the tail splits, dispatched last, are the short ones.  The 16 (token, head) rows of a KV group, column c = 2 t + head, are the B operand of
+// Multi-row passes (verify, short prompts) on the matrix cores.  Grid (NKV, NS), NS <= 32: the
+// prior slots' 64-slot blocks are dealt evenly to splits 0 .. NS - 2 (four or five blocks each
+// at 8192 slots, double-buffered through LDS) and split NS - 1 takes the pass's new rows; the
+// 8 x 32 grid is one workgroup per CU (80 KiB of LDS and 236 registers would let two share one),
+// and the tail splits, dispatched last, are the short ones.  (16 and 64 splits per group
+// measured 3-4 % slower per verify pass, counting the merge.)  The 16 (token, head) rows of a KV group, column c = 2 t + head, are the B operand of
 // S^T = K . Q^T (v_mfma_f32_16x16x32_f16, q split into fp16 hi + lo parts); wave w scores keys
 // 16 w .. 16 w + 15 of each block, and its accumulator (lane l: keys 4 (l / 16) + i, column
 // l % 16) is directly the B operand of O^T = V^T . P^T (v_mfma_f32_16x16x16_f16, P split hi + lo)
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(AttnArgs a) {
 // (m, l, o) are combined into the partial that the merge kernel reads.  Masked keys (past the
 // split's cache rows, or later tokens of the pass in the tail split) hold finite rows, so p = 0
 // contributes exactly nothing.
-constexpr int VA_SPLITS = 64;                             // splits of a group (at most)
+constexpr int VA_SPLITS = 32;                             // splits of a group (at most)
 constexpr int VA_KROW = 136, VA_VROW = 72, VA_QROW = 136;  // padded LDS rows (halves)
 // Column (halves) of key `key` in V^T row `row`: 4-key chunks XOR-swizzled by (row / 8) % 8, so
 // the staging writes (lane l of a half-wave: rows 4 l + j, one chunk) and the P.V reads (16
