@@ -141,10 +141,9 @@ def cpu_rows(budget_s=6.0):
     return {"cores": oracle.get_threads(), "kind": "port", "precision": "fp64 accumulation", "rows": rows}
 
 
-def run_q8_prefill():
+def run_q8_prefill(img):
     """The 4096-row vision-shaped prefill of the decode workload on the 28-layer q8 group-32
     decoder (the matrix-core GEMMs on q8 codes)."""
-    img = synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="bench-q8")
     vp = synth.visual_prompt(PREFILL, VIS_OFFSET, LLM_H, LLM_W, tag="bench-vis")
     e = eng.Engine(flags=0, image=img, max_context=PREFILL + 16, max_steps=4)
     e.prepare_mrope(VIS_OFFSET, LLM_H, LLM_W)
@@ -205,10 +204,11 @@ def verify_bytes_per_pass() -> int:
     return weight_bytes_per_token(WeightFormat.Q8) + kv_bytes_per_token(VERIFY_CTX)
 
 
-def run_verify(K, W):
+def run_verify(K, W, img=None):
     """K timed verify passes (each: 8 draft rows at slots 8192..8199, per-row argmax) of the
     28-layer q8 decoder over 8192 cache rows of fp16 N(0, 1)."""
-    img = synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="bench-q8")
+    if img is None:
+        img = synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="bench-q8")
     e = eng.Engine(image=img, max_context=VERIFY_CTX + VERIFY_M + 8, max_steps=8)
     for l in range(LAYERS):
         for kind in (0, 1):
@@ -496,7 +496,14 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(img, PREFILL)
     rows = None if args.no_cpu else cpu_rows()
     del img
-    q8 = None if args.no_prefill else run_q8_prefill()
+    q8 = ver = None
+    if not args.no_prefill:
+        img8 = synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="bench-q8")
+        q8 = run_q8_prefill(img8)
+        v = run_verify(10, 2, img8)  # the verify workload (--workload verify), a short run
+        ver = {"workload": v["config"]["workload"], "ms_per_pass": v["ms_per_step"], "passes_s": v["value"],
+               "roofline_frac": v["roofline"]["frac"], "GB_s": v["roofline"]["achieved"]}
+        del img8
 
     out = {
         "metric": "decode tok/s @bs1 (q4 2B VL decoder, 4k ctx)",
@@ -535,6 +542,7 @@ def main():
         "cpu_rows": rows,
         "text_context_1024": text,
         "prefill_q8_4096": q8,
+        "verify_q8_8192": ver,
     }
     print(json.dumps(out))
 
