@@ -17,7 +17,9 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/icua.h"
@@ -103,6 +105,35 @@ int null_state(State** out, int n) {
 
 }  // namespace
 
+// Packet areas of the persistent decode kernel live in uncached device memory: its all-to-all
+// exchanges (device-scope stores polled by device-scope loads, 256 workgroups) complete about
+// 10 % sooner there than in cached memory (2.28 against 2.55 us per round idle, 5.06 against
+// 5.53 us with 64 KiB of loads in flight per CU).  Uncached memory that a kernel has read is
+// never handed back to the allocator while the process runs: an engine returns its area to this
+// per-device pool, and the next engine created on that device takes it again.
+namespace {
+std::mutex g_sync_mu;
+std::vector<std::pair<int, void*>> g_sync_pool;  // (device, area), all persistent_sync_bytes() long
+}  // namespace
+
+static hipError_t take_sync_area(int dev, void** out) {
+    {
+        std::lock_guard<std::mutex> lk(g_sync_mu);
+        for (size_t i = 0; i < g_sync_pool.size(); ++i)
+            if (g_sync_pool[i].first == dev) {
+                *out = g_sync_pool[i].second;
+                g_sync_pool.erase(g_sync_pool.begin() + (long)i);
+                return hipSuccess;
+            }
+    }
+    return hipExtMallocWithFlags(out, persistent_sync_bytes(), hipDeviceMallocUncached);
+}
+
+static void return_sync_area(int dev, void* p) {
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    g_sync_pool.emplace_back(dev, p);
+}
+
 struct icua_engine {
     int fmt = 0, layers = 0, maxctx = 0, maxpass = 0, maxsteps = 0;
     uint32_t flags = 0;
@@ -134,8 +165,10 @@ struct icua_engine {
     std::vector<int32_t> cached_prefix;
     int mrope_key[3] = {-999, 0, 0};
     int last_logits_rows = 0;
-    // Persistent decode kernel: counter block and availability; whether the last decode call used it.
+    // Persistent decode kernel: packet area (from the uncached pool, on device psync_dev) and
+    // availability; whether the last decode call used it.
     unsigned* psync = nullptr;
+    int psync_dev = -1;
     bool last_persistent = false;
     bool persist_ok = false;
     // Matrix-core prefill buffers for chunks of up to pf_cap rows (allocated on first use).
@@ -647,7 +680,8 @@ struct icua_engine {
         HIPCK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
         HIPCK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         if (!coop || cus < PERSIST_WGS) return 0;
-        HIPCK(hipMalloc(&psync, persistent_sync_bytes()));
+        HIPCK(take_sync_area(dev, (void**)&psync));
+        psync_dev = dev;
         persist_ok = true;
         return 0;
     }
@@ -950,7 +984,8 @@ void icua_engine_destroy(icua_engine* e) {
         if (g) (void)hipGraphExecDestroy(g);
     void* bufs[] = {e->d_weights, e->x, e->qkv, e->attn, e->h, e->kv, e->rope, e->part, e->counters, e->kpart, e->kcnt, e->apre, e->fxpre, e->pval,
                     e->pidx, e->logits, e->out_tokens, e->prompt, e->argmax_rows, e->st, e->pooler,
-                    e->ds[0], e->ds[1], e->ds[2], e->psync, e->d_vision, e->vbuf};
+                    e->ds[0], e->ds[1], e->ds[2], e->d_vision, e->vbuf};
+    if (e->psync) return_sync_area(e->psync_dev, e->psync);
     e->free_pf();
     for (void* b : bufs)
         if (b) (void)hipFree(b);
