@@ -124,6 +124,17 @@ __device__ __forceinline__ float hi_of(uint64_t p) { return as_f32((uint32_t)(p 
 // 2^x (v_exp_f32): the persistent attention keeps scores in base-2 units.
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Lane pair swaps by DPP (a VALU move, no LDS round trip): lane l receives lane l ^ 1; and, within
+// each row of 16 lanes, lanes 0-7 receive lanes 8-15 and back (rotate by 8).
+__device__ __forceinline__ float xor1(float v) { return dpp<DPP_XOR1>(v); }
+__device__ __forceinline__ float xor8(float v) { return dpp<0x128>(v); }
+
+// SwiGLU of a gate / up pair: g sigmoid(g) u, with 2^x and the reciprocal on the transcendental
+// unit (each ~1 ulp).
+__device__ __forceinline__ float swiglu(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.f + ex2(-g * 1.4426950408889634f)) * u;
+}
+
 // 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l
 // (lds is wave-uniform).  Counted by the issuing wave's vector-memory counter.
 __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
@@ -690,6 +701,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 if (!qkv_wg) {
                     wx[0].load(P.wo, P.wo_sb, w, H, mw, lane);
                     load_kv_rows(kr, vr, kb, vb, j0, nprior, quad, ql);
+                    // The lower down half-block of row block w into LDS: it lands long before the
+                    // x' poll that a later request would delay.
+                    wd_request<FMT>(wdb, P.wd, P.wd_sb, w, 0, mw, lane);
                 }
                 const float* rope = a.rope + (size_t)pos * 128;
                 qn0 = P.q_norm[lane];
@@ -711,7 +725,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     const float rs = norm_scale<H>(S);
                     y[0] *= rs;
                     y[1] *= rs;
-                    const float n0 = __shfl_xor(y[0], 1), n1 = __shfl_xor(y[1], 1);
+                    const float n0 = xor1(y[0]), n1 = xor1(y[1]);
                     if (lane < 16 && !(lane & 1)) {
                         st64(ll + QKVP + (w - NWG / 2) * 8 + lane / 2, pack2(y[0], n0, r + 1));
                         st64(ll + QKVP + w * 8 + lane / 2, pack2(y[1], n1, r + 1));
@@ -910,7 +924,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         lsum = fmaf(S.misc[18 + 4 * ww + hh], f, lsum);
                     }
                     // o pairs (even lanes), then (l, m) with the maximum exact.
-                    const float acc_n = __shfl_xor(acc, 1);
+                    const float acc_n = xor1(acc);
                     if (!(d & 1)) st64(part + hh * PART2 + d / 2, pack2(acc, acc_n, r + 1));
                     if (d == 0) st64(part + hh * PART2 + HD / 2, pack2(lsum, mx, r + 1));
                 }
@@ -964,7 +978,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         float t = 0.f;
 #pragma unroll
                         for (int qq = 0; qq < 8; ++qq) t += q8[qq * 64 + tid];
-                        const float v = t * S.misc[0], vn = __shfl_xor(v, 1);
+                        const float v = t * S.misc[0], vn = xor1(v);
                         if (!(tid & 1)) st64(ll + ATTNP + ((2 * g + hh) * HD + d0 + tid) / 2, pack2(v, vn, r + 1));
                     }
                 }
@@ -1000,7 +1014,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 const float y = reduce_math<MATH>(S, acc1[0]);
                 if (wave == 0) {  // the owner keeps the residual as published (even rows rounded)
                     const float xn = lane < 16 ? (S.xown[lane] + S.xhi[lane]) + y : 0.f;
-                    const float xo = __shfl_xor(xn, 1);
+                    const float xo = xor1(xn);
                     if (lane < 16) {
                         S.xown[lane] = (lane & 1) ? xn : q19(xn);
                         if (!(lane & 1)) st64(ll + XP + w * 8 + lane / 2, pack2(xn, xo, 2 * r + 1));
@@ -1008,9 +1022,19 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 }
                 PK_TRACE(l, 8);
             }
-            // This layer's down half-block streams into LDS while the gate|up input is awaited
-            // and during gate|up (the math waves would otherwise idle at the next barrier).
-            if (math) wd_request<FMT>(wdb, P.wd, P.wd_sb, w % (NWG / 2), w / (NWG / 2), mw, lane);
+            // Workgroups 128..255 request the upper down half-block and the next layer's QKV
+            // blocks here, where they wait for no stage input (workgroups 0..127 run O): loads
+            // issued later would queue ahead of their x' and h polls.
+            if (math && qkv_wg) {
+                wd_request<FMT>(wdb, P.wd, P.wd_sb, w - NWG / 2, 1, mw, lane);
+                wx[0].forget();
+                wx[1].forget();
+                if (l + 1 < L) {
+                    const LayerPtrs& Pn = a.layers[l + 1];
+                    wx[0].load(Pn.wqkv, Pn.wqkv_sb, w - NWG / 2, H, mw, lane);
+                    wx[1].load(Pn.wqkv, Pn.wqkv_sb, w, H, mw, lane);
+                }
+            }
 
             // ---------------- RMSNorm + gate|up + SwiGLU: blocks 3w .. 3w + 2 --------------
             {
@@ -1036,8 +1060,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     for (int j = 0; j < 3; ++j) {
                         // Block 3w + j: gate units 8 (3w + j) + 0..7 in lanes 0-7, their up rows in 8-15.
                         y[j] *= rs;
-                        const float up = __shfl_xor(y[j], 8);
-                        const float hv = (y[j] / (1.f + expf(-y[j]))) * up, hn = __shfl_xor(hv, 1);
+                        const float hv = swiglu(y[j], xor8(y[j])), hn = xor1(hv);
                         if (lane < 8 && !(lane & 1)) st64(ll + HP + (3 * w + j) * 4 + lane / 2, pack2(hv, hn, r + 1));
                     }
                 }
@@ -1049,14 +1072,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 const int rb = w % (NWG / 2), half = w / (NWG / 2);
                 bool ok = true;
                 if (!math) ok = poll_vec<FFH / 2 / CT>(ll + HP + half * (FFH / 2), FFH / 2, r + 1, S.vec, err);
-                if (math) {
+                if (math && !qkv_wg) {
                     wx[0].forget();
                     wx[1].forget();
-                }
-                if (math && qkv_wg && l + 1 < L) {  // the next layer's QKV blocks
-                    const LayerPtrs& Pn = a.layers[l + 1];
-                    wx[0].load(Pn.wqkv, Pn.wqkv_sb, w - NWG / 2, H, mw, lane);
-                    wx[1].load(Pn.wqkv, Pn.wqkv_sb, w, H, mw, lane);
                 }
                 if (__syncthreads_or(!ok)) return;
                 PK_TRACE_X(l, 11);
@@ -1076,7 +1094,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE(l, 19);
                 if (wave == 0) {
                     const float v = lane < 16 ? (half == 0 ? S.xown[lane] + y : y) : 0.f;
-                    const float vn = __shfl_xor(v, 1);
+                    const float vn = xor1(v);
                     if (lane < 16) {
                         if (half == 0) S.xown[lane] = (lane & 1) ? v : q19(v);
                         if (!(lane & 1)) st64(ll + (half == 0 ? XP : XDP) + rb * 8 + lane / 2, pack2(v, vn, 2 * r + 2));
