@@ -252,7 +252,17 @@ struct Shared {
     float ored[MW][2][HD];
     float misc[64];
     int imisc[64];
+    int fail;                 // a wait of this workgroup failed (set only then; see sync_failed)
 };
+
+// Workgroup barrier that also tells every thread whether any thread's wait failed.  The flag is
+// written only on failure, so the common path is one barrier and one LDS read (the library's
+// __syncthreads_or costs three barriers and three LDS operations).
+__device__ __forceinline__ bool sync_failed(Shared& S, bool failed) {
+    if (failed) S.fail = 1;
+    __syncthreads();
+    return S.fail != 0;
+}
 
 // ------------------------------------------------------------------------------------------
 // Staging by the whole workgroup: units of 4 consecutive activations (u = tid + THREADS * j <
@@ -714,7 +724,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 rs = rope[2 * lane + 1];
                 load_norm8(nreg, P.mlp_norm + tid * 8);
             }
-            if (__syncthreads_or(!ok_in)) return;
+            if (sync_failed(S, !ok_in)) return;
             PK_TRACE_X(l, 1);
             if (qkv_wg) {
                 stage_c<FMT, H>(S, l == 0 ? S.emb : S.vec, true);
@@ -748,7 +758,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                                                             : H + NKV * HD + g * HD + (e - 3 * HD)) / 2;
                         },
                         r + 1, S.vec, err);
-                if (__syncthreads_or(!ok)) return;
+                if (sync_failed(S, !ok)) return;
             }
             PK_TRACE_X(l, 3);
             if (math) {
@@ -948,7 +958,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                             return (sj * 2 + hh) * PART2 + (e < 32 ? d0 / 2 + e : HD / 2);
                         },
                         r + 1, pl, err);
-                if (__syncthreads_or(!ok)) return;
+                if (sync_failed(S, !ok)) return;
                 PK_TRACE_X(l, 5);
                 // Split weights exp(m_s - max) and the normaliser (math wave 0, one lane per split).
                 if (math && wave == 0) {
@@ -1004,7 +1014,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
 #pragma unroll
                     for (int j = 0; j < 3; ++j) wgu[j].load(P.wgu, P.wgu_sb, 3 * w + j, H, mw, lane);
                 }
-                if (w < H / 16 && __syncthreads_or(!ok)) return;
+                if (w < H / 16 && sync_failed(S, !ok)) return;
             }
             if (w < H / 16) {
                 PK_TRACE_X(l, 7);
@@ -1046,7 +1056,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     // The next layer's attention norm, or the final norm.
                     load_norm8(nreg, (l + 1 < L ? a.layers[l + 1].attn_norm : a.final_norm) + tid * 8);
                 }
-                if (__syncthreads_or(!ok)) return;
+                if (sync_failed(S, !ok)) return;
                 PK_TRACE_X(l, 9);
                 stage_c<FMT, H>(S, S.vec, true);
                 PK_TRACE(l, 13);
@@ -1076,7 +1086,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     wx[0].forget();
                     wx[1].forget();
                 }
-                if (__syncthreads_or(!ok)) return;
+                if (sync_failed(S, !ok)) return;
                 PK_TRACE_X(l, 11);
                 stage_c<FMT, FFH>(S, S.vec, false);
                 PK_TRACE(l, 18);
@@ -1144,7 +1154,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             }
 #pragma unroll
             for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
-            if (__syncthreads_or(!ok)) return;
+            if (sync_failed(S, !ok)) return;
             PK_TRACE_X(L, 1);
             stage_c<FMT, H>(S, S.vec, true);
             float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
@@ -1202,7 +1212,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             const int tid = my_tid(), lane = tid % 64, wave = wave_id();
             bool ok = true;
             if (!MATH) ok = poll_vec<NWG / CT>(ll + LMP, NWG, (unsigned)step + 1, S.vec, err);
-            if (__syncthreads_or(!ok)) return;
+            if (sync_failed(S, !ok)) return;
             PK_TRACE_X(L, 3);
             float bv = -__builtin_inff();
             int bi = 0x7fffffff;
@@ -1329,6 +1339,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     __shared__ __align__(16) uint8_t wdb[WD_CODES + WD_SB];
     const int w = blockIdx.x;
     if (my_tid() < 4) S.zero[my_tid()] = 0u;
+    if (my_tid() == 0) S.fail = 0;
     // Control block and the embedding of the first token (written before this launch).
     const State* st = a.st;
     if (st->done || st->n < 1 || st->n > 2) return;  // a single row, or a forced pair (checked by the host too)
