@@ -95,9 +95,10 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
     v = fmaxf(v, dpp<DPP_XOR2>(v));
     v = fmaxf(v, dpp<DPP_XOR1>(v));
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
+    auto r = __builtin_amdgcn_permlane16_swap(as_u32(v), as_u32(v), false, false);
+    v = fmaxf(as_f32(r[0]), as_f32(r[1]));
+    auto q = __builtin_amdgcn_permlane32_swap(as_u32(v), as_u32(v), false, false);
+    return fmaxf(as_f32(q[0]), as_f32(q[1]));
 }
 
 // Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (every lane gets the result).
@@ -160,13 +161,28 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi)
         i = oi;
     }
 }
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
+    argmax_merge(v, i, dpp<CTRL>(v), dpp_i<CTRL>(i));
+}
+// Every lane gets the wave's (value, index) argmax: a butterfly of DPP moves within rows of 16
+// and two lane-swap steps across rows (no LDS round trips).  argmax_merge is symmetric, so the
+// order in which a swap returns the two lanes' pairs does not matter.
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        float ov = __shfl_xor(v, m);
-        int oi = __shfl_xor(i, m);
-        argmax_merge(v, i, ov, oi);
-    }
+    argmax_dpp<DPP_XOR1>(v, i);
+    argmax_dpp<DPP_XOR2>(v, i);
+    argmax_dpp<DPP_HALF_MIRROR>(v, i);
+    argmax_dpp<DPP_MIRROR>(v, i);
+    auto rv = __builtin_amdgcn_permlane16_swap(as_u32(v), as_u32(v), false, false);
+    auto ri = __builtin_amdgcn_permlane16_swap((uint32_t)i, (uint32_t)i, false, false);
+    v = as_f32(rv[0]);
+    i = (int)ri[0];
+    argmax_merge(v, i, as_f32(rv[1]), (int)ri[1]);
+    auto qv = __builtin_amdgcn_permlane32_swap(as_u32(v), as_u32(v), false, false);
+    auto qi = __builtin_amdgcn_permlane32_swap((uint32_t)i, (uint32_t)i, false, false);
+    v = as_f32(qv[0]);
+    i = (int)qi[0];
+    argmax_merge(v, i, as_f32(qv[1]), (int)qi[1]);
 }
 
 // ------------------------------------------------------------------------------------------

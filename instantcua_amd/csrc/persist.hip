@@ -1152,9 +1152,17 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
             }
+            // The exchange waves request their blocks once x is in; the math waves' requests
+            // also wait for the barrier, so that no bulk load queues ahead of the x poll.
+            if (!math) {
 #pragma unroll
-            for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
+                for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
+            }
             if (sync_failed(S, !ok)) return;
+            if (math) {
+#pragma unroll
+                for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
+            }
             PK_TRACE_X(L, 1);
             stage_c<FMT, H>(S, S.vec, true);
             float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
