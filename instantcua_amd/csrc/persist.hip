@@ -1169,20 +1169,22 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             QuadOps<FMT> lq[CW8 / 2];  // this wave's operand quads, the same for every block
 #pragma unroll
             for (int p = 0; p < CW8 / 2; ++p) lq[p] = quad_load<FMT>(S, wave * CW8 + 2 * p, lane);
+            // Every iteration issues the same refill (past the matrix it re-reads the last row
+            // block, an L2 hit, and the sums of blocks past the matrix are dropped): with the
+            // same loads on every path the compiler's waits stay exact, instead of draining every
+            // block in flight before each block's scales are used.
             for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
 #pragma unroll
                 for (int k = 0; k < LM_DEPTH; ++k) {
                     const int kb = k0 + k, rb = w + kb * NWG;
-                    if (rb < NRB) {
-                        float y = 0.f;
+                    float y = 0.f;
 #pragma unroll
-                        for (int p = 0; p < CW8 / 2; ++p)
-                            y = quad_scale<FMT>(lq[p], quad_mfma<FMT>(lq[p], wl[k].wv[2 * p], wl[k].wv[2 * p + 1]),
-                                                wl[k].sq[p], y);
-                        y = quad_rows(y);
-                        if (lane < 16) plm[(kb * WAVES + wave) * 16 + lane] = y;
-                        if (rb + LM_DEPTH * NWG < NRB) wl[k].load(a.E, a.Esb, rb + LM_DEPTH * NWG, H, wave, lane);
-                    }
+                    for (int p = 0; p < CW8 / 2; ++p)
+                        y = quad_scale<FMT>(lq[p], quad_mfma<FMT>(lq[p], wl[k].wv[2 * p], wl[k].wv[2 * p + 1]),
+                                            wl[k].sq[p], y);
+                    y = quad_rows(y);
+                    if (rb < NRB && lane < 16) plm[(kb * WAVES + wave) * 16 + lane] = y;
+                    wl[k].load(a.E, a.Esb, min(rb + LM_DEPTH * NWG, NRB - 1), H, wave, lane);
                 }
             }
             __syncthreads();
