@@ -141,3 +141,39 @@ def test_context_limit_stop_matches_graph_path(images):
     s0, s1 = states
     assert s0["done"] == 1 and s0["pos"] == 23 and s0["step"] == 13, s0
     assert (s0["pos"], s0["step"], s0["done"]) == (s1["pos"], s1["step"], s1["done"])
+
+
+def test_engines_alive_together_and_in_turn(oracle_mod, images):
+    """Each engine's persistent launches use a packet area of their own: two engines decode in
+    interleaved calls, then a third created after both are gone (it takes a pooled area back)
+    decodes again, each against the oracle."""
+    steps = 8
+    prompts = {name: synth.random_tokens(13, "pool-" + name) for name in ("q4", "q8")}
+    refs = {}
+    for name, toks in prompts.items():
+        om = oracle_mod.OracleModel(images[name], 128)
+        refs[name] = om.generate(toks, steps)
+    engines = {name: Engine(flags=0, image=images[name], max_context=128, max_steps=steps) for name in prompts}
+    try:
+        for name, e in engines.items():
+            e.eos = (-1, -1)
+            e.prefill(prompts[name], max_new=steps)
+        for n in (3, 4):  # calls alternate between the two engines: 1 + 3 + 4 tokens each
+            for e in engines.values():
+                e.decode_steps(n)
+                assert e.last_decode_persistent
+        for name, e in engines.items():
+            st = e.state()
+            assert st["step"] == steps, st
+            ref, margins, first_logits = refs[name]
+            compare_greedy(e.tokens(steps), ref, margins, first_logits.max() * np.ones(steps))
+    finally:
+        for e in engines.values():
+            e.close()
+    with Engine(flags=0, image=images["q4"], max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.prefill(prompts["q4"], max_new=steps)
+        e.decode_steps(steps - 1)
+        assert e.last_decode_persistent
+        ref, margins, first_logits = refs["q4"]
+        compare_greedy(e.tokens(steps), ref, margins, first_logits.max() * np.ones(steps))
