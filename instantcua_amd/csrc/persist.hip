@@ -253,6 +253,7 @@ struct Shared {
     float misc[64];
     int imisc[64];
     int fail;                 // a wait of this workgroup failed (set only then; see sync_failed)
+    int go;                   // round whose split partials a watching lane has seen complete
 };
 
 // Workgroup barrier that also tells every thread whether any thread's wait failed.  The flag is
@@ -1001,6 +1002,33 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // The gate|up blocks are requested here, a stage early, by every workgroup.  The
             // residual of the O rows is xown (previous x + lower-half down sums) + xhi (the
             // upper-half sums, long published): the same two terms every x reader adds.
+            //
+            // Workgroups 128..223 (no O, no merge) request their next stages' weights only once
+            // their KV group's split partials are all out: issued as their attention ends, these
+            // ~10 MB would queue at the memory controllers ahead of the mergers' polls of those
+            // partials.  The last split to publish is the one holding the new cache row (it
+            // waits for that row's acknowledgement first); their math waves watch its (l, m)
+            // packet, and nothing else of theirs is in flight then.
+            if (math && w >= NWG / 2 && w < MERGER0) {
+                // One lane watches; the other math waves wait for it in LDS.
+                if (wave == 0 && lane == 0) {
+                    const int s_tail = min(pos / chunk, ATT_SPLITS - 1);
+                    const uint64_t* q = ll + PARTP + (size_t)(g * ATT_SPLITS + s_tail) * 2 * PART2 + HD / 2;
+                    const unsigned tg = tag4(r + 1);
+                    for (int it = 0;; ++it) {
+                        if (tag_of(ld64(q)) == tg) break;
+                        if (it >= SPIN_LIMIT) raise_err(err);
+                        if (it >= SPIN_LIMIT || ((it & 63) == 63 && load_err(err))) {
+                            S.fail = 1;  // the next barrier returns
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    __hip_atomic_store(&S.go, (int)r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                while (__hip_atomic_load(&S.go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (int)r + 1)
+                    __builtin_amdgcn_s_sleep(1);
+            }
             {
                 bool ok = true;
                 if (w < H / 16 && !math) {
@@ -1349,7 +1377,10 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     __shared__ __align__(16) uint8_t wdb[WD_CODES + WD_SB];
     const int w = blockIdx.x;
     if (my_tid() < 4) S.zero[my_tid()] = 0u;
-    if (my_tid() == 0) S.fail = 0;
+    if (my_tid() == 0) {
+        S.fail = 0;
+        S.go = 0;
+    }
     // Control block and the embedding of the first token (written before this launch).
     const State* st = a.st;
     if (st->done || st->n < 1 || st->n > 2) return;  // a single row, or a forced pair (checked by the host too)
