@@ -37,10 +37,12 @@
 // ... sc1: coherent across the XCDs' L2s without cache flushes).  The low word is value a rounded
 // to a 19-bit mantissa whose low 4 bits carry the tag of the round (1..15), the high word value b
 // exact.  The exchange waves read consecutive packets in consecutive lanes and poll until each
-// carries the tag of the round they expect, so the data is its own flag.  A buffer is rewritten
-// only after every consumer of its previous round has read it: each producer first consumes
-// outputs that, through the stage chain, every such consumer produced after its read.  The packet
-// area is zeroed before each launch and tags start at 1, so a tag never matches stale data.  The
+// carries the tag of the round they expect, so the data is its own flag.  The packet area is
+// uncached device memory (the engine's pool; its all-to-all exchanges measure faster there).  A
+// buffer is rewritten only after every consumer of its previous round has read it: each producer
+// first consumes outputs that, through the stage chain, every such consumer produced after its
+// read.  The packet area is zeroed before each launch and tags start at 1, so a tag never
+// matches stale data.  The
 // one value read with plain loads across workgroups is the new K/V cache row: it is stored
 // device-scope, acknowledged before the writer's next packet, first read a step later, and rows
 // >= pos are never loaded early (a line cached early would go stale).  Every poll is bounded: a
