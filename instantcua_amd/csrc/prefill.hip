@@ -119,55 +119,59 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------
-// GEMM: a workgroup of 8 waves computes 128 tokens x 128 weight rows; wave w owns token blocks
-// 8 tm + 2 (w % 4), + 1 (32 tokens) against row blocks 4 (w / 4) .. + 3 (64 rows), two waves
-// per SIMD.  Each 128-K step, the weight chunks of the 8 row blocks (q4 one 1 KiB chunk, q8
-// two, f16 four) become fp16 B operands in LDS once (double-buffered) and are shared by the
-// waves; the waves' activation operands stream from global memory straight into registers one
-// 64-K half-step ahead.  Tiles are numbered token-tile-major and dealt to the 8 XCDs in
+// GEMM: a workgroup of 8 waves computes 128 tokens x 16 RB weight rows (RB = 8 or 16 row
+// blocks); wave w owns token blocks 8 tm + 2 (w % 4), + 1 (32 tokens) against row blocks
+// RB / 2 (w / 4) onwards (RB / 2 row blocks), two waves per SIMD, and takes its row blocks in halves
+// of four per group.  Each 128-K step, the weight chunks of the RB row blocks (q4 one 1 KiB
+// chunk, q8 two, f16 four) become fp16 B operands in LDS once (double-buffered, 64 or 128 KiB)
+// and are shared by the waves; the waves' activation operands stream from global memory
+// straight into registers one 64-K half-step ahead, each feeding 2 RB matrix-core products per
+// k-step.  The launch takes RB = 16 (half the activation traffic per product) where its tiles
+// still fill the CUs evenly.  Tiles are numbered token-tile-major and dealt to the 8 XCDs in
 // contiguous ranges, so the workgroups of one XCD share token tiles in its L2.
 
-template <int FMT, int K, int EPI>
+template <int FMT, int K, int EPI, int PG_RB>
 __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
+    static_assert(PG_RB == 8 || PG_RB == 16, "tile rows");
+    constexpr int NHF = PG_RB / 8;         // halves of four row blocks per wave
+    constexpr int TR = 16 * PG_RB;         // rows of a tile
     constexpr int NG = K / 64, NKS = K / 32, NC = K / 128;
     constexpr int CPS = FMT == FMT_Q4 ? 1 : FMT == FMT_Q8 ? 2 : 4;  // 1 KiB chunks per 128-K step
     constexpr int NCH = NC * CPS;                                      // chunks per row block
-    const int TN = a.N / 128, TM = a.Mpad / 128, T = TM * TN;
+    const int TN = a.N / (16 * PG_RB), TM = a.Mpad / 128, T = TM * TN;
     const int per = (T + 7) / 8;
     const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (tile >= T) return;
     const int tm = tile / TN, tn = tile % TN;
 
-    __shared__ uint4 Bs[2][8][4][64];   // fp16 codes: [buffer][row block][k-step][lane]
-    // Per-step words: [buffer][0..255] fp16 (scale, bias) of group 2 c + i / 128, row i % 128;
-    // [buffer][256 + 32 b + 16 g + t] float group sum of group 2 c + g, token 16 b + t of the tile.
+    __shared__ uint4 Bs[2][PG_RB][4][64];  // fp16 codes: [buffer][row block][k-step][lane]
+    // Per-step words: [buffer][i] fp16 (scale, bias) of group 2 c + i / TR, row i % TR.
     __shared__ __attribute__((aligned(16))) uint32_t Vs[2][512];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;
-    const int tb0 = tm * 8 + 2 * (wave & 3), rb0 = 4 * (wave >> 2);
+    const int tb0 = tm * 8 + 2 * (wave & 3), rb0 = (PG_RB / 2) * (wave >> 2);
     const uint16_t* xa = a.xa + (size_t)tb0 * NKS * 1024 + lane * 8;   // token block tb0 (+ NKS * 1024 for tb0 + 1)
-    // Staging: thread t unpacks nibble lane t % 64 of row block t / 64.
+    // Staging: thread t unpacks nibble lane t % 64 of row block t / 64 (and t / 64 + 8).
     const int srb = tid >> 6;
-    const uint8_t* wsrc = a.w + (size_t)(tn * 8 + srb) * NCH * 1024 + lane * 16;
-    // Thread t < 256 loads one scale word of its row, t >= 256 one group sum: one unconditional
-    // 4-byte load per step (stride 2 words or 32 floats per step).  q4: the (scale, bias) half2
-    // of 64-group 2 c + t / 128; q8: the scales of 32-groups 4 c + 2 (t / 128), + 1 (the same
-    // word offsets: a q8 row holds K / 64 words of scale pairs).  f16 weights have no scales.
-    const int vj = tid & 255;
-    const uint32_t* vsrc = tid < 256 ? (const uint32_t*)a.sb + (size_t)(tn * 128 + (vj & 127)) * NG + (vj >> 7)
-                                     : (const uint32_t*)a.xs + ((size_t)(tm * 8 + (vj >> 5)) * NG + ((vj >> 4) & 1)) * 16 + (vj & 15);
-    const int vstride = tid < 256 ? 2 : 32;
-    const bool vload = FMT != FMT_F16 && tid < 256;  // (the group sums of the upper half go unused)
+    const uint8_t* wsrc = a.w + (size_t)(tn * PG_RB + srb) * NCH * 1024 + lane * 16;
+    constexpr size_t WSRC2 = (size_t)8 * NCH * 1024;  // row block srb + 8
+    // Thread t < 2 TR loads one scale word per step (stride 2 words): row t % TR of the tile, q4
+    // the (scale, bias) half2 of 64-group 2 c + t / TR; q8 the scales of 32-groups
+    // 4 c + 2 (t / TR), + 1 (the same word offsets: a q8 row holds K / 64 words of scale pairs).
+    // f16 weights have no scales.
+    const uint32_t* vsrc = (const uint32_t*)a.sb + (size_t)(tn * TR + (tid % TR)) * NG + (tid / TR);
+    constexpr int vstride = 2;
+    const bool vload = FMT != FMT_F16 && (2 * TR >= 512 || tid < 2 * TR);
 
-    f32x4 acc[2][4];
+    f32x4 acc[2][4 * NHF];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < 4 * NHF; ++r) acc[i][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Activation operands of one 64-group (two k-steps), prefetched one group ahead.
     uint4 Ae[2][2][2], Ao[2][2][2];  // [token block][k-step of the group][hi, lo]
-    uint4 Wn[CPS];
+    uint4 Wn[NHF][CPS];
     uint32_t Vn = 0;
     auto aload = [&](int g, uint4(&A)[2][2][2]) {
 #pragma unroll
@@ -181,18 +185,22 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     };
     auto wload = [&](int c) {
 #pragma unroll
-        for (int j = 0; j < CPS; ++j) Wn[j] = *(const uint4*)(wsrc + (size_t)(c * CPS + j) * 1024);
+        for (int hb = 0; hb < NHF; ++hb)
+#pragma unroll
+            for (int j = 0; j < CPS; ++j) Wn[hb][j] = *(const uint4*)(wsrc + hb * WSRC2 + (size_t)(c * CPS + j) * 1024);
         if (vload) Vn = vsrc[(size_t)c * vstride];
     };
     // Nibble lane L (row L % 16, 16-K slot L / 16 of each group) -> fp16 lanes (L % 16) + 16 (2 (slot % 2) + h)
     // of k-step 2 gg + slot / 2, h = 0 for K 0..7 of the slot, 1 for K 8..15.
     auto lstore = [&](int b) {
+#pragma unroll
+      for (int hb = 0; hb < NHF; ++hb) {
+        const int sr = srb + 8 * hb;
         if constexpr (FMT == FMT_F16) {
             // f16 chunk j is k-step j, already in the B-operand lane layout.
 #pragma unroll
-            for (int j = 0; j < 4; ++j) Bs[b][srb][j][lane] = Wn[j];
-            Vs[b][tid] = Vn;
-            return;
+            for (int j = 0; j < 4; ++j) Bs[b][sr][j][lane] = Wn[hb][j];
+            continue;
         } else if constexpr (FMT == FMT_Q8) {
             // q8 chunk j: bytes 0-7 of a lane are k-step 2 j (K-slot lane / 16 of row lane % 16),
             // bytes 8-15 k-step 2 j + 1, the B-operand lane layout; a signed byte b spread into a
@@ -201,7 +209,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
             const f16x2 k1152 = {(f16)1152.f, (f16)1152.f};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const uint32_t dd[4] = {Wn[j].x, Wn[j].y, Wn[j].z, Wn[j].w};
+                const uint32_t dd[4] = {Wn[hb][j].x, Wn[hb][j].y, Wn[hb][j].z, Wn[hb][j].w};
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     uint32_t o[4];
@@ -213,14 +221,13 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                         o[2 * w2] = h2_bits(as_h2((s0 ^ 0x00800080u) | 0x64006400u) - k1152);
                         o[2 * w2 + 1] = h2_bits(as_h2((s1 ^ 0x00800080u) | 0x64006400u) - k1152);
                     }
-                    Bs[b][srb][2 * j + h][lane] = make_uint4(o[0], o[1], o[2], o[3]);
+                    Bs[b][sr][2 * j + h][lane] = make_uint4(o[0], o[1], o[2], o[3]);
                 }
             }
-            Vs[b][tid] = Vn;
-            return;
-        }
+            continue;
+        } else {
         const int r = lane & 15, slot = lane >> 4;
-        const uint32_t dd[4] = {Wn[0].x, Wn[0].y, Wn[0].z, Wn[0].w};
+        const uint32_t dd[4] = {Wn[hb][0].x, Wn[hb][0].y, Wn[hb][0].z, Wn[hb][0].w};
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
 #pragma unroll
@@ -237,22 +244,27 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                     o[j] = h2_bits(as_h2((sp & 0x000F000Fu) | 0x64006400u) - k1024);
                     o[2 + j] = h2_bits(as_h2(((sp >> 4) & 0x000F000Fu) | 0x64006400u) - k1024);
                 }
-                Bs[b][srb][2 * gg + (slot >> 1)][r + 16 * (2 * (slot & 1) + h)] = make_uint4(o[0], o[1], o[2], o[3]);
+                Bs[b][sr][2 * gg + (slot >> 1)][r + 16 * (2 * (slot & 1) + h)] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
+        }
+      }
         Vs[b][tid] = Vn;
     };
-    // One 64-group: the wave's 8 B fragments first, then 4 x 2 accumulator chains of 4 MFMAs.
+    // One 64-group, in two halves of four row blocks: a half's 8 B fragments first, then 4 x 2
+    // accumulator chains of 4 MFMAs, then its scale epilogue.
     auto group = [&](int b, int gg, const uint4(&Ac)[2][2][2]) {
+#pragma unroll
+      for (int hf = 0; hf < NHF; ++hf) {
         v8h Bf[4][2];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) Bf[r][kk] = __builtin_bit_cast(v8h, Bs[b][rb0 + r][2 * gg + kk][lane]);
+            for (int kk = 0; kk < 2; ++kk) Bf[r][kk] = __builtin_bit_cast(v8h, Bs[b][rb0 + 4 * hf + r][2 * gg + kk][lane]);
         float2 sb[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const f16x2 sb2 = as_h2(Vs[b][gg * 128 + (rb0 + r) * 16 + r16]);
+            const f16x2 sb2 = as_h2(Vs[b][gg * TR + (rb0 + 4 * hf + r) * 16 + r16]);
             sb[r] = make_float2((float)sb2.x, (float)sb2.y);  // q4 (scale, bias); q8 the two 32-groups' scales
         }
         if constexpr (FMT == FMT_Q8) {
@@ -277,9 +289,10 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(kk ? sb[r].y : sb[r].x, C[r][i][e], acc[i][r][e]);
+                        for (int e = 0; e < 4; ++e)
+                            acc[i][4 * hf + r][e] = fmaf(kk ? sb[r].y : sb[r].x, C[r][i][e], acc[i][4 * hf + r][e]);
             }
-            return;
+            continue;
         }
         f32x4 C[4][2];
 #pragma unroll
@@ -303,11 +316,12 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (FMT == FMT_F16)
-                        acc[i][r][e] += C[r][i][e];
+                        acc[i][4 * hf + r][e] += C[r][i][e];
                     else  // q4: the bias term sum_g b_g X_g went in before the loop
-                        acc[i][r][e] = fmaf(sb[r].x, C[r][i][e], acc[i][r][e]);
+                        acc[i][4 * hf + r][e] = fmaf(sb[r].x, C[r][i][e], acc[i][4 * hf + r][e]);
                 }
             }
+      }
     };
 
     // Even groups use Ae, odd groups Ao: each set is reloaded right after its group, so no
@@ -334,23 +348,27 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                 }
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint4* bp = (const uint4*)((const uint32_t*)a.sb + (size_t)(tn * 128 + (rb0 + r) * 16 + r16) * NG + 32 * cg + 8 * q);
-                const uint4 w0 = bp[0], w1 = bp[1];
-                const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            for (int hf = 0; hf < NHF; ++hf) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) Bb[r][j] = as_h2(wv[j]).y;
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const uint4* bp = (const uint4*)((const uint32_t*)a.sb +
+                                                     (size_t)(tn * TR + (rb0 + 4 * hf + r) * 16 + r16) * NG + 32 * cg + 8 * q);
+                    const uint4 w0 = bp[0], w1 = bp[1];
+                    const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    f32x4 B = f32x4{0.f, 0.f, 0.f, 0.f};
-                    B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xh[i], Bb[r], B, 0, 0, 0);
-                    B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xl[i], Bb[r], B, 0, 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[i][r][e] = fmaf(256.f, B[e], acc[i][r][e]);
+                    for (int j = 0; j < 8; ++j) Bb[r][j] = as_h2(wv[j]).y;
                 }
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        f32x4 B = f32x4{0.f, 0.f, 0.f, 0.f};
+                        B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xh[i], Bb[r], B, 0, 0, 0);
+                        B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xl[i], Bb[r], B, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[i][4 * hf + r][e] = fmaf(256.f, B[e], acc[i][4 * hf + r][e]);
+                    }
+            }
         }
     }
     lstore(0);
@@ -374,9 +392,9 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         const float4 tsv = *(const float4*)(a.ts + tq);
         const float tsc[4] = {tsv.x, tsv.y, tsv.z, tsv.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 4 * NHF; ++r) {
             const int rb = rb0 + r;
-            const int row = tn * 128 + rb * 16 + r16;
+            const int row = tn * TR + rb * 16 + r16;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = tq + e;
@@ -393,9 +411,9 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                         }
                         *xo = v;
                     }
-                } else {  // EPI_SWIGLU: block 8 tn + rb = gate units 8 (8 tn + rb) + 0..7, then their up rows
+                } else {  // EPI_SWIGLU: block RB tn + rb = gate units 8 (RB tn + rb) + 0..7, then their up rows
                     const float up = __shfl_xor(y, 8);
-                    if (t < a.M && r16 < 8) a.h[(size_t)t * FF + (tn * 8 + rb) * 8 + r16] = (y / (1.f + expf(-y))) * up;
+                    if (t < a.M && r16 < 8) a.h[(size_t)t * FF + (tn * PG_RB + rb) * 8 + r16] = (y / (1.f + expf(-y))) * up;
                 }
             }
         }
@@ -619,29 +637,43 @@ hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w
     return hipGetLastError();
 }
 
-template <int FMT>
-static hipError_t pf_gemm_fmt(int K, int epi, const PfGemmArgs& a, int grid, hipStream_t s) {
+template <int FMT, int RB>
+static hipError_t pf_gemm_rb(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
+    const int T = (a.Mpad / 128) * (a.N / (16 * RB));
+    const dim3 grid(8 * ((T + 7) / 8));
     if (K == H && epi == EPI_STORE)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_STORE>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_STORE, RB>), grid, dim3(512), 0, s, a);
     else if (K == H && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_RESID>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_RESID, RB>), grid, dim3(512), 0, s, a);
     else if (K == H && epi == EPI_SWIGLU)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_SWIGLU>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_SWIGLU, RB>), grid, dim3(512), 0, s, a);
     else if (K == FF && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, FF, EPI_RESID>), dim3(grid), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, FF, EPI_RESID, RB>), grid, dim3(512), 0, s, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
+// 256-row tiles (RB 16) where they fill the 256 CUs evenly (a whole number of tiles each, or at
+// least four); f16 weights keep 128-row tiles (their four B chunks per step would not fit the
+// registers of the larger tile).
+template <int FMT>
+static hipError_t pf_gemm_fmt(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
+    if constexpr (FMT == FMT_F16) {
+        return pf_gemm_rb<FMT, 8>(K, epi, a, s);
+    } else {
+        const int T16 = (a.Mpad / 128) * (a.N / 256);
+        const bool big = a.N % 256 == 0 && T16 >= 256 && (T16 % 256 == 0 || T16 >= 1024);
+        return big ? pf_gemm_rb<FMT, 16>(K, epi, a, s) : pf_gemm_rb<FMT, 8>(K, epi, a, s);
+    }
+}
+
 hipError_t launch_pf_gemm(int fmt, int K, int epi, const PfGemmArgs& a, hipStream_t s) {
     if (a.M < 1 || a.Mpad < a.M || a.Mpad % 128 || a.N % 128) return hipErrorInvalidValue;
-    const int T = (a.Mpad / 128) * (a.N / 128);
-    const int grid = 8 * ((T + 7) / 8);
     switch (fmt) {
-        case FMT_Q4: return pf_gemm_fmt<FMT_Q4>(K, epi, a, grid, s);
-        case FMT_Q8: return pf_gemm_fmt<FMT_Q8>(K, epi, a, grid, s);
-        case FMT_F16: return pf_gemm_fmt<FMT_F16>(K, epi, a, grid, s);
+        case FMT_Q4: return pf_gemm_fmt<FMT_Q4>(K, epi, a, s);
+        case FMT_Q8: return pf_gemm_fmt<FMT_Q8>(K, epi, a, s);
+        case FMT_F16: return pf_gemm_fmt<FMT_F16>(K, epi, a, s);
     }
     return hipErrorInvalidValue;
 }
