@@ -251,9 +251,15 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
       }
         Vs[b][tid] = Vn;
     };
-    // One 64-group, in two halves of four row blocks: a half's 8 B fragments first, then 4 x 2
-    // accumulator chains of 4 MFMAs, then its scale epilogue.
-    auto group = [&](int b, int gg, const uint4(&Ac)[2][2][2]) {
+    // One activation operand (token block tb0 + i, k-step kk of group g, hi / lo part hl).
+    auto aload1 = [&](int g, int i, int kk, int hl) {
+        return *(const uint4*)(xa + (size_t)i * NKS * 1024 + ((size_t)(2 * g + kk) * 2 + hl) * 512);
+    };
+    // One 64-group, in halves of four row blocks: a half's 8 B fragments first, then 4 x 2
+    // accumulator chains of 4 MFMAs, then its scale epilogue.  In the last half, each activation
+    // register is requested again for group gn (two groups on) as soon as its last product is
+    // issued, so the loads have two groups' work to land in.
+    auto group = [&](int b, int gg, uint4(&Ac)[2][2][2], int gn) {
 #pragma unroll
       for (int hf = 0; hf < NHF; ++hf) {
         v8h Bf[4][2];
@@ -277,13 +283,18 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                     for (int i = 0; i < 2; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int hl = 0; hl < 2; ++hl)
+                for (int hl = 0; hl < 2; ++hl) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
 #pragma unroll
                         for (int i = 0; i < 2; ++i)
                             C[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, Ac[i][kk][hl]),
                                                                              Bf[r][kk], C[r][i], 0, 0, 0);
+                    if (hf == NHF - 1) {
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) Ac[i][kk][hl] = aload1(gn, i, kk, hl);
+                    }
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -302,13 +313,18 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-            for (int hl = 0; hl < 2; ++hl)
+            for (int hl = 0; hl < 2; ++hl) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
                         C[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, Ac[i][kk][hl]), Bf[r][kk],
                                                                          C[r][i], 0, 0, 0);
+                if (hf == NHF - 1) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) Ac[i][kk][hl] = aload1(gn, i, kk, hl);
+                }
+            }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -324,9 +340,10 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
       }
     };
 
-    // Even groups use Ae, odd groups Ao: each set is reloaded right after its group, so no
-    // register copy waits on an outstanding load.
+    // Even groups use Ae, odd groups Ao: each register is reloaded (for two groups on) as its
+    // group's last product using it issues, so no register copy waits on an outstanding load.
     aload(0, Ae);
+    aload(1, Ao);
     wload(0);
     if constexpr (FMT == FMT_Q4) {
         // The q4 bias term sum_g b_g X_g of every output, on the matrix cores before the loop:
@@ -377,10 +394,8 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         const int b = c & 1;
         // The next step's codes (the last step reloads step 0 into the idle buffer: no branch).
         wload(c + 1 < NC ? c + 1 : 0);
-        aload(2 * c + 1, Ao);
-        group(b, 0, Ae);
-        aload(2 * c + 2 < NG ? 2 * c + 2 : 0, Ae);
-        group(b, 1, Ao);
+        group(b, 0, Ae, 2 * c + 2 < NG ? 2 * c + 2 : 0);
+        group(b, 1, Ao, 2 * c + 3 < NG ? 2 * c + 3 : 1);
         lstore(b ^ 1);
         __syncthreads();
     }
