@@ -119,26 +119,23 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------
-// GEMM: a workgroup of 8 waves computes 128 tokens x 16 RB weight rows (RB = 8 or 16 row
-// blocks); wave w owns token blocks 8 tm + 2 (w % 4), + 1 (32 tokens) against row blocks
-// RB / 2 (w / 4) onwards (RB / 2 row blocks), two waves per SIMD, and takes its row blocks in halves
-// of four per group.  Each 128-K step, the weight chunks of the RB row blocks (q4 one 1 KiB
-// chunk, q8 two, f16 four) become fp16 B operands in LDS once (double-buffered, 64 or 128 KiB)
-// and are shared by the waves; the waves' activation operands stream from global memory
-// straight into registers one 64-K half-step ahead, each feeding 2 RB matrix-core products per
-// k-step.  The launch takes RB = 16 (half the activation traffic per product) where its tiles
-// still fill the CUs evenly.  Tiles are numbered token-tile-major and dealt to the 8 XCDs in
-// contiguous ranges, so the workgroups of one XCD share token tiles in its L2.
-
-template <int FMT, int K, int EPI, int PG_RB>
+// GEMM: a workgroup of 8 waves computes 64 TB tokens x 16 RB weight rows (TB = 1 or 2 token
+// blocks per wave, RB = 8 or 16 row blocks); wave w owns token blocks 4 TB tm + TB (w % 4) ..
+// against row blocks RB / 2 (w / 4) onwards (RB / 2 row blocks), two waves per SIMD, and takes
+// its row blocks in halves of four per group.  Each 128-K step, the weight chunks of the RB row
+// blocks (q4 one 1 KiB chunk, q8 two, f16 four) become fp16 B operands in LDS once
+// (double-buffered, 64 or 128 KiB) and are shared by the waves; the waves' activation operands
+// stream from global memory straight into registers two 64-K groups ahead.  The launch takes
+// the largest tile (most products per operand byte) whose count still fills the CUs evenly.
+template <int FMT, int K, int EPI, int PG_RB, int TB>
 __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
-    static_assert(PG_RB == 8 || PG_RB == 16, "tile rows");
+    static_assert((PG_RB == 8 || PG_RB == 16) && (TB == 1 || TB == 2), "tile shape");
     constexpr int NHF = PG_RB / 8;         // halves of four row blocks per wave
     constexpr int TR = 16 * PG_RB;         // rows of a tile
     constexpr int NG = K / 64, NKS = K / 32, NC = K / 128;
     constexpr int CPS = FMT == FMT_Q4 ? 1 : FMT == FMT_Q8 ? 2 : 4;  // 1 KiB chunks per 128-K step
     constexpr int NCH = NC * CPS;                                      // chunks per row block
-    const int TN = a.N / (16 * PG_RB), TM = a.Mpad / 128, T = TM * TN;
+    const int TN = a.N / (16 * PG_RB), TM = a.Mpad / (64 * TB), T = TM * TN;
     const int per = (T + 7) / 8;
     const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (tile >= T) return;
@@ -149,7 +146,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t Vs[2][512];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;
-    const int tb0 = tm * 8 + 2 * (wave & 3), rb0 = (PG_RB / 2) * (wave >> 2);
+    const int tb0 = tm * 4 * TB + TB * (wave & 3), rb0 = (PG_RB / 2) * (wave >> 2);
     const uint16_t* xa = a.xa + (size_t)tb0 * NKS * 1024 + lane * 8;   // token block tb0 (+ NKS * 1024 for tb0 + 1)
     // Staging: thread t unpacks nibble lane t % 64 of row block t / 64 (and t / 64 + 8).
     const int srb = tid >> 6;
@@ -163,19 +160,19 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     constexpr int vstride = 2;
     const bool vload = FMT != FMT_F16 && (2 * TR >= 512 || tid < 2 * TR);
 
-    f32x4 acc[2][4 * NHF];
+    f32x4 acc[TB][4 * NHF];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TB; ++i)
 #pragma unroll
         for (int r = 0; r < 4 * NHF; ++r) acc[i][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Activation operands of one 64-group (two k-steps), prefetched one group ahead.
-    uint4 Ae[2][2][2], Ao[2][2][2];  // [token block][k-step of the group][hi, lo]
+    uint4 Ae[TB][2][2], Ao[TB][2][2];  // [token block][k-step of the group][hi, lo]
     uint4 Wn[NHF][CPS];
     uint32_t Vn = 0;
-    auto aload = [&](int g, uint4(&A)[2][2][2]) {
+    auto aload = [&](int g, uint4(&A)[TB][2][2]) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TB; ++i) {
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -259,7 +256,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     // accumulator chains of 4 MFMAs, then its scale epilogue.  In the last half, each activation
     // register is requested again for group gn (two groups on) as soon as its last product is
     // issued, so the loads have two groups' work to land in.
-    auto group = [&](int b, int gg, uint4(&Ac)[2][2][2], int gn) {
+    auto group = [&](int b, int gg, uint4(&Ac)[TB][2][2], int gn) {
 #pragma unroll
       for (int hf = 0; hf < NHF; ++hf) {
         v8h Bf[4][2];
@@ -277,39 +274,39 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
             // Two 32-groups, one k-step each.
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-                f32x4 C[4][2];
+                f32x4 C[4][TB];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int i = 0; i < TB; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int hl = 0; hl < 2; ++hl) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
 #pragma unroll
-                        for (int i = 0; i < 2; ++i)
+                        for (int i = 0; i < TB; ++i)
                             C[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, Ac[i][kk][hl]),
                                                                              Bf[r][kk], C[r][i], 0, 0, 0);
                     if (hf == NHF - 1) {
 #pragma unroll
-                        for (int i = 0; i < 2; ++i) Ac[i][kk][hl] = aload1(gn, i, kk, hl);
+                        for (int i = 0; i < TB; ++i) Ac[i][kk][hl] = aload1(gn, i, kk, hl);
                     }
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int i = 0; i < 2; ++i)
+                    for (int i = 0; i < TB; ++i)
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             acc[i][4 * hf + r][e] = fmaf(kk ? sb[r].y : sb[r].x, C[r][i][e], acc[i][4 * hf + r][e]);
             }
             continue;
         }
-        f32x4 C[4][2];
+        f32x4 C[4][TB];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < TB; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -317,18 +314,18 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int i = 0; i < 2; ++i)
+                    for (int i = 0; i < TB; ++i)
                         C[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, Ac[i][kk][hl]), Bf[r][kk],
                                                                          C[r][i], 0, 0, 0);
                 if (hf == NHF - 1) {
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) Ac[i][kk][hl] = aload1(gn, i, kk, hl);
+                    for (int i = 0; i < TB; ++i) Ac[i][kk][hl] = aload1(gn, i, kk, hl);
                 }
             }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < TB; ++i) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (FMT == FMT_F16)
@@ -352,9 +349,9 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         // one fma per output (acc += s C_g).
 #pragma unroll 1
         for (int cg = 0; cg < NG / 32; ++cg) {
-            v8h Xh[2], Xl[2], Bb[4];
+            v8h Xh[TB], Xl[TB], Bb[4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < TB; ++i) {
                 const float* xp = a.xs + ((size_t)(tb0 + i) * NG + 32 * cg + 8 * q) * 16 + r16;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -378,7 +375,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) {
+                    for (int i = 0; i < TB; ++i) {
                         f32x4 B = f32x4{0.f, 0.f, 0.f, 0.f};
                         B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xh[i], Bb[r], B, 0, 0, 0);
                         B = __builtin_amdgcn_mfma_f32_16x16x32_f16(Xl[i], Bb[r], B, 0, 0, 0);
@@ -400,9 +397,9 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         __syncthreads();
     }
 
-    // Epilogue: lane holds tokens 16 tb + 4 q + e of weight row 128 tn + 16 rb + r16.
+    // Epilogue: lane holds tokens 16 tb + 4 q + e of weight row TR tn + 16 rb + r16.
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < TB; ++i) {
         const int tq = (tb0 + i) * 16 + 4 * q;
         const float4 tsv = *(const float4*)(a.ts + tq);
         const float tsc[4] = {tsv.x, tsv.y, tsv.z, tsv.w};
@@ -652,35 +649,37 @@ hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w
     return hipGetLastError();
 }
 
-template <int FMT, int RB>
-static hipError_t pf_gemm_rb(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
-    const int T = (a.Mpad / 128) * (a.N / (16 * RB));
+template <int FMT, int RB, int TB>
+static hipError_t pf_gemm_shape(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
+    const int T = (a.Mpad / (64 * TB)) * (a.N / (16 * RB));
     const dim3 grid(8 * ((T + 7) / 8));
     if (K == H && epi == EPI_STORE)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_STORE, RB>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_STORE, RB, TB>), grid, dim3(512), 0, s, a);
     else if (K == H && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_RESID, RB>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_RESID, RB, TB>), grid, dim3(512), 0, s, a);
     else if (K == H && epi == EPI_SWIGLU)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_SWIGLU, RB>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_SWIGLU, RB, TB>), grid, dim3(512), 0, s, a);
     else if (K == FF && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, FF, EPI_RESID, RB>), grid, dim3(512), 0, s, a);
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, FF, EPI_RESID, RB, TB>), grid, dim3(512), 0, s, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-// 256-row tiles (RB 16) where they fill the 256 CUs evenly (a whole number of tiles each, or at
-// least four); f16 weights keep 128-row tiles (their four B chunks per step would not fit the
-// registers of the larger tile).
+// Tiles that fill the 256 CUs evenly: at least one each, and a whole number each or at least four.
+static bool even_fill(int tiles) { return tiles >= 256 && (tiles % 256 == 0 || tiles >= 1024); }
+
+// The largest tile whose count fills the CUs evenly: 128 tokens x 256 rows, 128 x 128, else
+// 64 x 128 (small prompts, whose 128-token tiles would leave CUs idle).  f16 weights keep 128-row
+// tiles (their four B chunks per step would not fit the registers of the larger tile).
 template <int FMT>
 static hipError_t pf_gemm_fmt(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
-    if constexpr (FMT == FMT_F16) {
-        return pf_gemm_rb<FMT, 8>(K, epi, a, s);
-    } else {
-        const int T16 = (a.Mpad / 128) * (a.N / 256);
-        const bool big = a.N % 256 == 0 && T16 >= 256 && (T16 % 256 == 0 || T16 >= 1024);
-        return big ? pf_gemm_rb<FMT, 16>(K, epi, a, s) : pf_gemm_rb<FMT, 8>(K, epi, a, s);
+    const int tm128 = a.Mpad / 128;
+    if (FMT != FMT_F16 && a.N % 256 == 0 && even_fill(tm128 * (a.N / 256))) {
+        if constexpr (FMT != FMT_F16) return pf_gemm_shape<FMT, 16, 2>(K, epi, a, s);
     }
+    if (even_fill(tm128 * (a.N / 128))) return pf_gemm_shape<FMT, 8, 2>(K, epi, a, s);
+    return pf_gemm_shape<FMT, 8, 1>(K, epi, a, s);
 }
 
 hipError_t launch_pf_gemm(int fmt, int K, int epi, const PfGemmArgs& a, hipStream_t s) {
