@@ -172,7 +172,6 @@ __device__ __forceinline__ bool spin_tags(uint64_t (&p)[NP], At at, unsigned rou
             return false;
         }
         if ((it & 63) == 63 && load_err(err)) return false;
-        __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int i = 0; i < NP; ++i)
             if (tag_of(p[i]) != tag) p[i] = ld64(at(i));  // a filler always carries the tag
