@@ -65,9 +65,10 @@ constexpr int ATT_SPLITS = NWG / NKV;     // 32
 constexpr int SPIN_LIMIT = 2000000;       // polls (>= ~1 us each) before a wait gives up
 constexpr int PART2 = HD / 2 + 1;         // packets of one head's partial: o pairs, (l, m)
 constexpr int ATT_QW = MT / 16;           // 16 quarter-waves of math threads
-constexpr int ATT_SPQ = 9;                // cache slots per quarter-wave per block
+constexpr int ATT_SPQ = 9;                // cache slots per quarter-wave per block (P.V)
 constexpr int ATT_BLOCK = ATT_QW * ATT_SPQ;  // 144 slots per block
-constexpr int ATT_PAD = 192;              // score row length (3 per lane of a wave)
+constexpr int ATT_NT = (ATT_SPQ + 3) / 4;    // score tiles of 16 slots per math wave per block
+constexpr int ATT_PAD = 192;              // merge weights row length
 constexpr int MERGE_PARTS = 4;            // workgroups merging one group's partials
 constexpr int MERGER0 = NWG - NKV * MERGE_PARTS;  // workgroups 224..255: splits 28..31 of each group
 static_assert(MERGER0 >= H / 16, "mergers must not have O / down work");
@@ -247,7 +248,10 @@ struct Shared {
     float nw[H];              // RMSNorm weights of the current stage
     float xown[16];           // residual rows of this workgroup's O / down block (workgroups < 128)
     float xhi[16];            // the upper-half down sums of those rows from the previous layer
-    float qs[2][HD];          // attention: two query heads
+    // attention: the two query heads as fp16 hi and lo parts, rows (hi 2g, hi 2g + 1, lo 2g,
+    // lo 2g + 1): the A operand rows of the score tiles
+    alignas(16) uint16_t qf[4][HD];
+    alignas(16) float pw[MW][2][4][12];  // probabilities of a math wave's slots, [head][lane / 16][i]
     float ktail[HD], vtail[HD];
     float sc[2][ATT_PAD];
     float ored[MW][2][HD];
@@ -582,20 +586,53 @@ __device__ __forceinline__ void norm_rope(float& a, float& b, float w0, float w1
     b = b2;
 }
 
-// Math threads: the cached K/V rows j0 + quad + 16 i (< j0 + nprior) of one split, 8 dims
-// (16 B) per lane; zeros past the split.
-__device__ __forceinline__ void load_kv_rows(uint4 (&kr)[ATT_SPQ], uint4 (&vr)[ATT_SPQ], const uint16_t* kb,
-                                             const uint16_t* vb, int j0, int nprior, int quad, int ql) {
+// Math threads: the cache rows of one attention block (block slots 0 .. ATT_BLOCK - 1 at split
+// row j0 + b0) that this lane holds; only rows < nprior come from the cache, zeros elsewhere.
+//   K, for the score tiles: tile T of math wave mw has 16 columns; column c = lane % 16 is block
+//     slot att_slot(T, c, mw) = 16 (4 T + c / 4) + 4 mw + c % 4, and the lane holds its 16 bytes
+//     at dims 32 j + 8 (lane / 16), j = 0..3 (the B operand of v_mfma_f32_16x16x32_f16).
+//   V, for P.V: block slots quad + 16 i (quad = 4 mw + lane / 16), 8 dims (16 B) at 8 (lane % 16).
+// So the slot of V row (quad, i) is column 4 (i % 4) + lane / 16 of tile i / 4 of the same wave.
+__device__ __forceinline__ int att_slot(int T, int c, int mw) { return 16 * (4 * T + (c >> 2)) + 4 * mw + (c & 3); }
+
+__device__ __forceinline__ void load_kv_block(uint4 (&kt)[ATT_NT][4], uint4 (&vr)[ATT_SPQ], const uint16_t* kb,
+                                              const uint16_t* vb, int j0, int b0, int nprior, int tid) {
+    const int lane = tid % 64, mw = tid / 64, c = lane & 15, kq = lane >> 4, quad = tid / 16, ql = tid % 16;
 #pragma unroll
-    for (int i = 0; i < ATT_SPQ; ++i) {
-        const int p = quad + ATT_QW * i;
-        kr[i] = make_uint4(0u, 0u, 0u, 0u);
-        vr[i] = kr[i];
-        if (p < nprior) {
-            kr[i] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 8 * ql);
-            vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
+    for (int T = 0; T < ATT_NT; ++T) {
+        const int p = b0 + att_slot(T, c, mw);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kt[T][j] = make_uint4(0u, 0u, 0u, 0u);
+        if (4 * T + (c >> 2) < ATT_SPQ && p < nprior) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kt[T][j] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 32 * j + 8 * kq);
         }
     }
+#pragma unroll
+    for (int i = 0; i < ATT_SPQ; ++i) {
+        const int p = b0 + quad + ATT_QW * i;
+        vr[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (p < nprior) vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
+    }
+}
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ h8 as_h8(uint4 v) { return __builtin_bit_cast(h8, u32x4{v.x, v.y, v.z, v.w}); }
+// Eight fp32 values that are exact in fp16, packed as fp16.
+__device__ __forceinline__ uint4 pack8_f16(const float* f) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = (uint32_t)f2h(f[2 * j]) | ((uint32_t)f2h(f[2 * j + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Max over the 16 lanes of each row of 16 (every lane gets its row's maximum).
+__device__ __forceinline__ float max16(float v) {
+    v = fmaxf(v, dpp<DPP_MIRROR>(v));
+    v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp<DPP_XOR2>(v));
+    return fmaxf(v, dpp<DPP_XOR1>(v));
 }
 
 __device__ __forceinline__ void load_norm8(float (&n)[8], const float* p) {
@@ -697,7 +734,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // step) and their K/V rows after the QKV publish.
             const bool qkv_wg = w >= NWG / 2;
             PK_TRACE(l, 0);
-            uint4 kr[ATT_SPQ], vr[ATT_SPQ];
+            uint4 kt[ATT_NT][4], vr[ATT_SPQ];
             float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rs = 0.f;
             // Exchange waves poll the stage input first; math waves skip that branch and issue
             // their loads at once.  Keeping the loads after the poll in program order lets the
@@ -712,7 +749,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
                 if (!qkv_wg) {
                     wx[0].load(P.wo, P.wo_sb, w, H, mw, lane);
-                    load_kv_rows(kr, vr, kb, vb, j0, nprior, quad, ql);
+                    load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
                     // The lower down half-block of row block w into LDS: it lands long before the
                     // x' poll that a later request would delay.
                     wd_request<FMT>(wdb, P.wd, P.wd_sb, w, 0, mw, lane);
@@ -743,7 +780,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         st64(ll + QKVP + w * 8 + lane / 2, pack2(y[1], n1, r + 1));
                     }
                 }
-                if (math) load_kv_rows(kr, vr, kb, vb, j0, nprior, quad, ql);
+                if (math) load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
             }
             PK_TRACE(l, 2);
 
@@ -770,8 +807,12 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     // 1/sqrt(128) and log2(e): scores come out in base-2 units, so every softmax
                     // exponential of this split and of the merge is one v_exp_f32.
                     const float qscale = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
-                    S.qs[wave][lane] = x0 * qscale;
-                    S.qs[wave][lane + 64] = x1 * qscale;
+                    const float qa = x0 * qscale, qb = x1 * qscale;
+                    const uint16_t ha = f2h(qa), hb = f2h(qb);
+                    S.qf[wave][lane] = ha;
+                    S.qf[wave][lane + 64] = hb;
+                    S.qf[2 + wave][lane] = f2h(qa - h2f(ha));
+                    S.qf[2 + wave][lane + 64] = f2h(qb - h2f(hb));
                 } else if (wave == 2 && tail) {
                     float k0 = S.vec[2 * HD + lane], k1 = S.vec[2 * HD + lane + 64];
                     norm_rope(k0, k1, kn0, kn1, rc, rs);
@@ -794,117 +835,101 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 __builtin_amdgcn_s_waitcnt(0);
             }
             {
-                // Online softmax per quarter-wave (its 9 slots of every block) in registers; the
-                // 16 quarter-waves' (max, sum, o) are combined by lane swaps and once through LDS.
-                float q[2][8];
+                // Scores on the matrix cores: per block, each math wave multiplies the query rows
+                // (the fp16 hi and lo parts of both heads, replicated over the 16 A rows) with its
+                // ATT_NT tiles of 16 cache rows (v_mfma_f32_16x16x32_f16, four products of 32 dims
+                // each); every lane then holds the scores of its column's slot.  The online softmax
+                // runs per wave (every lane holds the wave's running maximum and sum); the
+                // probabilities move through LDS (wave-local) to the P.V layout, where each
+                // quarter-wave takes 9 V rows, 8 dims per lane.
                 float m_run[2] = {-__builtin_inff(), -__builtin_inff()}, l_run[2] = {0.f, 0.f};
                 float o[2][8];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int d = 0; d < 8; ++d) {
-                        q[hh][d] = math ? S.qs[hh][8 * ql + d] : 0.f;
-                        o[hh][d] = 0.f;
-                    }
+                    for (int d = 0; d < 8; ++d) o[hh][d] = 0.f;
                 PK_TRACE(l, 21);
                 if (math) {
+                    const int c = lane & 15, kq = lane >> 4;
 #ifdef ICUA_PERSIST_TRACE
                     __builtin_amdgcn_s_waitcnt(0);
                     PK_TRACE(l, 25);
 #endif
                     for (int b0 = 0; b0 < ntot; b0 += ATT_BLOCK) {
                         const int nb = min(ATT_BLOCK, ntot - b0);
-                        if (b0 > 0) {
-#pragma unroll
-                            for (int i = 0; i < ATT_SPQ; ++i) {
-                                const int p = b0 + quad + ATT_QW * i;
-                                if (p < nprior) {
-                                    kr[i] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 8 * ql);
-                                    vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
-                                }
-                            }
-                        }
+                        if (b0 > 0) load_kv_block(kt, vr, kb, vb, j0, b0, nprior, tid);
                         // The new row (block slot pos - j0 - b0) comes from LDS, not from the cache.
                         const int pnew = tail ? pos - j0 - b0 : -1;
 #pragma unroll
-                        for (int i = 0; i < ATT_SPQ; ++i) {
-                            if (quad + ATT_QW * i == pnew) {
-                                uint32_t kk[4], vv[4];
+                        for (int T = 0; T < ATT_NT; ++T)
+                            if (4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) == pnew) {
 #pragma unroll
-                                for (int j = 0; j < 4; ++j) {
-                                    kk[j] = (uint32_t)f2h(S.ktail[8 * ql + 2 * j]) |
-                                            ((uint32_t)f2h(S.ktail[8 * ql + 2 * j + 1]) << 16);
-                                    vv[j] = (uint32_t)f2h(S.vtail[8 * ql + 2 * j]) |
-                                            ((uint32_t)f2h(S.vtail[8 * ql + 2 * j + 1]) << 16);
-                                }
-                                kr[i] = make_uint4(kk[0], kk[1], kk[2], kk[3]);
-                                vr[i] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
+                                for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail + 32 * j + 8 * kq);
                             }
-                        }
-                        // Scores of the quarter-wave's slots (every lane of the quarter holds all 9).
-                        float sc[2][ATT_SPQ];
 #pragma unroll
-                        for (int i = 0; i < ATT_SPQ; ++i) {
-                            const int p = quad + ATT_QW * i;
-                            const uint32_t dk[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
-                            float acc0 = 0.f, acc1 = 0.f;
+                        for (int i = 0; i < ATT_SPQ; ++i)
+                            if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail + 8 * ql);
+                        // D[variant][slot]: lane l holds rows 4 (l / 16) + r, i.e. variant r.
+                        float sc[2][ATT_NT];
 #pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                const f16x2 hk = as_h2(dk[j]);
-                                const float k0 = (float)hk.x, k1 = (float)hk.y;
-                                acc0 = fmaf(q[0][2 * j], k0, acc0);
-                                acc0 = fmaf(q[0][2 * j + 1], k1, acc0);
-                                acc1 = fmaf(q[1][2 * j], k0, acc1);
-                                acc1 = fmaf(q[1][2 * j + 1], k1, acc1);
-                            }
-                            acc0 = sum16(acc0);
-                            acc1 = sum16(acc1);
-                            sc[0][i] = (p < nb) ? acc0 : -__builtin_inff();
-                            sc[1][i] = (p < nb) ? acc1 : -__builtin_inff();
+                        for (int T = 0; T < ATT_NT; ++T) {
+                            f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)  // A: the query rows (read from LDS for each tile)
+                                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const h8*)&S.qf[lane & 3][32 * j + 8 * kq],
+                                                                           as_h8(kt[T][j]), D, 0, 0, 0);
+                            const bool ok = 4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) < nb;
+                            sc[0][T] = ok ? D[0] + D[2] : -__builtin_inff();
+                            sc[1][T] = ok ? D[1] + D[3] : -__builtin_inff();
                         }
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh) {
-                            float mb = m_run[hh];
+                            float mb = sc[hh][0];
 #pragma unroll
-                            for (int i = 0; i < ATT_SPQ; ++i) mb = fmaxf(mb, sc[hh][i]);
-                            // mb is finite as soon as the quarter has seen one valid slot.
+                            for (int T = 1; T < ATT_NT; ++T) mb = fmaxf(mb, sc[hh][T]);
+                            // mb is finite as soon as the wave has seen one valid slot.
+                            mb = fmaxf(max16(mb), m_run[hh]);
                             const float corr = (m_run[hh] == -__builtin_inff()) ? 0.f : ex2(m_run[hh] - mb);
                             float ls = 0.f;
 #pragma unroll
-                            for (int i = 0; i < ATT_SPQ; ++i) {
-                                sc[hh][i] = (sc[hh][i] == -__builtin_inff()) ? 0.f : ex2(sc[hh][i] - mb);
-                                ls += sc[hh][i];
+                            for (int T = 0; T < ATT_NT; ++T) {
+                                sc[hh][T] = (sc[hh][T] == -__builtin_inff()) ? 0.f : ex2(sc[hh][T] - mb);
+                                ls += sc[hh][T];
                             }
-                            l_run[hh] = l_run[hh] * corr + ls;
+                            l_run[hh] = l_run[hh] * corr + sum16(ls);
                             m_run[hh] = mb;
 #pragma unroll
                             for (int d = 0; d < 8; ++d) o[hh][d] *= corr;
+                            if (lane < 16) {
+#pragma unroll
+                                for (int T = 0; T < ATT_NT; ++T) S.pw[mw][hh][c & 3][4 * T + (c >> 2)] = sc[hh][T];
+                            }
                         }
+                        // The probabilities of this wave's slots were written by its own lanes 0-15:
+                        // a wave's LDS accesses complete in order, so no barrier is needed.
+                        __builtin_amdgcn_wave_barrier();
 #pragma unroll
                         for (int i = 0; i < ATT_SPQ; ++i) {
+                            const float p0 = S.pw[mw][0][kq][i], p1 = S.pw[mw][1][kq][i];
                             const uint32_t dv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
                                 const f16x2 hv = as_h2(dv[j]);
                                 const float v0 = (float)hv.x, v1 = (float)hv.y;
-                                o[0][2 * j] = fmaf(sc[0][i], v0, o[0][2 * j]);
-                                o[0][2 * j + 1] = fmaf(sc[0][i], v1, o[0][2 * j + 1]);
-                                o[1][2 * j] = fmaf(sc[1][i], v0, o[1][2 * j]);
-                                o[1][2 * j + 1] = fmaf(sc[1][i], v1, o[1][2 * j + 1]);
+                                o[0][2 * j] = fmaf(p0, v0, o[0][2 * j]);
+                                o[0][2 * j + 1] = fmaf(p0, v1, o[0][2 * j + 1]);
+                                o[1][2 * j] = fmaf(p1, v0, o[1][2 * j]);
+                                o[1][2 * j + 1] = fmaf(p1, v1, o[1][2 * j + 1]);
                             }
                         }
+                        __builtin_amdgcn_wave_barrier();
                     }
-                    // Combine the wave's 4 quarter-waves (lanes l, l ^ 16, l ^ 32, l ^ 48 hold the
-                    // same dims): rescale to their common max, then sum.
+                    // The wave's 4 quarter-waves (lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same
+                    // dims) share the running maximum: their sums add.
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const float mw4 = max_x4(m_run[hh]);
-                        const float f = (m_run[hh] == -__builtin_inff()) ? 0.f : ex2(m_run[hh] - mw4);
-                        l_run[hh] = sum_x4(l_run[hh] * f);
+                    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                        for (int d = 0; d < 8; ++d) o[hh][d] = sum_x4(o[hh][d] * f);
-                        m_run[hh] = mw4;
-                    }
+                        for (int d = 0; d < 8; ++d) o[hh][d] = sum_x4(o[hh][d]);
                     if (lane < 16) {
 #pragma unroll
                         for (int hh = 0; hh < 2; ++hh)
