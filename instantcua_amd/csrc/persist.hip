@@ -55,6 +55,8 @@ namespace icua {
 namespace pk {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int THREADS = 512, WAVES = 8;
 constexpr int MW = 4;                     // math waves 0..3
@@ -366,7 +368,7 @@ template <int K>
 __device__ __forceinline__ float norm_scale(const Shared& S) {
     const float tot = ((S.misc[40] + S.misc[41]) + (S.misc[42] + S.misc[43])) +
                       ((S.misc[44] + S.misc[45]) + (S.misc[46] + S.misc[47]));
-    return 1.0f / sqrtf(tot / (float)K + EPS);
+    return __builtin_amdgcn_rsqf(tot * (1.0f / (float)K) + EPS);  // v_rsq_f32 (1 ulp)
 }
 
 // Two 1 KiB chunks (c, c + 1) of a 16-row block against the staged operands: a quad of four
@@ -578,7 +580,7 @@ __device__ __forceinline__ void reduce_math_n(Shared& S, const float (&acc)[N], 
 
 __device__ __forceinline__ void norm_rope(float& a, float& b, float w0, float w1, float c, float sn) {
     const float ss = wave_sum(a * a + b * b);
-    const float scale = 1.0f / sqrtf(ss / (float)HD + EPS);
+    const float scale = __builtin_amdgcn_rsqf(ss * (1.0f / (float)HD) + EPS);  // v_rsq_f32 (1 ulp)
     a = a * scale * w0;
     b = b * scale * w1;
     const float a2 = a * c - b * sn, b2 = b * c + a * sn;
@@ -597,27 +599,28 @@ __device__ __forceinline__ int att_slot(int T, int c, int mw) { return 16 * (4 *
 
 __device__ __forceinline__ void load_kv_block(uint4 (&kt)[ATT_NT][4], uint4 (&vr)[ATT_SPQ], const uint16_t* kb,
                                               const uint16_t* vb, int j0, int b0, int nprior, int tid) {
+    // Buffer loads over the split's cached rows j0 .. j0 + nprior - 1: a load past them returns
+    // zeros without touching memory, so every lane issues the same loads with no branches.
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(kb + (size_t)j0 * HD), (short)0, nprior * HD * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(vb + (size_t)j0 * HD), (short)0, nprior * HD * 2, 0x00020000);
     const int lane = tid % 64, mw = tid / 64, c = lane & 15, kq = lane >> 4, quad = tid / 16, ql = tid % 16;
 #pragma unroll
     for (int T = 0; T < ATT_NT; ++T) {
-        const int p = b0 + att_slot(T, c, mw);
+        // Columns of tile 2 past i = ATT_SPQ - 1 hold no slot: their offset is pushed past the buffer.
+        const int p = 4 * T + (c >> 2) < ATT_SPQ ? b0 + att_slot(T, c, mw) : (1 << 20);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) kt[T][j] = make_uint4(0u, 0u, 0u, 0u);
-        if (4 * T + (c >> 2) < ATT_SPQ && p < nprior) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) kt[T][j] = *(const uint4*)(kb + (size_t)(j0 + p) * HD + 32 * j + 8 * kq);
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(krs, (p * HD + 32 * j + 8 * kq) * 2, 0, 0);
+            kt[T][j] = make_uint4(v.x, v.y, v.z, v.w);
         }
     }
 #pragma unroll
     for (int i = 0; i < ATT_SPQ; ++i) {
-        const int p = b0 + quad + ATT_QW * i;
-        vr[i] = make_uint4(0u, 0u, 0u, 0u);
-        if (p < nprior) vr[i] = *(const uint4*)(vb + (size_t)(j0 + p) * HD + 8 * ql);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(vrs, ((b0 + quad + ATT_QW * i) * HD + 8 * ql) * 2, 0, 0);
+        vr[i] = make_uint4(v.x, v.y, v.z, v.w);
     }
 }
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ h8 as_h8(uint4 v) { return __builtin_bit_cast(h8, u32x4{v.x, v.y, v.z, v.w}); }
 // Eight fp32 values that are exact in fp16, packed as fp16.
 __device__ __forceinline__ uint4 pack8_f16(const float* f) {
@@ -769,6 +772,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 stage_c<FMT, H>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[2] = {0.f, 0.f}, y[2] = {0.f, 0.f};
                 if (math) mac_blocks<FMT, CW2, 2>(S, wx, mw, lane, acc);
+                PK_TRACE(l, 28);
                 reduce_math_n<MATH, 2>(S, acc, y);
                 if (wave == 0) {  // rows 2i, 2i + 1 of a block in packet i (even lanes)
                     const float rs = norm_scale<H>(S);
@@ -780,6 +784,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         st64(ll + QKVP + w * 8 + lane / 2, pack2(y[1], n1, r + 1));
                     }
                 }
+                PK_TRACE(l, 30);
                 if (math) load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
             }
             PK_TRACE(l, 2);
@@ -859,16 +864,18 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         const int nb = min(ATT_BLOCK, ntot - b0);
                         if (b0 > 0) load_kv_block(kt, vr, kb, vb, j0, b0, nprior, tid);
                         // The new row (block slot pos - j0 - b0) comes from LDS, not from the cache.
-                        const int pnew = tail ? pos - j0 - b0 : -1;
+                        if (tail) {
+                            const int pnew = pos - j0 - b0;
 #pragma unroll
-                        for (int T = 0; T < ATT_NT; ++T)
-                            if (4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) == pnew) {
+                            for (int T = 0; T < ATT_NT; ++T)
+                                if (4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) == pnew) {
 #pragma unroll
-                                for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail + 32 * j + 8 * kq);
-                            }
+                                    for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail + 32 * j + 8 * kq);
+                                }
 #pragma unroll
-                        for (int i = 0; i < ATT_SPQ; ++i)
-                            if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail + 8 * ql);
+                            for (int i = 0; i < ATT_SPQ; ++i)
+                                if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail + 8 * ql);
+                        }
                         // D[variant][slot]: lane l holds rows 4 (l / 16) + r, i.e. variant r.
                         float sc[2][ATT_NT];
 #pragma unroll
@@ -908,6 +915,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         // The probabilities of this wave's slots were written by its own lanes 0-15:
                         // a wave's LDS accesses complete in order, so no barrier is needed.
                         __builtin_amdgcn_wave_barrier();
+                        PK_TRACE(l, 27);
 #pragma unroll
                         for (int i = 0; i < ATT_SPQ; ++i) {
                             const float p0 = S.pw[mw][0][kq][i], p1 = S.pw[mw][1][kq][i];
@@ -924,6 +932,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         }
                         __builtin_amdgcn_wave_barrier();
                     }
+                    PK_TRACE(l, 29);
                     // The wave's 4 quarter-waves (lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same
                     // dims) share the running maximum: their sums add.
 #pragma unroll
@@ -1116,6 +1125,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE(l, 13);
                 float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
                 if (math) mac_blocks<FMT, CW2, 3>(S, wgu, mw, lane, acc);
+                PK_TRACE(l, 26);
                 reduce_math_n<MATH, 3>(S, acc, y);
                 PK_TRACE(l, 14);
                 if (wave == 0) {

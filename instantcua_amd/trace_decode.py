@@ -32,10 +32,14 @@ from instantcua_amd.modelfile import WeightFormat  # noqa: E402
 LAYER_POINTS = [
     (0, "math", "layer start (QKV stage entered)"),
     (1, "exch", "x polled (workgroups 128..255)"),
-    (2, "math", "q|k|v published, K/V rows requested"),
+    (28, "math", "QKV matrix-core sums (before the reduction)"),
+    (30, "math", "q|k|v published"),
+    (2, "math", "K/V rows requested"),
     (3, "exch", "q|k|v of the group polled"),
     (21, "math", "attention operands built"),
     (25, "math", "K/V rows landed"),
+    (27, "math", "scores and softmax done (last block)"),
+    (29, "math", "P.V done"),
     (22, "math", "attention loop done"),
     (20, "math", "split partial published"),
     (5, "exch", "partials polled (mergers 224..255)"),
@@ -45,6 +49,7 @@ LAYER_POINTS = [
     (8, "math", "O rows + residual published"),
     (9, "exch", "x' polled"),
     (13, "math", "x' staged (RMSNorm weights applied)"),
+    (26, "math", "gate|up matrix-core sums (before the reduction)"),
     (14, "math", "gate|up matrix-core sums reduced"),
     (10, "math", "SwiGLU published"),
     (11, "exch", "h half polled"),
