@@ -158,33 +158,64 @@ def run_q8_prefill(img):
             "prefill_mfma_frac": round(PREFILL_FLOPS / (ms * 1e-3) / MFMA_F16_PEAK, 4)}
 
 
+def forced_compare(e, n_prompt, fixture, n, first_logits=None):
+    """Compares the first n greedy tokens of the engine's decode (token 0 from the prefill) with an
+    oracle fixture, every step: a divergence counts as a near-tie when the oracle's top-1/top-2
+    margin at that step is below 1e-3 of its top-1 logit, and the decode then continues
+    teacher-forced from the oracle's token (icua_set_position) so that the later steps are
+    compared too.  Untimed; it rewrites the cache rows from the first near-tie on."""
+    path = os.path.join(ROOT, "tests", "golden", fixture)
+    if not os.path.exists(path):
+        return None
+    with np.load(path, allow_pickle=False) as z:
+        ref, margins, top1, first = z["greedy"], z["margins"], z["top1"], z["first_logits"]
+    n = min(n, ref.size)
+    out = {"fixture": fixture, "steps_compared": n}
+    if first_logits is not None:
+        out["first_logits_rel_err"] = float(np.max(np.abs(first_logits.astype(np.float64) - first))
+                                            / np.max(np.abs(first)))
+    got, ties, i = e.tokens(n), [], 0
+    while True:
+        diff = np.nonzero(got[i:n] != ref[i:n])[0]
+        if diff.size == 0:
+            break
+        j = i + int(diff[0])
+        if margins[j] >= 1e-3 * max(abs(float(top1[j])), 1.0):
+            out.update(identical=False, first_divergence=j, oracle_margin=float(margins[j]))
+            return out
+        ties.append(j)
+        if j == n - 1:
+            break
+        e.set_position(n_prompt + j, int(ref[j]), j + 1, n)
+        e.decode_steps(n - 1 - j)
+        got, i = e.tokens(n), j + 1
+    out.update(identical=True, oracle_near_ties_teacher_forced=ties)
+    return out
+
+
 def run_text_context(img, steps=256):
     """The 1024-token text workload: prefill of 1024 random ids, then steps - 1 greedy decode steps
-    (one launch of the persistent kernel), the tokens checked against the oracle fixture."""
+    (one launch of the persistent kernel), every token checked against the oracle fixture."""
     toks = synth.random_tokens(1024, "c3-prompt")
     e = eng.Engine(flags=0, image=img, max_context=toks.size + steps + 8, max_steps=steps)
     e.eos = (-1, -1)
-    e.prefill(toks, max_new=steps)  # loads the code objects
+    e.prefill(toks, max_new=steps, write_logits=True)  # loads the code objects
+    first = e.logits(1)[0].copy()
     e.prefill(toks, max_new=steps)
     prefill_ms = e.last_timing["prefill_ms"]
     e.decode_steps(steps - 1)
     dec_ms = e.last_timing["decode_ms"]
-    got = e.tokens(steps)
     persistent = e.last_decode_persistent
+    parity = forced_compare(e, toks.size, "oracle_c3_28layer.npz", steps, first)
     e.close()
     launch_bytes = sum(weight_bytes_per_token() + kv_bytes_per_token(toks.size + i + 1) for i in range(steps - 1))
     out = {"workload": "28-layer q4 decoder, 1024-token text prefill + 255 greedy decode steps",
            "prefill_tok_s": round(toks.size / (prefill_ms / 1e3), 1), "prefill_ms": round(prefill_ms, 3),
            "decode_tok_s": round((steps - 1) / (dec_ms / 1e3), 1), "decode_us_per_token": round(dec_ms * 1e3 / (steps - 1), 1),
-           "decode_roofline_frac": round(launch_bytes / (dec_ms * 1e-3) / HBM_PEAK, 4), "persistent": persistent}
-    fx = os.path.join(ROOT, "tests", "golden", "oracle_c3_28layer.npz")
-    if os.path.exists(fx):
-        with np.load(fx, allow_pickle=False) as z:
-            ref = z["greedy"]
-        same = int(np.argmax(np.concatenate([got != ref, [True]])))
-        out["greedy_identical_to_oracle_fixture"] = f"{same}/{steps}"
+           "decode_roofline_frac": round(launch_bytes / (dec_ms * 1e-3) / HBM_PEAK, 4), "persistent": persistent,
+           "greedy_vs_oracle": parity}
     log(f"text context: prefill {out['prefill_tok_s']:.0f} tok/s, decode {out['decode_tok_s']:.0f} tok/s "
-        f"({out['decode_roofline_frac']:.3f} of roofline)")
+        f"({out['decode_roofline_frac']:.3f} of roofline); oracle parity {parity}")
     return out
 
 
@@ -489,6 +520,9 @@ def main():
     log(f"decode: {ms_per_step * 1e3:.1f} us/token ({value:.0f} tok/s), {achieved / 1e9:.0f} GB/s; "
         f"wall {wall * 1e3:.1f} ms; persistent kernel: {e.persistent_decode}")
 
+    # Parity of the timed workload itself (untimed, after the timing): its greedy tokens against
+    # the oracle fixture of the same model and prompt, every step compared.
+    parity = None if args.no_prefill else forced_compare(e, PREFILL, "oracle_c4_28layer.npz", 1 + W + K)
     g = gemv_roofline()
     e.close()
 
@@ -522,6 +556,7 @@ def main():
                                "(16 text + 32x32 visual + 3056 text, DeepStack), greedy decode",
                    "prefill_tokens": PREFILL, "context_at_timing": [PREFILL + W, PREFILL + W + K],
                    "batch": 1, "grammar_pairs": grammar, "forced_pairs_in_timed_steps": forced_pairs},
+        "greedy_vs_oracle": parity,
         "decode_roofline_frac": round(achieved / HBM_PEAK, 4),
         "decode_bytes_per_token": int(bytes_tok),
         "prefill_tok_s": None if args.no_prefill else round(PREFILL / (prefill_ms / 1e3), 1),

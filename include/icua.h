@@ -199,8 +199,11 @@ int icua_dequant(int fmt, const void* d_codes, const void* d_sb, int K, int row0
  * cols must be a multiple of the group size.  All pointers are device buffers. */
 int icua_quantize(int fmt, const float* d_m, int rows, int cols, void* d_codes, void* d_sb);
 /* icua_quantize without any device allocation.  No counterpart in the reference: it is for
- * callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that
- * forbid hipMalloc).  The q4 quantiser's per-group scratch (one byte per 64-weight group) is a
+ * callers that must not allocate device memory (serving loops, harnesses that forbid hipMalloc).
+ * It launches on the null stream and synchronises the device before returning, so it cannot be
+ * recorded into a stream capture; its first call on a device looks up the scratch array's
+ * address (hipGetSymbolAddress), so make that call outside any capture.  The q4 quantiser's
+ * per-group scratch (one byte per 64-weight group) is a
  * static device array of 8 MiB per GPU, so rows * cols / 64 must not exceed 8,388,608 (larger
  * matrices fail with an error; icua_quantize takes any size).  Every call on one GPU shares that
  * array: calls that overlap on one GPU (other host threads, other streams) race.  Each call

@@ -688,7 +688,9 @@ struct icua_engine {
 
     bool use_persistent() const { return persist_ok && !(flags & ICUA_FLAG_GRAPH_DECODE); }
 
-    int enqueue_persistent(int k) {
+    // One persistent launch: nr = 1, k single-row passes (ending early at a forced pair, which it
+    // leaves pending); nr = 2, the pending pair as one two-row pass (k = 1).
+    int enqueue_persistent(int k, int nr) {
         PersistArgs a{};
         for (int l = 0; l < layers; ++l) {
             const LayerW& w = L[l];
@@ -707,8 +709,9 @@ struct icua_engine {
         a.st = st;
         a.out_tokens = out_tokens;
         a.ll = (uint64_t*)psync;
-        HIPCK(hipMemsetAsync(psync, 0, persistent_sync_bytes(), stream));
-        HIPCK(launch_persistent(fmt, a, stream));
+        HIPCK(hipMemsetAsync(psync, 0, persistent_clear_bytes(nr), stream));
+        HIPCK(hipMemsetAsync(psync + persistent_error_slot(), 0, sizeof(unsigned), stream));
+        HIPCK(launch_persistent(fmt, nr, a, stream));
         return 0;
     }
 
@@ -912,8 +915,8 @@ struct icua_engine {
     int decode_steps(int k, double* ms_out) {
         if (k < 0) return fail("negative step count");
         bool persistent = use_persistent();
+        State s;
         if (persistent) {  // single-row passes, or a pending forced pair (run as two rows)
-            State s;
             if (read_state(s)) return -1;
             if (s.n < 1 || s.n > 2 || (s.n == 2 && !(s.flags & STATE_FLAG_GRAMMAR))) persistent = false;
         }
@@ -921,14 +924,32 @@ struct icua_engine {
         const int mt = decode_mt();
         if (!persistent && ensure_graph(mt)) return -1;
         HIPCK(hipEventRecord(ev0, stream));
+        HIPCK(hipEventRecord(ev1, stream));
         if (persistent) {
-            if (k > 0 && enqueue_persistent(k)) return -1;
+            // k passes: launches of single-row passes, and each forced grammar pair as one launch
+            // of a two-row pass (Shaders.swift:1553: the reference's n = 2 pass).  A single-row
+            // launch ends at a commit that forces a pair; the control block then holds n = 2.
+            // ev1 follows the last launch (the host reads the control block between launches).
+            int left = k;
+            while (left > 0 && !s.done) {
+                const int nr = s.n == 2 ? 2 : 1, step0 = s.step;
+                if (enqueue_persistent(nr == 2 ? 1 : left, nr)) return -1;
+                HIPCK(hipEventRecord(ev1, stream));
+                if (read_state(s)) return -1;  // waits for the launch
+                if (check_persistent()) return -1;
+                // Tokens committed, less the forced token of a pair left pending for the next pass.
+                const int passes = s.step - step0 - (s.n == 2 && !s.done ? 1 : 0);
+                if (passes <= 0) {
+                    if (s.done) break;
+                    return fail("persistent decode kernel made no progress");
+                }
+                left -= passes;
+            }
         } else {
             for (int i = 0; i < k; ++i) HIPCK(hipGraphLaunch(graph[mt == 1 ? 0 : 1], stream));
+            HIPCK(hipEventRecord(ev1, stream));
         }
-        HIPCK(hipEventRecord(ev1, stream));
         HIPCK(hipEventSynchronize(ev1));
-        if (persistent && k > 0 && check_persistent()) return -1;
         float ms = 0;
         HIPCK(hipEventElapsedTime(&ms, ev0, ev1));
         if (ms_out) *ms_out = ms;
@@ -1090,10 +1111,10 @@ int icua_generate(icua_engine* e, const int32_t* tokens, int n, int vis_offset, 
     if (e->read_state(s)) return -1;
     while (!s.done && s.step < s.maxsteps) {
         // Batches of 8 passes on the graph path (Engine.swift:771-792).  The persistent kernel
-        // runs to the stop on the device (EOS, ')', the step limit): a forced pair takes one step
-        // more than the tokens it commits, so twice the remaining tokens bound its steps.
+        // runs to the stop on the device (EOS, ')', the step limit); a pass commits at least one
+        // token, so the remaining tokens bound its passes.
         const int left = s.maxsteps - s.step;
-        const int count = e->use_persistent() ? 2 * left + 1 : std::min(8, left);
+        const int count = e->use_persistent() ? left : std::min(8, left);
         const int step0 = s.step, pos0 = s.pos;
         double ms = 0;
         if (e->decode_steps(count, &ms)) return -1;

@@ -30,13 +30,16 @@ struct PersistArgs {
     const float* final_norm;
     const float* rope;        // [maxctx][64] (cos, sin)
     uint16_t* kv;             // [layers][2][NKV][maxctx][HD] fp16
-    float* x;                 // residual row [H]: the next token's embedding, in and out
+    float* x;                 // residual rows [2][H]: the next pass's token embeddings, in and out
     State* st;
     int* out_tokens;
     uint64_t* ll;             // packet area of persistent_sync_bytes(), zeroed before the launch
 };
 
-hipError_t launch_persistent(int fmt, const PersistArgs& a, hipStream_t s);
+// nr = 1: a.nsteps single-token steps (ending early, with the pair pending in the control
+// block, when a commit forces a grammar pair); nr = 2: the pending pair as one two-row pass
+// (a.nsteps must be 1), which commits the pair's next token.
+hipError_t launch_persistent(int fmt, int nr, const PersistArgs& a, hipStream_t s);
 // One-token GEMV y[N] = W x (W tiled, q4 or q8, K = 2048 or 6144) on the lm_head stage's
 // streaming schedule; hipErrorInvalidValue for other shapes or more than 160 x 256 row blocks.
 hipError_t launch_gemv_stream(int fmt, const uint8_t* w, const uint8_t* sb, const float* x, float* y, int N, int K,
@@ -45,5 +48,7 @@ hipError_t launch_gemv_stream(int fmt, const uint8_t* w, const uint8_t* sb, cons
 // the index (in 32-bit words) of its error flag: non-zero after a launch means a wait timed out.
 size_t persistent_sync_bytes();
 int persistent_error_slot();
+// Bytes of the packet area a launch of nr-row passes uses (cleared before it, with the error flag).
+size_t persistent_clear_bytes(int nr);
 
 }  // namespace icua

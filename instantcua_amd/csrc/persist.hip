@@ -82,17 +82,24 @@ static_assert(FFH / 128 / MW == 6 && FFH / 64 / MW == 12, "q4 down half: 6 chunk
 
 // Packet area (64-bit packets of two values, elements 2k and 2k + 1 of a vector in packet k),
 // zeroed before every launch.  The residual after a layer is x = XP + XDP: XP carries the lower
-// half's sum added to the residual, XDP the upper half's sum.
-constexpr int XP = 0;                   // residual x [H / 2] (after O: complete; after down: + lower half)
-constexpr int XDP = XP + H / 2;         // upper-half down sums [H / 2]
-constexpr int QKVP = XDP + H / 2;       // fused q|k|v [QKV / 2]
-constexpr int ATTNP = QKVP + QKV / 2;   // merged attention [H / 2]
-constexpr int HP = ATTNP + H / 2;       // SwiGLU activations [FF / 2]
-constexpr int LMP = HP + FF / 2;        // argmax partials [NWG] (index, value)
-constexpr int PARTP = LMP + NWG;        // attention partials [NKV][32][2][PART2]
-constexpr int PACKETS = PARTP + NKV * ATT_SPLITS * 2 * PART2;
-constexpr int ERRW = PACKETS * 2;       // error flag (32-bit word index)
-constexpr int GROUP_PARTS = ATT_SPLITS * 2 * PART2;  // 4160 packets of one group's partials
+// half's sum added to the residual, XDP the upper half's sum.  A pass of NR rows keeps NR copies
+// of each vector area, row after row (row t of a vector of n packets at area + t n).
+template <int NR>
+struct Pk {
+    static constexpr int XP = 0;                        // residual x [NR][H / 2] (after O: complete; after down: + lower half)
+    static constexpr int XDP = XP + NR * H / 2;         // upper-half down sums [NR][H / 2]
+    static constexpr int QKVP = XDP + NR * H / 2;       // fused q|k|v [NR][QKV / 2]
+    static constexpr int ATTNP = QKVP + NR * QKV / 2;   // merged attention [NR][H / 2]
+    static constexpr int HP = ATTNP + NR * H / 2;       // SwiGLU activations [NR][FF / 2]
+    static constexpr int LMP = HP + NR * FF / 2;        // argmax partials [NWG] (index, value)
+    static constexpr int PARTP = LMP + NWG;             // attention partials [NKV][32][NR][2][PART2]
+    static constexpr int GROUP_PARTS = ATT_SPLITS * NR * 2 * PART2;  // packets of one group's partials
+    static constexpr int PACKETS = PARTP + NKV * GROUP_PARTS;
+};
+constexpr int ERRW = Pk<2>::PACKETS * 2;  // error flag (32-bit word index), past either layout
+// The single-row layout's areas.
+constexpr int XP = Pk<1>::XP, XDP = Pk<1>::XDP, QKVP = Pk<1>::QKVP, ATTNP = Pk<1>::ATTNP, HP = Pk<1>::HP,
+              LMP = Pk<1>::LMP, PARTP = Pk<1>::PARTP, GROUP_PARTS = Pk<1>::GROUP_PARTS;
 
 // threadIdx.x behind an empty asm: per-lane address math derived from it is recomputed where it
 // is used instead of being hoisted out of the step / layer loops and held live (which spills).
@@ -241,26 +248,29 @@ constexpr int WD_CODES = (FFH / 64) * 1024, WD_SB = 16 * MW * 48;
 static_assert(((VOCAB / 16 + NWG - 1) / NWG) * WAVES * 16 * 4 <= WD_CODES + WD_SB, "lm_head partial sums fit the down block buffer");
 
 struct Shared {
-    uint8_t A[A_BYTES];       // activation operands; the merger's fp32 partials during the merge
+    // Small fields first: an LDS access reaches 64 KiB past its address register, so the fields
+    // read at fixed offsets stay within the first 64 KiB of the struct.
     uint32_t zero[4];         // operand rows 3..15 of every tile (16 zero bytes)
-    float fx[192 * 2];        // per-group (2^(e-21), sum X * 2^(e-21))
-    float red[3 * MW * 64];   // math-wave partial sums (up to 3 blocks)
-    float vec[FF];            // input vector of the current stage (fp32)
-    float emb[H];             // embedding of the token being decoded
-    float nw[H];              // RMSNorm weights of the current stage
-    float xown[16];           // residual rows of this workgroup's O / down block (workgroups < 128)
-    float xhi[16];            // the upper-half down sums of those rows from the previous layer
-    // attention: the two query heads as fp16 hi and lo parts, rows (hi 2g, hi 2g + 1, lo 2g,
-    // lo 2g + 1): the A operand rows of the score tiles
-    alignas(16) uint16_t qf[4][HD];
-    alignas(16) float pw[MW][2][4][12];  // probabilities of a math wave's slots, [head][lane / 16][i]
-    float ktail[HD], vtail[HD];
-    float sc[2][ATT_PAD];
-    float ored[MW][2][HD];
     float misc[64];
     int imisc[64];
     int fail;                 // a wait of this workgroup failed (set only then; see sync_failed)
     int go;                   // round whose split partials a watching lane has seen complete
+    float xown[2][16];        // residual rows of this workgroup's O / down block (workgroups < 128), per pass row
+    float xhi[2][16];         // the upper-half down sums of those rows from the previous layer
+    float aml[MW][8];         // per math wave and row: (m head 0, m head 1, l head 0, l head 1)
+    float fx[192 * 2];        // per-group (2^(e-21), sum X * 2^(e-21))
+    float red[6 * MW * 64];   // math-wave partial sums (up to 6 blocks: 3 blocks x 2 rows)
+    // attention: the two query heads of each pass row t as fp16 hi and lo parts, rows 4 t + (hi 2g,
+    // hi 2g + 1, lo 2g, lo 2g + 1): the A operand rows of the score tiles
+    alignas(16) uint16_t qf[8][HD];
+    alignas(16) float pw[MW][2][2][4][12];  // probabilities of a math wave's slots, [row][head][lane / 16][i]
+    float ktail[2][HD], vtail[2][HD];      // the pass's new K / V rows (fp16 values)
+    float sc[2][ATT_PAD];
+    float ored[MW][4][HD];    // per math wave: o of (row, head)
+    float nw[H];              // RMSNorm weights of the current stage
+    uint8_t A[A_BYTES];       // activation operands; the merger's fp32 partials during the merge
+    float vec[FF];            // input vector of the current stage (fp32)
+    float emb[2 * H];         // embeddings of the pass's tokens (row t at t H)
 };
 
 // Workgroup barrier that also tells every thread whether any thread's wait failed.  The flag is
@@ -286,78 +296,83 @@ __device__ __forceinline__ bool sync_failed(Shared& S, bool failed) {
 // magic constant 1.5 * 2^23 (round to nearest even, as rint); the slices are the bytes of
 // (v + 0x808080) ^ 0x808080, which three byte permutes gather into the hi / mid / lo rows.  When
 // K / 4 is not a multiple of THREADS the last unit row is held by the first waves only (whole
-// waves, so whole groups).
-template <int FMT, int K>
-__device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed) {
+// waves, so whole groups).  NRS rows (src + t K) are staged with one barrier: row t's groups
+// follow row t - 1's (group offset t K / G) and its sum of squares goes to S.misc[40 + 8 t + wave].
+template <int FMT, int K, int NRS = 1, class SH>
+__device__ __forceinline__ void stage_c(SH& S, const float* src, bool normed) {
     constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
     constexpr int TILE = (FMT == FMT_Q4) ? 192 : 96;
     constexpr int SLOT = (FMT == FMT_Q4) ? 16 : 8;  // bytes of a K-slot row
     constexpr int NU = (K / 4 + THREADS - 1) / THREADS;
     constexpr uint32_t MAGIC = 0x4B400000u;        // 1.5 * 2^23
     static_assert((K / 4) % 64 == 0, "units of whole waves");
+    static_assert(NRS * (K / G) * TILE <= A_BYTES && NRS * (K / G) * 2 <= 384, "operands fit S.A / S.fx");
     const int tid = my_tid(), lane = tid % 64, wave = wave_id();
-    float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < NU; ++j) {
-        const int u = tid + THREADS * j;
-        if ((K / 4) % THREADS != 0 && u >= K / 4) continue;
-        const float4 a4 = ((const float4*)src)[u];
-        float v[4] = {a4.x, a4.y, a4.z, a4.w};
+    for (int rw = 0; rw < NRS; ++rw) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int u = tid + THREADS * j;
+            if ((K / 4) % THREADS != 0 && u >= K / 4) continue;
+            const float4 a4 = ((const float4*)(src + rw * K))[u];
+            float v[4] = {a4.x, a4.y, a4.z, a4.w};
+            if (normed) {
+                const float4 wn = ((const float4*)S.nw)[u];
+                ss = fmaf(v[0], v[0], ss);
+                ss = fmaf(v[1], v[1], ss);
+                ss = fmaf(v[2], v[2], ss);
+                ss = fmaf(v[3], v[3], ss);
+                v[0] *= wn.x;
+                v[1] *= wn.y;
+                v[2] *= wn.z;
+                v[3] *= wn.w;
+            }
+            const float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
+            bits = max(bits, dpp_i<DPP_XOR1>(bits));
+            bits = max(bits, dpp_i<DPP_XOR2>(bits));
+            bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
+            if constexpr (G == 64) bits = max(bits, dpp_i<DPP_MIRROR>(bits));
+            // e: exponent of the group maximum, clamped so that 2^(21 - e) and 2^(e - 21) are normal
+            // (an all-zero group gives X = 0 with any e).
+            const int e = min(max(((bits >> 23) & 0xFF) - 127, -100), 126);
+            const float p = as_f32((uint32_t)(148 - e) << 23);  // 2^(21 - e)
+            uint32_t t[4];
+            int xs = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t f = as_u32(__builtin_fmaf(v[i], p, as_f32(MAGIC)));  // MAGIC + rint(v 2^(21-e))
+                xs += (int)(f - MAGIC);
+                t[i] = (f + 0x408080u) ^ 0x808080u;  // bytes: lo, mid, hi slices as int8
+            }
+            const uint32_t p01 = __builtin_amdgcn_perm(t[1], t[0], 0x05010400u);  // l0 l1 m0 m1
+            const uint32_t p23 = __builtin_amdgcn_perm(t[3], t[2], 0x05010400u);  // l2 l3 m2 m3
+            const uint32_t q01 = __builtin_amdgcn_perm(t[1], t[0], 0x0C0C0602u);  // h0 h1
+            const uint32_t q23 = __builtin_amdgcn_perm(t[3], t[2], 0x0C0C0602u);  // h2 h3
+            const uint32_t lo = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+            const uint32_t mid = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
+            const uint32_t hi = __builtin_amdgcn_perm(q23, q01, 0x05040100u);
+            xs += dpp_i<DPP_XOR1>(xs);
+            xs += dpp_i<DPP_XOR2>(xs);
+            xs += dpp_i<DPP_HALF_MIRROR>(xs);
+            if constexpr (G == 64) xs += dpp_i<DPP_MIRROR>(xs);
+            const int k0 = u * 4, gl = rw * (K / G) + k0 / G, kk = k0 % G;
+            uint8_t* A = S.A + gl * TILE;
+            const int q = kk / SLOT, j0 = kk % SLOT;
+            *(uint32_t*)(A + (3 * q + 0) * SLOT + j0) = hi;
+            *(uint32_t*)(A + (3 * q + 1) * SLOT + j0) = mid;
+            *(uint32_t*)(A + (3 * q + 2) * SLOT + j0) = lo;
+            if (kk == 0) {
+                const float f = as_f32((uint32_t)(106 + e) << 23);  // 2^(e - 21)
+                S.fx[gl * 2] = f;
+                S.fx[gl * 2 + 1] = (float)xs * f;
+            }
+        }
         if (normed) {
-            const float4 wn = ((const float4*)S.nw)[u];
-            ss = fmaf(v[0], v[0], ss);
-            ss = fmaf(v[1], v[1], ss);
-            ss = fmaf(v[2], v[2], ss);
-            ss = fmaf(v[3], v[3], ss);
-            v[0] *= wn.x;
-            v[1] *= wn.y;
-            v[2] *= wn.z;
-            v[3] *= wn.w;
+            ss = wave_sum(ss);
+            if (lane == 0) S.misc[40 + 8 * rw + wave] = ss;
         }
-        const float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
-        bits = max(bits, dpp_i<DPP_XOR1>(bits));
-        bits = max(bits, dpp_i<DPP_XOR2>(bits));
-        bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
-        if constexpr (G == 64) bits = max(bits, dpp_i<DPP_MIRROR>(bits));
-        // e: exponent of the group maximum, clamped so that 2^(21 - e) and 2^(e - 21) are normal
-        // (an all-zero group gives X = 0 with any e).
-        const int e = min(max(((bits >> 23) & 0xFF) - 127, -100), 126);
-        const float p = as_f32((uint32_t)(148 - e) << 23);  // 2^(21 - e)
-        uint32_t t[4];
-        int xs = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t f = as_u32(__builtin_fmaf(v[i], p, as_f32(MAGIC)));  // MAGIC + rint(v 2^(21-e))
-            xs += (int)(f - MAGIC);
-            t[i] = (f + 0x408080u) ^ 0x808080u;  // bytes: lo, mid, hi slices as int8
-        }
-        const uint32_t p01 = __builtin_amdgcn_perm(t[1], t[0], 0x05010400u);  // l0 l1 m0 m1
-        const uint32_t p23 = __builtin_amdgcn_perm(t[3], t[2], 0x05010400u);  // l2 l3 m2 m3
-        const uint32_t q01 = __builtin_amdgcn_perm(t[1], t[0], 0x0C0C0602u);  // h0 h1
-        const uint32_t q23 = __builtin_amdgcn_perm(t[3], t[2], 0x0C0C0602u);  // h2 h3
-        const uint32_t lo = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
-        const uint32_t mid = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
-        const uint32_t hi = __builtin_amdgcn_perm(q23, q01, 0x05040100u);
-        xs += dpp_i<DPP_XOR1>(xs);
-        xs += dpp_i<DPP_XOR2>(xs);
-        xs += dpp_i<DPP_HALF_MIRROR>(xs);
-        if constexpr (G == 64) xs += dpp_i<DPP_MIRROR>(xs);
-        const int k0 = u * 4, gl = k0 / G, kk = k0 % G;
-        uint8_t* A = S.A + gl * TILE;
-        const int q = kk / SLOT, j0 = kk % SLOT;
-        *(uint32_t*)(A + (3 * q + 0) * SLOT + j0) = hi;
-        *(uint32_t*)(A + (3 * q + 1) * SLOT + j0) = mid;
-        *(uint32_t*)(A + (3 * q + 2) * SLOT + j0) = lo;
-        if (kk == 0) {
-            const float f = as_f32((uint32_t)(106 + e) << 23);  // 2^(e - 21)
-            S.fx[gl * 2] = f;
-            S.fx[gl * 2 + 1] = (float)xs * f;
-        }
-    }
-    if (normed) {
-        ss = wave_sum(ss);
-        if (lane == 0) S.misc[40 + wave] = ss;
     }
     __syncthreads();
 }
@@ -365,9 +380,9 @@ __device__ __forceinline__ void stage_c(Shared& S, const float* src, bool normed
 // RMS factor of the last normed staging of a K-vector: 1/sqrt(mean(v^2) + eps) from the eight
 // waves' sums (valid after the staging's barrier, until the next normed staging).
 template <int K>
-__device__ __forceinline__ float norm_scale(const Shared& S) {
-    const float tot = ((S.misc[40] + S.misc[41]) + (S.misc[42] + S.misc[43])) +
-                      ((S.misc[44] + S.misc[45]) + (S.misc[46] + S.misc[47]));
+__device__ __forceinline__ float norm_scale(const Shared& S, int t = 0) {
+    const float* m = S.misc + 40 + 8 * t;  // row t of a multi-row staging
+    const float tot = ((m[0] + m[1]) + (m[2] + m[3])) + ((m[4] + m[5]) + (m[6] + m[7]));
     return __builtin_amdgcn_rsqf(tot * (1.0f / (float)K) + EPS);  // v_rsq_f32 (1 ulp)
 }
 
@@ -384,13 +399,14 @@ struct QuadOps {
     float f, fX;
 };
 
-template <int FMT>
-__device__ __forceinline__ QuadOps<FMT> quad_load(const Shared& S, int c, int lane) {
+template <int FMT, class SH>
+__device__ __forceinline__ QuadOps<FMT> quad_load(const SH& S, int c, int lane, int g0 = 0) {
     QuadOps<FMT> o;
     const int r = lane & 15, q = lane >> 4, sl = r & 3, jr = r >> 2;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int gl = 2 * c + j;  // groups 2c, 2c + 1 (chunk c), 2c + 2, 2c + 3 (chunk c + 1)
+        // groups 2c, 2c + 1 (chunk c), 2c + 2, 2c + 3 (chunk c + 1) of the row staged at group g0
+        const int gl = g0 + 2 * c + j;
         const bool on = jr == j && sl < 3;
         if constexpr (FMT == FMT_Q4) {
             const uint8_t* ap = on ? S.A + gl * 192 + (3 * q + sl) * 16 : (const uint8_t*)S.zero;
@@ -401,7 +417,7 @@ __device__ __forceinline__ QuadOps<FMT> quad_load(const Shared& S, int c, int la
             o.A[j] = v4i{(int)(uint32_t)v, (int)(uint32_t)((uint64_t)v >> 32), 0, 0};
         }
     }
-    const float2 fx = *(const float2*)(S.fx + (2 * c + q) * 2);
+    const float2 fx = *(const float2*)(S.fx + (g0 + 2 * c + q) * 2);
     o.f = fx.x;
     o.fX = fx.y;
     return o;
@@ -488,12 +504,13 @@ struct WB {
 // operand tiles are read from LDS once for all blocks.  acc[b] is block b's total of this wave in
 // lanes 0-15.
 template <int FMT, int CW, int NB>
-__device__ __forceinline__ void mac_blocks(const Shared& S, const WB<FMT, CW>* wb, int mw, int lane, float (&acc)[NB]) {
+__device__ __forceinline__ void mac_blocks(const Shared& S, const WB<FMT, CW>* wb, int mw, int lane, float (&acc)[NB],
+                                           int g0 = 0) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.f;
 #pragma unroll
     for (int p = 0; p < CW / 2; ++p) {
-        const QuadOps<FMT> o = quad_load<FMT>(S, mw * CW + 2 * p, lane);
+        const QuadOps<FMT> o = quad_load<FMT>(S, mw * CW + 2 * p, lane, g0);
         v4i C[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) C[b] = quad_mfma<FMT>(o, wb[b].wv[2 * p], wb[b].wv[2 * p + 1]);
@@ -528,7 +545,7 @@ __device__ __forceinline__ void wd_request(uint8_t* wdb, const uint8_t* wd, cons
 // quad (two chunks) at a time; the total in lanes 0-15.  The wave's scale columns in LDS are
 // 16 rows x 48 B: (scale, bias) words of its 12 q4 groups, or the scales of its 24 q8 groups.
 template <int FMT>
-__device__ __forceinline__ float wd_mac_lds(const Shared& S, const uint8_t* wdb, int mw, int lane) {
+__device__ __forceinline__ float wd_mac_lds(const Shared& S, const uint8_t* wdb, int mw, int lane, int g0 = 0) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CWD = FFH / CHK / MW;
     static_assert(CWD % 2 == 0, "whole quads");
@@ -540,7 +557,7 @@ __device__ __forceinline__ float wd_mac_lds(const Shared& S, const uint8_t* wdb,
         const uint4 w1 = *(const uint4*)(wdb + (mw * CWD + 2 * p + 1) * 1024 + lane * 16);
         const int gq = 4 * p + (lane >> 4);  // the lane's group among the wave's
         const uint32_t sq = FMT == FMT_Q4 ? *(const uint32_t*)(sbr + 4 * gq) : (uint32_t) * (const uint16_t*)(sbr + 2 * gq);
-        const QuadOps<FMT> o = quad_load<FMT>(S, mw * CWD + 2 * p, lane);
+        const QuadOps<FMT> o = quad_load<FMT>(S, mw * CWD + 2 * p, lane, g0);
         acc = quad_scale<FMT>(o, quad_mfma<FMT>(o, w0, w1), sq, acc);
     }
     return quad_rows(acc);
@@ -559,10 +576,10 @@ __device__ __forceinline__ float reduce_math(Shared& S, float acc) {
     return s;
 }
 
-// reduce_math for N <= 3 blocks at once (one barrier).
+// reduce_math for N <= 6 blocks at once (one barrier).
 template <bool MATH, int N>
 __device__ __forceinline__ void reduce_math_n(Shared& S, const float (&acc)[N], float (&out)[N]) {
-    static_assert(N <= 3, "S.red holds three blocks");
+    static_assert(N <= 6, "S.red holds six blocks");
     const int tid = my_tid(), lane = tid % 64, wave = wave_id();
     if (MATH) {
 #pragma unroll
@@ -662,13 +679,14 @@ __device__ uint64_t g_trace[NWG][MAX_LAYERS + 1][32];
 #define PK_TRACE(layer, ev) PK_TRACE_AT(layer, ev, 0)
 #define PK_TRACE_X(layer, ev) PK_TRACE_AT(layer, ev, MT)
 
-// The decode loop of one role (MATH: waves 0-3, else waves 4-7).  Each role is compiled as its
-// own copy of the loop, so the register allocator never has to fit the math waves' weight tiles
-// and the exchange waves' poll buffers side by side.  Both copies execute the same sequence of
-// workgroup barriers (s_barrier counts waves, not call sites), so they stay in lockstep.
+// The decode loop of one role (MATH: waves 0-3, else waves 4-7): a.nsteps single-token steps.
+// Each role is compiled as its own copy of the loop, so the register allocator never has to fit
+// the math waves' weight tiles and the exchange waves' poll buffers side by side.  Both copies
+// execute the same sequence of workgroup barriers (s_barrier counts waves, not call sites), so
+// they stay in lockstep.  A commit that forces a grammar pair ends the loop with the pair pending
+// (control block n = 2): the pair runs as one two-row pass (decode_pass_loop) in the next launch.
 template <int FMT, bool MATH>
-__device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp,
-                                            bool pair) {
+__device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
     constexpr int NRB = VOCAB / 16;     // lm_head row blocks
@@ -680,13 +698,6 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     State* st = a.st;
     const int maxsteps = st->maxsteps, eos0 = st->eos0, eos1 = st->eos1, maxctx = st->maxctx;
     const bool grammar = (st->flags & STATE_FLAG_GRAMMAR) != 0;
-    // A forced pair (grammar pairs, Shaders.swift:1537-1561) is the reference's two-token pass:
-    // here it runs as two single-row steps.  `skip` marks a step whose token is the first of a
-    // pair: its logits are not used, and the forced token `pend` (already committed) follows at
-    // the next slot.  A launch that starts with a pair (n = 2) reads the forced token back from
-    // the token list.
-    bool skip = pair;
-    int pend = pair ? a.out_tokens[stp - 1] : -1;
     const int L = a.nlayers;
     float nreg[8];  // math threads: norm weights of the next normed stage (8 each)
     if (MATH) load_norm8(nreg, a.layers[0].attn_norm + my_tid() * 8);
@@ -821,10 +832,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 } else if (wave == 2 && tail) {
                     float k0 = S.vec[2 * HD + lane], k1 = S.vec[2 * HD + lane + 64];
                     norm_rope(k0, k1, kn0, kn1, rc, rs);
-                    S.ktail[lane] = h2f(f2h(k0));
-                    S.ktail[lane + 64] = h2f(f2h(k1));
-                    S.vtail[lane] = h2f(f2h(S.vec[3 * HD + lane]));
-                    S.vtail[lane + 64] = h2f(f2h(S.vec[3 * HD + lane + 64]));
+                    S.ktail[0][lane] = h2f(f2h(k0));
+                    S.ktail[0][lane + 64] = h2f(f2h(k1));
+                    S.vtail[0][lane] = h2f(f2h(S.vec[3 * HD + lane]));
+                    S.vtail[0][lane + 64] = h2f(f2h(S.vec[3 * HD + lane + 64]));
                 }
             }
             __syncthreads();
@@ -832,7 +843,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 // The new cache row (fp16), device-scope stores by exchange threads, acknowledged
                 // before this workgroup publishes its partials.
                 const int c = tid - MT;
-                const float* src = c < 64 ? S.ktail : S.vtail;
+                const float* src = c < 64 ? S.ktail[0] : S.vtail[0];
                 uint16_t* dst = (uint16_t*)(c < 64 ? kb : vb) + (size_t)pos * HD;
                 const int d = 2 * (c % 64);
                 const uint32_t v = (uint32_t)f2h(src[d]) | ((uint32_t)f2h(src[d + 1]) << 16);
@@ -870,11 +881,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                             for (int T = 0; T < ATT_NT; ++T)
                                 if (4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) == pnew) {
 #pragma unroll
-                                    for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail + 32 * j + 8 * kq);
+                                    for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail[0] + 32 * j + 8 * kq);
                                 }
 #pragma unroll
                             for (int i = 0; i < ATT_SPQ; ++i)
-                                if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail + 8 * ql);
+                                if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail[0] + 8 * ql);
                         }
                         // D[variant][slot]: lane l holds rows 4 (l / 16) + r, i.e. variant r.
                         float sc[2][ATT_NT];
@@ -909,7 +920,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                             for (int d = 0; d < 8; ++d) o[hh][d] *= corr;
                             if (lane < 16) {
 #pragma unroll
-                                for (int T = 0; T < ATT_NT; ++T) S.pw[mw][hh][c & 3][4 * T + (c >> 2)] = sc[hh][T];
+                                for (int T = 0; T < ATT_NT; ++T) S.pw[mw][0][hh][c & 3][4 * T + (c >> 2)] = sc[hh][T];
                             }
                         }
                         // The probabilities of this wave's slots were written by its own lanes 0-15:
@@ -918,7 +929,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         PK_TRACE(l, 27);
 #pragma unroll
                         for (int i = 0; i < ATT_SPQ; ++i) {
-                            const float p0 = S.pw[mw][0][kq][i], p1 = S.pw[mw][1][kq][i];
+                            const float p0 = S.pw[mw][0][0][kq][i], p1 = S.pw[mw][0][1][kq][i];
                             const uint32_t dv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
@@ -1068,9 +1079,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 bool ok = true;
                 if (w < H / 16 && !math) {
                     if (l > 0)
-                        ok = poll_vec<1>(ll + XDP + w * 8, 8, 2 * r, S.xhi, err);
+                        ok = poll_vec<1>(ll + XDP + w * 8, 8, 2 * r, S.xhi[0], err);
                     else if (tid - MT < 16)
-                        S.xhi[tid - MT] = 0.f;
+                        S.xhi[0][tid - MT] = 0.f;
                     ok = ok && poll_vec<H / 2 / CT>(ll + ATTNP, H / 2, r + 1, S.vec, err);
                 }
                 if (math) {
@@ -1086,10 +1097,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 if (math) mac_blocks<FMT, CW2, 1>(S, wx, mw, lane, acc1);
                 const float y = reduce_math<MATH>(S, acc1[0]);
                 if (wave == 0) {  // the owner keeps the residual as published (even rows rounded)
-                    const float xn = lane < 16 ? (S.xown[lane] + S.xhi[lane]) + y : 0.f;
+                    const float xn = lane < 16 ? (S.xown[0][lane] + S.xhi[0][lane]) + y : 0.f;
                     const float xo = xor1(xn);
                     if (lane < 16) {
-                        S.xown[lane] = (lane & 1) ? xn : q19(xn);
+                        S.xown[0][lane] = (lane & 1) ? xn : q19(xn);
                         if (!(lane & 1)) st64(ll + XP + w * 8 + lane / 2, pack2(xn, xo, 2 * r + 1));
                     }
                 }
@@ -1167,37 +1178,15 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 const float y = reduce_math<MATH>(S, yd);
                 PK_TRACE(l, 19);
                 if (wave == 0) {
-                    const float v = lane < 16 ? (half == 0 ? S.xown[lane] + y : y) : 0.f;
+                    const float v = lane < 16 ? (half == 0 ? S.xown[0][lane] + y : y) : 0.f;
                     const float vn = xor1(v);
                     if (lane < 16) {
-                        if (half == 0) S.xown[lane] = (lane & 1) ? v : q19(v);
+                        if (half == 0) S.xown[0][lane] = (lane & 1) ? v : q19(v);
                         if (!(lane & 1)) st64(ll + (half == 0 ? XP : XDP) + rb * 8 + lane / 2, pack2(v, vn, 2 * r + 2));
                     }
                 }
                 PK_TRACE(l, 12);
             }
-        }
-
-        if (skip) {
-            // ---------------- first token of a forced pair: no lm_head, no commit -------------
-            const int tid = my_tid();
-            skip = false;
-            pos += 1;
-            const int tok = pend;
-            pend = -1;
-            if (w == 0 && tid == 0) {
-                st->pos = pos;
-                st->n = 1;
-                st->vis_offset = -1;
-                st->logits_rows = 0;
-            }
-            for (int i = tid; i < H; i += THREADS) S.emb[i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)tok, i, H);
-            __syncthreads();
-            if (tid < 16 && w < H / 16) S.xown[tid] = S.emb[w * 16 + tid];
-            if (w == 0 && step == a.nsteps - 1)
-                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row for the host
-            if (MATH) load_norm8(nreg, a.layers[0].attn_norm + tid * 8);  // for the next step
-            continue;
         }
 
         // ---------------- final RMSNorm + lm_head + per-workgroup argmax ---------------------
@@ -1304,6 +1293,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             int tok = S.imisc[0];
             for (int ww = 1; ww < WAVES; ++ww) argmax_merge(b2, tok, S.misc[ww], S.imisc[ww]);
             bool stop;
+            int forced = -1;  // a forced pair's second token: the pair is the next launch's pass
             if (stp >= maxsteps) {  // nothing may be written past out_tokens[maxsteps - 1]
                 stop = true;
             } else {
@@ -1320,18 +1310,16 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     ((stp == 1 && (tok == 3678 || tok == 7241 || tok == 12476 || tok == 10855 || tok == 11862 ||
                                    tok == 1339 || tok == 1472 || tok == 24769)) ||
                      tok == 11)) {
-                    const int forced = tok == 11 ? 220 : 7;
+                    forced = tok == 11 ? 220 : 7;
                     if (w == 0 && tid == 0) a.out_tokens[stp] = forced;
                     stp += 1;
-                    pend = forced;
-                    skip = true;
                     stop = stp >= maxsteps;  // the pair's pass would start at the step limit
                 }
             }
             if (w == 0 && tid == 0) {
                 st->pos = pos;
                 st->step = stp;
-                st->n = (skip && !stop) ? 2 : 1;
+                st->n = (forced >= 0 && !stop) ? 2 : 1;
                 st->vis_offset = -1;
                 st->logits_rows = 0;
                 if (stop) st->done = 1;
@@ -1341,13 +1329,793 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             __syncthreads();  // every thread has read S.misc / S.imisc
             for (int i = tid; i < H; i += THREADS) S.emb[i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)tok, i, H);
             __syncthreads();
-            if (tid < 16 && w < H / 16) S.xown[tid] = S.emb[w * 16 + tid];
-            if (w == 0 && step == a.nsteps - 1) {
-                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row(s) for the host
-                if (skip)
-                    for (int i = tid; i < H; i += THREADS) a.x[H + i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)pend, i, H);
+            if (tid < 16 && w < H / 16) S.xown[0][tid] = S.emb[w * 16 + tid];
+            if (w == 0 && (forced >= 0 || step == a.nsteps - 1)) {
+                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row(s) for the next launch
+                if (forced >= 0)
+                    for (int i = tid; i < H; i += THREADS) a.x[H + i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)forced, i, H);
             }
             PK_TRACE(L, 4);
+            if (forced >= 0) break;  // the pair runs as the next launch's two-row pass
+        }
+    }
+}
+
+// The same stages for passes of NR token rows, used for a forced grammar pair (NR = 2,
+// Shaders.swift:1537-1561: the reference's n = 2 pass, Shaders.swift:529-595 / 735-788 /
+// 1304-1418): the two tokens at slots pos, pos + 1 go through every layer together, so each
+// weight tile is streamed once for both rows.  Every GEMV stage stages NR rows and multiplies each
+// against the same weight registers; the attention scores all NR rows' query heads in one
+// matrix-core product (row 1 also sees slot pos + 1, row 0 does not); lm_head and the commit use
+// the last row.  The packet areas hold NR copies of each vector (Pk<NR>).  The single-row loop
+// above stays a separate function: its register allocation is tuned, and the row loops here
+// would cost it spills.
+template <int FMT, bool MATH, int NR>
+__device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp) {
+    using PK = Pk<NR>;
+    constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
+    constexpr int G = (FMT == FMT_Q4) ? 64 : 32;  // quantisation group (staged operand groups)
+    constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
+    constexpr int NRB = VOCAB / 16;     // lm_head row blocks
+    constexpr int CW8 = H / CHK / WAVES;  // lm_head chunks per wave (all eight waves)
+    constexpr int LM_DEPTH = 4;           // lm_head blocks in flight per wave
+    constexpr int LM_BLOCKS = (NRB + NWG - 1) / NWG;  // 38 block slots per workgroup
+    constexpr int NV = 4 * NR;            // query-operand variants: row, hi / lo, head
+    uint64_t* ll = a.ll;
+    unsigned* err = (unsigned*)a.ll + ERRW;
+    State* st = a.st;
+    const int maxsteps = st->maxsteps, eos0 = st->eos0, eos1 = st->eos1, maxctx = st->maxctx;
+    const bool grammar = (st->flags & STATE_FLAG_GRAMMAR) != 0;
+    const int L = a.nlayers;
+    float nreg[8];  // math threads: norm weights of the next normed stage (8 each)
+    if (MATH) load_norm8(nreg, a.layers[0].attn_norm + my_tid() * 8);
+    // Math waves: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127) of
+    // the current layer.
+    WB<FMT, CW2> wx[2];
+    __syncthreads();
+
+    for (int step = 0; step < a.nsteps; ++step) {
+        if (pos + NR > maxctx) break;  // the commit stops earlier; guards the cache rows
+        if (MATH) {
+            wx[0].forget();
+            wx[1].forget();
+        }
+        if (MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
+            wx[0].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w - NWG / 2, H, wave_id(), my_tid() % 64);
+            wx[1].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w, H, wave_id(), my_tid() % 64);
+        }
+        for (int l = 0; l < L; ++l) {
+            const LayerPtrs& P = a.layers[l];
+            const unsigned r = (unsigned)(step * L + l);  // round of this layer
+            const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+            constexpr bool math = MATH;
+            const int mw = wave;  // math wave index (valid when math)
+
+            // Attention geometry of this workgroup: KV group g, split s.  The pos + NR rows of the
+            // group (rows < pos and the pass's new rows) are spread evenly over the 32 splits; the
+            // split holding row pos + t writes it.  Only rows < pos are loaded from the cache.
+            // Query row t sees rows <= pos + t: ntot_t of this split's rows.
+            const int g = w % NKV, s = w / NKV;
+            const int tot = pos + NR;
+            const int chunk = (tot + ATT_SPLITS - 1) / ATT_SPLITS;
+            const int j0 = min(s * chunk, tot), j1 = min(j0 + chunk, tot);
+            // Recomputed where used (values kept live across the layer would cost registers).
+            auto tl = [&](int t) { return (j0 <= pos + t) && (pos + t < j1); };  // row pos + t is in this split
+            const bool tail = (j0 < pos + NR) && (pos < j1);                       // a new row is in this split
+            const int nprior = max(0, min(j1, pos) - j0);
+            const int ntot = j1 - j0;
+            const uint16_t* kb = a.kv + ((size_t)(l * 2 + 0) * NKV + g) * a.maxctx * HD;
+            const uint16_t* vb = a.kv + ((size_t)(l * 2 + 1) * NKV + g) * a.maxctx * HD;
+            const int quad = tid / 16, ql = tid % 16;  // math threads: 16 quarter-waves, 8 dims per lane
+
+            // Math-wave register tiles: each is requested while the exchange waves wait for the
+            // input of its stage or of an earlier one.  The down half-block streams into LDS.
+            WB<FMT, CW2> wgu[3];
+
+            // ---------------- QKV: row blocks w - 128 and w (workgroups 128..255) ------------
+            // Workgroups 0..127 need no x here.  Loads issued just before the x poll of
+            // workgroups 128..255 would queue ahead of it on their CU: their QKV blocks are
+            // requested during the previous layer's down stage (layer 0's at the start of the
+            // step) and their K/V rows after the QKV publish.
+            const bool qkv_wg = w >= NWG / 2;
+            PK_TRACE(l, 0);
+            uint4 kt[ATT_NT][4], vr[ATT_SPQ];
+            float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc[NR], rs[NR];
+            // Exchange waves poll the stage input first; math waves skip that branch and issue
+            // their loads at once.  Keeping the loads after the poll in program order lets the
+            // poll's registers and the weight tiles share the register file.
+            bool ok_in = true;
+            if (l > 0 && !math && qkv_wg) ok_in = poll_sum<NR * H / 2 / CT>(ll + PK::XP, ll + PK::XDP, 2 * r, S.vec, err);
+            if (math) {
+                // This layer's norm weights into LDS; then the QKV blocks and the loads for the
+                // stages ahead: the first block of K/V rows, the per-head norms and the rope rows,
+                // the O block and the mlp norm.
+#pragma unroll
+                for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
+                if (!qkv_wg) {
+                    wx[0].load(P.wo, P.wo_sb, w, H, mw, lane);
+                    load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
+                    // The lower down half-block of row block w into LDS: it lands long before the
+                    // x' poll that a later request would delay.
+                    wd_request<FMT>(wdb, P.wd, P.wd_sb, w, 0, mw, lane);
+                }
+                qn0 = P.q_norm[lane];
+                qn1 = P.q_norm[lane + 64];
+                kn0 = P.k_norm[lane];
+                kn1 = P.k_norm[lane + 64];
+#pragma unroll
+                for (int t = 0; t < NR; ++t) {
+                    const float* rope = a.rope + (size_t)(pos + t) * 128;
+                    rc[t] = rope[2 * lane];
+                    rs[t] = rope[2 * lane + 1];
+                }
+                load_norm8(nreg, P.mlp_norm + tid * 8);
+            }
+            if (sync_failed(S, !ok_in)) return;
+            PK_TRACE_X(l, 1);
+            if (qkv_wg) {
+                stage_c<FMT, H, NR>(S, l == 0 ? S.emb : S.vec, true);
+                float acc[2 * NR], y[2 * NR];
+#pragma unroll
+                for (int t = 0; t < NR; ++t) {
+                    float at[2] = {0.f, 0.f};
+                    if (math) mac_blocks<FMT, CW2, 2>(S, wx, mw, lane, at, t * (H / G));
+                    acc[2 * t] = at[0];
+                    acc[2 * t + 1] = at[1];
+                }
+                PK_TRACE(l, 28);
+                reduce_math_n<MATH, 2 * NR>(S, acc, y);
+                if (wave == 0) {  // rows 2i, 2i + 1 of a block in packet i (even lanes)
+#pragma unroll
+                    for (int t = 0; t < NR; ++t) {
+                        const float rsn = norm_scale<H>(S, t);
+                        const float y0 = y[2 * t] * rsn, y1 = y[2 * t + 1] * rsn;
+                        const float n0 = xor1(y0), n1 = xor1(y1);
+                        if (lane < 16 && !(lane & 1)) {
+                            uint64_t* q = ll + PK::QKVP + t * (QKV / 2);
+                            st64(q + (w - NWG / 2) * 8 + lane / 2, pack2(y0, n0, r + 1));
+                            st64(q + w * 8 + lane / 2, pack2(y1, n1, r + 1));
+                        }
+                    }
+                }
+                PK_TRACE(l, 30);
+                if (math) load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
+            }
+            PK_TRACE(l, 2);
+
+            // ---------------- attention: group g, split s ----------------------------------
+            {
+                bool ok = true;
+                if (!math)  // row t: q heads 2g, 2g+1 -> vec[512t + 0..255], k -> +256..383, v -> +384..511
+                    ok = poll_map<NR>(
+                        ll + PK::QKVP, NR * 2 * HD,
+                        [&](int k) {  // packet of gathered elements 2k, 2k + 1
+                            const int t = k / (2 * HD), e = 2 * (k % (2 * HD));
+                            return t * (QKV / 2) + (e < 2 * HD ? 2 * g * HD + e
+                                                               : e < 3 * HD ? H + g * HD + (e - 2 * HD)
+                                                                            : H + NKV * HD + g * HD + (e - 3 * HD)) / 2;
+                        },
+                        r + 1, S.vec, err);
+                if (sync_failed(S, !ok)) return;
+            }
+            PK_TRACE_X(l, 3);
+            if (math) {
+                // Query rows: wave (t, h) = (wave / 2, wave % 2) of the NR rows; then the new K/V rows
+                // of this split, a wave per row.  1/sqrt(128) and log2(e) are folded into q: scores
+                // come out in base-2 units, so every softmax exponential of this split and of the
+                // merge is one v_exp_f32.
+                if (wave < 2 * NR) {
+                    const int t = wave >> 1, hh = wave & 1;
+                    float x0 = S.vec[512 * t + hh * HD + lane], x1 = S.vec[512 * t + hh * HD + lane + 64];
+                    norm_rope(x0, x1, qn0, qn1, rc[t], rs[t]);
+                    const float qscale = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
+                    const float qa = x0 * qscale, qb = x1 * qscale;
+                    const uint16_t ha = f2h(qa), hb = f2h(qb);
+                    S.qf[4 * t + hh][lane] = ha;
+                    S.qf[4 * t + hh][lane + 64] = hb;
+                    S.qf[4 * t + 2 + hh][lane] = f2h(qa - h2f(ha));
+                    S.qf[4 * t + 2 + hh][lane + 64] = f2h(qb - h2f(hb));
+                }
+                const int kw = NR == 1 ? 2 : 0;  // first wave of the new-row normalisation
+                if (wave >= kw && wave < kw + NR && tl(wave - kw)) {
+                    const int t = wave - kw;
+                    float k0 = S.vec[512 * t + 2 * HD + lane], k1 = S.vec[512 * t + 2 * HD + lane + 64];
+                    norm_rope(k0, k1, kn0, kn1, rc[t], rs[t]);
+                    S.ktail[t][lane] = h2f(f2h(k0));
+                    S.ktail[t][lane + 64] = h2f(f2h(k1));
+                    S.vtail[t][lane] = h2f(f2h(S.vec[512 * t + 3 * HD + lane]));
+                    S.vtail[t][lane + 64] = h2f(f2h(S.vec[512 * t + 3 * HD + lane + 64]));
+                }
+            }
+            __syncthreads();
+            if (tail && !math && tid < MT + 128) {
+                // The new cache rows (fp16), device-scope stores by exchange threads, acknowledged
+                // before this workgroup publishes its partials.
+                const int c = tid - MT;
+#pragma unroll
+                for (int t = 0; t < NR; ++t) {
+                    if (!tl(t)) continue;
+                    const float* src = c < 64 ? S.ktail[t] : S.vtail[t];
+                    uint16_t* dst = (uint16_t*)(c < 64 ? kb : vb) + (size_t)(pos + t) * HD;
+                    const int d = 2 * (c % 64);
+                    const uint32_t v = (uint32_t)f2h(src[d]) | ((uint32_t)f2h(src[d + 1]) << 16);
+                    __hip_atomic_store((uint32_t*)(dst + d), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                __builtin_amdgcn_s_waitcnt(0);
+            }
+            {
+                // Scores on the matrix cores: per block, each math wave multiplies the query rows
+                // (the fp16 hi and lo parts of both heads of each pass row, replicated over the 16 A
+                // rows) with its ATT_NT tiles of 16 cache rows (v_mfma_f32_16x16x32_f16, four
+                // products of 32 dims each); every lane then holds the scores of its column's slot
+                // for pass row t = (lane / 16) % NR.  The online softmax runs per wave and row
+                // (every lane holds its row's running maximum and sum); the probabilities move
+                // through LDS (wave-local) to the P.V layout, where each quarter-wave takes 9 V
+                // rows, 8 dims per lane, for every pass row.
+                const int tq = (lane >> 4) & (NR - 1);  // pass row of this lane's scores
+                float m_run[2] = {-__builtin_inff(), -__builtin_inff()}, l_run[2] = {0.f, 0.f};
+                float o[NR][2][8];
+#pragma unroll
+                for (int t = 0; t < NR; ++t)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int d = 0; d < 8; ++d) o[t][hh][d] = 0.f;
+                PK_TRACE(l, 21);
+                if (math) {
+                    const int c = lane & 15, kq = lane >> 4;
+#ifdef ICUA_PERSIST_TRACE
+                    __builtin_amdgcn_s_waitcnt(0);
+                    PK_TRACE(l, 25);
+#endif
+                    // Rows this lane's pass row sees (the split's rows up to slot pos + tq).
+                    const int ntq = NR == 1 ? ntot : max(0, min(j1, pos + tq + 1) - j0);
+                    for (int b0 = 0; b0 < ntot; b0 += ATT_BLOCK) {
+                        const int nb = min(ATT_BLOCK, ntq - b0);
+                        if (b0 > 0) load_kv_block(kt, vr, kb, vb, j0, b0, nprior, tid);
+                        // The new rows (block slot pos + t - j0 - b0) come from LDS, not from the cache.
+                        if (tail) {
+#pragma unroll
+                            for (int t = 0; t < NR; ++t) {
+                                if (!tl(t)) continue;
+                                const int pnew = pos + t - j0 - b0;
+#pragma unroll
+                                for (int T = 0; T < ATT_NT; ++T)
+                                    if (4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) == pnew) {
+#pragma unroll
+                                        for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail[t] + 32 * j + 8 * kq);
+                                    }
+#pragma unroll
+                                for (int i = 0; i < ATT_SPQ; ++i)
+                                    if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail[t] + 8 * ql);
+                            }
+                        }
+                        // D[variant][slot]: lane l holds rows 4 (l / 16) + r, i.e. variant
+                        // (4 (l / 16) + r) % NV: row tq, hi (r = 0, 1) or lo (r = 2, 3) of head r % 2.
+                        float sc[2][ATT_NT];
+#pragma unroll
+                        for (int T = 0; T < ATT_NT; ++T) {
+                            f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)  // A: the query rows (read from LDS for each tile)
+                                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    *(const h8*)&S.qf[lane & (NV - 1)][32 * j + 8 * kq], as_h8(kt[T][j]), D, 0, 0, 0);
+                            const bool ok = 4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) < nb;
+                            sc[0][T] = ok ? D[0] + D[2] : -__builtin_inff();
+                            sc[1][T] = ok ? D[1] + D[3] : -__builtin_inff();
+                        }
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            float mb = sc[hh][0];
+#pragma unroll
+                            for (int T = 1; T < ATT_NT; ++T) mb = fmaxf(mb, sc[hh][T]);
+                            // mb is finite as soon as the wave has seen one valid slot of the row.
+                            mb = fmaxf(max16(mb), m_run[hh]);
+                            const float corr = (m_run[hh] == -__builtin_inff()) ? 0.f : ex2(m_run[hh] - mb);
+                            float ls = 0.f;
+#pragma unroll
+                            for (int T = 0; T < ATT_NT; ++T) {
+                                sc[hh][T] = (sc[hh][T] == -__builtin_inff()) ? 0.f : ex2(sc[hh][T] - mb);
+                                ls += sc[hh][T];
+                            }
+                            l_run[hh] = l_run[hh] * corr + sum16(ls);
+                            m_run[hh] = mb;
+                            // o of row t is rescaled by row t's factor, which lanes 16 t .. hold.
+#pragma unroll
+                            for (int t = 0; t < NR; ++t) {
+                                float ct = corr;
+                                if constexpr (NR > 1) ct = __shfl(corr, 16 * t);
+#pragma unroll
+                                for (int d = 0; d < 8; ++d) o[t][hh][d] *= ct;
+                            }
+                            if (lane < 16 * NR) {
+#pragma unroll
+                                for (int T = 0; T < ATT_NT; ++T) S.pw[mw][tq][hh][c & 3][4 * T + (c >> 2)] = sc[hh][T];
+                            }
+                        }
+                        // The probabilities of this wave's slots were written by its own lanes:
+                        // a wave's LDS accesses complete in order, so no barrier is needed.
+                        __builtin_amdgcn_wave_barrier();
+                        PK_TRACE(l, 27);
+#pragma unroll
+                        for (int i = 0; i < ATT_SPQ; ++i) {
+                            float p[NR][2];
+#pragma unroll
+                            for (int t = 0; t < NR; ++t) {
+                                p[t][0] = S.pw[mw][t][0][kq][i];
+                                p[t][1] = S.pw[mw][t][1][kq][i];
+                            }
+                            const uint32_t dv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                const f16x2 hv = as_h2(dv[j]);
+                                const float v0 = (float)hv.x, v1 = (float)hv.y;
+#pragma unroll
+                                for (int t = 0; t < NR; ++t)
+#pragma unroll
+                                    for (int hh = 0; hh < 2; ++hh) {
+                                        o[t][hh][2 * j] = fmaf(p[t][hh], v0, o[t][hh][2 * j]);
+                                        o[t][hh][2 * j + 1] = fmaf(p[t][hh], v1, o[t][hh][2 * j + 1]);
+                                    }
+                            }
+                        }
+                        __builtin_amdgcn_wave_barrier();
+                    }
+                    PK_TRACE(l, 29);
+                    // The wave's 4 quarter-waves (lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same
+                    // dims) share each row's running maximum: their sums add.
+#pragma unroll
+                    for (int t = 0; t < NR; ++t)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                            for (int d = 0; d < 8; ++d) o[t][hh][d] = sum_x4(o[t][hh][d]);
+                    if (lane < 16) {
+#pragma unroll
+                        for (int t = 0; t < NR; ++t)
+#pragma unroll
+                            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                                for (int d = 0; d < 8; ++d) S.ored[mw][2 * t + hh][8 * ql + d] = o[t][hh][d];
+                    }
+                    if ((lane & 15) == 0 && lane < 16 * NR) {  // row tq's (m, l) per head
+                        S.aml[mw][4 * tq + 0] = m_run[0];
+                        S.aml[mw][4 * tq + 1] = m_run[1];
+                        S.aml[mw][4 * tq + 2] = l_run[0];
+                        S.aml[mw][4 * tq + 3] = l_run[1];
+                    }
+                }
+                PK_TRACE(l, 22);
+                __syncthreads();
+                if (math) {
+                    // The split's partials: per pass row and head, the 4 waves rescaled to their
+                    // common max.
+                    uint64_t* part = ll + PK::PARTP + (size_t)(g * ATT_SPLITS + s) * NR * 2 * PART2;
+                    const int hh = tid / HD, d = tid % HD;
+#pragma unroll
+                    for (int t = 0; t < NR; ++t) {
+                        float mx = -__builtin_inff();
+#pragma unroll
+                        for (int ww = 0; ww < MW; ++ww) mx = fmaxf(mx, S.aml[ww][4 * t + hh]);
+                        float acc = 0.f, lsum = 0.f;
+#pragma unroll
+                        for (int ww = 0; ww < MW; ++ww) {
+                            const float mwv = S.aml[ww][4 * t + hh];
+                            const float f = (mwv == -__builtin_inff()) ? 0.f : ex2(mwv - mx);
+                            acc = fmaf(S.ored[ww][2 * t + hh][d], f, acc);
+                            lsum = fmaf(S.aml[ww][4 * t + 2 + hh], f, lsum);
+                        }
+                        // o pairs (even lanes), then (l, m) with the maximum exact.
+                        uint64_t* pt = part + (2 * t + hh) * PART2;
+                        const float acc_n = xor1(acc);
+                        if (!(d & 1)) st64(pt + d / 2, pack2(acc, acc_n, r + 1));
+                        if (d == 0) st64(pt + HD / 2, pack2(lsum, mx, r + 1));
+                    }
+                }
+                PK_TRACE(l, 20);
+            }
+            PK_TRACE(l, 4);
+
+            // ---------------- merge of group g: workgroups 224..255 ------------------------
+            // Split s = 28 + p of group g (workgroup 224 + 8p + g, no O / down work) merges part
+            // p = 0..3 of the group's output for every pass row: head 2g + p / 2, elements
+            // 64 (p % 2) .. + 63.
+            if (w >= MERGER0) {
+                const int p = s - (ATT_SPLITS - MERGE_PARTS), hh = p / 2, d0 = 64 * (p % 2);
+                float* pl = (float*)S.A;  // [NR][32][64 + 2]: o elements d0.., l, m of head hh per split
+                static_assert(NR * ATT_SPLITS * 66 * 4 <= A_BYTES, "the merge's partials fit S.A");
+                const uint64_t* gp = ll + PK::PARTP + (size_t)g * PK::GROUP_PARTS;
+                bool ok = true;
+                if (!math)
+                    ok = poll_map<(NR * ATT_SPLITS * 33 + CT - 1) / CT>(
+                        gp, NR * ATT_SPLITS * 33,
+                        [&](int k) {
+                            const int t = k / (ATT_SPLITS * 33), sj = (k / 33) % ATT_SPLITS, e = k % 33;
+                            return (sj * NR * 2 + 2 * t + hh) * PART2 + (e < 32 ? d0 / 2 + e : HD / 2);
+                        },
+                        r + 1, pl, err);
+                if (sync_failed(S, !ok)) return;
+                PK_TRACE_X(l, 5);
+#pragma unroll
+                for (int t = 0; t < NR; ++t) {
+                    const float* plt = pl + t * ATT_SPLITS * 66;
+                    // Split weights exp(m_s - max) and the normaliser (math wave 0, one lane per split).
+                    if (math && wave == 0) {
+                        const int sl = lane % ATT_SPLITS;
+                        const float m = plt[sl * 66 + 65];
+                        const float mx = wave_max(m);  // finite: the split holding row pos + t sees a row
+                        const float wgt = (m == -__builtin_inff()) ? 0.f : ex2(m - mx);
+                        const float lw = wave_sum(lane < ATT_SPLITS ? wgt * plt[sl * 66 + 64] : 0.f);
+                        if (lane < ATT_SPLITS) S.sc[0][lane] = wgt;
+                        if (lane == 0) S.misc[0] = 1.0f / lw;
+                    }
+                    __syncthreads();
+                    // Weighted sum of the split outputs: thread (q, e) over splits 4q .. 4q + 3, the
+                    // eight quarters combined through LDS.
+                    {
+                        const int q = tid / 64, e = tid % 64;
+                        float O = 0.f;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int sj = q * 4 + j;
+                            O = fmaf(S.sc[0][sj], plt[sj * 66 + e], O);
+                        }
+                        float* q8 = &S.ored[0][0][0];  // [8][64]
+                        q8[q * 64 + e] = O;
+                        __syncthreads();
+                        if (tid < 64) {
+                            float tt = 0.f;
+#pragma unroll
+                            for (int qq = 0; qq < 8; ++qq) tt += q8[qq * 64 + tid];
+                            const float v = tt * S.misc[0], vn = xor1(v);
+                            if (!(tid & 1))
+                                st64(ll + PK::ATTNP + t * (H / 2) + ((2 * g + hh) * HD + d0 + tid) / 2, pack2(v, vn, r + 1));
+                        }
+                    }
+                    if (NR > 1) __syncthreads();  // S.sc, S.misc[0] and the sums are rewritten for the next row
+                }
+                PK_TRACE(l, 17);
+                __syncthreads();  // the partials in S.A are read before the next staging
+                PK_TRACE(l, 6);
+            }
+
+            // ---------------- O projection + residual: workgroups 0..127 -------------------
+            // The gate|up blocks are requested here, a stage early, by every workgroup.  The
+            // residual of the O rows is xown (previous x + lower-half down sums) + xhi (the
+            // upper-half sums, long published): the same two terms every x reader adds.
+            //
+            // Workgroups 128..223 (no O, no merge) request their next stages' weights only once
+            // their KV group's split partials are all out: issued as their attention ends, these
+            // ~10 MB would queue at the memory controllers ahead of the mergers' polls of those
+            // partials.  The last split to publish is the one holding the newest cache row (it
+            // waits for that row's acknowledgement first); their math waves watch one of its
+            // (l, m) packets, and nothing else of theirs is in flight then.
+            if (math && w >= NWG / 2 && w < MERGER0) {
+                // One lane watches; the other math waves wait for it in LDS.
+                if (wave == 0 && lane == 0) {
+                    const int s_tail = min((pos + NR - 1) / chunk, ATT_SPLITS - 1);
+                    const uint64_t* q = ll + PK::PARTP + (size_t)(g * ATT_SPLITS + s_tail) * NR * 2 * PART2 +
+                                        (NR - 1) * 2 * PART2 + HD / 2;
+                    const unsigned tg = tag4(r + 1);
+                    for (int it = 0;; ++it) {
+                        if (tag_of(ld64(q)) == tg) break;
+                        if (it >= SPIN_LIMIT) raise_err(err);
+                        if (it >= SPIN_LIMIT || ((it & 63) == 63 && load_err(err))) {
+                            S.fail = 1;  // the next barrier returns
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    __hip_atomic_store(&S.go, (int)r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                while (__hip_atomic_load(&S.go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (int)r + 1)
+                    __builtin_amdgcn_s_sleep(1);
+            }
+            {
+                bool ok = true;
+                if (w < H / 16 && !math) {
+                    if (l > 0) {
+#pragma unroll
+                        for (int t = 0; t < NR; ++t)
+                            ok = ok && poll_vec<1>(ll + PK::XDP + t * (H / 2) + w * 8, 8, 2 * r, S.xhi[t], err);
+                    } else if (tid - MT < 16 * NR) {
+                        S.xhi[(tid - MT) / 16][(tid - MT) % 16] = 0.f;
+                    }
+                    ok = ok && poll_vec<NR * H / 2 / CT>(ll + PK::ATTNP, NR * H / 2, r + 1, S.vec, err);
+                }
+                if (math) {
+#pragma unroll
+                    for (int j = 0; j < 3; ++j) wgu[j].load(P.wgu, P.wgu_sb, 3 * w + j, H, mw, lane);
+                }
+                if (w < H / 16 && sync_failed(S, !ok)) return;
+            }
+            if (w < H / 16) {
+                PK_TRACE_X(l, 7);
+                stage_c<FMT, H, NR>(S, S.vec, false);
+                float acc[NR], y[NR];
+#pragma unroll
+                for (int t = 0; t < NR; ++t) {
+                    float at[1] = {0.f};
+                    if (math) mac_blocks<FMT, CW2, 1>(S, wx, mw, lane, at, t * (H / G));
+                    acc[t] = at[0];
+                }
+                reduce_math_n<MATH, NR>(S, acc, y);
+                if (wave == 0) {  // the owner keeps the residual as published (even rows rounded)
+#pragma unroll
+                    for (int t = 0; t < NR; ++t) {
+                        const float xn = lane < 16 ? (S.xown[t][lane] + S.xhi[t][lane]) + y[t] : 0.f;
+                        const float xo = xor1(xn);
+                        if (lane < 16) {
+                            S.xown[t][lane] = (lane & 1) ? xn : q19(xn);
+                            if (!(lane & 1)) st64(ll + PK::XP + t * (H / 2) + w * 8 + lane / 2, pack2(xn, xo, 2 * r + 1));
+                        }
+                    }
+                }
+                PK_TRACE(l, 8);
+            }
+            // Workgroups 128..255 request the upper down half-block and the next layer's QKV
+            // blocks here, where they wait for no stage input (workgroups 0..127 run O): loads
+            // issued later would queue ahead of their x' and h polls.
+            if (math && qkv_wg) {
+                wd_request<FMT>(wdb, P.wd, P.wd_sb, w - NWG / 2, 1, mw, lane);
+                wx[0].forget();
+                wx[1].forget();
+                if (l + 1 < L) {
+                    const LayerPtrs& Pn = a.layers[l + 1];
+                    wx[0].load(Pn.wqkv, Pn.wqkv_sb, w - NWG / 2, H, mw, lane);
+                    wx[1].load(Pn.wqkv, Pn.wqkv_sb, w, H, mw, lane);
+                }
+            }
+
+            // ---------------- RMSNorm + gate|up + SwiGLU: blocks 3w .. 3w + 2 --------------
+            {
+                bool ok = true;
+                if (!math) ok = poll_vec<NR * H / 2 / CT>(ll + PK::XP, NR * H / 2, 2 * r + 1, S.vec, err);
+                if (math) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
+                    // The next layer's attention norm, or the final norm.
+                    load_norm8(nreg, (l + 1 < L ? a.layers[l + 1].attn_norm : a.final_norm) + tid * 8);
+                }
+                if (sync_failed(S, !ok)) return;
+                PK_TRACE_X(l, 9);
+                stage_c<FMT, H, NR>(S, S.vec, true);
+                PK_TRACE(l, 13);
+                float acc[3 * NR], y[3 * NR];
+#pragma unroll
+                for (int t = 0; t < NR; ++t) {
+                    float at[3] = {0.f, 0.f, 0.f};
+                    if (math) mac_blocks<FMT, CW2, 3>(S, wgu, mw, lane, at, t * (H / G));
+#pragma unroll
+                    for (int j = 0; j < 3; ++j) acc[3 * t + j] = at[j];
+                }
+                PK_TRACE(l, 26);
+                reduce_math_n<MATH, 3 * NR>(S, acc, y);
+                PK_TRACE(l, 14);
+                if (wave == 0) {
+#pragma unroll
+                    for (int t = 0; t < NR; ++t) {
+                        const float rsn = norm_scale<H>(S, t);
+#pragma unroll
+                        for (int j = 0; j < 3; ++j) {
+                            // Block 3w + j: gate units 8 (3w + j) + 0..7 in lanes 0-7, their up rows in 8-15.
+                            const float yj = y[3 * t + j] * rsn;
+                            const float hv = swiglu(yj, xor8(yj)), hn = xor1(hv);
+                            if (lane < 8 && !(lane & 1))
+                                st64(ll + PK::HP + t * (FF / 2) + (3 * w + j) * 4 + lane / 2, pack2(hv, hn, r + 1));
+                        }
+                    }
+                }
+                PK_TRACE(l, 10);
+            }
+
+            // ---------------- down: K half w / 128 of row block w % 128 --------------------
+            {
+                const int rb = w % (NWG / 2), half = w / (NWG / 2);
+                bool ok = true;
+                if (!math) {  // row t's half: HP + t FF / 2 + half FFH / 2 .. -> vec[t FFH ..]
+                    if constexpr (NR == 1)
+                        ok = poll_vec<FFH / 2 / CT>(ll + PK::HP + half * (FFH / 2), FFH / 2, r + 1, S.vec, err);
+                    else
+                        ok = poll_map<NR * FFH / 2 / CT>(
+                            ll + PK::HP, NR * FFH / 2,
+                            [&](int k) { return (k / (FFH / 2)) * (FF / 2) + half * (FFH / 2) + k % (FFH / 2); },
+                            r + 1, S.vec, err);
+                }
+                if (math && !qkv_wg) {
+                    wx[0].forget();
+                    wx[1].forget();
+                }
+                if (sync_failed(S, !ok)) return;
+                PK_TRACE_X(l, 11);
+                stage_c<FMT, FFH, NR>(S, S.vec, false);
+                PK_TRACE(l, 18);
+                float yd[NR];
+#pragma unroll
+                for (int t = 0; t < NR; ++t) yd[t] = 0.f;
+                if (math) {
+                    // This wave's down-block requests have landed (and the QKV prefetch, issued
+                    // after them, too: vector memory counts complete in order).
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                    PK_TRACE(l, 23);
+#pragma unroll
+                    for (int t = 0; t < NR; ++t) yd[t] = wd_mac_lds<FMT>(S, wdb, mw, lane, t * (FFH / G));
+                    PK_TRACE(l, 24);
+                }
+                float y[NR];
+                reduce_math_n<MATH, NR>(S, yd, y);
+                PK_TRACE(l, 19);
+                if (wave == 0) {
+#pragma unroll
+                    for (int t = 0; t < NR; ++t) {
+                        const float v = lane < 16 ? (half == 0 ? S.xown[t][lane] + y[t] : y[t]) : 0.f;
+                        const float vn = xor1(v);
+                        if (lane < 16) {
+                            if (half == 0) S.xown[t][lane] = (lane & 1) ? v : q19(v);
+                            if (!(lane & 1))
+                                st64(ll + (half == 0 ? PK::XP : PK::XDP) + t * (H / 2) + rb * 8 + lane / 2,
+                                     pack2(v, vn, 2 * r + 2));
+                        }
+                    }
+                }
+                PK_TRACE(l, 12);
+            }
+        }
+
+        // ---------------- final RMSNorm + lm_head + per-workgroup argmax ---------------------
+        // Over the pass's last row only (the reference commits the last row's argmax).
+        {
+            const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+            constexpr bool math = MATH;
+            const unsigned r_last = (unsigned)(step * L + L - 1);
+            PK_TRACE(L, 0);
+            // All eight waves stream the blocks w + k * 256 (chunks wave * CW8 ..), LM_DEPTH in
+            // flight per wave; the exchange waves issue theirs once their poll is done.  Each
+            // wave's per-block partial sums go to LDS; one reduction and argmax at the end.
+            WB<FMT, CW8> wl[LM_DEPTH];
+            bool ok = true;
+            if (!math)
+                ok = poll_sum<H / 2 / CT>(ll + PK::XP + (NR - 1) * (H / 2), ll + PK::XDP + (NR - 1) * (H / 2),
+                                          2 * r_last + 2, S.vec, err);
+            if (math) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
+            }
+            // The exchange waves request their blocks once x is in; the math waves' requests
+            // also wait for the barrier, so that no bulk load queues ahead of the x poll.
+            if (!math) {
+#pragma unroll
+                for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
+            }
+            if (sync_failed(S, !ok)) return;
+            if (math) {
+#pragma unroll
+                for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, a.Esb, w + k * NWG, H, wave, lane);
+            }
+            PK_TRACE_X(L, 1);
+            stage_c<FMT, H>(S, S.vec, true);
+            float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
+            QuadOps<FMT> lq[CW8 / 2];  // this wave's operand quads, the same for every block
+#pragma unroll
+            for (int p = 0; p < CW8 / 2; ++p) lq[p] = quad_load<FMT>(S, wave * CW8 + 2 * p, lane);
+            // Every iteration issues the same refill (past the matrix it re-reads the last row
+            // block, an L2 hit, and the sums of blocks past the matrix are dropped): with the
+            // same loads on every path the compiler's waits stay exact, instead of draining every
+            // block in flight before each block's scales are used.
+            for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
+#pragma unroll
+                for (int k = 0; k < LM_DEPTH; ++k) {
+                    const int kb = k0 + k, rb = w + kb * NWG;
+                    float y = 0.f;
+#pragma unroll
+                    for (int p = 0; p < CW8 / 2; ++p)
+                        y = quad_scale<FMT>(lq[p], quad_mfma<FMT>(lq[p], wl[k].wv[2 * p], wl[k].wv[2 * p + 1]),
+                                            wl[k].sq[p], y);
+                    y = quad_rows(y);
+                    if (rb < NRB && lane < 16) plm[(kb * WAVES + wave) * 16 + lane] = y;
+                    wl[k].load(a.E, a.Esb, min(rb + LM_DEPTH * NWG, NRB - 1), H, wave, lane);
+                }
+            }
+            __syncthreads();
+            float best = -__builtin_inff();
+            int besti = 0x7fffffff;
+            const float rsn = norm_scale<H>(S);
+            for (int e = tid; e < LM_BLOCKS * 16; e += THREADS) {  // (block, row) pairs
+                const int kb = e / 16, rw = e % 16;
+                if (w + kb * NWG < NRB) {
+                    const float* pp = plm + kb * WAVES * 16 + rw;
+                    float y = 0.f;
+#pragma unroll
+                    for (int wv = 0; wv < WAVES; ++wv) y += pp[wv * 16];
+                    argmax_merge(best, besti, y * rsn, (w + kb * NWG) * 16 + rw);
+                }
+            }
+            wave_argmax(best, besti);
+            if (lane == 0) {
+                S.misc[8 + wave] = best;
+                S.imisc[8 + wave] = besti;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                for (int wv = 1; wv < WAVES; ++wv) argmax_merge(best, besti, S.misc[8 + wv], S.imisc[8 + wv]);
+                // (index << 4 | tag, value): the value exact, ids < 2^27 exact in the low word.
+                const uint32_t lo = ((uint32_t)min(besti, 0x07FFFFFF) << 4) | tag4((unsigned)step + 1);
+                st64(ll + PK::LMP + w, (uint64_t)lo | ((uint64_t)as_u32(best) << 32));
+            }
+            PK_TRACE(L, 2);
+            if (math) load_norm8(nreg, a.layers[0].attn_norm + tid * 8);  // for the next step
+        }
+
+        // ---------------- greedy commit, evaluated by every workgroup ------------------------
+        {
+            const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+            bool ok = true;
+            if (!MATH) ok = poll_vec<NWG / CT>(ll + PK::LMP, NWG, (unsigned)step + 1, S.vec, err);
+            if (sync_failed(S, !ok)) return;
+            PK_TRACE_X(L, 3);
+            float bv = -__builtin_inff();
+            int bi = 0x7fffffff;
+            if (tid < NWG) {
+                bv = S.vec[2 * tid + 1];
+                bi = (int)(as_u32(S.vec[2 * tid]) >> 4);
+            }
+            wave_argmax(bv, bi);
+            if (lane == 0) {
+                S.misc[wave] = bv;
+                S.imisc[wave] = bi;
+            }
+            __syncthreads();
+            float b2 = S.misc[0];
+            int tok = S.imisc[0];
+            for (int ww = 1; ww < WAVES; ++ww) argmax_merge(b2, tok, S.misc[ww], S.imisc[ww]);
+            bool stop, pair = false;
+            int forced = -1;
+            if (stp >= maxsteps) {  // nothing may be written past out_tokens[maxsteps - 1]
+                stop = true;
+            } else {
+                const bool bad = tok < 0 || tok >= VOCAB;  // no finite logit (NaN model): stop on token 0
+                if (bad) tok = 0;
+                if (w == 0 && tid == 0) a.out_tokens[stp] = tok;
+                stp += 1;
+                pos += NR;
+                stop = bad || tok == eos0 || tok == eos1 || (grammar && tok == 8) || stp >= maxsteps ||
+                       pos + 2 > maxctx;
+                // Grammar pairs: after a first-step action token, or after 11, the next token is
+                // forced (7, or 220 after 11); it is committed now, and the next pass carries both
+                // tokens (n = 2): this launch ends and the pair runs as one two-row pass.
+                if (!stop && grammar &&
+                    ((stp == 1 && (tok == 3678 || tok == 7241 || tok == 12476 || tok == 10855 || tok == 11862 ||
+                                   tok == 1339 || tok == 1472 || tok == 24769)) ||
+                     tok == 11)) {
+                    forced = tok == 11 ? 220 : 7;
+                    if (w == 0 && tid == 0) a.out_tokens[stp] = forced;
+                    stp += 1;
+                    pair = true;
+                    stop = stp >= maxsteps;  // the pair's pass would start at the step limit
+                }
+            }
+            if (w == 0 && tid == 0) {
+                st->pos = pos;
+                st->step = stp;
+                st->n = pair && !stop ? 2 : 1;
+                st->vis_offset = -1;
+                st->logits_rows = 0;
+                if (stop) st->done = 1;
+            }
+            if (stop) break;
+            // Next token's embedding (Shaders.swift:464-476), in every workgroup.
+            __syncthreads();  // every thread has read S.misc / S.imisc
+            for (int i = tid; i < H; i += THREADS) S.emb[i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)tok, i, H);
+            __syncthreads();
+            if (tid < 16 && w < H / 16) S.xown[0][tid] = S.emb[w * 16 + tid];
+            if (w == 0 && (pair || step == a.nsteps - 1)) {
+                for (int i = tid; i < H; i += THREADS) a.x[i] = S.emb[i];  // residual row(s) for the next launch
+                if (pair)
+                    for (int i = tid; i < H; i += THREADS) a.x[H + i] = dequant_tiled(FMT, a.E, a.Esb, (size_t)forced, i, H);
+            }
+            PK_TRACE(L, 4);
+            if (pair) break;  // the pair is the next launch's pass
         }
     }
 }
@@ -1360,13 +2128,21 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
 // wait in LDS for one reduction at the end.  Every lane does useful work: the four groups of a
 // quad accumulate into one matrix-core result (lanes 16j.. hold group j's sums).
 constexpr int GS_MAX_BLOCKS = 160;  // row blocks per workgroup (part[] below)
+// The staging state the isolated GEMV uses (the decode kernel's Shared holds the same members).
+struct GemvShared {
+    uint8_t A[A_BYTES];
+    uint32_t zero[4];
+    float fx[192 * 2];
+    float nw[H];
+    float misc[64];
+};
 template <int FMT, int K>
 __global__ __launch_bounds__(THREADS, 1) void gemv_stream_kernel(const uint8_t* w, const uint8_t* sb, const float* x,
                                                                   float* y, int nrb) {
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CW = K / CHK / WAVES;  // chunks per wave: q4 2 / 6, q8 4 / 12
     constexpr int DEPTH = CW <= 2 ? 4 : CW <= 6 ? 2 : 1;
-    __shared__ Shared S;
+    __shared__ GemvShared S;
     __shared__ float part[GS_MAX_BLOCKS * WAVES * 16];
     const int wg = blockIdx.x, G = gridDim.x, tid = my_tid(), lane = tid % 64, wave = wave_id();
     const int nb = (nrb - wg + G - 1) / G;  // blocks of this workgroup (the host keeps wg < nrb)
@@ -1405,7 +2181,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemv_stream_kernel(const uint8_t* 
     }
 }
 
-template <int FMT>
+template <int FMT, int NR>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
     __shared__ Shared S;
     // The LDS-DMA destination (down half-block; lm_head partial sums later) is an object of its
@@ -1417,29 +2193,34 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(PersistArgs a) {
         S.fail = 0;
         S.go = 0;
     }
-    // Control block and the embedding of the first token (written before this launch).
+    // Control block and the embeddings of the pass's tokens (written before this launch).  The
+    // NR = 1 kernel runs single-row passes, the NR = 2 kernel one forced pair (checked by the host too).
     const State* st = a.st;
-    if (st->done || st->n < 1 || st->n > 2) return;  // a single row, or a forced pair (checked by the host too)
-    const bool pair = st->n == 2;
-    for (int i = my_tid(); i < H; i += THREADS) S.emb[i] = a.x[i];
-    if (my_tid() < 16 && w < H / 16) S.xown[my_tid()] = a.x[w * 16 + my_tid()];
-    if (wave_id() < MW)
-        decode_loop<FMT, true>(a, S, wdb, w, st->pos, st->step, pair);
-    else
-        decode_loop<FMT, false>(a, S, wdb, w, st->pos, st->step, pair);
+    if (st->done || st->n != NR) return;
+    for (int i = my_tid(); i < NR * H; i += THREADS) S.emb[i] = a.x[i];
+    if (my_tid() < 16 * NR && w < H / 16) S.xown[my_tid() / 16][my_tid() % 16] = a.x[(my_tid() / 16) * H + w * 16 + my_tid() % 16];
+    if constexpr (NR == 1) {
+        if (wave_id() < MW)
+            decode_loop<FMT, true>(a, S, wdb, w, st->pos, st->step);
+        else
+            decode_loop<FMT, false>(a, S, wdb, w, st->pos, st->step);
+    } else {
+        if (wave_id() < MW)
+            decode_pass_loop<FMT, true, NR>(a, S, wdb, w, st->pos, st->step);
+        else
+            decode_pass_loop<FMT, false, NR>(a, S, wdb, w, st->pos, st->step);
+    }
 }
 
 }  // namespace pk
 
-hipError_t launch_persistent(int fmt, const PersistArgs& a, hipStream_t s) {
+hipError_t launch_persistent(int fmt, int nr, const PersistArgs& a, hipStream_t s) {
     void* args[] = {(void*)&a};
-    if (fmt == FMT_Q4)
-        return hipLaunchCooperativeKernel((const void*)pk::decode_kernel<FMT_Q4>, dim3(pk::NWG), dim3(pk::THREADS),
-                                          args, 0, s);
-    if (fmt == FMT_Q8)
-        return hipLaunchCooperativeKernel((const void*)pk::decode_kernel<FMT_Q8>, dim3(pk::NWG), dim3(pk::THREADS),
-                                          args, 0, s);
-    return hipErrorInvalidValue;
+    const void* k = nullptr;
+    if (fmt == FMT_Q4) k = nr == 2 ? (const void*)pk::decode_kernel<FMT_Q4, 2> : (const void*)pk::decode_kernel<FMT_Q4, 1>;
+    if (fmt == FMT_Q8) k = nr == 2 ? (const void*)pk::decode_kernel<FMT_Q8, 2> : (const void*)pk::decode_kernel<FMT_Q8, 1>;
+    if (!k || (nr != 1 && nr != 2) || (nr == 2 && a.nsteps != 1)) return hipErrorInvalidValue;
+    return hipLaunchCooperativeKernel(k, dim3(pk::NWG), dim3(pk::THREADS), args, 0, s);
 }
 
 hipError_t launch_gemv_stream(int fmt, const uint8_t* w, const uint8_t* sb, const float* x, float* y, int N, int K,
@@ -1461,7 +2242,10 @@ extern "C" int icua_debug_persist_trace(uint64_t* out) {
 }
 #endif
 
-size_t persistent_sync_bytes() { return ((size_t)pk::PACKETS + 32) * sizeof(uint64_t); }
+size_t persistent_sync_bytes() { return ((size_t)pk::Pk<2>::PACKETS + 32) * sizeof(uint64_t); }
 int persistent_error_slot() { return pk::ERRW; }
+size_t persistent_clear_bytes(int nr) {
+    return (size_t)(nr == 2 ? pk::Pk<2>::PACKETS : pk::Pk<1>::PACKETS) * sizeof(uint64_t);
+}
 
 }  // namespace icua

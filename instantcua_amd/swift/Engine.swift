@@ -59,6 +59,11 @@ public final class Engine {
     public var useGrammarPairs: Bool = true { didSet { applyFlags() } }
     public var useVisionDeltaCache: Bool = true { didSet { applyFlags() } }
     private var writeFirstLogits = false
+    /// The engine's message for the last generate / generateVision call that failed (nil after a
+    /// call that succeeded).  Those calls keep the reference's non-throwing signature and return
+    /// an empty array on failure; this tells an empty answer from an error, e.g. "persistent
+    /// decode kernel: a synchronisation wait timed out".
+    public private(set) var lastError: String?
 
     public struct Timing {
         public var visionMs = 0.0, prefillMs = 0.0, decodeMs = 0.0, totalMs = 0.0
@@ -86,6 +91,10 @@ public final class Engine {
         }
     }
 
+    /// `copyWeights` and `pinMemory` are accepted for source compatibility with the reference's
+    /// initializer and have no effect here: the engine always copies the weights into GPU memory
+    /// (repacked into matrix-core tiles) while it loads, and releases the file mapping before this
+    /// initializer returns, so there is neither a no-copy mode nor host memory to pin.
     public init(modelPath: String, maxContext: Int = 2048, maxPass: Int = 512, maxSteps: Int = 256,
                 copyWeights: Bool = false, pinMemory: Bool = true) throws {
         var h: OpaquePointer?
@@ -154,6 +163,7 @@ public final class Engine {
         let rc = tokens.withUnsafeBufferPointer { t in
             icua_generate(handle, t.baseAddress, Int32(tokens.count), Int32(visOffset), Int32(maxNewTokens), &out, &n)
         }
+        lastError = rc == 0 ? nil : String(cString: icua_last_error())
         return rc == 0 ? Array(out[0..<Int(n)]) : []
     }
 
@@ -171,6 +181,7 @@ public final class Engine {
             icua_generate_vision(handle, rgbBytes.assumingMemoryBound(to: UInt8.self), Int32(width), Int32(height),
                                  t.baseAddress, Int32(tokens.count), Int32(maxNewTokens), &out, &n)
         }
+        lastError = rc == 0 ? nil : String(cString: icua_last_error())
         return rc == 0 ? Array(out[0..<Int(n)]) : []
     }
 

@@ -531,7 +531,7 @@ static float top2_margin(const float* v, int n, int best) {
 }
 
 int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, int vis_offset, int n_vis,
-                const float* const* deepstack, int steps, int32_t* out_tokens, float* margins,
+                const float* const* deepstack, int steps, int32_t* out_tokens, float* margins, float* top1,
                 float* out_first_logits) {
     float* logits = (float*)malloc(sizeof(float) * OR_VOCAB);
     int rc = or_pass(m, toks, n, 0, pooler, vis_offset, n_vis, deepstack, 1, logits);
@@ -543,12 +543,14 @@ int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, in
     int tok = or_argmax(logits, OR_VOCAB);
     out_tokens[0] = tok;
     if (margins) margins[0] = top2_margin(logits, OR_VOCAB, tok);
+    if (top1) top1[0] = logits[tok];
     for (int s = 1; s < steps; ++s) {
         rc = or_pass(m, &tok, 1, n + s - 1, NULL, -1, 0, NULL, 1, logits);
         if (rc) break;
         tok = or_argmax(logits, OR_VOCAB);
         out_tokens[s] = tok;
         if (margins) margins[s] = top2_margin(logits, OR_VOCAB, tok);
+        if (top1) top1[s] = logits[tok];
     }
     free(logits);
     return rc;

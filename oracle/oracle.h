@@ -103,10 +103,11 @@ int or_argmax(const float* v, int n);
 /* Greedy generation: prefill `toks` (n) at slot 0 with the visual inputs as in or_pass,
  * then decode until `steps` tokens are produced (the first from the prefill).  No EOS
  * stop.  out_tokens[steps]; margins[steps] (top-1 minus top-2 logit, may be NULL);
- * out_first_logits[VOCAB] (may be NULL).  Returns 0 on success. */
+ * top1[steps] (the top-1 logit of each step, may be NULL); out_first_logits[VOCAB] (may be
+ * NULL).  Returns 0 on success. */
 int or_generate(or_model* m, const int32_t* toks, int n, const float* pooler, int vis_offset,
                 int n_vis, const float* const* deepstack, int steps, int32_t* out_tokens,
-                float* margins, float* out_first_logits);
+                float* margins, float* top1, float* out_first_logits);
 
 /* The reference's token loop (Engine.swift:741-817) with its commit rules (Shaders.swift:
  * 1531-1561): prefill `toks` (n) at slot 0 with the visual inputs as in or_pass, then passes

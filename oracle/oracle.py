@@ -62,7 +62,7 @@ def lib():
                               C.c_int, C.c_void_p]
         L.or_argmax.argtypes = [_f32p, C.c_int]
         L.or_generate.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
-                                  _i32p, C.c_void_p, C.c_void_p]
+                                  _i32p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.or_generate_commit.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                          C.c_int, C.c_int, C.c_int, C.c_int, _i32p]
         L.or_quant_q8.argtypes = [_f32p, C.c_int, C.c_int, C.c_void_p, _u16p]
@@ -246,19 +246,21 @@ class OracleModel:
             raise RuntimeError("oracle: " + lib().or_last_error().decode())
         return out[:n]
 
-    def generate(self, toks, steps: int, pooler=None, vis_offset: int = -1, deepstack=None):
-        """Greedy tokens, top-2 margins and first logits (prefill at slot 0, no EOS stop)."""
+    def generate(self, toks, steps: int, pooler=None, vis_offset: int = -1, deepstack=None, with_top1=False):
+        """Greedy tokens, top-2 margins and first logits (prefill at slot 0, no EOS stop); with
+        `with_top1`, also each step's top-1 logit."""
         toks = np.ascontiguousarray(toks, dtype=np.int32)
         pool, keep, ds_ptr = self._visual(pooler, deepstack)
         n_vis = 0 if pool is None else pool.shape[0]
         out = np.empty(steps, dtype=np.int32)
         margins = np.empty(steps, dtype=np.float32)
+        top1 = np.empty(steps, dtype=np.float32)
         first = np.empty(VOCAB, dtype=np.float32)
         rc = lib().or_generate(self.h, toks, toks.size, _ptr(pool), vis_offset, n_vis, ds_ptr, steps, out,
-                               _ptr(margins), _ptr(first))
+                               _ptr(margins), _ptr(top1), _ptr(first))
         if rc:
             raise RuntimeError("oracle: " + lib().or_last_error().decode())
-        return out, margins, first
+        return (out, margins, first, top1) if with_top1 else (out, margins, first)
 
 
 # ---------------------------------------------------------------------------------------------

@@ -64,3 +64,31 @@ def fp16_close(got, ref, max_ulp=1, row_tol=1e-6, frac_over_1ulp=0.0):
     assert not bad.any(), f"{bad.sum()} cache values beyond {max_ulp} ulp / {row_tol:g} of the row"
     over = (d > ulp).mean()
     assert over <= frac_over_1ulp, f"{over:.3g} of the cache values beyond one ulp"
+
+
+def compare_greedy_forced(e, n_prompt, ref, margins, top1, steps):
+    """Compares all `steps` greedy tokens of a decode (token 0 from the prefill, the rest from
+    e.decode_steps) with the oracle's, step by step.  A divergence must be a near-tie of the
+    oracle at that step (its margin below 1e-3 of that step's top-1 logit); the decode then
+    continues teacher-forced: icua_set_position feeds the oracle's token at its slot and the later
+    steps are decoded again, so every step after a near-tie is compared as well
+    (qwen3vl_ref.py:294-336 is the loop being followed).  Returns the near-tie steps."""
+    got = e.tokens(steps)
+    ties = []
+    i = 0
+    while True:
+        diff = np.nonzero(got[i:] != ref[i:steps])[0]
+        if diff.size == 0:
+            return ties
+        j = i + int(diff[0])
+        if not near_tie(float(margins[j]), float(top1[j])):
+            raise AssertionError(
+                f"greedy divergence at step {j}: gpu {got[j]} oracle {ref[j]} "
+                f"(oracle top-2 margin {margins[j]:.4g}, top-1 {top1[j]:.4g}; earlier near-ties {ties})")
+        ties.append(j)
+        if j == steps - 1:
+            return ties
+        e.set_position(n_prompt + j, int(ref[j]), j + 1, steps)
+        e.decode_steps(steps - 1 - j)
+        got = e.tokens(steps)
+        i = j + 1

@@ -13,8 +13,8 @@ oracle_c4_28layer.npz
     32 x 32 grid of fp16 N(0, 1) visual rows with 3D M-RoPE and three DeepStack sets added after
     layers 0-2, then 3056 text tokens (4096 in all); then 128 greedy tokens.
 
-Each holds the prompt, the greedy tokens with the oracle's top-1 minus top-2 margin per step, the
-first-token logits (float32, the whole vocabulary) and K / V rows of layers 0 and 27 at a few
+Each holds the prompt, the greedy tokens with the oracle's top-1 logit and top-1 minus top-2 margin
+per step, the first-token logits (float32, the whole vocabulary) and K / V rows of layers 0 and 27 at a few
 cache slots (fp16 bit patterns [2][8][len(slots)][128]).
 
 usage: python tests/golden/make_golden_28.py [c3] [c4]
@@ -78,21 +78,22 @@ def run(which: str, img: np.ndarray, sha: bytes) -> None:
     if which == "c3":
         toks, steps = c3_prompt(), C3_STEPS
         om = oracle.OracleModel(img, C3_PROMPT + steps + 8)
-        out, margins, first = om.generate(toks, steps)
+        out, margins, first, top1 = om.generate(toks, steps, with_top1=True)
         extra = {}
     else:
         vp, steps = c4_prompt(), C4_STEPS
         toks = vp.tokens
         om = oracle.OracleModel(img, C4_PROMPT + steps + 8)
         om.prepare_mrope(vp.vis_offset, vp.llm_h, vp.llm_w)
-        out, margins, first = om.generate(toks, steps, pooler=vp.pooler.astype(np.float32),
-                                          vis_offset=vp.vis_offset,
-                                          deepstack=[d.astype(np.float32) for d in vp.deepstack])
+        out, margins, first, top1 = om.generate(toks, steps, pooler=vp.pooler.astype(np.float32),
+                                                vis_offset=vp.vis_offset,
+                                                deepstack=[d.astype(np.float32) for d in vp.deepstack],
+                                                with_top1=True)
         extra = {"vis_offset": np.int32(vp.vis_offset), "grid": np.array([vp.llm_h, vp.llm_w], np.int32)}
     slots = kv_slots(toks.size, steps)
     np.savez_compressed(os.path.join(HERE, f"oracle_{which}_28layer.npz"),
                         image_sha256=np.frombuffer(sha, dtype=np.uint8), prompt=toks.astype(np.int32),
-                        greedy=out, margins=margins, first_logits=first, kv_layers=np.array(KV_LAYERS, np.int32),
+                        greedy=out, margins=margins, top1=top1, first_logits=first, kv_layers=np.array(KV_LAYERS, np.int32),
                         kv_slots=slots, kv=_kv_rows(om, slots), **extra)
     om.close()
     print(f"{which}: {steps} tokens in {time.time() - t0:.0f}s; first {list(out[:8])}", flush=True)

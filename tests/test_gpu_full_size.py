@@ -7,11 +7,13 @@ wrote them; the oracle needs minutes of CPU time at these sizes):
 * vision-shaped context: a 4096-token prefill (16 text tokens, a 32 x 32 grid of visual rows with
   3D M-RoPE and DeepStack after layers 0-2, 3056 text tokens) and 127 persistent decode steps.
 
-Checked: the model image is the fixture's (sha256); first-token logits within the stated 1e-2
-tolerance (max |d| / max |ref|, fp32 logits); the greedy tokens identical, a divergence allowed
-only at an oracle near-tie; K/V cache rows of layers 0 and 27 at prompt and decode slots within
-a bound scaled by the row (differences of fp32 accumulation order carried through 28 layers and
-rounded to fp16).
+Checked: the model image is the fixture's (sha256); first-token logits within 1e-4 (max |d| /
+max |ref|, fp32 logits; the north-star tolerance is 1e-2, the kernels meet 4.5e-5 and 9.2e-6);
+every one of the greedy tokens compared with the oracle's: a divergence is allowed only at an
+oracle near-tie (margin below 1e-3 of that step's top-1 logit), after which the decode continues
+teacher-forced from the oracle's token so the remaining steps are compared too; K/V cache rows
+of layers 0 and 27 at prompt and decode slots within a bound scaled by the row (differences of
+fp32 accumulation order carried through 28 layers and rounded to fp16).
 
 Also here: one 4096-row matrix-core prefill chunk of a 2-layer model against the oracle run live."""
 import hashlib
@@ -20,7 +22,7 @@ import os
 import numpy as np
 import pytest
 
-from conftest import compare_greedy, rel_err
+from conftest import compare_greedy, compare_greedy_forced, rel_err
 from instantcua_amd import synth
 from instantcua_amd.engine import Engine
 from instantcua_amd.modelfile import Dims, WeightFormat
@@ -61,16 +63,16 @@ def _check(e, fx, steps, label):
     lg = e.logits(1)[0]
     e.decode_steps(steps - 1)
     st = e.state()
-    got = e.tokens(st["step"])
     err = rel_err(lg, fx["first_logits"])
-    print(f"{label}: first-token logits rel err {err:.3g}")
-    assert err < 1e-2, err
     assert st["step"] == steps and st["done"] == 1, st
-    n, note = compare_greedy(got, fx["greedy"], fx["margins"], fx["first_logits"].max() * np.ones(steps))
-    print(f"{label}: {n}/{steps} greedy tokens identical ({note})")
-    # Decode step i writes the K/V row of token i - 1 at slot prompt + i - 1: rows from the first
-    # divergent token on hold different tokens and are not compared.
-    slots = fx["kv_slots"][fx["kv_slots"] < fx["prompt"].size + n]
+    ties = compare_greedy_forced(e, fx["prompt"].size, g, fx["margins"], fx["top1"], steps)
+    note = f"{label}: first-token logits rel err {err:.3g}; {steps}/{steps} greedy steps compared, " \
+           f"oracle near-ties (teacher-forced past them) at steps {ties}"
+    print(note)
+    assert err < 1e-4, note
+    # Decode step i writes the K/V row of token i - 1 at slot prompt + i - 1; after a near-tie the
+    # decode was repeated from the oracle's token, so every row holds the oracle's sequence.
+    slots = fx["kv_slots"]
     for i, l in enumerate(fx["kv_layers"]):
         for kind in (0, 1):
             got_rows = np.stack([e.read_kv(int(l), kind, int(s), 1)[:, 0] for s in slots], axis=1)

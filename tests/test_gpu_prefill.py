@@ -129,3 +129,39 @@ def test_two_chunks_match_pass_path(q4_small):
     assert mm[0] == ps[0]
     for kind in (2, 3):
         fp16_close(mm[kind], ps[kind], max_ulp=2, row_tol=2e-3, frac_over_1ulp=5e-2)
+
+
+@pytest.mark.parametrize("fmt", [WeightFormat.Q8, WeightFormat.F16], ids=["q8", "f16"])
+@pytest.mark.parametrize("n", [1024, 4096])
+def test_large_tile_prefill_matches_oracle(oracle_mod, n, fmt):
+    """Prompts long enough for the larger GEMM tiles (prefill.hip pf_gemm_fmt picks the largest
+    tile whose count fills the 256 CUs evenly), q8 and f16, against the oracle run live:
+
+      n = 1024: q8 QKV and gate|up on 128 x 128 tiles (8 row-tiles x 32 / 96 column tiles), O and
+                down on 64 x 128; f16 the same.
+      n = 4096: q8 every GEMM on 128 x 256 tiles (32 x 16 / 8 / 48 / 8 tiles); f16 (never 256-row
+                tiles) every GEMM on 128 x 128.
+
+    Checked: first logits within 1e-4, K/V rows of the last layer at spread slots, first greedy
+    tokens."""
+    img = small_image(fmt)
+    toks = synth.random_tokens(n, f"pf-large-{n}")
+    steps = 3
+    om = oracle_mod.OracleModel(img, n + 8)
+    ref, margins, first = om.generate(toks, steps)
+    slots = sorted({0, 1, 127, 128, n // 2, n - 129, n - 1})
+    with Engine(flags=0, image=img, max_context=n + 8, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        assert not e.pass_prefill
+        e.prefill(toks, max_new=steps, write_logits=True)
+        lg = e.logits(1)[0]
+        assert e.last_timing["prefill_tokens"] == n
+        kv = [np.stack([e.read_kv(LAYERS - 1, kind, s, 1)[:, 0] for s in slots], axis=1) for kind in (0, 1)]
+        e.decode_steps(steps - 1)
+        got = e.tokens(steps)
+    err = rel_err(lg, first)
+    print(f"fmt {fmt} n {n}: first-token logits rel err {err:.3g}")
+    assert err < 1e-4, err
+    for kind in (0, 1):
+        fp16_close(kv[kind], om.kv(LAYERS - 1, kind)[:, slots], max_ulp=2, row_tol=2e-3, frac_over_1ulp=5e-2)
+    compare_greedy(got, ref, margins, first.max() * np.ones(steps))

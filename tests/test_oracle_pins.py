@@ -314,16 +314,17 @@ def test_greedy_decode_is_consistent_with_passes(oracle_mod):
     img = synth.build_model_image(WeightFormat.Q4, n_layers=1, tag="pin4")
     toks = synth.random_tokens(6, "pin4")
     om = oracle_mod.OracleModel(img, 32)
-    out, margins, first = om.generate(toks, 4)
+    out, margins, first, top1 = om.generate(toks, 4, with_top1=True)
     om2 = oracle_mod.OracleModel(img, 32)
     lg = om2.run_pass(toks, 0)[0]
-    assert np.array_equal(lg, first) and lg.argmax() == out[0]
+    assert np.array_equal(lg, first) and lg.argmax() == out[0] and top1[0] == lg.max()
     seq = [int(out[0])]
     for s in range(1, 4):
         lg = om2.run_pass(np.array([seq[-1]], np.int32), len(toks) + s - 1)[0]
         seq.append(int(lg.argmax()))
         srt = np.sort(lg)
         assert abs((srt[-1] - srt[-2]) - margins[s]) < 1e-6
+        assert top1[s] == srt[-1]
     assert seq == list(out)
 
 
