@@ -275,3 +275,17 @@ def visual_prompt(n_total: int, vis_offset: int, llm_h: int, llm_w: int, tag: st
     pooler = fp16_normal((n_vis, Dims.hidden), tag, 1)
     ds = [fp16_normal((n_vis, Dims.hidden), tag, 2 + i) for i in range(3)]
     return VisualPrompt(toks, vis_offset, llm_h, llm_w, pooler, ds)
+
+
+def scale_embedding_rows(img: np.ndarray, scales: dict) -> np.ndarray:
+    """Copy of a q4 image whose tied-embedding rows `tok` are multiplied by `c` (their fp16
+    (scale, bias) words), so that those tokens win the argmax often: the grammar-pair workloads
+    use it to make the forced pairs (Shaders.swift:1537-1561) fire on a random-init model."""
+    img = img.copy()
+    table = np.frombuffer(img[16:16 + 16 * TensorID.count].tobytes(), dtype="<u8").reshape(-1, 2)
+    off = int(table[TensorID.embed_sb, 0])
+    n = Dims.vocab * (Dims.hidden // 64) * 4
+    sb = img[off:off + n].view(np.float16).reshape(Dims.vocab, Dims.hidden // 64, 2)
+    for tok, c in scales.items():
+        sb[tok] = (sb[tok].astype(np.float32) * c).astype(np.float16)
+    return img

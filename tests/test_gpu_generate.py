@@ -6,23 +6,11 @@ import pytest
 
 from conftest import compare_greedy
 from instantcua_amd import synth
+from instantcua_amd.synth import scale_embedding_rows
 from instantcua_amd.engine import Engine
-from instantcua_amd.modelfile import Dims, TensorID, WeightFormat
+from instantcua_amd.modelfile import Dims, WeightFormat
 
 pytestmark = pytest.mark.gpu
-
-
-def scale_embedding_rows(img: np.ndarray, scales: dict) -> np.ndarray:
-    """Copy of a q4 image whose tied-embedding rows `tok` are multiplied by `c` (their fp16
-    (scale, bias) words), so that those tokens win the argmax often."""
-    img = img.copy()
-    table = np.frombuffer(img[16:16 + 16 * TensorID.count].tobytes(), dtype="<u8").reshape(-1, 2)
-    off = int(table[TensorID.embed_sb, 0])
-    n = Dims.vocab * (Dims.hidden // 64) * 4
-    sb = img[off:off + n].view(np.float16).reshape(Dims.vocab, Dims.hidden // 64, 2)
-    for tok, c in scales.items():
-        sb[tok] = (sb[tok].astype(np.float32) * c).astype(np.float16)
-    return img
 
 
 @pytest.fixture(scope="module")
