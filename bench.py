@@ -219,6 +219,42 @@ def run_text_context(img, steps=256):
     return out
 
 
+def run_grammar_pairs(img, n_prompt=9, steps=24):
+    """The reference's product setting: grammar pairs on (Shaders.swift:1537-1561) with forced
+    pairs firing.  The 28-layer q4 decoder with the embedding rows of tokens 11 and 3678 scaled by
+    8 (synth.scale_embedding_rows) forces a space after 11 five times in its 24 tokens (9-token
+    prompt); each forced pair runs as one two-row pass.  Reported: us per committed token and per pass, against the same model
+    and prompt decoded without the rules (single-row passes only), and the tokens against the
+    oracle fixture of this workload."""
+    im = synth.scale_embedding_rows(img, {11: 8.0, 3678: 8.0})
+    toks = synth.random_tokens(n_prompt, "gram", 3)
+    e = eng.Engine(image=im, max_context=n_prompt + steps + 8, max_steps=steps)
+    e.eos = (-1, -1)
+    e.generate(toks, max_new_tokens=steps)  # loads the code objects
+    p0 = e.pair_passes
+    got = e.generate(toks, max_new_tokens=steps)
+    dec_ms = e.last_timing["decode_ms"]
+    pairs = e.pair_passes - p0
+    e.grammar_pairs = False
+    e.generate(toks, max_new_tokens=steps)
+    plain_ms = e.last_timing["decode_ms"]
+    e.close()
+    decoded = len(got) - 1  # the first token comes from the prefill
+    passes = decoded - pairs
+    out = {"workload": f"28-layer q4 decoder (tokens 11, 3678 scaled x8), {n_prompt}-token prompt, {steps} tokens, "
+                       "grammar pairs on",
+           "tokens": len(got), "pair_passes": pairs, "passes": passes,
+           "decode_us_per_committed_token": round(dec_ms * 1e3 / decoded, 1),
+           "decode_us_per_pass": round(dec_ms * 1e3 / passes, 1),
+           "without_rules_us_per_token": round(plain_ms * 1e3 / (steps - 1), 1)}
+    path = os.path.join(ROOT, "tests", "golden", "oracle_pairs_28layer.npz")
+    if os.path.exists(path):
+        with np.load(path, allow_pickle=False) as z:
+            out["tokens_equal_oracle_fixture"] = bool(list(z[f"tokens_{n_prompt}"]) == list(got))
+    log(f"grammar pairs: {out}")
+    return out
+
+
 # Speculative verify workload: 8 random drafts over 8192 cache rows of a 28-layer q8 decoder.
 VERIFY_CTX, VERIFY_M = 8192, 8
 # Isolated q4 GEMV sweep (K, N): fused QKV, O, gate+up, down, lm_head.
@@ -527,6 +563,7 @@ def main():
     e.close()
 
     text = run_text_context(img)
+    gram = run_grammar_pairs(img)
     cpu = None if args.no_cpu else cpu_baseline(img, PREFILL)
     rows = None if args.no_cpu else cpu_rows()
     del img
@@ -576,6 +613,7 @@ def main():
         "cpu_baseline": cpu,
         "cpu_rows": rows,
         "text_context_1024": text,
+        "grammar_pairs_28": gram,
         "prefill_q8_4096": q8,
         "verify_q8_8192": ver,
     }

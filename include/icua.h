@@ -56,6 +56,7 @@ typedef struct {
     int32_t vision; /* 1 if the model file holds the vision tower and its mergers */
     int32_t last_decode_persistent; /* 1 if the last icua_decode_steps call ran as the persistent kernel */
     int32_t visual_rows; /* rows of the pooler / DeepStack buffers (ICUA_BUF_POOLER, ...), 0 if unset */
+    int32_t pair_passes; /* forced grammar pairs run as one two-row persistent launch, since create */
 } icua_info_t;
 
 /* Last error message of the calling thread ("" if none). */

@@ -170,6 +170,7 @@ struct icua_engine {
     unsigned* psync = nullptr;
     int psync_dev = -1;
     bool last_persistent = false;
+    int pair_passes = 0;  // two-row persistent launches (forced grammar pairs) since create
     bool persist_ok = false;
     // Matrix-core prefill buffers for chunks of up to pf_cap rows (allocated on first use).
     int pf_cap = 0;
@@ -934,6 +935,7 @@ struct icua_engine {
             while (left > 0 && !s.done) {
                 const int nr = s.n == 2 ? 2 : 1, step0 = s.step;
                 if (enqueue_persistent(nr == 2 ? 1 : left, nr)) return -1;
+                pair_passes += nr == 2;
                 HIPCK(hipEventRecord(ev1, stream));
                 if (read_state(s)) return -1;  // waits for the launch
                 if (check_persistent()) return -1;
@@ -1029,6 +1031,7 @@ int icua_engine_info(icua_engine* e, icua_info_t* out) {
     out->persistent_decode = e->persist_ok ? 1 : 0;
     out->last_decode_persistent = e->last_persistent ? 1 : 0;
     out->visual_rows = e->n_vis;
+    out->pair_passes = e->pair_passes;
     return 0;
 }
 

@@ -65,7 +65,7 @@ class _Info(C.Structure):
     _fields_ = [("format", C.c_int32), ("layers", C.c_int32), ("max_context", C.c_int32),
                 ("max_pass", C.c_int32), ("max_steps", C.c_int32), ("weight_bytes", C.c_int64),
                 ("kv_bytes", C.c_int64), ("persistent_decode", C.c_int32), ("vision", C.c_int32),
-                ("last_decode_persistent", C.c_int32), ("visual_rows", C.c_int32)]
+                ("last_decode_persistent", C.c_int32), ("visual_rows", C.c_int32), ("pair_passes", C.c_int32)]
 
 
 _lib = None
@@ -225,6 +225,13 @@ class Engine:
         self.weight_bytes = info.weight_bytes
         self.kv_bytes = info.kv_bytes
         self.persistent_decode = bool(info.persistent_decode)
+
+    @property
+    def pair_passes(self) -> int:
+        """Forced grammar pairs that ran as one two-row launch of the persistent kernel."""
+        info = _Info()
+        _check(lib().icua_engine_info(self._h, C.byref(info)))
+        return int(info.pair_passes)
 
     @property
     def last_decode_persistent(self) -> bool:

@@ -140,3 +140,35 @@ def test_prefill_chunk_of_4096_rows_matches_the_oracle(oracle_mod):
         print(f"4096-row chunk: layer 1 {'KV'[kind]} max |d| / row max {worst:.3g}")
         assert ok, worst
     compare_greedy(got, ref, margins, first.max() * np.ones(steps))
+
+
+@pytest.mark.parametrize("n", [9, 600])
+def test_grammar_pairs_28_layers_match_the_oracle_fixture(model28, n):
+    """The reference's product setting on the 28-layer benchmark decoder: grammar pairs on, with
+    the embedding rows of tokens 11 and 3678 scaled so that forced pairs fire (5 pairs in 24
+    tokens).  Each pair runs as one two-row pass of the persistent kernel (pair_passes counts
+    them); the tokens equal the oracle's token loop (tests/golden/make_golden_pairs.py).  With a
+    9-token prompt the pair's two rows fall in different attention splits; with 600 one split
+    holds both rows and ~18 cached rows."""
+    img, sha = model28
+    fx = _fixture("oracle_pairs_28layer.npz")
+    assert sha == fx["image_sha256"].tobytes(), "the synthetic model differs from the fixture's"
+    im = synth.scale_embedding_rows(img, {int(t): float(c) for t, c in fx["scales"]})
+    toks, ref = fx[f"prompt_{n}"], [int(t) for t in fx[f"tokens_{n}"]]
+    steps = len(ref)
+    # Pairs whose pass runs: (11, 220) anywhere, or a step-1 action followed by 7, with the
+    # forced token before the last step (a pair forced into the last step ends the loop).
+    actions = (3678, 7241, 12476, 10855, 11862, 1339, 1472, 24769)
+    pairs = sum(1 for i in range(steps - 2) if (ref[i], ref[i + 1]) == (11, 220) or
+                (i == 0 and ref[0] in actions and ref[1] == 7))
+    assert pairs >= 2, ref
+    with Engine(image=im, max_context=n + steps + 8, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        assert e.grammar_pairs and e.persistent_decode
+        p0 = e.pair_passes
+        got = e.generate(toks, max_new_tokens=steps)
+        assert e.last_decode_persistent
+        ran = e.pair_passes - p0
+    print(f"grammar pairs, prompt {n}: {len(got)} tokens, {ran} two-row passes; identical: {got == ref}")
+    assert got == ref, (got, ref)
+    assert ran == pairs, (ran, pairs)
