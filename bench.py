@@ -35,9 +35,9 @@ VIS_OFFSET, LLM_H, LLM_W = 16, 32, 32
 PREFILL = 4096
 # HBM bytes the persistent decode launch moves per algorithmic byte, from rocprofv3 FETCH_SIZE
 # (scaled by 1.964, the factor that makes it read a GEMV of known footprint correctly) plus
-# WRITE_SIZE over a 16-step launch at this context: 1.4794 GB per step against 1.4392 GB of
+# WRITE_SIZE over a 16-step launch at this context: 1.4766 GB per step against 1.4391 GB of
 # weights and K/V (profiles/decode_q4_4k_persistent_counters.md).
-DECODE_TRAFFIC_RATIO = 1.4794 / 1.4392
+DECODE_TRAFFIC_RATIO = 1.4766 / 1.4391
 
 
 def weight_bytes_per_token(fmt=WeightFormat.Q4) -> int:
@@ -495,15 +495,19 @@ def main():
         sys.exit(2)
     if args.workload == "verify":
         print(json.dumps(run_verify(args.steps, args.warmup)))
+        dump_maps()
         return
     if args.workload == "gemv":
         print(json.dumps(run_gemv(200)))
+        dump_maps()
         return
     if args.workload == "vision":
         print(json.dumps(run_vision(args.steps, args.warmup)))
+        dump_maps()
         return
     if args.workload == "quant":
         print(json.dumps(run_quant(20)))
+        dump_maps()
         return
 
     K, W = args.steps, args.warmup
@@ -604,6 +608,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
                      "traffic": int(launch_bytes * DECODE_TRAFFIC_RATIO) if e_persistent else None,
+                     "traffic_source": ("algorithmic bytes x 1.026, the HBM/algorithmic ratio rocprofv3 "
+                                        "FETCH_SIZE (x1.964 calibration) + WRITE_SIZE read for a 16-step "
+                                        "launch of this kernel at this context") if e_persistent else None,
                      "kernel": "pk::decode_kernel<2> (q4 persistent decode)" if e_persistent
                                else "decode step graph (q4)",
                      "launch_ms": round(dec_ms, 4), "bytes_per_launch": int(launch_bytes)},
@@ -618,6 +625,17 @@ def main():
         "verify_q8_8192": ver,
     }
     print(json.dumps(out))
+    dump_maps()
+
+
+def dump_maps():
+    """With ICUA_MAPS_OUT=path, copies this process's memory map (/proc/self/maps) to path as the
+    benchmark returns, so that the addresses of a crash in the exit handlers that run afterwards
+    (the profiler's, under rocprofv3) can be matched to the mappings that hold them."""
+    path = os.environ.get("ICUA_MAPS_OUT")
+    if path:
+        with open("/proc/self/maps") as f, open(path, "w") as g:
+            g.write(f.read())
 
 
 if __name__ == "__main__":
