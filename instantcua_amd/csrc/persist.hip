@@ -521,6 +521,30 @@ __device__ __forceinline__ void mac_blocks(const Shared& S, const WB<FMT, CW>* w
     for (int b = 0; b < NB; ++b) acc[b] = quad_rows(acc[b]);
 }
 
+// mac_blocks for NR staged rows (row t at group offset t * gstride): acc[t * NB + b].  Each quad's
+// weight registers are multiplied by every row before the next quad is touched, so they are free
+// once the quad is done, as in the one-row loop.
+template <int FMT, int CW, int NB, int NR>
+__device__ __forceinline__ void mac_rows(const Shared& S, const WB<FMT, CW>* wb, int mw, int lane,
+                                         float (&acc)[NR * NB], int gstride) {
+#pragma unroll
+    for (int b = 0; b < NR * NB; ++b) acc[b] = 0.f;
+#pragma unroll
+    for (int p = 0; p < CW / 2; ++p) {
+#pragma unroll
+        for (int t = 0; t < NR; ++t) {
+            const QuadOps<FMT> o = quad_load<FMT>(S, mw * CW + 2 * p, lane, t * gstride);
+            v4i C[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) C[b] = quad_mfma<FMT>(o, wb[b].wv[2 * p], wb[b].wv[2 * p + 1]);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[t * NB + b] = quad_scale<FMT>(o, C[b], wb[b].sq[p], acc[t * NB + b]);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NR * NB; ++b) acc[b] = quad_rows(acc[b]);
+}
+
 // Down half-block `half` of row block rb straight into wdb (math wave mw requests the chunks
 // and the scale columns it multiplies later, so each wave reads back only its own requests).
 template <int FMT>
@@ -574,6 +598,25 @@ __device__ __forceinline__ float reduce_math(Shared& S, float acc) {
     float s = 0.f;
     if (wave == 0) s = (S.red[lane] + S.red[64 + lane]) + (S.red[128 + lane] + S.red[192 + lane]);
     return s;
+}
+
+// The math waves' partials of N <= 6 blocks into S.red (one barrier); red_total(S, j) then reads
+// block j's total (math wave 0, lanes 0-15 meaningful) where it is used, so that no wave holds
+// the N totals in registers across the stage.
+template <bool MATH, int N>
+__device__ __forceinline__ void reduce_math_store(Shared& S, const float (&acc)[N]) {
+    static_assert(N <= 6, "S.red holds six blocks");
+    const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+    if (MATH) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) S.red[(j * MW + wave) * 64 + lane] = acc[j];
+    }
+    __syncthreads();
+}
+__device__ __forceinline__ float red_total(const Shared& S, int j) {
+    const int lane = my_tid() % 64;
+    const float* r = S.red + j * MW * 64;
+    return (r[lane] + r[64 + lane]) + (r[128 + lane] + r[192 + lane]);
 }
 
 // reduce_math for N <= 6 blocks at once (one barrier).
@@ -1455,21 +1498,15 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
             PK_TRACE_X(l, 1);
             if (qkv_wg) {
                 stage_c<FMT, H, NR>(S, l == 0 ? S.emb : S.vec, true);
-                float acc[2 * NR], y[2 * NR];
-#pragma unroll
-                for (int t = 0; t < NR; ++t) {
-                    float at[2] = {0.f, 0.f};
-                    if (math) mac_blocks<FMT, CW2, 2>(S, wx, mw, lane, at, t * (H / G));
-                    acc[2 * t] = at[0];
-                    acc[2 * t + 1] = at[1];
-                }
+                float acc[2 * NR] = {};
+                if (math) mac_rows<FMT, CW2, 2, NR>(S, wx, mw, lane, acc, H / G);
                 PK_TRACE(l, 28);
-                reduce_math_n<MATH, 2 * NR>(S, acc, y);
+                reduce_math_store<MATH, 2 * NR>(S, acc);
                 if (wave == 0) {  // rows 2i, 2i + 1 of a block in packet i (even lanes)
 #pragma unroll
                     for (int t = 0; t < NR; ++t) {
                         const float rsn = norm_scale<H>(S, t);
-                        const float y0 = y[2 * t] * rsn, y1 = y[2 * t + 1] * rsn;
+                        const float y0 = red_total(S, 2 * t) * rsn, y1 = red_total(S, 2 * t + 1) * rsn;
                         const float n0 = xor1(y0), n1 = xor1(y1);
                         if (lane < 16 && !(lane & 1)) {
                             uint64_t* q = ll + PK::QKVP + t * (QKV / 2);
@@ -1832,18 +1869,13 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
             if (w < H / 16) {
                 PK_TRACE_X(l, 7);
                 stage_c<FMT, H, NR>(S, S.vec, false);
-                float acc[NR], y[NR];
-#pragma unroll
-                for (int t = 0; t < NR; ++t) {
-                    float at[1] = {0.f};
-                    if (math) mac_blocks<FMT, CW2, 1>(S, wx, mw, lane, at, t * (H / G));
-                    acc[t] = at[0];
-                }
-                reduce_math_n<MATH, NR>(S, acc, y);
+                float acc[NR] = {};
+                if (math) mac_rows<FMT, CW2, 1, NR>(S, wx, mw, lane, acc, H / G);
+                reduce_math_store<MATH, NR>(S, acc);
                 if (wave == 0) {  // the owner keeps the residual as published (even rows rounded)
 #pragma unroll
                     for (int t = 0; t < NR; ++t) {
-                        const float xn = lane < 16 ? (S.xown[t][lane] + S.xhi[t][lane]) + y[t] : 0.f;
+                        const float xn = lane < 16 ? (S.xown[t][lane] + S.xhi[t][lane]) + red_total(S, t) : 0.f;
                         const float xo = xor1(xn);
                         if (lane < 16) {
                             S.xown[t][lane] = (lane & 1) ? xn : q19(xn);
@@ -1881,16 +1913,10 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
                 PK_TRACE_X(l, 9);
                 stage_c<FMT, H, NR>(S, S.vec, true);
                 PK_TRACE(l, 13);
-                float acc[3 * NR], y[3 * NR];
-#pragma unroll
-                for (int t = 0; t < NR; ++t) {
-                    float at[3] = {0.f, 0.f, 0.f};
-                    if (math) mac_blocks<FMT, CW2, 3>(S, wgu, mw, lane, at, t * (H / G));
-#pragma unroll
-                    for (int j = 0; j < 3; ++j) acc[3 * t + j] = at[j];
-                }
+                float acc[3 * NR] = {};
+                if (math) mac_rows<FMT, CW2, 3, NR>(S, wgu, mw, lane, acc, H / G);
                 PK_TRACE(l, 26);
-                reduce_math_n<MATH, 3 * NR>(S, acc, y);
+                reduce_math_store<MATH, 3 * NR>(S, acc);
                 PK_TRACE(l, 14);
                 if (wave == 0) {
 #pragma unroll
@@ -1899,7 +1925,7 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
 #pragma unroll
                         for (int j = 0; j < 3; ++j) {
                             // Block 3w + j: gate units 8 (3w + j) + 0..7 in lanes 0-7, their up rows in 8-15.
-                            const float yj = y[3 * t + j] * rsn;
+                            const float yj = red_total(S, 3 * t + j) * rsn;
                             const float hv = swiglu(yj, xor8(yj)), hn = xor1(hv);
                             if (lane < 8 && !(lane & 1))
                                 st64(ll + PK::HP + t * (FF / 2) + (3 * w + j) * 4 + lane / 2, pack2(hv, hn, r + 1));
@@ -1943,13 +1969,13 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
                     for (int t = 0; t < NR; ++t) yd[t] = wd_mac_lds<FMT>(S, wdb, mw, lane, t * (FFH / G));
                     PK_TRACE(l, 24);
                 }
-                float y[NR];
-                reduce_math_n<MATH, NR>(S, yd, y);
+                reduce_math_store<MATH, NR>(S, yd);
                 PK_TRACE(l, 19);
                 if (wave == 0) {
 #pragma unroll
                     for (int t = 0; t < NR; ++t) {
-                        const float v = lane < 16 ? (half == 0 ? S.xown[t][lane] + y[t] : y[t]) : 0.f;
+                        const float yt = red_total(S, t);
+                        const float v = lane < 16 ? (half == 0 ? S.xown[t][lane] + yt : yt) : 0.f;
                         const float vn = xor1(v);
                         if (lane < 16) {
                             if (half == 0) S.xown[t][lane] = (lane & 1) ? v : q19(v);
