@@ -78,31 +78,82 @@ def gemv_roofline(iters=200, K=Dims.hidden, N=Dims.gu_rows):
     return {"kernel": f"q4 GEMV {K}x{N}", "us": us, "bytes": traffic, "copies": copies}
 
 
-def cpu_baseline(img, ctx, seconds=10.0):
-    """Oracle decode steps at the same context on the host cores (KV filled with fp16 N(0,1))."""
+def _cpu_model(img, ctx, max_steps):
+    """The oracle's model state over img with K/V slots 0..ctx-1 filled with fp16 N(0,1)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
     oracle.build()
-    max_steps = 40
     om = oracle.OracleModel(img, ctx + max_steps + 2)
     for l in range(om.layers):
         for kind in (0, 1):
             om.kv(l, kind)[:, :ctx] = synth.fp16_normal((Dims.kv_heads, ctx, Dims.head_dim), f"cpu-kv{kind}", l)
-    tok = np.array([1], dtype=np.int32)
-    om.run_pass(tok, ctx)  # warm
+    return oracle, om
+
+
+def _time_steps(step, seconds, max_steps):
+    """Runs step(i) until `seconds` have passed or max_steps ran; (steps, seconds)."""
     n, t0 = 0, time.perf_counter()
     while True:
-        om.run_pass(tok, ctx + 1 + n)
+        step(n)
         n += 1
         if time.perf_counter() - t0 > seconds or n >= max_steps:
-            break
-    dt = time.perf_counter() - t0
+            return n, time.perf_counter() - t0
+
+
+def cpu_baseline(img, ctx, seconds=10.0):
+    """Decode steps of the fp32 CPU port (oracle/port32.c) at the same context on the host cores
+    (K/V filled with fp16 N(0,1))."""
+    max_steps = 512
+    oracle, om = _cpu_model(img, ctx, max_steps)
+    tok = np.array([1], dtype=np.int32)
+    om.port32_pass(tok, ctx)  # warm
+    n, dt = _time_steps(lambda i: om.port32_pass(tok, ctx + 1 + i), seconds, max_steps)
     threads = oracle.get_threads()
     om.close()
     return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "precision": "fp64 accumulation over fp32 storage (the oracle's arithmetic; an fp32 port would be faster)",
-            "sample": f"{n} decode steps of the 28-layer q4 decoder at {ctx}-token context (oracle, fp64 accumulation)"}
+            "precision": "fp32 arithmetic and accumulation, fp16 KV cache",
+            "sample": f"{n} decode steps of the 28-layer q4 decoder at {ctx}-token context "
+                      "(fp32 CPU port, OpenMP over all host threads)"}
+
+
+def cpu_oracle_decode(img, ctx, seconds=8.0):
+    """The fp64-accumulating oracle's decode step at the same context (beside the fp32 port)."""
+    max_steps = 40
+    oracle, om = _cpu_model(img, ctx, max_steps)
+    tok = np.array([1], dtype=np.int32)
+    om.run_pass(tok, ctx)  # warm
+    n, dt = _time_steps(lambda i: om.run_pass(tok, ctx + 1 + i), seconds, max_steps)
+    threads = oracle.get_threads()
+    om.close()
+    return {"config": f"28-layer q4 decode at {ctx}-token context, oracle (fp64 accumulation over fp32 storage)",
+            "tok_s": round(n / dt, 2), "steps_timed": n, "cores": threads}
+
+
+def cpu_text_context(img, n_prompt=1024, steps=256, seconds=12.0):
+    """The 1024-token text workload on the fp32 CPU port: the whole prefill, then decode steps for
+    `seconds` (at most `steps`); decode tok/s over all 256 steps is extrapolated from them."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    oracle.build()
+    om = oracle.OracleModel(img, n_prompt + steps + 2)
+    toks = synth.random_tokens(n_prompt, "c3-prompt")  # the GPU text workload's prompt
+    t0 = time.perf_counter()
+    logits = om.port32_pass(toks, 0)
+    prefill_s = time.perf_counter() - t0
+    state = {"tok": np.array([int(np.argmax(logits))], dtype=np.int32)}
+
+    def step(i):
+        state["tok"][0] = int(np.argmax(om.port32_pass(state["tok"], n_prompt + i)))
+
+    n, dt = _time_steps(step, seconds, steps - 1)
+    threads = oracle.get_threads()
+    om.close()
+    return {"config": f"28-layer q4 decoder, {n_prompt}-token text prefill + {steps} greedy decode steps, "
+                      "fp32 CPU port", "prefill_tok_s": round(n_prompt / prefill_s, 1), "prefill_s": round(prefill_s, 2),
+            "decode_tok_s": round(n / dt, 2), "decode_steps_timed": n,
+            "decode_extrapolated": n < steps - 1, "cores": threads}
 
 
 def cpu_rows(budget_s=6.0):
@@ -138,7 +189,7 @@ def cpu_rows(budget_s=6.0):
         dt = (time.perf_counter() - t0) / n
         nbytes = m.codes.nbytes + m.sb.nbytes
         rows.append({"config": f"q4 GEMV {K}x{N}", "us": round(dt * 1e6, 1), "GB_s": round(nbytes / dt / 1e9, 2)})
-    return {"cores": oracle.get_threads(), "kind": "port", "precision": "fp64 accumulation", "rows": rows}
+    return {"cores": oracle.get_threads(), "kind": "port", "precision": "fp64 accumulation (the oracle)", "rows": rows}
 
 
 def run_q8_prefill(img):
@@ -569,7 +620,11 @@ def main():
     text = run_text_context(img)
     gram = run_grammar_pairs(img)
     cpu = None if args.no_cpu else cpu_baseline(img, PREFILL)
-    rows = None if args.no_cpu else cpu_rows()
+    rows = None
+    if not args.no_cpu:
+        rows = cpu_rows()
+        rows["oracle_decode_4k"] = cpu_oracle_decode(img, PREFILL)
+        rows["text_context_1024_fp32_port"] = cpu_text_context(img)
     del img
     q8 = ver = None
     if not args.no_prefill:

@@ -2,6 +2,7 @@
  * The arithmetic contract and the reference files each part follows are stated in
  * oracle.h.  Nothing in the product library links this file. */
 #include "oracle.h"
+#include "oracle_model.h"
 
 #include <math.h>
 #include <omp.h>
@@ -194,21 +195,6 @@ void or_mrope_table(int maxctx, int vis_offset, int llm_h, int llm_w, float* out
 
 /* ------------------------------------------------------------------------------------------ */
 /* Model. */
-
-typedef struct {
-    const float *attn_norm, *q_norm, *k_norm, *mlp_norm;
-    const uint8_t *wqkv, *wqkv_sb, *wo, *wo_sb, *wgu, *wgu_sb, *wd, *wd_sb;
-} or_layer_w;
-
-struct or_model {
-    int fmt, layers, maxctx;
-    const uint8_t* img;
-    const uint8_t *embed, *embed_sb;
-    const float* final_norm;
-    or_layer_w L[OR_MAXLAYERS];
-    uint16_t* kv; /* [layers][2][NKV][maxctx][HD] */
-    float* rope;  /* [maxctx][64][2] */
-};
 
 enum { T_LLM_BASE = 315, T_LAYER_BASE = 318, T_PER_LAYER = 14, T_COUNT = 710 };
 

@@ -123,6 +123,12 @@ int or_generate_commit(or_model* m, const int32_t* toks, int n, const float* poo
                        const float* const* deepstack, int max_steps, int eos0, int eos1, int grammar,
                        int32_t* out_tokens);
 
+/* fp32 CPU port (port32.c) -- the benchmark's CPU baseline, not the checker: a pass of n text
+ * tokens at slots pos .. pos+n-1 in fp32 arithmetic (fused dequantise-and-dot GEMVs, fp16 KV
+ * cache written as the oracle does), logits of the last row.  Returns -1 if the pass exceeds
+ * the context. */
+int p32_pass(or_model* m, const int32_t* toks, int n, int pos, float* logits);
+
 /* Group-wise quantisers of the .icua converter, restated in float32 with the reference's
  * operation order (Sources/Engine/Convert.swift:214-320; built with -ffp-contract=off).
  * m is row-major [rows][cols].

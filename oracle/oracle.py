@@ -82,6 +82,7 @@ def lib():
         L.or_vit_block.argtypes = [C.c_void_p, C.c_size_t, C.c_int, _f32p, C.c_int, C.c_int]
         L.or_set_threads.argtypes = [C.c_int]
         L.or_get_threads.restype = C.c_int
+        L.p32_pass.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_int, _f32p]
         _lib = L
     return _lib
 
@@ -206,6 +207,16 @@ class OracleModel:
     def lm_head(self, x: np.ndarray) -> np.ndarray:
         out = np.empty(VOCAB, dtype=np.float32)
         lib().or_lm_head(self.h, np.ascontiguousarray(x, dtype=np.float32), out)
+        return out
+
+    def port32_pass(self, toks, pos: int) -> np.ndarray:
+        """The fp32 CPU port (port32.c, the benchmark's CPU baseline, not the checker): a pass of
+        text tokens at slots pos.., writing their K/V into this model's cache; the last row's
+        logits."""
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        out = np.empty(VOCAB, dtype=np.float32)
+        if lib().p32_pass(self.h, toks, toks.size, pos, out) != 0:
+            raise RuntimeError("port32 pass exceeds the context")
         return out
 
     @staticmethod
