@@ -45,6 +45,8 @@ def weight_bytes_per_token(fmt=WeightFormat.Q4) -> int:
     def mat(rows, K):
         if fmt == WeightFormat.Q4:
             return rows * K // 2 + rows * (K // 64) * 4
+        if fmt == WeightFormat.F16:
+            return rows * K * 2
         return rows * K + rows * (K // 32) * 2
     H, FF = Dims.hidden, Dims.ff
     layer = mat(Dims.qkv_rows, H) + mat(H, H) + mat(Dims.gu_rows, H) + mat(H, FF)
@@ -207,6 +209,35 @@ def run_q8_prefill(img):
     return {"workload": "28-layer q8 g32 decoder, the same 4096-token vision-context prefill",
             "prefill_tok_s": round(PREFILL / (ms / 1e3), 1), "prefill_ms": round(ms, 2),
             "prefill_mfma_frac": round(PREFILL_FLOPS / (ms * 1e-3) / MFMA_F16_PEAK, 4)}
+
+
+def run_f16_decode(steps=32, warmup=4):
+    """The 4k-context vision workload on a 28-layer f16 decoder: f16 weights decode on the
+    per-stage kernels (one step per HIP-graph replay); tok/s and the fraction of the HBM roofline
+    (2-byte weights plus K/V per token).  The weights are random f16 bit patterns (a timing run)."""
+    img = synth.build_model_image(WeightFormat.F16, n_layers=LAYERS, tag="bench-f16", f16_bits=True)
+    vp = synth.visual_prompt(PREFILL, VIS_OFFSET, LLM_H, LLM_W, tag="bench-vis")
+    e = eng.Engine(image=img, max_context=PREFILL + warmup + steps + 8, max_steps=warmup + steps + 2)
+    e.eos = (-1, -1)
+    e.prepare_mrope(VIS_OFFSET, LLM_H, LLM_W)
+    e.set_visual(vp.pooler.astype(np.float32), [d.astype(np.float32) for d in vp.deepstack])
+    e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=warmup + steps + 1)
+    e.decode_steps(warmup)
+    e.decode_steps(steps)
+    dec_ms = e.last_timing["decode_ms"]
+    persistent = e.last_decode_persistent
+    e.close()
+    del img
+    nbytes = sum(weight_bytes_per_token(WeightFormat.F16) + kv_bytes_per_token(PREFILL + warmup + i + 1)
+                 for i in range(steps))
+    out = {"workload": "28-layer f16 decoder, the same 4096-token vision-context prefill, greedy decode",
+           "steps": steps, "decode_tok_s": round(steps / (dec_ms / 1e3), 1),
+           "decode_us_per_token": round(dec_ms * 1e3 / steps, 1),
+           "bytes_per_token": int(nbytes / steps), "GB_s": round(nbytes / (dec_ms * 1e-3) / 1e9, 1),
+           "roofline_frac": round(nbytes / (dec_ms * 1e-3) / HBM_PEAK, 4),
+           "path": "persistent kernel" if persistent else "per-stage kernels, HIP graph per step"}
+    log(f"f16 decode: {out['decode_us_per_token']} us/token, {out['roofline_frac']:.3f} of roofline ({out['path']})")
+    return out
 
 
 def forced_compare(e, n_prompt, fixture, n, first_logits=None):
@@ -626,8 +657,9 @@ def main():
         rows["oracle_decode_4k"] = cpu_oracle_decode(img, PREFILL)
         rows["text_context_1024_fp32_port"] = cpu_text_context(img)
     del img
-    q8 = ver = None
+    q8 = ver = f16 = None
     if not args.no_prefill:
+        f16 = run_f16_decode()
         img8 = synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="bench-q8")
         q8 = run_q8_prefill(img8)
         v = run_verify(10, 2, img8)  # the verify workload (--workload verify), a short run
@@ -678,6 +710,7 @@ def main():
         "grammar_pairs_28": gram,
         "prefill_q8_4096": q8,
         "verify_q8_8192": ver,
+        "decode_f16_4k": f16,
     }
     print(json.dumps(out))
     dump_maps()

@@ -19,6 +19,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <unordered_map>
 #include <utility>
@@ -85,6 +86,13 @@ struct Insn {
     int32_t op, a, b, guard;
 };
 
+// Longest piece one match may return, in bytes.  The matcher reads at most this many bytes past a
+// match's start, as if the text ended there, so its visited set (MAX_PIECE * n_code bits, n_code
+// <= 4096) and its backtracking stack stay bounded, and so does the BPE of one piece.  Hugging
+// Face's pre-tokenizer has no such limit: a run of more than 16 KiB that its split pattern takes
+// as one piece (e.g. 16 Ki spaces or letters in a row) is cut into pieces of 16 KiB here.
+constexpr size_t MAX_PIECE = 16384;
+
 // Per-call state of the matcher: the visited set of one attempt (bit (p - start) * n_code + pc,
 // cleared after the attempt up to the highest word it touched) and the backtracking stack.
 struct MatchScratch {
@@ -107,8 +115,10 @@ struct Splitter {
     }
 
     // End of the leftmost-first match that starts at byte `start`, or `start` when there is none
-    // (the compiler rejects patterns that match the empty string).
+    // (the compiler rejects patterns that match the empty string); the text is read up to
+    // start + MAX_PIECE at most.
     size_t match(const uint8_t* s, size_t start, size_t n, MatchScratch& sc) const {
+        n = std::min(n, start + MAX_PIECE);
         size_t top = 0, end = start;
         bool found = false;
         sc.stack.clear();
@@ -244,34 +254,52 @@ struct icua_tok {
 
 
     // --- BPE --------------------------------------------------------------------------------
-    // Merges the adjacent pair of lowest rank, leftmost first, until none applies.
+    // Merges the adjacent pair of lowest rank, leftmost first, until none applies.  The symbols
+    // form a linked list and the candidate pairs a min-heap of (rank, left position): a popped
+    // pair is still current when its left symbol is alive and the pair there still has that rank
+    // (every merge rule has its own rank, so the rank names the pair).  O(n log n) per piece.
     void bpe(const uint8_t* s, size_t n, std::vector<int32_t>& out) const {
-        std::vector<int32_t> sym(n);
-        for (size_t i = 0; i < n; ++i) sym[i] = byte_tok[s[i]];
+        if (n == 0) return;
+        std::vector<int32_t> id(n);
+        std::vector<int32_t> prv(n), nxt(n);  // -1: none
+        for (size_t i = 0; i < n; ++i) {
+            id[i] = byte_tok[s[i]];
+            prv[i] = (int32_t)i - 1;
+            nxt[i] = i + 1 < n ? (int32_t)i + 1 : -1;
+        }
         auto rank_of = [&](int32_t a, int32_t b, int32_t* res) -> uint32_t {
             auto it = merge.find((uint64_t)(uint32_t)a << 32 | (uint32_t)b);
             if (it == merge.end()) return UINT32_MAX;
-            *res = (int32_t)(it->second & 0xFFFFFFFFu);
+            if (res) *res = (int32_t)(it->second & 0xFFFFFFFFu);
             return (uint32_t)(it->second >> 32);
         };
-        while (sym.size() > 1) {
-            uint32_t best = UINT32_MAX;
-            size_t bi = 0;
-            int32_t bres = -1;
-            for (size_t i = 0; i + 1 < sym.size(); ++i) {
-                int32_t res;
-                const uint32_t r = rank_of(sym[i], sym[i + 1], &res);
-                if (r < best) {
-                    best = r;
-                    bi = i;
-                    bres = res;
-                }
-            }
-            if (best == UINT32_MAX) break;
-            sym[bi] = bres;
-            sym.erase(sym.begin() + bi + 1);
+        std::vector<uint64_t> heap;  // (rank << 32 | left position), smallest on top
+        auto push = [&](int32_t i) {
+            if (i < 0 || nxt[i] < 0) return;
+            const uint32_t r = rank_of(id[i], id[nxt[i]], nullptr);
+            if (r == UINT32_MAX) return;
+            heap.push_back((uint64_t)r << 32 | (uint32_t)i);
+            std::push_heap(heap.begin(), heap.end(), std::greater<uint64_t>());
+        };
+        for (size_t i = 0; i + 1 < n; ++i) push((int32_t)i);
+        std::vector<uint8_t> dead(n, 0);
+        while (!heap.empty()) {
+            std::pop_heap(heap.begin(), heap.end(), std::greater<uint64_t>());
+            const uint64_t top = heap.back();
+            heap.pop_back();
+            const int32_t i = (int32_t)(uint32_t)top;
+            if (dead[i] || nxt[i] < 0) continue;
+            int32_t res;
+            if (rank_of(id[i], id[nxt[i]], &res) != (uint32_t)(top >> 32)) continue;  // a stale pair
+            const int32_t j = nxt[i];
+            id[i] = res;
+            dead[j] = 1;
+            nxt[i] = nxt[j];
+            if (nxt[j] >= 0) prv[nxt[j]] = i;
+            push(prv[i]);
+            push(i);
         }
-        out.insert(out.end(), sym.begin(), sym.end());
+        for (int32_t i = 0; i >= 0; i = nxt[i]) out.push_back(id[i]);
     }
     // Split's "isolated" behaviour: every match is a piece and so is every gap between matches.
     void encode_segment(const uint8_t* p, size_t n, std::vector<int32_t>& out) const {

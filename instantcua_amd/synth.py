@@ -137,8 +137,12 @@ def _layout(sizes: dict):
     return table, total
 
 
-def fill_matrix(fmt: int, rows: int, cols: int, codes: np.ndarray, sb: np.ndarray, rng: np.random.Generator) -> None:
-    """Fill code bytes and scale bytes (uint8 views) of one quantised matrix in place."""
+def fill_matrix(fmt: int, rows: int, cols: int, codes: np.ndarray, sb: np.ndarray, rng: np.random.Generator,
+                f16_bits: bool = False) -> None:
+    """Fill code bytes and scale bytes (uint8 views) of one quantised matrix in place.  With
+    f16_bits, f16 weights are random bit patterns of magnitude 2^-7 .. 2^-3 with a random sign and
+    mantissa, the matrix tiled from one random 4 MiB block (an order of magnitude faster than
+    normal values; for timing runs, where the values do not matter)."""
     if fmt == WeightFormat.Q4:
         codes[:] = rng.integers(0, 256, size=codes.size, dtype=np.uint8)
         g = rows * (cols // 64)
@@ -153,6 +157,12 @@ def fill_matrix(fmt: int, rows: int, cols: int, codes: np.ndarray, sb: np.ndarra
         g = rows * (cols // 32)
         s = (np.abs(rng.standard_normal(g, dtype=np.float32) * np.float32(0.02)) / np.float32(127)).astype(np.float16)
         sb.view(np.float16)[:] = s
+    elif f16_bits:
+        bits = codes.view(np.uint16)
+        block = np.frombuffer(rng.bytes(2 * min(bits.size, 1 << 21)), dtype=np.uint16) & np.uint16(0x8FFF)
+        block |= np.uint16(0x2000)  # sign, exponent 8 .. 11 (2^-7 <= |w| < 2^-3), mantissa
+        for i in range(0, bits.size, block.size):
+            bits[i:i + block.size] = block[:bits.size - i]
     else:
         codes.view(np.float16)[:] = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.05)).astype(np.float16)
 
@@ -178,9 +188,9 @@ def copy_embedding_row(img: np.ndarray, src: int, dst: int) -> None:
 
 
 def build_model_image(fmt: int, n_layers: int = Dims.layers, tag: str = "model", vision: bool = False,
-                      zero_vision_blocks: bool = False) -> np.ndarray:
+                      zero_vision_blocks: bool = False, f16_bits: bool = False) -> np.ndarray:
     """Return a complete in-memory ``.icua`` image (uint8 array) of a synthetic decoder, with the
-    vision tower and its mergers when ``vision`` is set."""
+    vision tower and its mergers when ``vision`` is set (f16_bits: see fill_matrix)."""
     sizes = model_tensor_sizes(fmt, n_layers)
     if vision:
         for tid, dt, shape in vision_tensor_specs():
@@ -196,7 +206,7 @@ def build_model_image(fmt: int, n_layers: int = Dims.layers, tag: str = "model",
         return img[off:off + n]
 
     H, V = Dims.hidden, Dims.vocab
-    fill_matrix(fmt, V, H, view(TensorID.embed), view(TensorID.embed_sb), _rng(tag, -1, TensorID.embed))
+    fill_matrix(fmt, V, H, view(TensorID.embed), view(TensorID.embed_sb), _rng(tag, -1, TensorID.embed), f16_bits)
     view(TensorID.final_norm).view(np.float32)[:] = _norm_weights(_rng(tag, -1, TensorID.final_norm), H)
     for l in range(n_layers):
         L = lambda k: TensorID.llm_layer(l, k)
@@ -204,7 +214,7 @@ def build_model_image(fmt: int, n_layers: int = Dims.layers, tag: str = "model",
                         (TensorID.k_norm, Dims.head_dim), (TensorID.mlp_norm, H)):
             view(L(slot)).view(np.float32)[:] = _norm_weights(_rng(tag, l, L(slot)), n)
         for wid, sid, rows, cols in _layer_mats():
-            fill_matrix(fmt, rows, cols, view(L(wid)), view(L(sid)), _rng(tag, l, L(wid)))
+            fill_matrix(fmt, rows, cols, view(L(wid)), view(L(sid)), _rng(tag, l, L(wid)), f16_bits)
     if vision:
         _fill_vision(view, tag, zero_vision_blocks)
     return img

@@ -155,6 +155,49 @@ def test_rejects_other_pipelines(tmp_path, pair):
         itok.Tokenizer(str(p))  # not a compiled file
 
 
+_RUN_SCRIPT = r"""
+import ctypes as C, resource, sys
+import numpy as np
+sys.path.insert(0, sys.argv[2])
+from instantcua_amd import tokenizer as itok
+tok = itok.Tokenizer(sys.argv[1])
+text = b" " * (4 << 20)
+out = np.zeros(len(text) + 1, dtype=np.int32)  # touched: its pages count before the call
+n = C.c_size_t(0)
+fn = itok._lib().icua_tok_encode
+assert fn(tok._h, b"a b", 3, 0, out.ctypes.data_as(C.c_void_p), out.size, C.byref(n)) == 0
+before = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss
+assert fn(tok._h, text, len(text), 0, out.ctypes.data_as(C.c_void_p), out.size, C.byref(n)) == 0
+after = resource.getrusage(resource.RUSAGE_SELF).ru_maxrss
+print(n.value, after - before)
+"""
+
+
+def test_long_runs_are_cut_into_bounded_pieces(pair, tmp_path):
+    """A match reads at most 16 KiB past its start (tokenizer.cpp MAX_PIECE): below that the pieces
+    are HF's; a longer run becomes pieces of 16 KiB, the text still round-trips, and the memory an
+    encode takes does not grow with the run (a visited set and stack per byte of a 4 MiB run would
+    take ~100 MB; the limit here is the output buffers')."""
+    hf, ours = pair
+    for s in [" " * 5000 + "x", "a" * 9000, "7" * 12000, "\n" * 3000 + "y", "日" * 5000]:
+        assert ours.encode(s) == hf_ids(hf, s)
+    for s in [" " * 70000, "b" * 50000 + " c", "x" + "\t" * 40000]:
+        assert ours.decode(ours.encode(s)) == s
+    import os
+    import subprocess
+    import sys
+    js = str(tmp_path / "tokenizer.json")
+    hf.save(js)
+    ict = str(tmp_path / "tokenizer.ict")
+    itok.compile(js, ict)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _RUN_SCRIPT, ict, root], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    n_tokens, grew_kib = (int(v) for v in r.stdout.split())
+    assert 0 < n_tokens <= 4 << 20
+    assert grew_kib < 48 * 1024, grew_kib
+
+
 def test_invalid_utf8_is_rejected(pair):
     import ctypes as C
     _, ours = pair
