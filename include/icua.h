@@ -96,12 +96,13 @@ int icua_set_visual(icua_engine* e, const float* pooler, const float* const* dee
 int icua_prefill(icua_engine* e, const int32_t* tokens, int n, int start_pos, int vis_offset, int max_new,
                  int write_logits);
 
-/* k x Engine.encodeDecodeStep (Engine.swift:675-681), GPU-resident with token feedback on the
- * device; returns after completion.  Steps after a stop are no-ops.  q4 / q8 models run all k
- * steps in one persistent cooperative kernel (one workgroup per CU), where a forced grammar pair
- * takes two single-row steps (the first of them commits nothing); f16 models, or
- * ICUA_FLAG_GRAPH_DECODE, replay a captured HIP graph of the per-stage kernels per step, where a
- * forced pair is one two-row pass.  Both paths compute the same arithmetic. */
+/* k x Engine.encodeDecodeStep (Engine.swift:675-681): k passes, GPU-resident with token feedback
+ * on the device; returns after completion.  Passes after a stop are no-ops.  A pass commits one
+ * token, or two when its commit forces a grammar pair, whose two tokens then go through the next
+ * pass together (n = 2, Shaders.swift:1553).  q4 / q8 models run the single-row passes in one
+ * persistent cooperative kernel (one workgroup per CU) and a pair's pass in a launch of the
+ * kernel's two-row form; f16 models, or ICUA_FLAG_GRAPH_DECODE, replay a captured HIP graph of
+ * the per-stage kernels per pass.  Both paths compute the same arithmetic. */
 int icua_decode_steps(icua_engine* e, int k);
 
 /* Engine.generateVision (Engine.swift:696-827) minus the vision encoder: prefill + greedy decode

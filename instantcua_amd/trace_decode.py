@@ -7,6 +7,7 @@ workgroup's QKV start), as the median over layers 4..23 of the median, earliest 
 workgroup; then the same for the final norm, lm_head and the greedy commit.
 
 Usage (on a GPU):  python -m instantcua_amd.trace_decode [--layers 28] [--pos 4096] [--steps 16]
+                   python -m instantcua_amd.trace_decode --pairs   (a one-row and a grammar-pair pass)
 The model is the 28-layer q4 group-64 decoder of the decode benchmark; the cache rows before
 --pos are left zero (the bytes moved per step do not depend on their values).
 """
@@ -86,6 +87,42 @@ def read_trace(layers: int, pos: int, steps: int):
     return buf.astype(np.float64) / 100.0, us_tok  # microseconds
 
 
+def read_pair_traces(layers: int):
+    """The last one-row pass and the last grammar-pair pass (two rows) of a greedy decode on the
+    q4 decoder whose embedding rows of tokens 11 and 3678 are scaled by 8, so that pairs are
+    forced; one decode_steps(1) call per pass.  [(name, trace, decode_steps ms), ...]."""
+    eng.LIB_PATH = TRACE_LIB
+    if not os.path.exists(TRACE_LIB):
+        raise SystemExit(f"{TRACE_LIB} is missing: build it with python -m instantcua_amd.build --trace")
+    img = synth.scale_embedding_rows(synth.build_model_image(WeightFormat.Q4, n_layers=layers, tag="bench-q4"),
+                                     {11: 8.0, 3678: 8.0})
+    toks = synth.random_tokens(9, "gram", 3)
+
+    def grab():
+        buf = np.zeros((256, 29, 32), dtype=np.uint64)
+        if eng.lib().icua_debug_persist_trace(buf.ctypes.data_as(C.c_void_p)) != 0:
+            raise SystemExit("the loaded library has no trace")
+        return buf.astype(np.float64) / 100.0
+
+    single = pair = None
+    with eng.Engine(image=img, max_context=64, max_steps=40) as e:
+        e.eos = (-1, -1)
+        assert e.persistent_decode and e.grammar_pairs
+        for _ in range(2):  # the first round loads the code objects
+            e.prefill(toks, max_new=40)
+            while not e.state()["done"]:
+                was_pair = e.state()["n"] == 2
+                e.decode_steps(1)
+                got = (grab(), e.last_timing["decode_ms"])
+                if was_pair:
+                    pair = got
+                else:
+                    single = got
+    if pair is None:
+        raise SystemExit("no grammar pair was forced")
+    return [("single-row pass", *single), ("pair pass", *pair)]
+
+
 def table(t, layer_ids, points, title):
     rows = [f"| {title} | stamped by | median WG (us) | earliest WG | latest WG |", "|---|---|---|---|---|"]
     for ev, who, what in points:
@@ -108,7 +145,18 @@ def main():
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--pos", type=int, default=4096)
     ap.add_argument("--steps", type=int, default=16)
+    ap.add_argument("--pairs", action="store_true",
+                    help="tabulate a one-row pass and a grammar-pair pass of the pair-forcing model instead")
     a = ap.parse_args()
+    if a.pairs:
+        for name, t, ms in read_pair_traces(a.layers):
+            starts = [np.min(t[:, l, 0][t[:, l, 0] > 0]) for l in range(a.layers + 1)]
+            print(f"## {name}: decode_steps(1) {ms * 1e3:.1f} us; layer period median "
+                  f"{np.median(np.diff(starts[:a.layers])[4:24]):.2f} us; lm_head+commit "
+                  f"{np.max(t[:, a.layers, 4]) - starts[a.layers]:.2f} us\n")
+            print(table(t, list(range(4, 24)), LAYER_POINTS, "layer point"))
+            print()
+        return
     t, us_tok = read_trace(a.layers, a.pos, a.steps)
     L = a.layers
     starts = [np.min(t[:, l, 0][t[:, l, 0] > 0]) for l in range(L + 1)]
