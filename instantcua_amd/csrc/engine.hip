@@ -675,7 +675,6 @@ struct icua_engine {
     // The persistent kernel needs all PERSIST_WGS workgroups (one per CU) resident at once.
     int init_persistent() {
         persist_ok = false;
-        if (fmt != 2 && fmt != 1) return 0;
         int dev = 0, coop = 0, cus = 0;
         HIPCK(hipGetDevice(&dev));
         HIPCK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
@@ -934,8 +933,15 @@ struct icua_engine {
             int left = k;
             while (left > 0 && !s.done) {
                 const int nr = s.n == 2 ? 2 : 1, step0 = s.step;
-                if (enqueue_persistent(nr == 2 ? 1 : left, nr)) return -1;
-                pair_passes += nr == 2;
+                if (nr == 2 && fmt == FMT_F16) {
+                    // The kernel has no two-row form for f16 weights: the pair's pass is one replay
+                    // of the per-stage graph (built on first use), which runs n = 2 passes.
+                    if (ensure_graph(MAXM)) return -1;
+                    HIPCK(hipGraphLaunch(graph[1], stream));
+                } else {
+                    if (enqueue_persistent(nr == 2 ? 1 : left, nr)) return -1;
+                    pair_passes += nr == 2;
+                }
                 HIPCK(hipEventRecord(ev1, stream));
                 if (read_state(s)) return -1;  // waits for the launch
                 if (check_persistent()) return -1;

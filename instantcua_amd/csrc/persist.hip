@@ -705,6 +705,129 @@ __device__ __forceinline__ void load_norm8(float (&n)[8], const float* p) {
 }
 
 // ------------------------------------------------------------------------------------------
+// f16 weights (Shaders.swift:459-531, the FMT == 0 branch of the reference's decode kernels).  A
+// 16-row block of a K = 2048 f16 matrix is 64 KiB, four times a q4 block: it cannot wait in the
+// registers ahead of its stage as the int8 tiles do, so the f16 stages stream their blocks (all
+// eight waves, each a K-slice of every block) once the stage input is in, and multiply them on
+// v_mfma_f32_16x16x32_f16: the repacked tile chunk is already the B operand (16 rows x 32 K), and
+// the A operand is the staged vector's 32 K as fp16 hi (row 0) and lo (row 1) parts; rows 2..15
+// read S.zero.  Every 32-K chunk of the staged vector is scaled by the power of two that puts its
+// largest |v| in [2^14, 2^15), so that hi + lo hold ~22 bits of each value, and the chunk's two
+// sums are scaled back by 2^(e - 14) as they are accumulated.
+
+constexpr int F16_CHK = 32;  // K per 1 KiB f16 chunk
+
+// The K values of src (fp32, times S.nw when normed) -> S.A, chunk c at c * 128 bytes: 32 fp16 hi
+// parts, then 32 lo parts, of v * 2^(14 - e_c); S.fx[c] = 2^(e_c - 14); each wave's sum of squares
+// to S.misc[40 + wave] (normed), as stage_c leaves them for norm_scale.  Whole workgroup, one
+// barrier.  A unit is 4 consecutive values; the 8 lanes of a chunk find its maximum by DPP.
+template <int K>
+__device__ __forceinline__ void stage_f16(Shared& S, const float* src, bool normed) {
+    static_assert((K / 4) % 64 == 0 && (K / F16_CHK) * 128 <= A_BYTES && K / F16_CHK <= 384, "operands fit S.A / S.fx");
+    constexpr int NU = (K / 4 + THREADS - 1) / THREADS;
+    const int tid = my_tid(), lane = tid % 64, wave = wave_id();
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+        const int u = tid + THREADS * j;
+        if ((K / 4) % THREADS != 0 && u >= K / 4) continue;  // whole waves
+        const float4 a4 = ((const float4*)src)[u];
+        float v[4] = {a4.x, a4.y, a4.z, a4.w};
+        if (normed) {
+            const float4 wn = ((const float4*)S.nw)[u];
+            ss = fmaf(v[0], v[0], ss);
+            ss = fmaf(v[1], v[1], ss);
+            ss = fmaf(v[2], v[2], ss);
+            ss = fmaf(v[3], v[3], ss);
+            v[0] *= wn.x;
+            v[1] *= wn.y;
+            v[2] *= wn.z;
+            v[3] *= wn.w;
+        }
+        const float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        int bits = (int)as_u32(amax);  // order of non-negative floats = order of their bits
+        bits = max(bits, dpp_i<DPP_XOR1>(bits));
+        bits = max(bits, dpp_i<DPP_XOR2>(bits));
+        bits = max(bits, dpp_i<DPP_HALF_MIRROR>(bits));
+        // e: exponent of the chunk maximum, clamped so that 2^(14 - e) and 2^(e - 14) are normal.
+        const int e = min(max(((bits >> 23) & 0xFF) - 127, -100), 100);
+        const float p = as_f32((uint32_t)(141 - e) << 23);  // 2^(14 - e)
+        uint32_t hw[2], lw[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float x0 = v[2 * i] * p, x1 = v[2 * i + 1] * p;
+            const uint16_t h0 = f2h(x0), h1 = f2h(x1);
+            hw[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            lw[i] = (uint32_t)f2h(x0 - h2f(h0)) | ((uint32_t)f2h(x1 - h2f(h1)) << 16);
+        }
+        const int k0 = u * 4, c = k0 / F16_CHK, kk = k0 % F16_CHK;
+        uint8_t* A = S.A + c * 128;
+        *(uint2*)(A + 2 * kk) = make_uint2(hw[0], hw[1]);
+        *(uint2*)(A + 64 + 2 * kk) = make_uint2(lw[0], lw[1]);
+        if (kk == 0) S.fx[c] = as_f32((uint32_t)(113 + e) << 23);  // 2^(e - 14)
+    }
+    if (normed) {
+        ss = wave_sum(ss);
+        if (lane == 0) S.misc[40 + wave] = ss;
+    }
+    __syncthreads();
+}
+
+// A wave's K-slice of NB f16 blocks: chunks c0 + i, i < CPW, of blocks rb[b] (NCB chunks per
+// block), one 16-byte lane slice each.
+template <int NB, int CPW>
+struct WF {
+    uint4 wv[NB][CPW];
+    __device__ __forceinline__ void load(const uint8_t* w, const int (&rb)[NB], int ncb, int c0, int lane) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < CPW; ++i)
+                wv[b][i] = ((const uint4*)(w + ((size_t)rb[b] * ncb + c0 + i) * 1024))[lane];
+    }
+};
+
+// acc[b] += the slice's products with the staged chunks s0 + i (the slice's chunk index within the
+// staged vector); the sums land in lanes 0-15 (row lane of the block), other lanes add zeros.
+template <int NB, int CPW>
+__device__ __forceinline__ void mac_f16(const Shared& S, const WF<NB, CPW>& wf, int s0, int lane, float (&acc)[NB]) {
+    const int r = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+        const int c = s0 + i;
+        const uint8_t* ap = r < 2 ? S.A + c * 128 + 64 * r + 16 * q : (const uint8_t*)S.zero;
+        const h8 A = *(const h8*)ap;
+        const float f = S.fx[c];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const f32x4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, as_h8(wf.wv[b][i]), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            acc[b] = fmaf(D[0] + D[1], f, acc[b]);
+        }
+    }
+}
+
+// The partials of N <= 3 blocks from the NWV waves that computed them (lanes 0-15 of waves
+// w0 .. w0 + NWV - 1) into S.red; one barrier.  red_sum then adds them in a fixed order.
+template <int N>
+__device__ __forceinline__ void red_store16(Shared& S, const float (&acc)[N], int slot) {
+    static_assert(N * WAVES * 16 <= 6 * MW * 64, "S.red holds the partials");
+    const int lane = my_tid() % 64;
+    if (slot >= 0 && lane < 16) {
+#pragma unroll
+        for (int b = 0; b < N; ++b) S.red[(b * WAVES + slot) * 16 + lane] = acc[b];
+    }
+    __syncthreads();
+}
+template <int NWV>
+__device__ __forceinline__ float red_sum16(const Shared& S, int b) {
+    const float* r = S.red + b * WAVES * 16 + my_tid() % 16;
+    float t = r[0];
+#pragma unroll
+    for (int i = 1; i < NWV; ++i) t += r[16 * i];
+    return t;
+}
+
+// ------------------------------------------------------------------------------------------
 // Stage timeline of the last step of a launch (per workgroup, per layer, 32 event slots; steady
 // clock), compiled only with -DICUA_PERSIST_TRACE for profiling builds.  PK_TRACE is recorded by
 // math thread 0, PK_TRACE_X by exchange thread 0.
@@ -730,6 +853,8 @@ __device__ uint64_t g_trace[NWG][MAX_LAYERS + 1][32];
 // (control block n = 2): the pair runs as one two-row pass (decode_pass_loop) in the next launch.
 template <int FMT, bool MATH>
 __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp) {
+    constexpr bool F16 = FMT == FMT_F16;  // f16 tiles stream through their stages (stage_f16 above)
+    constexpr int XW = WAVES - MW;        // exchange waves
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
     constexpr int NRB = VOCAB / 16;     // lm_head row blocks
@@ -751,11 +876,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
 
     for (int step = 0; step < a.nsteps; ++step) {
         if (pos + 1 > maxctx) break;  // the commit stops earlier; guards the cache row
-        if (MATH) {
+        if (!F16 && MATH) {
             wx[0].forget();
             wx[1].forget();
         }
-        if (MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
+        if (!F16 && MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
             wx[0].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w - NWG / 2, H, wave_id(), my_tid() % 64);
             wx[1].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w, H, wave_id(), my_tid() % 64);
         }
@@ -789,7 +914,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // workgroups 128..255 would queue ahead of it on their CU: their QKV blocks are
             // requested during the previous layer's down stage (layer 0's at the start of the
             // step) and their K/V rows after the QKV publish.
-            const bool qkv_wg = w >= NWG / 2;
+            const bool qkv_wg = F16 || w >= NWG / 2;  // f16: one block per workgroup
             PK_TRACE(l, 0);
             uint4 kt[ATT_NT][4], vr[ATT_SPQ];
             float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rs = 0.f;
@@ -804,7 +929,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 // the O block and the mlp norm.
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
-                if (!qkv_wg) {
+                if (!F16 && !qkv_wg) {
                     wx[0].load(P.wo, P.wo_sb, w, H, mw, lane);
                     load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
                     // The lower down half-block of row block w into LDS: it lands long before the
@@ -822,7 +947,24 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             }
             if (sync_failed(S, !ok_in)) return;
             PK_TRACE_X(l, 1);
-            if (qkv_wg) {
+            if constexpr (F16) {
+                // Row block w: every wave requests its 8-chunk K-slice, then the staging.
+                WF<1, H / F16_CHK / WAVES> wq;
+                constexpr int CPW = H / F16_CHK / WAVES;
+                wq.load(P.wqkv, {w}, H / F16_CHK, wave * CPW, lane);
+                stage_f16<H>(S, l == 0 ? S.emb : S.vec, true);
+                float acc[1] = {0.f};
+                mac_f16(S, wq, wave * CPW, lane, acc);
+                PK_TRACE(l, 28);
+                red_store16<1>(S, acc, wave);
+                if (wave == 0) {  // rows 2i, 2i + 1 of the block in packet i (even lanes)
+                    const float y0 = red_sum16<WAVES>(S, 0) * norm_scale<H>(S);
+                    const float n0 = xor1(y0);
+                    if (lane < 16 && !(lane & 1)) st64(ll + QKVP + w * 8 + lane / 2, pack2(y0, n0, r + 1));
+                }
+                PK_TRACE(l, 30);
+                if (math) load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
+            } else if (qkv_wg) {
                 stage_c<FMT, H>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[2] = {0.f, 0.f}, y[2] = {0.f, 0.f};
                 if (math) mac_blocks<FMT, CW2, 2>(S, wx, mw, lane, acc);
@@ -1031,6 +1173,12 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE(l, 20);
             }
             PK_TRACE(l, 4);
+            // f16: the exchange waves of workgroups 0..127 request their O block (64 KiB) now; it
+            // lands during the merge and is multiplied by them after the attention-output poll.
+            WF<1, H / F16_CHK / XW> wof;
+            if constexpr (F16) {
+                if (!math && w < H / 16) wof.load(P.wo, {w}, H / F16_CHK, (wave - MW) * (H / F16_CHK / XW), lane);
+            }
 
             // ---------------- merge of group g: workgroups 224..255 ------------------------
             // Split s = 28 + p of group g (workgroup 224 + 8p + g, no O / down work) merges part
@@ -1098,7 +1246,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // partials.  The last split to publish is the one holding the new cache row (it
             // waits for that row's acknowledgement first); their math waves watch its (l, m)
             // packet, and nothing else of theirs is in flight then.
-            if (math && w >= NWG / 2 && w < MERGER0) {
+            if (!F16 && math && w >= NWG / 2 && w < MERGER0) {
                 // One lane watches; the other math waves wait for it in LDS.
                 if (wave == 0 && lane == 0) {
                     const int s_tail = min(pos / chunk, ATT_SPLITS - 1);
@@ -1127,7 +1275,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         S.xhi[0][tid - MT] = 0.f;
                     ok = ok && poll_vec<H / 2 / CT>(ll + ATTNP, H / 2, r + 1, S.vec, err);
                 }
-                if (math) {
+                if (!F16 && math) {
 #pragma unroll
                     for (int j = 0; j < 3; ++j) wgu[j].load(P.wgu, P.wgu_sb, 3 * w + j, H, mw, lane);
                 }
@@ -1135,10 +1283,19 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             }
             if (w < H / 16) {
                 PK_TRACE_X(l, 7);
-                stage_c<FMT, H>(S, S.vec, false);
-                float acc1[1] = {0.f};
-                if (math) mac_blocks<FMT, CW2, 1>(S, wx, mw, lane, acc1);
-                const float y = reduce_math<MATH>(S, acc1[0]);
+                float y = 0.f;
+                if constexpr (F16) {
+                    stage_f16<H>(S, S.vec, false);
+                    float acc1[1] = {0.f};
+                    if (!math) mac_f16(S, wof, (wave - MW) * (H / F16_CHK / XW), lane, acc1);
+                    red_store16<1>(S, acc1, math ? -1 : wave - MW);
+                    y = red_sum16<XW>(S, 0);
+                } else {
+                    stage_c<FMT, H>(S, S.vec, false);
+                    float acc1[1] = {0.f};
+                    if (math) mac_blocks<FMT, CW2, 1>(S, wx, mw, lane, acc1);
+                    y = reduce_math<MATH>(S, acc1[0]);
+                }
                 if (wave == 0) {  // the owner keeps the residual as published (even rows rounded)
                     const float xn = lane < 16 ? (S.xown[0][lane] + S.xhi[0][lane]) + y : 0.f;
                     const float xo = xor1(xn);
@@ -1152,7 +1309,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // Workgroups 128..255 request the upper down half-block and the next layer's QKV
             // blocks here, where they wait for no stage input (workgroups 0..127 run O): loads
             // issued later would queue ahead of their x' and h polls.
-            if (math && qkv_wg) {
+            if (!F16 && math && qkv_wg) {
                 wd_request<FMT>(wdb, P.wd, P.wd_sb, w - NWG / 2, 1, mw, lane);
                 wx[0].forget();
                 wx[1].forget();
@@ -1175,12 +1332,28 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 }
                 if (sync_failed(S, !ok)) return;
                 PK_TRACE_X(l, 9);
-                stage_c<FMT, H>(S, S.vec, true);
-                PK_TRACE(l, 13);
                 float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
-                if (math) mac_blocks<FMT, CW2, 3>(S, wgu, mw, lane, acc);
-                PK_TRACE(l, 26);
-                reduce_math_n<MATH, 3>(S, acc, y);
+                if constexpr (F16) {
+                    // Blocks 3w .. 3w + 2 (192 KiB): every wave's K-slice, requested before the staging.
+                    constexpr int CPW = H / F16_CHK / WAVES;
+                    WF<3, CPW> wg;
+                    wg.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * CPW, lane);
+                    stage_f16<H>(S, S.vec, true);
+                    PK_TRACE(l, 13);
+                    mac_f16(S, wg, wave * CPW, lane, acc);
+                    PK_TRACE(l, 26);
+                    red_store16<3>(S, acc, wave);
+                    if (wave == 0) {
+#pragma unroll
+                        for (int j = 0; j < 3; ++j) y[j] = red_sum16<WAVES>(S, j);
+                    }
+                } else {
+                    stage_c<FMT, H>(S, S.vec, true);
+                    PK_TRACE(l, 13);
+                    if (math) mac_blocks<FMT, CW2, 3>(S, wgu, mw, lane, acc);
+                    PK_TRACE(l, 26);
+                    reduce_math_n<MATH, 3>(S, acc, y);
+                }
                 PK_TRACE(l, 14);
                 if (wave == 0) {
                     const float rs = norm_scale<H>(S);
@@ -1200,12 +1373,26 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 const int rb = w % (NWG / 2), half = w / (NWG / 2);
                 bool ok = true;
                 if (!math) ok = poll_vec<FFH / 2 / CT>(ll + HP + half * (FFH / 2), FFH / 2, r + 1, S.vec, err);
-                if (math && !qkv_wg) {
+                if (!F16 && math && !qkv_wg) {
                     wx[0].forget();
                     wx[1].forget();
                 }
                 if (sync_failed(S, !ok)) return;
                 PK_TRACE_X(l, 11);
+                float y = 0.f;
+                if constexpr (F16) {
+                    // K half `half` of row block rb (96 KiB): chunks half * 96 .. of the block.
+                    constexpr int CPW = FFH / F16_CHK / WAVES;
+                    WF<1, CPW> wd;
+                    wd.load(P.wd, {rb}, FF / F16_CHK, half * (FFH / F16_CHK) + wave * CPW, lane);
+                    stage_f16<FFH>(S, S.vec, false);
+                    PK_TRACE(l, 18);
+                    float acc1[1] = {0.f};
+                    mac_f16(S, wd, wave * CPW, lane, acc1);
+                    PK_TRACE(l, 24);
+                    red_store16<1>(S, acc1, wave);
+                    y = red_sum16<WAVES>(S, 0);
+                } else {
                 stage_c<FMT, FFH>(S, S.vec, false);
                 PK_TRACE(l, 18);
                 float yd = 0.f;
@@ -1218,7 +1405,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     yd = wd_mac_lds<FMT>(S, wdb, mw, lane);
                     PK_TRACE(l, 24);
                 }
-                const float y = reduce_math<MATH>(S, yd);
+                y = reduce_math<MATH>(S, yd);
+                }
                 PK_TRACE(l, 19);
                 if (wave == 0) {
                     const float v = lane < 16 ? (half == 0 ? S.xown[0][lane] + y : y) : 0.f;
@@ -1241,13 +1429,42 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // All eight waves stream the blocks w + k * 256 (chunks wave * CW8 ..), LM_DEPTH in
             // flight per wave; the exchange waves issue theirs once their poll is done.  Each
             // wave's per-block partial sums go to LDS; one reduction and argmax at the end.
-            WB<FMT, CW8> wl[LM_DEPTH];
             bool ok = true;
             if (!math) ok = poll_sum<H / 2 / CT>(ll + XP, ll + XDP, 2 * r_last + 2, S.vec, err);
             if (math) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
             }
+            float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
+            if constexpr (F16) {
+                // f16 embedding blocks (64 KiB): each wave's 8-chunk K-slice of blocks w + k * 256,
+                // LM_DEPTH in flight, requested once x is in (the exchange waves') or after the
+                // barrier (the math waves').
+                constexpr int CPW = H / F16_CHK / WAVES;
+                WF<1, CPW> wl[LM_DEPTH];
+                if (!math) {
+#pragma unroll
+                    for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, {w + k * NWG}, H / F16_CHK, wave * CPW, lane);
+                }
+                if (sync_failed(S, !ok)) return;
+                if (math) {
+#pragma unroll
+                    for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, {w + k * NWG}, H / F16_CHK, wave * CPW, lane);
+                }
+                PK_TRACE_X(L, 1);
+                stage_f16<H>(S, S.vec, true);
+                for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
+#pragma unroll
+                    for (int k = 0; k < LM_DEPTH; ++k) {
+                        const int kb = k0 + k, rb = w + kb * NWG;
+                        float y1[1] = {0.f};
+                        mac_f16(S, wl[k], wave * CPW, lane, y1);
+                        if (rb < NRB && lane < 16) plm[(kb * WAVES + wave) * 16 + lane] = y1[0];
+                        wl[k].load(a.E, {min(rb + LM_DEPTH * NWG, NRB - 1)}, H / F16_CHK, wave * CPW, lane);
+                    }
+                }
+            } else {
+            WB<FMT, CW8> wl[LM_DEPTH];
             // The exchange waves request their blocks once x is in; the math waves' requests
             // also wait for the barrier, so that no bulk load queues ahead of the x poll.
             if (!math) {
@@ -1261,7 +1478,6 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             }
             PK_TRACE_X(L, 1);
             stage_c<FMT, H>(S, S.vec, true);
-            float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
             QuadOps<FMT> lq[CW8 / 2];  // this wave's operand quads, the same for every block
 #pragma unroll
             for (int p = 0; p < CW8 / 2; ++p) lq[p] = quad_load<FMT>(S, wave * CW8 + 2 * p, lane);
@@ -1282,6 +1498,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     if (rb < NRB && lane < 16) plm[(kb * WAVES + wave) * 16 + lane] = y;
                     wl[k].load(a.E, a.Esb, min(rb + LM_DEPTH * NWG, NRB - 1), H, wave, lane);
                 }
+            }
             }
             __syncthreads();
             float best = -__builtin_inff();
@@ -2245,6 +2462,7 @@ hipError_t launch_persistent(int fmt, int nr, const PersistArgs& a, hipStream_t 
     const void* k = nullptr;
     if (fmt == FMT_Q4) k = nr == 2 ? (const void*)pk::decode_kernel<FMT_Q4, 2> : (const void*)pk::decode_kernel<FMT_Q4, 1>;
     if (fmt == FMT_Q8) k = nr == 2 ? (const void*)pk::decode_kernel<FMT_Q8, 2> : (const void*)pk::decode_kernel<FMT_Q8, 1>;
+    if (fmt == FMT_F16 && nr == 1) k = (const void*)pk::decode_kernel<FMT_F16, 1>;  // f16 pairs: the graph path
     if (!k || (nr != 1 && nr != 2) || (nr == 2 && a.nsteps != 1)) return hipErrorInvalidValue;
     return hipLaunchCooperativeKernel(k, dim3(pk::NWG), dim3(pk::THREADS), args, 0, s);
 }

@@ -288,14 +288,20 @@ def visual_prompt(n_total: int, vis_offset: int, llm_h: int, llm_w: int, tag: st
 
 
 def scale_embedding_rows(img: np.ndarray, scales: dict) -> np.ndarray:
-    """Copy of a q4 image whose tied-embedding rows `tok` are multiplied by `c` (their fp16
-    (scale, bias) words), so that those tokens win the argmax often: the grammar-pair workloads
-    use it to make the forced pairs (Shaders.swift:1537-1561) fire on a random-init model."""
+    """Copy of an image whose tied-embedding rows `tok` are multiplied by `c` (q4: their fp16
+    (scale, bias) words; q8: their scales; f16: the values), so that those tokens win the argmax
+    often: the grammar-pair workloads use it to make the forced pairs (Shaders.swift:1537-1561)
+    fire on a random-init model."""
     img = img.copy()
+    fmt = int(img[8:12].view("<u4")[0])
     table = np.frombuffer(img[16:16 + 16 * TensorID.count].tobytes(), dtype="<u8").reshape(-1, 2)
-    off = int(table[TensorID.embed_sb, 0])
-    n = Dims.vocab * (Dims.hidden // 64) * 4
-    sb = img[off:off + n].view(np.float16).reshape(Dims.vocab, Dims.hidden // 64, 2)
+    if fmt == WeightFormat.F16:
+        off = int(table[TensorID.embed, 0])
+        rows = img[off:off + Dims.vocab * Dims.hidden * 2].view(np.float16).reshape(Dims.vocab, Dims.hidden)
+    else:
+        off = int(table[TensorID.embed_sb, 0])
+        per_row = (Dims.hidden // 64) * 4 if fmt == WeightFormat.Q4 else (Dims.hidden // 32) * 2
+        rows = img[off:off + Dims.vocab * per_row].view(np.float16).reshape(Dims.vocab, -1)
     for tok, c in scales.items():
-        sb[tok] = (sb[tok].astype(np.float32) * c).astype(np.float16)
+        rows[tok] = (rows[tok].astype(np.float32) * c).astype(np.float16)
     return img

@@ -54,6 +54,30 @@ def test_grammar_pairs_match_the_oracle(oracle_mod, grammar_base, scales, seed, 
     assert st["done"] == 1 and st["step"] == len(ref)
 
 
+@pytest.mark.parametrize("scales,seed", [({11: 8, 3678: 8, 8: 3}, 2), ({11: 4, 3678: 8}, 4)])
+def test_grammar_pairs_f16_match_the_oracle(oracle_mod, scales, seed):
+    """f16 weights: single-row passes on the persistent kernel, each forced pair's two-row pass on
+    the per-stage graph (the kernel has no two-row f16 form); both sequences force two pairs."""
+    img = scale_embedding_rows(synth.build_model_image(WeightFormat.F16, n_layers=2, tag="f16-grammar"), scales)
+    toks = synth.random_tokens(9, "gram", seed)
+    steps = 20
+    om = oracle_mod.OracleModel(img, 128)
+    ref = [int(t) for t in om.generate_commit(toks, steps, grammar=True)]
+    assert sum(a == 11 and b == 220 for a, b in zip(ref, ref[1:])) == 2, ref
+    with Engine(flags=0, image=img, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.grammar_pairs = True
+        got = e.generate(toks, max_new_tokens=steps)
+        assert e.last_decode_persistent
+        assert e.pair_passes == 0  # the pairs ran on the graph
+        e.prefill(toks, max_new=steps)
+        for _ in range(steps):  # one pass per call: pairs pending between calls
+            e.decode_steps(1)
+        got_split = e.tokens(e.state()["step"])
+    assert got == ref, (got, ref)
+    assert list(got_split) == ref, (list(got_split), ref)
+
+
 @pytest.mark.parametrize("split", [1, 2, 3])
 def test_grammar_pairs_across_decode_calls(oracle_mod, grammar_base, split):
     """A forced pair left pending at the end of a decode call (state n = 2) continues in the next

@@ -17,7 +17,8 @@ LAYERS = 2
 @pytest.fixture(scope="module")
 def images():
     return {"q4": synth.build_model_image(WeightFormat.Q4, n_layers=LAYERS, tag="q4-small"),
-            "q8": synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="q8-small")}
+            "q8": synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="q8-small"),
+            "f16": synth.build_model_image(WeightFormat.F16, n_layers=LAYERS, tag="f16-small")}
 
 
 def _fp16_close(got, ref, max_ulp=1, row_tol=1e-6, frac_over_1ulp=0.0):
@@ -53,13 +54,18 @@ def _random_cache(pos, tag):
             for l in range(LAYERS) for k in range(2)}
 
 
-def test_persistent_path_is_available(images):
-    with Engine(flags=0, image=images["q4"], max_context=128) as e:
+@pytest.mark.parametrize("fmt_name", ["q4", "f16"])
+def test_persistent_path_is_available(images, fmt_name):
+    with Engine(flags=0, image=images[fmt_name], max_context=128) as e:
         assert e.persistent_decode, "the persistent decode kernel did not initialise on this device"
         assert not e.graph_decode
+        e.eos = (-1, -1)
+        e.prefill(synth.random_tokens(5, "avail"), max_new=4)
+        e.decode_steps(3)
+        assert e.last_decode_persistent
 
 
-@pytest.mark.parametrize("fmt_name,pos", [("q4", 4095), ("q8", 1000), ("q4", 9000)])
+@pytest.mark.parametrize("fmt_name,pos", [("q4", 4095), ("q8", 1000), ("q4", 9000), ("f16", 4095), ("f16", 300)])
 def test_long_context_decode(oracle_mod, images, fmt_name, pos):
     """Decode from a prefilled random cache: 4095 slots (uneven splits), 9000 (several 256-slot
     blocks per split)."""
@@ -90,7 +96,7 @@ def test_long_context_decode(oracle_mod, images, fmt_name, pos):
             _fp16_close(rows, om.kv(l, k)[:, pos:pos + steps], max_ulp=2, row_tol=2e-3, frac_over_1ulp=5e-2)
 
 
-@pytest.mark.parametrize("fmt_name", ["q4", "q8"])
+@pytest.mark.parametrize("fmt_name", ["q4", "q8", "f16"])
 def test_persistent_matches_graph_path(oracle_mod, images, fmt_name):
     """Same prompt through both decode paths: tokens agree with the oracle and with each other,
     the cache rows they write agree to an fp16 ulp, and split calls equal one call."""
