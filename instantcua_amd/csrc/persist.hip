@@ -717,6 +717,17 @@ __device__ __forceinline__ void load_norm8(float (&n)[8], const float* p) {
 
 constexpr int F16_CHK = 32;  // K per 1 KiB f16 chunk
 
+// Workgroup barrier for data exchanged through LDS only: waits for this wave's LDS accesses, not
+// for its vector-memory loads (__syncthreads would drain the weight slices in flight, so a stage
+// could not stage its input while its tiles land).  The empty asm statements keep the compiler
+// from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // vmcnt 63, expcnt 7, lgkmcnt 0
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // The K values of src (fp32, times S.nw when normed) -> S.A, chunk c at c * 128 bytes: 32 fp16 hi
 // parts, then 32 lo parts, of v * 2^(14 - e_c); S.fx[c] = 2^(e_c - 14); each wave's sum of squares
 // to S.misc[40 + wave] (normed), as stage_c leaves them for norm_scale.  Whole workgroup, one
@@ -770,7 +781,7 @@ __device__ __forceinline__ void stage_f16(Shared& S, const float* src, bool norm
         ss = wave_sum(ss);
         if (lane == 0) S.misc[40 + wave] = ss;
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // A wave's K-slice of NB f16 blocks: chunks c0 + i, i < CPW, of blocks rb[b] (NCB chunks per
@@ -778,12 +789,21 @@ __device__ __forceinline__ void stage_f16(Shared& S, const float* src, bool norm
 template <int NB, int CPW>
 struct WF {
     uint4 wv[NB][CPW];
+    // Blocks B0 .. B1 - 1 of the NB (all by default).
+    template <int B0 = 0, int B1 = NB>
     __device__ __forceinline__ void load(const uint8_t* w, const int (&rb)[NB], int ncb, int c0, int lane) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+        for (int b = B0; b < B1; ++b)
 #pragma unroll
             for (int i = 0; i < CPW; ++i)
                 wv[b][i] = ((const uint4*)(w + ((size_t)rb[b] * ncb + c0 + i) * 1024))[lane];
+    }
+    // Ends the live range of the slice's registers (as WB::forget).
+    __device__ __forceinline__ void forget() {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < CPW; ++i) asm volatile("" : "=v"(wv[b][i].x), "=v"(wv[b][i].y), "=v"(wv[b][i].z), "=v"(wv[b][i].w));
     }
 };
 
@@ -816,7 +836,7 @@ __device__ __forceinline__ void red_store16(Shared& S, const float (&acc)[N], in
 #pragma unroll
         for (int b = 0; b < N; ++b) S.red[(b * WAVES + slot) * 16 + lane] = acc[b];
     }
-    __syncthreads();
+    lds_barrier();
 }
 template <int NWV>
 __device__ __forceinline__ float red_sum16(const Shared& S, int b) {
@@ -872,6 +892,15 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // Math waves: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127) of
     // the current layer.
     WB<FMT, CW2> wx[2];
+    // f16: each wave's K-slices of its QKV block, gate|up blocks and down half-block.  The math
+    // waves request theirs a stage ahead (QKV after the previous down publish, gate|up after the
+    // attention partial or the merge, down after the SwiGLU publish); the exchange waves once
+    // their stage input is in.
+    constexpr int F16_CPW = H / F16_CHK / WAVES, F16_CPWD = FFH / F16_CHK / WAVES;
+    constexpr int F16_GU_EARLY = 1;  // gate|up blocks whose math-wave slices are requested early
+    WF<1, F16_CPW> wqf;
+    WF<3, F16_CPW> wgf;
+    WF<1, F16_CPWD> wdf;
     __syncthreads();
 
     for (int step = 0; step < a.nsteps; ++step) {
@@ -879,6 +908,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
         if (!F16 && MATH) {
             wx[0].forget();
             wx[1].forget();
+        }
+        if constexpr (F16) {
+            if (MATH) wqf.load(a.layers[0].wqkv, {w}, H / F16_CHK, wave_id() * F16_CPW, my_tid() % 64);
         }
         if (!F16 && MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
             wx[0].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w - NWG / 2, H, wave_id(), my_tid() % 64);
@@ -908,6 +940,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // Math-wave register tiles: each is requested while the exchange waves wait for the
             // input of its stage or of an earlier one.  The down half-block streams into LDS.
             WB<FMT, CW2> wgu[3];
+            if constexpr (F16) {  // slices loaded under role conditions: last layer's values are dead
+                wgf.forget();
+                wdf.forget();
+                if (!math) wqf.forget();
+            }
 
             // ---------------- QKV: row blocks w - 128 and w (workgroups 128..255) ------------
             // Workgroups 0..127 need no x here.  Loads issued just before the x poll of
@@ -948,13 +985,12 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             if (sync_failed(S, !ok_in)) return;
             PK_TRACE_X(l, 1);
             if constexpr (F16) {
-                // Row block w: every wave requests its 8-chunk K-slice, then the staging.
-                WF<1, H / F16_CHK / WAVES> wq;
-                constexpr int CPW = H / F16_CHK / WAVES;
-                wq.load(P.wqkv, {w}, H / F16_CHK, wave * CPW, lane);
+                // Row block w: the exchange waves request their 8-chunk K-slices now (the math
+                // waves' are in flight since the previous layer), then the staging.
+                if (!math) wqf.load(P.wqkv, {w}, H / F16_CHK, wave * F16_CPW, lane);
                 stage_f16<H>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[1] = {0.f};
-                mac_f16(S, wq, wave * CPW, lane, acc);
+                mac_f16(S, wqf, wave * F16_CPW, lane, acc);
                 PK_TRACE(l, 28);
                 red_store16<1>(S, acc, wave);
                 if (wave == 0) {  // rows 2i, 2i + 1 of the block in packet i (even lanes)
@@ -1178,6 +1214,12 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             WF<1, H / F16_CHK / XW> wof;
             if constexpr (F16) {
                 if (!math && w < H / 16) wof.load(P.wo, {w}, H / F16_CHK, (wave - MW) * (H / F16_CHK / XW), lane);
+                // The math waves' gate|up slices (the mergers' after the merge: in flight during
+                // their partials poll, they would delay it).
+                if (math && w < MERGER0) wgf.load<0, F16_GU_EARLY>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                // Workgroups 128..223 (no O, no merge) idle until the x' poll: their exchange waves
+                // request all of their slices now.
+                if (!math && w >= H / 16 && w < MERGER0) wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
             }
 
             // ---------------- merge of group g: workgroups 224..255 ------------------------
@@ -1232,6 +1274,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 }
                 PK_TRACE(l, 17);
                 __syncthreads();  // the partials in S.A are read before the next staging
+                if constexpr (F16) {
+                    if (math) wgf.load<0, F16_GU_EARLY>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                    else wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                }
                 PK_TRACE(l, 6);
             }
 
@@ -1334,13 +1380,16 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE_X(l, 9);
                 float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
                 if constexpr (F16) {
-                    // Blocks 3w .. 3w + 2 (192 KiB): every wave's K-slice, requested before the staging.
-                    constexpr int CPW = H / F16_CHK / WAVES;
-                    WF<3, CPW> wg;
-                    wg.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * CPW, lane);
+                    // Blocks 3w .. 3w + 2 (192 KiB): the math waves' remaining K-slices now, and the
+                    // O workgroups' exchange waves' (the others' are in flight since their attention
+                    // partial or merge).
+                    if (math)
+                        wgf.load<F16_GU_EARLY, 3>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                    else if (w < H / 16)  // the O workgroups' exchange waves (their O publish went first)
+                        wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
                     stage_f16<H>(S, S.vec, true);
                     PK_TRACE(l, 13);
-                    mac_f16(S, wg, wave * CPW, lane, acc);
+                    mac_f16(S, wgf, wave * F16_CPW, lane, acc);
                     PK_TRACE(l, 26);
                     red_store16<3>(S, acc, wave);
                     if (wave == 0) {
@@ -1366,6 +1415,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     }
                 }
                 PK_TRACE(l, 10);
+                if constexpr (F16) {  // the math waves' down slices
+                    if (math)
+                        wdf.load(P.wd, {w % (NWG / 2)}, FF / F16_CHK, (w / (NWG / 2)) * (FFH / F16_CHK) + wave * F16_CPWD, lane);
+                }
             }
 
             // ---------------- down: K half w / 128 of row block w % 128 --------------------
@@ -1382,13 +1435,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 float y = 0.f;
                 if constexpr (F16) {
                     // K half `half` of row block rb (96 KiB): chunks half * 96 .. of the block.
-                    constexpr int CPW = FFH / F16_CHK / WAVES;
-                    WF<1, CPW> wd;
-                    wd.load(P.wd, {rb}, FF / F16_CHK, half * (FFH / F16_CHK) + wave * CPW, lane);
+                    if (!math) wdf.load(P.wd, {rb}, FF / F16_CHK, half * (FFH / F16_CHK) + wave * F16_CPWD, lane);
                     stage_f16<FFH>(S, S.vec, false);
                     PK_TRACE(l, 18);
                     float acc1[1] = {0.f};
-                    mac_f16(S, wd, wave * CPW, lane, acc1);
+                    mac_f16(S, wdf, wave * F16_CPWD, lane, acc1);
                     PK_TRACE(l, 24);
                     red_store16<1>(S, acc1, wave);
                     y = red_sum16<WAVES>(S, 0);
@@ -1417,6 +1468,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     }
                 }
                 PK_TRACE(l, 12);
+                if constexpr (F16) {  // the math waves' QKV slices of the next layer
+                    if (math && l + 1 < L) wqf.load(a.layers[l + 1].wqkv, {w}, H / F16_CHK, wave * F16_CPW, lane);
+                }
             }
         }
 
@@ -1438,19 +1492,13 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             float* plm = (float*)wdb;  // [LM_BLOCKS][WAVES][16] partial sums
             if constexpr (F16) {
                 // f16 embedding blocks (64 KiB): each wave's 8-chunk K-slice of blocks w + k * 256,
-                // LM_DEPTH in flight, requested once x is in (the exchange waves') or after the
-                // barrier (the math waves').
+                // LM_DEPTH in flight, requested once x is in (a barrier before the staging would
+                // otherwise wait for them).
                 constexpr int CPW = H / F16_CHK / WAVES;
                 WF<1, CPW> wl[LM_DEPTH];
-                if (!math) {
-#pragma unroll
-                    for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, {w + k * NWG}, H / F16_CHK, wave * CPW, lane);
-                }
                 if (sync_failed(S, !ok)) return;
-                if (math) {
 #pragma unroll
-                    for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, {w + k * NWG}, H / F16_CHK, wave * CPW, lane);
-                }
+                for (int k = 0; k < LM_DEPTH; ++k) wl[k].load(a.E, {w + k * NWG}, H / F16_CHK, wave * CPW, lane);
                 PK_TRACE_X(L, 1);
                 stage_f16<H>(S, S.vec, true);
                 for (int k0 = 0; k0 < LM_BLOCKS; k0 += LM_DEPTH) {
