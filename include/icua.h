@@ -99,10 +99,11 @@ int icua_prefill(icua_engine* e, const int32_t* tokens, int n, int start_pos, in
 /* k x Engine.encodeDecodeStep (Engine.swift:675-681): k passes, GPU-resident with token feedback
  * on the device; returns after completion.  Passes after a stop are no-ops.  A pass commits one
  * token, or two when its commit forces a grammar pair, whose two tokens then go through the next
- * pass together (n = 2, Shaders.swift:1553).  q4 / q8 models run the single-row passes in one
- * persistent cooperative kernel (one workgroup per CU) and a pair's pass in a launch of the
- * kernel's two-row form; f16 models, or ICUA_FLAG_GRAPH_DECODE, replay a captured HIP graph of
- * the per-stage kernels per pass.  Both paths compute the same arithmetic. */
+ * pass together (n = 2, Shaders.swift:1553).  The single-row passes run in one persistent
+ * cooperative kernel (one workgroup per CU), and a pair's pass in a launch of the kernel's
+ * two-row form (q4 / q8) or as one replay of the per-stage graph (f16); ICUA_FLAG_GRAPH_DECODE
+ * replays a captured HIP graph of the per-stage kernels per pass.  All paths compute the same
+ * arithmetic. */
 int icua_decode_steps(icua_engine* e, int k);
 
 /* Engine.generateVision (Engine.swift:696-827) minus the vision encoder: prefill + greedy decode
