@@ -783,34 +783,39 @@ struct icua_engine {
         g.row0 = row0;
         g.vis_offset = vis_offset;
         g.n_vis = n_vis;
+        // fp16 operands: hi + lo parts (~22 bits), or with ICUA_FLAG_PREFILL_FP16 the hi part alone
+        // (fp16 activations, queries and probabilities: the reference engine's precision).
+        const int parts = (flags & ICUA_FLAG_PREFILL_FP16) ? 1 : 2;
+        g.parts = parts;
         // 1. RMSNorm + fused QKV.
-        HIPCK(launch_pf_prep(H, 1, px, w.attn_norm, M, Mpad, pxa, pxs, pts, stream));
+        HIPCK(launch_pf_prep(H, 1, px, w.attn_norm, M, Mpad, pxa, pxs, pts, parts, stream));
         g.w = w.wqkv;
         g.sb = w.wqkv_sb;
         g.N = QKV;
         g.y = pqkv;
         HIPCK(launch_pf_gemm(fmt, H, EPI_STORE, g, stream));
         // 2. q/k norm + M-RoPE + KV write, causal flash attention.
-        PfQkArgs qa{pqkv, w.q_norm, w.k_norm, rope, kv_ptr(l, 0), kv_ptr(l, 1), pqh, pql, M, p0, maxctx};
+        uint16_t* ql = parts == 2 ? pql : nullptr;
+        PfQkArgs qa{pqkv, w.q_norm, w.k_norm, rope, kv_ptr(l, 0), kv_ptr(l, 1), pqh, ql, M, p0, maxctx};
         HIPCK(launch_pf_qk(qa, stream));
-        PfAttnArgs aa{pqh, pql, kv_ptr(l, 0), kv_ptr(l, 1), patt, M, p0, maxctx};
+        PfAttnArgs aa{pqh, ql, kv_ptr(l, 0), kv_ptr(l, 1), patt, M, p0, maxctx};
         HIPCK(launch_pf_attn(aa, stream));
         // 3. O projection + residual.
-        HIPCK(launch_pf_prep(H, 0, patt, nullptr, M, Mpad, pxa, pxs, pts, stream));
+        HIPCK(launch_pf_prep(H, 0, patt, nullptr, M, Mpad, pxa, pxs, pts, parts, stream));
         g.w = w.wo;
         g.sb = w.wo_sb;
         g.N = H;
         g.y = px;
         HIPCK(launch_pf_gemm(fmt, H, EPI_RESID, g, stream));
         // 4. RMSNorm + gate|up + SwiGLU.
-        HIPCK(launch_pf_prep(H, 1, px, w.mlp_norm, M, Mpad, pxa, pxs, pts, stream));
+        HIPCK(launch_pf_prep(H, 1, px, w.mlp_norm, M, Mpad, pxa, pxs, pts, parts, stream));
         g.w = w.wgu;
         g.sb = w.wgu_sb;
         g.N = GU;
         g.h = ph;
         HIPCK(launch_pf_gemm(fmt, H, EPI_SWIGLU, g, stream));
         // 5. Down projection + residual (+ DeepStack after layers 0-2 at visual rows).
-        HIPCK(launch_pf_prep(FF, 0, ph, nullptr, M, Mpad, pxa, pxs, pts, stream));
+        HIPCK(launch_pf_prep(FF, 0, ph, nullptr, M, Mpad, pxa, pxs, pts, parts, stream));
         g.w = w.wd;
         g.sb = w.wd_sb;
         g.N = H;

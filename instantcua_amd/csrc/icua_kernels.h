@@ -105,9 +105,10 @@ hipError_t launch_set_pass(State* st, int pos, int n, int logits_rows, hipStream
 
 // ---- Matrix-core prefill (prefill.hip), q4 weights, passes of M <= Mpad tokens (Mpad % 128 == 0).
 // Activation operands of one GEMM input: fp16 hi / lo parts of the row-scaled activations
-// [Mpad / 16][K / 32][2][64][8], group sums [Mpad / 16][K / 64][16] and row scales [Mpad].
+// [Mpad / 16][K / 32][parts][64][8] (parts 2: hi and lo; 1: hi alone), group sums
+// [Mpad / 16][K / 64][16] and row scales [Mpad].
 hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint16_t* xa,
-                          float* xs, float* ts, hipStream_t s);
+                          float* xs, float* ts, int parts, hipStream_t s);
 
 struct PfGemmArgs {
     const uint16_t* xa;     // activation operands (launch_pf_prep)
@@ -121,6 +122,7 @@ struct PfGemmArgs {
     const float* ds;        // EPI_RESID: DeepStack rows [n_vis][H] or null
     int row0;               // prompt row of pass row 0
     int vis_offset, n_vis;
+    int parts;              // operand parts of xa (1 or 2, as launch_pf_prep wrote them)
 };
 // fmt: FMT_Q4 / FMT_Q8 / FMT_F16 (sb unused for f16); epi: EPI_STORE / EPI_RESID / EPI_SWIGLU;
 // K = 2048 (any epilogue) or 6144 (EPI_RESID).
@@ -141,7 +143,7 @@ hipError_t launch_pf_qk(const PfQkArgs& a, hipStream_t s);
 
 struct PfAttnArgs {
     const uint16_t* qh;
-    const uint16_t* ql;
+    const uint16_t* ql;     // null: queries and probabilities as fp16 hi parts alone
     const uint16_t* kc;
     const uint16_t* vc;
     float* out;             // attention rows [M][H] fp32

@@ -36,7 +36,7 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 // block share, so rows are dealt to the 8 XCDs (workgroup i runs on XCD i % 8) in contiguous
 // ranges: the lines are completed in one L2 rather than written back in parts from eight.
 
-template <int K, bool NORM>
+template <int K, bool NORM, int HL>
 __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ src, const float* __restrict__ norm_w,
                                                       int M, uint16_t* __restrict__ xa, float* __restrict__ xs,
                                                       float* __restrict__ ts) {
@@ -101,7 +101,10 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
             const float x0 = ldexpf(v[j][2 * i], sh), x1 = ldexpf(v[j][2 * i + 1], sh);
             const f16 h0 = (f16)x0, h1 = (f16)x1;
             const f16 l0 = (f16)(x0 - (float)h0), l1 = (f16)(x1 - (float)h1);
-            gs += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
+            if constexpr (HL == 2)
+                gs += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
+            else
+                gs += (float)h0 + (float)h1;
             hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
             lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
         }
@@ -110,9 +113,9 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
         gs += dpp<DPP_XOR2>(gs);
         gs += dpp<DPP_HALF_MIRROR>(gs);
         const int ks = k0 / 32, qq = (k0 % 32) / 8;
-        uint16_t* base = xa + ((size_t)(tb * NKS + ks) * 2) * 512 + (tr + 16 * qq) * 8;
+        uint16_t* base = xa + ((size_t)(tb * NKS + ks) * HL) * 512 + (tr + 16 * qq) * 8;
         *(uint4*)base = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        *(uint4*)(base + 512) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        if constexpr (HL == 2) *(uint4*)(base + 512) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
         if (k0 % 64 == 0) xs[(size_t)(tb * NG + k0 / 64) * 16 + tr] = gs;
     }
     if (tid == 0) ts[t] = ldexpf(1.0f, -sh);
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const float* __restrict__ 
 // (double-buffered, 64 or 128 KiB) and are shared by the waves; the waves' activation operands
 // stream from global memory straight into registers two 64-K groups ahead.  The launch takes
 // the largest tile (most products per operand byte) whose count still fills the CUs evenly.
-template <int FMT, int K, int EPI, int PG_RB, int TB>
+template <int FMT, int K, int EPI, int PG_RB, int TB, int HL>
 __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     static_assert((PG_RB == 8 || PG_RB == 16) && (TB == 1 || TB == 2), "tile shape");
     constexpr int NHF = PG_RB / 8;         // halves of four row blocks per wave
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;
     const int tb0 = tm * 4 * TB + TB * (wave & 3), rb0 = (PG_RB / 2) * (wave >> 2);
-    const uint16_t* xa = a.xa + (size_t)tb0 * NKS * 1024 + lane * 8;   // token block tb0 (+ NKS * 1024 for tb0 + 1)
+    const uint16_t* xa = a.xa + (size_t)tb0 * NKS * 512 * HL + lane * 8;   // token block tb0 (+ NKS * 512 HL for tb0 + 1)
     // Staging: thread t unpacks nibble lane t % 64 of row block t / 64 (and t / 64 + 8).
     const int srb = tid >> 6;
     const uint8_t* wsrc = a.w + (size_t)(tn * PG_RB + srb) * NCH * 1024 + lane * 16;
@@ -167,17 +170,17 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         for (int r = 0; r < 4 * NHF; ++r) acc[i][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Activation operands of one 64-group (two k-steps), prefetched one group ahead.
-    uint4 Ae[TB][2][2], Ao[TB][2][2];  // [token block][k-step of the group][hi, lo]
+    uint4 Ae[TB][2][HL], Ao[TB][2][HL];  // [token block][k-step of the group][hi, lo]
     uint4 Wn[NHF][CPS];
     uint32_t Vn = 0;
-    auto aload = [&](int g, uint4(&A)[TB][2][2]) {
+    auto aload = [&](int g, uint4(&A)[TB][2][HL]) {
 #pragma unroll
         for (int i = 0; i < TB; ++i) {
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                for (int hl = 0; hl < 2; ++hl)
-                    A[i][kk][hl] = *(const uint4*)(xa + (size_t)i * NKS * 1024 + ((size_t)(2 * g + kk) * 2 + hl) * 512);
+                for (int hl = 0; hl < HL; ++hl)
+                    A[i][kk][hl] = *(const uint4*)(xa + (size_t)i * NKS * 512 * HL + ((size_t)(2 * g + kk) * HL + hl) * 512);
         }
     };
     auto wload = [&](int c) {
@@ -250,13 +253,13 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     };
     // One activation operand (token block tb0 + i, k-step kk of group g, hi / lo part hl).
     auto aload1 = [&](int g, int i, int kk, int hl) {
-        return *(const uint4*)(xa + (size_t)i * NKS * 1024 + ((size_t)(2 * g + kk) * 2 + hl) * 512);
+        return *(const uint4*)(xa + (size_t)i * NKS * 512 * HL + ((size_t)(2 * g + kk) * HL + hl) * 512);
     };
     // One 64-group, in halves of four row blocks: a half's 8 B fragments first, then 4 x 2
     // accumulator chains of 4 MFMAs, then its scale epilogue.  In the last half, each activation
     // register is requested again for group gn (two groups on) as soon as its last product is
     // issued, so the loads have two groups' work to land in.
-    auto group = [&](int b, int gg, uint4(&Ac)[TB][2][2], int gn) {
+    auto group = [&](int b, int gg, uint4(&Ac)[TB][2][HL], int gn) {
 #pragma unroll
       for (int hf = 0; hf < NHF; ++hf) {
         v8h Bf[4][2];
@@ -280,7 +283,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                     for (int i = 0; i < TB; ++i) C[r][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int hl = 0; hl < 2; ++hl) {
+                for (int hl = 0; hl < HL; ++hl) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -310,7 +313,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-            for (int hl = 0; hl < 2; ++hl) {
+            for (int hl = 0; hl < HL; ++hl) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 
 // ------------------------------------------------------------------------------------------
 // Per-head q/k RMSNorm + M-RoPE of every prompt row, K/V written to the fp16 cache, queries
-// pre-scaled by 1/sqrt(128) and split into fp16 hi + lo.  Grid (M, 8): wave 4 y + w handles
+// pre-scaled by log2(e) / sqrt(128) and split into fp16 hi + lo.  Grid (M, 8): wave 4 y + w handles
 // vector 4 y + w of row x (q heads 0-15, k groups 16-23, v groups 24-31).
 
 __global__ __launch_bounds__(256) void pf_qk_kernel(PfQkArgs a) {
@@ -446,15 +449,19 @@ __global__ __launch_bounds__(256) void pf_qk_kernel(PfQkArgs a) {
     if (vec < NH) {
         float x0 = row[vec * HD + lane], x1 = row[vec * HD + lane + 64];
         norm_rope_pair(x0, x1, a.q_norm, cs, lane);
-        const float qscale = 1.0f / sqrtf((float)HD);
+        // 1/sqrt(128) and log2(e): the scores come out in base-2 units, so every softmax
+        // exponential of the attention is one v_exp_f32.
+        const float qscale = (1.0f / sqrtf((float)HD)) * 1.4426950408889634f;
         x0 *= qscale;
         x1 *= qscale;
         const size_t o = ((size_t)t * NH + vec) * HD + lane;
         const f16 h0 = (f16)x0, h1 = (f16)x1;
         a.qh[o] = __builtin_bit_cast(uint16_t, h0);
         a.qh[o + 64] = __builtin_bit_cast(uint16_t, h1);
-        a.ql[o] = f2h(x0 - (float)h0);
-        a.ql[o + 64] = f2h(x1 - (float)h1);
+        if (a.ql) {
+            a.ql[o] = f2h(x0 - (float)h0);
+            a.ql[o + 64] = f2h(x1 - (float)h1);
+        }
     } else if (vec < NH + NKV) {
         const int g = vec - NH;
         float k0 = row[H + g * HD + lane], k1 = row[H + g * HD + lane + 64];
@@ -483,6 +490,7 @@ constexpr int PA_VROW = 68;   // halves per V^T row in LDS (64 keys + 4 pad)
 constexpr int PA_BUF = PA_KB * PA_KROW + HD * PA_VROW;  // halves per buffer
 constexpr size_t PA_LDS = 2 * PA_BUF * 2;
 
+template <int HL>
 __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
     extern __shared__ __align__(16) uint16_t pa_lds[];
     const int QB = (a.M + 63) / 64;
@@ -503,7 +511,7 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             Qh[ks] = *(const v8h*)(a.qh + qo + 32 * ks);
-            Ql[ks] = *(const v8h*)(a.ql + qo + 32 * ks);
+            if constexpr (HL == 2) Ql[ks] = *(const v8h*)(a.ql + qo + 32 * ks);
         }
     }
     const uint16_t* kg = a.kc + (size_t)g * a.maxctx * HD;
@@ -567,7 +575,7 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
                 for (int ks = 0; ks < 4; ++ks) {
                     const v8h kf = *(const v8h*)(Ks + (kt * 16 + r16) * PA_KROW + 32 * ks + 8 * q);
                     S[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, Qh[ks], S[kt], 0, 0, 0);
-                    S[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, Ql[ks], S[kt], 0, 0, 0);
+                    if constexpr (HL == 2) S[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, Ql[ks], S[kt], 0, 0, 0);
                 }
             }
             float mb = -__builtin_inff();
@@ -581,13 +589,13 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
                 }
             mb = max_x4(mb);
             const float m_new = fmaxf(m_run, mb);  // finite: key slot 0 is in block 0
-            const float corr = (m_run == -__builtin_inff()) ? 0.f : expf(m_run - m_new);
+            const float corr = (m_run == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
             float p[4][4], ls = 0.f;
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    p[kt][i] = (S[kt][i] == -__builtin_inff()) ? 0.f : expf(S[kt][i] - m_new);
+                    p[kt][i] = (S[kt][i] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(S[kt][i] - m_new);
                     ls += p[kt][i];
                 }
             ls = sum_x4(ls);
@@ -615,7 +623,7 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
                     const v4h va = *(const v4h*)vp, vb = *(const v4h*)(vp + 16);
                     const v8h vf = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
                     O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Ph, O[dt], 0, 0, 0);
-                    O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Pl, O[dt], 0, 0, 0);
+                    if constexpr (HL == 2) O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Pl, O[dt], 0, 0, 0);
                 }
             }
         }
@@ -635,15 +643,39 @@ __global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
 
 // ------------------------------------------------------------------------------------------
 
-hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint16_t* xa,
-                          float* xs, float* ts, hipStream_t s) {
-    if (M < 1 || Mpad < M || Mpad % 128) return hipErrorInvalidValue;
+template <int HL>
+static hipError_t pf_prep_hl(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint16_t* xa,
+                             float* xs, float* ts, hipStream_t s) {
     if (K == H && norm)
-        hipLaunchKernelGGL((pf_prep_kernel<H, true>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
+        hipLaunchKernelGGL((pf_prep_kernel<H, true, HL>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
     else if (K == H)
-        hipLaunchKernelGGL((pf_prep_kernel<H, false>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
+        hipLaunchKernelGGL((pf_prep_kernel<H, false, HL>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
     else if (K == FF && !norm)
-        hipLaunchKernelGGL((pf_prep_kernel<FF, false>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
+        hipLaunchKernelGGL((pf_prep_kernel<FF, false, HL>), dim3(Mpad), dim3(256), 0, s, src, norm_w, M, xa, xs, ts);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w, int M, int Mpad, uint16_t* xa,
+                          float* xs, float* ts, int parts, hipStream_t s) {
+    if (M < 1 || Mpad < M || Mpad % 128 || (parts != 1 && parts != 2)) return hipErrorInvalidValue;
+    return parts == 2 ? pf_prep_hl<2>(K, norm, src, norm_w, M, Mpad, xa, xs, ts, s)
+                      : pf_prep_hl<1>(K, norm, src, norm_w, M, Mpad, xa, xs, ts, s);
+}
+
+template <int FMT, int RB, int TB, int HL>
+static hipError_t pf_gemm_shape_hl(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
+    const int T = (a.Mpad / (64 * TB)) * (a.N / (16 * RB));
+    const dim3 grid(8 * ((T + 7) / 8));
+    if (K == H && epi == EPI_STORE)
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_STORE, RB, TB, HL>), grid, dim3(512), 0, s, a);
+    else if (K == H && epi == EPI_RESID)
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_RESID, RB, TB, HL>), grid, dim3(512), 0, s, a);
+    else if (K == H && epi == EPI_SWIGLU)
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_SWIGLU, RB, TB, HL>), grid, dim3(512), 0, s, a);
+    else if (K == FF && epi == EPI_RESID)
+        hipLaunchKernelGGL((pf_gemm_kernel<FMT, FF, EPI_RESID, RB, TB, HL>), grid, dim3(512), 0, s, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -651,19 +683,7 @@ hipError_t launch_pf_prep(int K, int norm, const float* src, const float* norm_w
 
 template <int FMT, int RB, int TB>
 static hipError_t pf_gemm_shape(int K, int epi, const PfGemmArgs& a, hipStream_t s) {
-    const int T = (a.Mpad / (64 * TB)) * (a.N / (16 * RB));
-    const dim3 grid(8 * ((T + 7) / 8));
-    if (K == H && epi == EPI_STORE)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_STORE, RB, TB>), grid, dim3(512), 0, s, a);
-    else if (K == H && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_RESID, RB, TB>), grid, dim3(512), 0, s, a);
-    else if (K == H && epi == EPI_SWIGLU)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, H, EPI_SWIGLU, RB, TB>), grid, dim3(512), 0, s, a);
-    else if (K == FF && epi == EPI_RESID)
-        hipLaunchKernelGGL((pf_gemm_kernel<FMT, FF, EPI_RESID, RB, TB>), grid, dim3(512), 0, s, a);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
+    return a.parts == 1 ? pf_gemm_shape_hl<FMT, RB, TB, 1>(K, epi, a, s) : pf_gemm_shape_hl<FMT, RB, TB, 2>(K, epi, a, s);
 }
 
 // Tiles that fill the 256 CUs evenly: at least one each, and a whole number each or at least four.
@@ -683,7 +703,8 @@ static hipError_t pf_gemm_fmt(int K, int epi, const PfGemmArgs& a, hipStream_t s
 }
 
 hipError_t launch_pf_gemm(int fmt, int K, int epi, const PfGemmArgs& a, hipStream_t s) {
-    if (a.M < 1 || a.Mpad < a.M || a.Mpad % 128 || a.N % 128) return hipErrorInvalidValue;
+    if (a.M < 1 || a.Mpad < a.M || a.Mpad % 128 || a.N % 128 || (a.parts != 1 && a.parts != 2))
+        return hipErrorInvalidValue;
     switch (fmt) {
         case FMT_Q4: return pf_gemm_fmt<FMT_Q4>(K, epi, a, s);
         case FMT_Q8: return pf_gemm_fmt<FMT_Q8>(K, epi, a, s);
@@ -702,13 +723,17 @@ hipError_t launch_pf_attn(const PfAttnArgs& a, hipStream_t s) {
     if (a.M < 1 || a.p0 < 0 || a.p0 + a.M > a.maxctx) return hipErrorInvalidValue;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)pf_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)PA_LDS);
-        if (e != hipSuccess) return e;
+        for (const void* k : {(const void*)pf_attn_kernel<1>, (const void*)pf_attn_kernel<2>}) {
+            hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PA_LDS);
+            if (e != hipSuccess) return e;
+        }
         attr_set = true;
     }
     const int QB = (a.M + 63) / 64;
-    hipLaunchKernelGGL(pf_attn_kernel, dim3(QB * NKV), dim3(512), PA_LDS, s, a);
+    if (a.ql)
+        hipLaunchKernelGGL(pf_attn_kernel<2>, dim3(QB * NKV), dim3(512), PA_LDS, s, a);
+    else
+        hipLaunchKernelGGL(pf_attn_kernel<1>, dim3(QB * NKV), dim3(512), PA_LDS, s, a);
     return hipGetLastError();
 }
 

@@ -30,6 +30,7 @@ FLAG_GRAPH_DECODE = 4
 FLAG_PASS_PREFILL = 8
 FLAG_VISION_DELTA_CACHE = 16
 FLAG_FIRST_LOGITS = 32
+FLAG_PREFILL_FP16 = 64
 
 EXPORTS = [
     "icua_last_error", "icua_engine_create", "icua_engine_create_from_memory", "icua_engine_destroy",
@@ -306,6 +307,16 @@ class Engine:
     @pass_prefill.setter
     def pass_prefill(self, v: bool):
         self.set_flags((self._flags | FLAG_PASS_PREFILL) if v else (self._flags & ~FLAG_PASS_PREFILL))
+
+    @property
+    def prefill_fp16(self) -> bool:
+        """Matrix-core prefill on fp16 operands alone (the reference engine's precision) instead
+        of fp16 hi + lo parts."""
+        return bool(self._flags & FLAG_PREFILL_FP16)
+
+    @prefill_fp16.setter
+    def prefill_fp16(self, v: bool):
+        self.set_flags((self._flags | FLAG_PREFILL_FP16) if v else (self._flags & ~FLAG_PREFILL_FP16))
 
     def set_flags(self, flags: int) -> None:
         _check(lib().icua_set_flags(self._h, flags))
