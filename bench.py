@@ -194,6 +194,30 @@ def cpu_rows(budget_s=6.0):
     return {"cores": oracle.get_threads(), "kind": "port", "precision": "fp64 accumulation (the oracle)", "rows": rows}
 
 
+def run_fp16_prefill(img, steps=128):
+    """The 4096-row vision prefill of the decode workload with ICUA_FLAG_PREFILL_FP16 (GEMM and
+    attention operands as fp16 alone, the reference engine's precision, instead of fp16 hi + lo):
+    time, matrix-core fraction, and the greedy decode after it against the oracle fixture."""
+    vp = synth.visual_prompt(PREFILL, VIS_OFFSET, LLM_H, LLM_W, tag="bench-vis")
+    e = eng.Engine(image=img, max_context=PREFILL + steps + 16, max_steps=steps + 2)
+    e.eos = (-1, -1)
+    e.prefill_fp16 = True
+    e.prepare_mrope(VIS_OFFSET, LLM_H, LLM_W)
+    e.set_visual(vp.pooler.astype(np.float32), [d.astype(np.float32) for d in vp.deepstack])
+    e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=steps)  # loads the code objects
+    e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=steps, write_logits=True)
+    ms = e.last_timing["prefill_ms"]
+    first = e.logits(1)[0].copy()
+    e.decode_steps(steps - 1)
+    parity = forced_compare(e, PREFILL, "oracle_c4_28layer.npz", steps, first)
+    e.close()
+    out = {"workload": "28-layer q4 decoder, the 4096-token vision-context prefill, fp16 operands",
+           "prefill_ms": round(ms, 2), "prefill_tok_s": round(PREFILL / (ms / 1e3), 1),
+           "prefill_mfma_frac": round(PREFILL_FLOPS / (ms * 1e-3) / MFMA_F16_PEAK, 4), "greedy_vs_oracle": parity}
+    log(f"fp16-operand prefill: {ms:.1f} ms; parity {parity}")
+    return out
+
+
 def run_q8_prefill(img):
     """The 4096-row vision-shaped prefill of the decode workload on the 28-layer q8 group-32
     decoder (the matrix-core GEMMs on q8 codes)."""
@@ -650,6 +674,7 @@ def main():
 
     text = run_text_context(img)
     gram = run_grammar_pairs(img)
+    pf16 = None if args.no_prefill else run_fp16_prefill(img)
     cpu = None if args.no_cpu else cpu_baseline(img, PREFILL)
     rows = None
     if not args.no_cpu:
@@ -708,6 +733,7 @@ def main():
         "cpu_rows": rows,
         "text_context_1024": text,
         "grammar_pairs_28": gram,
+        "prefill_fp16_operands_4096": pf16,
         "prefill_q8_4096": q8,
         "verify_q8_8192": ver,
         "decode_f16_4k": f16,
