@@ -218,6 +218,24 @@ def run_fp16_prefill(img, steps=128):
     return out
 
 
+def run_prefill(img, fp16=False):
+    """The 4096-row vision-shaped prefill of the decode workload alone, twice (the first launch of
+    each kernel loads its code object; the second is timed): a short run for kernel traces."""
+    vp = synth.visual_prompt(PREFILL, VIS_OFFSET, LLM_H, LLM_W, tag="bench-vis")
+    e = eng.Engine(image=img, max_context=PREFILL + 16, max_steps=4)
+    e.prefill_fp16 = fp16
+    e.prepare_mrope(VIS_OFFSET, LLM_H, LLM_W)
+    e.set_visual(vp.pooler.astype(np.float32), [d.astype(np.float32) for d in vp.deepstack])
+    e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=2)
+    e.prefill(vp.tokens, vis_offset=VIS_OFFSET, max_new=2)
+    ms = e.last_timing["prefill_ms"]
+    e.close()
+    return {"workload": "28-layer q4 decoder, the 4096-token vision-context prefill"
+                        + (", fp16 operands" if fp16 else ", fp16 hi + lo operands"),
+            "prefill_ms": round(ms, 2), "prefill_tok_s": round(PREFILL / (ms / 1e3), 1),
+            "prefill_mfma_frac": round(PREFILL_FLOPS / (ms * 1e-3) / MFMA_F16_PEAK, 4)}
+
+
 def run_q8_prefill(img):
     """The 4096-row vision-shaped prefill of the decode workload on the 28-layer q8 group-32
     decoder (the matrix-core GEMMs on q8 codes)."""
@@ -590,10 +608,13 @@ def main():
     ap.add_argument("--no-prefill", action="store_true",
                     help="profiling runs: start decoding at the same 4096-slot context without the prefill "
                          "(cache rows stay zero; same bytes per step), so a profile holds only the decode launch")
-    ap.add_argument("--workload", choices=["decode", "verify", "gemv", "quant", "vision"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "verify", "gemv", "quant", "vision", "prefill",
+                                           "prefill-fp16", "f16-decode"], default="decode",
                     help="decode: the 4k-context q4 decode (default); verify: 8-draft q8 verify over 8192 rows; "
                          "gemv: isolated q4 GEMV sweep; quant: converter quantisers over the backbone shapes; "
-                         "vision: the vision tower on a 640x384 frame")
+                         "vision: the vision tower on a 640x384 frame; prefill / prefill-fp16: the decode "
+                         "workload's 4096-row q4 prefill alone (fp16 hi + lo or fp16 operands); f16-decode: "
+                         "the same decode on a 28-layer f16 decoder")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU decode is a design note only",
@@ -613,6 +634,15 @@ def main():
         return
     if args.workload == "quant":
         print(json.dumps(run_quant(20)))
+        dump_maps()
+        return
+    if args.workload in ("prefill", "prefill-fp16"):
+        img = synth.build_model_image(WeightFormat.Q4, n_layers=LAYERS, tag="bench-q4")
+        print(json.dumps(run_prefill(img, args.workload == "prefill-fp16")))
+        dump_maps()
+        return
+    if args.workload == "f16-decode":
+        print(json.dumps(run_f16_decode(args.steps, args.warmup)))
         dump_maps()
         return
 

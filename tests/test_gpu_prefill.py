@@ -69,6 +69,36 @@ def test_prefill_matches_oracle(oracle_mod, q4_small, n, fmt):
           f"prefill {t['prefill_ms']:.2f} ms")
 
 
+@pytest.mark.parametrize("fmt", [WeightFormat.Q4, WeightFormat.Q8, WeightFormat.F16], ids=["q4", "q8", "f16"])
+def test_prefill_fp16_operands_match_oracle(oracle_mod, q4_small, fmt):
+    """ICUA_FLAG_PREFILL_FP16: the GEMMs and the attention on fp16 operands alone (the reference
+    engine's precision) instead of fp16 hi + lo.  The error is then that of fp16 activations
+    (~2^-12 per operand): first logits within the stated 1e-2 (measured 1-3e-3), K/V rows within
+    1e-2 of their row, and the greedy tokens of the oracle (a divergence only at a near-tie)."""
+    n = 400
+    img = q4_small if fmt == WeightFormat.Q4 else small_image(fmt)
+    toks = synth.random_tokens(n, f"pf-oracle-{n}")
+    steps = 6
+    om = oracle_mod.OracleModel(img, n + 16)
+    ref, margins, first = om.generate(toks, steps)
+    with Engine(flags=0, image=img, max_context=n + 16, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.prefill_fp16 = True
+        e.prefill(toks, max_new=steps, write_logits=True)
+        lg = e.logits(1)[0]
+        kv = {(l, k): e.read_kv(l, k, 0, n) for l in range(LAYERS) for k in range(2)}
+        e.decode_steps(steps - 1)
+        got = e.tokens(steps)
+    err = rel_err(lg, first)
+    print(f"fmt {fmt}: fp16-operand prefill, first-logit rel err {err:.3g}")
+    assert err < 1e-2
+    for (l, k), rows in kv.items():
+        g = rows.astype(np.float32)
+        r = om.kv(l, k)[:, :n].astype(np.float32)
+        assert np.all(np.abs(g - r) <= 1e-2 * np.abs(r).max(axis=-1, keepdims=True)), (l, k)
+    compare_greedy(got, ref, margins, first.max() * np.ones(steps))
+
+
 def test_prefill_continuation_at_offset(oracle_mod, q4_small):
     """A second prefill call at start_pos 200 attends over the cache rows of the first."""
     toks = synth.random_tokens(500, "pf-offset")
