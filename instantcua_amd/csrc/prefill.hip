@@ -479,164 +479,257 @@ __global__ __launch_bounds__(256) void pf_qk_kernel(PfQkArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Causal GQA flash attention.  Workgroup = (KV group g, 64-token query block); wave w handles
-// head 2 g + w / 4 for tokens 16 (w % 4) .. + 15.  Key blocks of 64 slots are staged in LDS
-// (K row-major, V transposed; double-buffered) and shared by the 8 waves.  Slots at or beyond
-// p0 + M are staged as zeros; causal masking uses cache slots.
+// Causal GQA flash attention.  Workgroup = (KV group g, 64-token query block), 8 waves.  Wave w
+// handles head 2 g + ((w >> 1) & 1) for tokens 32 (w & 1) .. + 31 of the block as two 16-row
+// query tiles, so every K and V operand it reads from LDS feeds two products.  Each iteration
+// stages 128 key slots in LDS as two 64-slot halves (K row-major, V transposed; double-buffered)
+// and wave w takes half w >> 2: the two key-parity waves of a (head, tokens) pair keep separate
+// running softmax states, merged through LDS after the last iteration.  Slots at or beyond the
+// block's last query are masked for all of its queries; causal masking uses cache slots.  The
+// softmax denominators come from the matrix cores too: a ones operand against the probabilities.
 
-constexpr int PA_KB = 64;     // keys per block
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int PA_KB = 64;     // keys per half
 constexpr int PA_KROW = 136;  // halves per K row in LDS (128 + 8 pad)
 constexpr int PA_VROW = 68;   // halves per V^T row in LDS (64 keys + 4 pad)
-constexpr int PA_BUF = PA_KB * PA_KROW + HD * PA_VROW;  // halves per buffer
-constexpr size_t PA_LDS = 2 * PA_BUF * 2;
+constexpr int PA_BUF = PA_KB * PA_KROW + HD * PA_VROW;  // halves per 64-slot half
+constexpr size_t PA_LDS = 4 * PA_BUF * 2;                // two stages of two halves: 139,264 B
 
 template <int HL>
-__global__ __launch_bounds__(512) void pf_attn_kernel(PfAttnArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void pf_attn_kernel(PfAttnArgs a) {
     extern __shared__ __align__(16) uint16_t pa_lds[];
     const int QB = (a.M + 63) / 64;
     const int g = (int)(blockIdx.x % NKV), qb = QB - 1 - (int)(blockIdx.x / NKV);
     if (qb < 0) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;
-    const int head = 2 * g + (wave >> 2);
-    const int t0 = qb * 64 + (wave & 3) * 16;
-    const int kv_end = a.p0 + a.M;
-    const int nkb = (a.p0 + min(a.M, qb * 64 + 64) - 1) / PA_KB + 1;
+    const int par = wave >> 2, wi = wave & 3;
+    const int head = 2 * g + (wi >> 1);
+    const int t0 = qb * 64 + 32 * (wi & 1);
+    const int kv_lim = a.p0 + min(a.M, qb * 64 + 64);  // past the block's last query slot
+    const int nkb = (kv_lim - 1) / PA_KB + 1;          // 64-slot key halves with unmasked keys
+    const int nit = (nkb + 1) / 2;
     const bool active = t0 < a.M;
-    const int w_last = a.p0 + min(a.M - 1, t0 + 15);
-    const int qslot = a.p0 + t0 + r16;
+    const int w_first = a.p0 + t0;
+    const int w_last = a.p0 + min(a.M - 1, t0 + 31);
 
-    v8h Qh[4], Ql[4];
-    {
-        const size_t qo = ((size_t)(t0 + r16) * NH + head) * HD + 8 * q;
+    v8h Qh[2][4], Ql[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const size_t qo = ((size_t)(t0 + 16 * u + r16) * NH + head) * HD + 8 * q;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            Qh[ks] = *(const v8h*)(a.qh + qo + 32 * ks);
-            if constexpr (HL == 2) Ql[ks] = *(const v8h*)(a.ql + qo + 32 * ks);
+            Qh[u][ks] = *(const v8h*)(a.qh + qo + 32 * ks);
+            if constexpr (HL == 2) Ql[u][ks] = *(const v8h*)(a.ql + qo + 32 * ks);
         }
     }
     const uint16_t* kg = a.kc + (size_t)g * a.maxctx * HD;
     const uint16_t* vg = a.vc + (size_t)g * a.maxctx * HD;
 
-    // Staging: K key tid / 8, dims 16 (tid % 8) .. + 15; V keys 4 (tid / 32) .. + 3, dims
-    // 4 (tid % 32) .. + 3 (transposed in registers, 8-byte LDS writes).
-    uint4 kr[2];
-    uint2 vr[4];
-    auto gload = [&](int kb) {
-        const int ks = kb * PA_KB + (tid >> 3);
-        if (ks < kv_end) {
-            const uint4* p = (const uint4*)(kg + (size_t)ks * HD + 16 * (tid & 7));
-            kr[0] = p[0];
-            kr[1] = p[1];
-        } else {
-            kr[0] = kr[1] = make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int vs = kb * PA_KB + 4 * (tid >> 5) + i;
-            vr[i] = vs < kv_end ? *(const uint2*)(vg + (size_t)vs * HD + 4 * (tid & 31)) : make_uint2(0u, 0u);
-        }
+    // Staging of half hb: K key tid / 8, dims 16 (tid % 8) .. + 15; V keys 4 (tid / 32) .. + 3,
+    // dims 4 (tid % 32) .. + 3 (transposed in registers, 8-byte LDS writes).
+    uint4 kr0[2], kr1[2];
+    uint2 vr0[4], vr1[4];
+    // Staging through buffer resources bounded at kv_lim: slots at or past it (masked for every
+    // query of the block) read as zeros, with no branch.  Half hb of iteration it: K key tid / 8,
+    // dims 16 (tid % 8) .. + 15; V keys 4 (tid / 32) .. + 3, dims 4 (tid % 32) .. + 3 (transposed
+    // in registers, 8-byte LDS writes).
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kg, (short)0, kv_lim * HD * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vg, (short)0, kv_lim * HD * 2, 0x00020000);
+    struct Half {
+        u32x4 k0, k1;
+        u32x2 v0, v1, v2, v3;
     };
-    auto lstore = [&](int buf) {
-        uint16_t* Ks = pa_lds + buf * PA_BUF;
+    Half h0, h1;
+    const int koff = ((tid >> 3) * HD + 16 * (tid & 7)) * 2, voff = (4 * (tid >> 5) * HD + 4 * (tid & 31)) * 2;
+    auto gload_half = [&](int base, Half& h) {
+        const int o = base * HD * 2;
+        h.k0 = __builtin_amdgcn_raw_buffer_load_b128(krs, o + koff, 0, 0);
+        h.k1 = __builtin_amdgcn_raw_buffer_load_b128(krs, o + koff + 16, 0, 0);
+        h.v0 = __builtin_amdgcn_raw_buffer_load_b64(vrs, o + voff, 0, 0);
+        h.v1 = __builtin_amdgcn_raw_buffer_load_b64(vrs, o + voff + HD * 2, 0, 0);
+        h.v2 = __builtin_amdgcn_raw_buffer_load_b64(vrs, o + voff + HD * 4, 0, 0);
+        h.v3 = __builtin_amdgcn_raw_buffer_load_b64(vrs, o + voff + HD * 6, 0, 0);
+    };
+    auto gload = [&](int it) {
+        gload_half(2 * it * PA_KB, h0);
+        gload_half((2 * it + 1) * PA_KB, h1);
+    };
+    auto lstore_half = [&](uint16_t* Ks, const Half& h) {
         uint16_t* Vt = Ks + PA_KB * PA_KROW;
-        uint4* kd = (uint4*)(Ks + (tid >> 3) * PA_KROW + 16 * (tid & 7));
-        kd[0] = kr[0];
-        kd[1] = kr[1];
+        u32x4* kd = (u32x4*)(Ks + (tid >> 3) * PA_KROW + 16 * (tid & 7));
+        kd[0] = h.k0;
+        kd[1] = h.k1;
         const int d0 = 4 * (tid & 31), k0 = 4 * (tid >> 5);
+        // Output row d0 + j holds dim d0 + j of keys k0 .. k0 + 3: byte selects from the four rows.
+        const u32x2 vr[4] = {h.v0, h.v1, h.v2, h.v3};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint32_t e[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) e[i] = ((j < 2 ? vr[i].x : vr[i].y) >> (16 * (j & 1))) & 0xFFFFu;
-            *(uint2*)(Vt + (d0 + j) * PA_VROW + k0) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+            const int w = j >> 1;
+            const unsigned sel = (j & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of two words
+            *(u32x2*)(Vt + (d0 + j) * PA_VROW + k0) =
+                u32x2{__builtin_amdgcn_perm(vr[1][w], vr[0][w], sel), __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel)};
         }
     };
+    auto lstore = [&](int stage) {
+        lstore_half(pa_lds + (2 * stage) * PA_BUF, h0);
+        lstore_half(pa_lds + (2 * stage + 1) * PA_BUF, h1);
+    };
 
-    f32x4 O[8];
+    f32x4 O[2][8], Lr[2];  // Lr: the running denominator of query r16 in every element
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -__builtin_inff(), l_run = 0.f;
+    for (int u = 0; u < 2; ++u) {
+        Lr[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) O[u][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float m_run[2] = {-__builtin_inff(), -__builtin_inff()};
+    const f16 one = (f16)1.0f;
+    const v8h ones = {one, one, one, one, one, one, one, one};
 
     gload(0);
     lstore(0);
     __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        if (kb + 1 < nkb) gload(kb + 1);
+    for (int it = 0; it < nit; ++it) {
+        const int st = it & 1;
+        if (it + 1 < nit) gload(it + 1);
+        const int kb = 2 * it + par;
         if (active && kb * PA_KB <= w_last) {
-            const uint16_t* Ks = pa_lds + buf * PA_BUF;
+            const uint16_t* Ks = pa_lds + (2 * st + par) * PA_BUF;
             const uint16_t* Vt = Ks + PA_KB * PA_KROW;
-            // S^T tiles: keys 16 kt + (4 q + i) of this lane, query r16.
-            f32x4 S[4];
+            // S^T tiles: keys 16 kt + (4 q + i) of this lane, query r16 of tile u.
+            f32x4 S[2][4];
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
-                S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                S[0][kt] = S[1][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     const v8h kf = *(const v8h*)(Ks + (kt * 16 + r16) * PA_KROW + 32 * ks + 8 * q);
-                    S[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, Qh[ks], S[kt], 0, 0, 0);
-                    if constexpr (HL == 2) S[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, Ql[ks], S[kt], 0, 0, 0);
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        S[u][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, Qh[u][ks], S[u][kt], 0, 0, 0);
+                        if constexpr (HL == 2)
+                            S[u][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, Ql[u][ks], S[u][kt], 0, 0, 0);
+                    }
                 }
             }
-            float mb = -__builtin_inff();
+            // Masking only where some key of the half lies past some query of the wave (a
+            // wave-uniform branch: the halves below the diagonal skip it).
+            if (kb * PA_KB + PA_KB - 1 > w_first) {
+                asm volatile("");  // keeps the branch: the selects below are not speculated
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+                for (int u = 0; u < 2; ++u) {
+                    const int qslot = w_first + 16 * u + r16;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = kb * PA_KB + kt * 16 + 4 * q + i;
-                    if (key > qslot) S[kt][i] = -__builtin_inff();
-                    mb = fmaxf(mb, S[kt][i]);
+                    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (kb * PA_KB + kt * 16 + 4 * q + i > qslot) S[u][kt][i] = -__builtin_inff();
                 }
-            mb = max_x4(mb);
-            const float m_new = fmaxf(m_run, mb);  // finite: key slot 0 is in block 0
-            const float corr = (m_run == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-            float p[4][4], ls = 0.f;
+            }
+            v8h Ph[2][2], Pl[2][2];
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+            for (int u = 0; u < 2; ++u) {
+                float mb = -__builtin_inff();
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    p[kt][i] = (S[kt][i] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(S[kt][i] - m_new);
-                    ls += p[kt][i];
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mb = fmaxf(mb, S[u][kt][i]);
+                mb = max_x4(mb);
+                const float m_new = fmaxf(m_run[u], mb);
+                const float corr = m_new == m_run[u] ? 1.f
+                                 : m_run[u] == -__builtin_inff() ? 0.f
+                                 : __builtin_amdgcn_exp2f(m_run[u] - m_new);
+                // A query whose keys so far are all masked keeps m = -inf: subtract 0 there, so
+                // that every masked score gives exp2(-inf) = 0 without a per-element test.
+                const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+                float p[4][4];
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) p[kt][i] = __builtin_amdgcn_exp2f(S[u][kt][i] - m_use);
+                m_run[u] = m_new;
+                // The running maximum settles after the first blocks: rescale only when it moved.
+                if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) Lr[u][i] *= corr;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) O[u][dt][i] *= corr;
                 }
-            ls = sum_x4(ls);
-            l_run = l_run * corr + ls;
-            m_run = m_new;
+                // P^T of key tiles 2c, 2c + 1 is the B operand over keys {32 c + 4 q + i, 32 c + 16 + 4 q + i}.
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
+                for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) O[dt][i] *= corr;
-            // P^T of key tiles 2c, 2c + 1 is the B operand over keys {32 c + 4 q + i, 32 c + 16 + 4 q + i}.
+                    for (int i = 0; i < 4; ++i) {
+                        const f16 h0 = (f16)p[2 * c][i], h1 = (f16)p[2 * c + 1][i];
+                        Ph[u][c][i] = h0;
+                        Ph[u][c][4 + i] = h1;
+                        if constexpr (HL == 2) {
+                            Pl[u][c][i] = (f16)(p[2 * c][i] - (float)h0);
+                            Pl[u][c][4 + i] = (f16)(p[2 * c + 1][i] - (float)h1);
+                        }
+                    }
+            }
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                v8h Ph, Pl;
+            for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const f16 h0 = (f16)p[2 * c][i], h1 = (f16)p[2 * c + 1][i];
-                    Ph[i] = h0;
-                    Ph[4 + i] = h1;
-                    Pl[i] = (f16)(p[2 * c][i] - (float)h0);
-                    Pl[4 + i] = (f16)(p[2 * c + 1][i] - (float)h1);
+                for (int u = 0; u < 2; ++u) {
+                    Lr[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, Ph[u][c], Lr[u], 0, 0, 0);
+                    if constexpr (HL == 2) Lr[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, Pl[u][c], Lr[u], 0, 0, 0);
                 }
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt) {
                     const uint16_t* vp = Vt + (dt * 16 + r16) * PA_VROW + 32 * c + 4 * q;
                     const v4h va = *(const v4h*)vp, vb = *(const v4h*)(vp + 16);
                     const v8h vf = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
-                    O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Ph, O[dt], 0, 0, 0);
-                    if constexpr (HL == 2) O[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Pl, O[dt], 0, 0, 0);
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        O[u][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Ph[u][c], O[u][dt], 0, 0, 0);
+                        if constexpr (HL == 2)
+                            O[u][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Pl[u][c], O[u][dt], 0, 0, 0);
+                    }
                 }
-            }
         }
-        if (kb + 1 < nkb) lstore(buf ^ 1);
+        if (it + 1 < nit) lstore(st ^ 1);
         __syncthreads();
     }
-    const int t = t0 + r16;
-    if (active && t < a.M) {
-        const float inv = 1.0f / l_run;
+
+    // Key-parity merge: waves 4..7 hand (O, m, l) to waves 0..3 through LDS (free after the loop's
+    // last barrier).  Waves 0..3 always have a finite maximum: half 0 holds key slot 0.
+    float* mo = (float*)pa_lds;               // [4 waves][2 tiles][8 dim tiles][64 lanes] x 4
+    float* mml = mo + 4 * 2 * 8 * 64 * 4;     // [4 waves][2 tiles][64 lanes] x (m, l)
+    if (par == 1) {
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            const float4 o = make_float4(O[dt][0] * inv, O[dt][1] * inv, O[dt][2] * inv, O[dt][3] * inv);
-            *(float4*)(a.out + (size_t)t * H + head * HD + dt * 16 + 4 * q) = o;
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) *(f32x4*)(mo + (((wi * 2 + u) * 8 + dt) * 64 + lane) * 4) = O[u][dt];
+            *(float2*)(mml + ((wi * 2 + u) * 64 + lane) * 2) = make_float2(m_run[u], Lr[u][0]);
+        }
+    }
+    __syncthreads();
+    if (par == 0 && active) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int t = t0 + 16 * u + r16;
+            const float2 ml1 = *(const float2*)(mml + ((wi * 2 + u) * 64 + lane) * 2);
+            const float m = fmaxf(m_run[u], ml1.x);
+            const float f0 = m == m_run[u] ? 1.f : __builtin_amdgcn_exp2f(m_run[u] - m);
+            const float f1 = ml1.x == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ml1.x - m);
+            const float inv = 1.0f / (Lr[u][0] * f0 + ml1.y * f1);
+            if (t < a.M) {
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) {
+                    const f32x4 o1 = *(const f32x4*)(mo + (((wi * 2 + u) * 8 + dt) * 64 + lane) * 4);
+                    const float4 o = make_float4((O[u][dt][0] * f0 + o1[0] * f1) * inv, (O[u][dt][1] * f0 + o1[1] * f1) * inv,
+                                                 (O[u][dt][2] * f0 + o1[2] * f1) * inv, (O[u][dt][3] * f0 + o1[3] * f1) * inv);
+                    *(float4*)(a.out + (size_t)t * H + head * HD + dt * 16 + 4 * q) = o;
+                }
+            }
         }
     }
 }
