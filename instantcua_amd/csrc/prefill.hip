@@ -614,6 +614,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     }
                 }
             }
+            // Schedule: the K operands of key tile kt + 1 are read while tile kt's products issue.
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 8 * HL, 0);
+                if (kt < 2) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            }
             // Masking only where some key of the half lies past some query of the wave (a
             // wave-uniform branch: the halves below the diagonal skip it).
             if (kb * PA_KB + PA_KB - 1 > w_first) {
@@ -694,6 +702,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                             O[u][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, Pl[u][c], O[u][dt], 0, 0, 0);
                     }
                 }
+            // Schedule (fp16 operands alone; the hi + lo instance measured faster without it):
+            // each group of four V operands is read two groups ahead of its products.
+            if constexpr (HL == 1) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+                __builtin_amdgcn_sched_group_barrier(0x002 | 0x400, 200, 1);
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+                    if (k < 2) __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+                }
+            }
         }
         if (it + 1 < nit) lstore(st ^ 1);
         __syncthreads();
