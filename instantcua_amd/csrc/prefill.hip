@@ -138,6 +138,11 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     constexpr int NG = K / 64, NKS = K / 32, NC = K / 128;
     constexpr int CPS = FMT == FMT_Q4 ? 1 : FMT == FMT_Q8 ? 2 : 4;  // 1 KiB chunks per 128-K step
     constexpr int NCH = NC * CPS;                                      // chunks per row block
+    // DQ: the B operands are the dequantised weights in fp16 (q4 s q + b, q8 s q: the reference
+    // engine's prefill precision, taken with fp16 operands alone) or the f16 weights themselves,
+    // so the products accumulate straight into the outputs; otherwise q4 / q8 codes are exact
+    // fp16 integers and each group's sums take their scale in an epilogue.
+    constexpr bool DQ = HL == 1 || FMT == FMT_F16;
     const int TN = a.N / (16 * PG_RB), TM = a.Mpad / (64 * TB), T = TM * TN;
     const int per = (T + 7) / 8;
     const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
@@ -161,7 +166,12 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     // f16 weights have no scales.
     const uint32_t* vsrc = (const uint32_t*)a.sb + (size_t)(tn * TR + (tid % TR)) * NG + (tid / TR);
     constexpr int vstride = 2;
-    const bool vload = FMT != FMT_F16 && (2 * TR >= 512 || tid < 2 * TR);
+    const bool vload = !DQ && (2 * TR >= 512 || tid < 2 * TR);
+    // DQ q4 / q8: the unpacking thread's own scale words, row (tn RB + srb + 8 hb) 16 + lane % 16,
+    // words 2 c and 2 c + 1 of step c (q4 the (scale, bias) of 64-groups 2 c, 2 c + 1; q8 the
+    // scales of 32-groups 4 c .. 4 c + 3).
+    const uint32_t* dsrc = (const uint32_t*)a.sb + (size_t)((tn * PG_RB + srb) * 16 + (lane & 15)) * NG;
+    constexpr size_t DSRC2 = (size_t)8 * 16 * NG;  // row block srb + 8
 
     f32x4 acc[TB][4 * NHF];
 #pragma unroll
@@ -173,6 +183,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     uint4 Ae[TB][2][HL], Ao[TB][2][HL];  // [token block][k-step of the group][hi, lo]
     uint4 Wn[NHF][CPS];
     uint32_t Vn = 0;
+    uint32_t Dn[NHF][2];
     auto aload = [&](int g, uint4(&A)[TB][2][HL]) {
 #pragma unroll
         for (int i = 0; i < TB; ++i) {
@@ -189,6 +200,12 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
             for (int j = 0; j < CPS; ++j) Wn[hb][j] = *(const uint4*)(wsrc + hb * WSRC2 + (size_t)(c * CPS + j) * 1024);
         if (vload) Vn = vsrc[(size_t)c * vstride];
+        if constexpr (DQ && FMT != FMT_F16) {
+#pragma unroll
+            for (int hb = 0; hb < NHF; ++hb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) Dn[hb][j] = dsrc[hb * DSRC2 + 2 * c + j];
+        }
     };
     // Nibble lane L (row L % 16, 16-K slot L / 16 of each group) -> fp16 lanes (L % 16) + 16 (2 (slot % 2) + h)
     // of k-step 2 gg + slot / 2, h = 0 for K 0..7 of the slot, 1 for K 8..15.
@@ -213,13 +230,22 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     uint32_t o[4];
+                    // DQ: k-step 2 j + h is 32-group 4 c + 2 j + h, the scale in half h of word 2 c + j.
+                    const f16 sc = DQ ? (h ? as_h2(Dn[hb][j]).y : as_h2(Dn[hb][j]).x) : (f16)1.f;
+                    const f16x2 sc2 = {sc, sc};
 #pragma unroll
                     for (int w2 = 0; w2 < 2; ++w2) {
                         const uint32_t d = dd[2 * h + w2];
                         const uint32_t s0 = __builtin_amdgcn_perm(d, d, 0x0C010C00u);  // b0, b1
                         const uint32_t s1 = __builtin_amdgcn_perm(d, d, 0x0C030C02u);  // b2, b3
-                        o[2 * w2] = h2_bits(as_h2((s0 ^ 0x00800080u) | 0x64006400u) - k1152);
-                        o[2 * w2 + 1] = h2_bits(as_h2((s1 ^ 0x00800080u) | 0x64006400u) - k1152);
+                        f16x2 q0 = as_h2((s0 ^ 0x00800080u) | 0x64006400u) - k1152;
+                        f16x2 q1 = as_h2((s1 ^ 0x00800080u) | 0x64006400u) - k1152;
+                        if constexpr (DQ) {
+                            q0 = q0 * sc2;
+                            q1 = q1 * sc2;
+                        }
+                        o[2 * w2] = h2_bits(q0);
+                        o[2 * w2 + 1] = h2_bits(q1);
                     }
                     Bs[b][sr][2 * j + h][lane] = make_uint4(o[0], o[1], o[2], o[3]);
                 }
@@ -230,6 +256,9 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         const uint32_t dd[4] = {Wn[hb][0].x, Wn[hb][0].y, Wn[hb][0].z, Wn[hb][0].w};
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
+            // DQ: 64-group 2 c + gg of this row, (scale, bias) in word 2 c + gg.
+            const f16x2 sbw = as_h2(DQ ? Dn[hb][gg] : 0x00003C00u);
+            const f16x2 sc2 = {sbw.x, sbw.x}, bi2 = {sbw.y, sbw.y};
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t d = dd[2 * gg + h];
@@ -241,15 +270,21 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                     // value 1024 + q, and one packed fp16 subtraction leaves q exactly.
                     const uint32_t sp = __builtin_amdgcn_perm(d, d, 0x0C000C00u | ((2u * j + 1u) << 16) | (2u * j));
                     const f16x2 k1024 = {(f16)1024.f, (f16)1024.f};
-                    o[j] = h2_bits(as_h2((sp & 0x000F000Fu) | 0x64006400u) - k1024);
-                    o[2 + j] = h2_bits(as_h2(((sp >> 4) & 0x000F000Fu) | 0x64006400u) - k1024);
+                    f16x2 qa = as_h2((sp & 0x000F000Fu) | 0x64006400u) - k1024;
+                    f16x2 qb = as_h2(((sp >> 4) & 0x000F000Fu) | 0x64006400u) - k1024;
+                    if constexpr (DQ) {  // one rounding each: fma in fp16
+                        qa = __builtin_elementwise_fma(qa, sc2, bi2);
+                        qb = __builtin_elementwise_fma(qb, sc2, bi2);
+                    }
+                    o[j] = h2_bits(qa);
+                    o[2 + j] = h2_bits(qb);
                 }
                 Bs[b][sr][2 * gg + (slot >> 1)][r + 16 * (2 * (slot & 1) + h)] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
         }
       }
-        Vs[b][tid] = Vn;
+        if constexpr (!DQ) Vs[b][tid] = Vn;
     };
     // One activation operand (token block tb0 + i, k-step kk of group g, hi / lo part hl).
     auto aload1 = [&](int g, int i, int kk, int hl) {
@@ -267,6 +302,24 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) Bf[r][kk] = __builtin_bit_cast(v8h, Bs[b][rb0 + 4 * hf + r][2 * gg + kk][lane]);
+        if constexpr (DQ) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int hl = 0; hl < HL; ++hl) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int i = 0; i < TB; ++i)
+                            acc[i][4 * hf + r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                __builtin_bit_cast(v8h, Ac[i][kk][hl]), Bf[r][kk], acc[i][4 * hf + r], 0, 0, 0);
+                    if (hf == NHF - 1) {
+#pragma unroll
+                        for (int i = 0; i < TB; ++i) Ac[i][kk][hl] = aload1(gn, i, kk, hl);
+                    }
+                }
+            continue;
+        }
         float2 sb[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -331,10 +384,8 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
             for (int i = 0; i < TB; ++i) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    if constexpr (FMT == FMT_F16)
-                        acc[i][4 * hf + r][e] += C[r][i][e];
-                    else  // q4: the bias term sum_g b_g X_g went in before the loop
-                        acc[i][4 * hf + r][e] = fmaf(sb[r].x, C[r][i][e], acc[i][4 * hf + r][e]);
+                    // q4: the bias term sum_g b_g X_g went in before the loop
+                    acc[i][4 * hf + r][e] = fmaf(sb[r].x, C[r][i][e], acc[i][4 * hf + r][e]);
                 }
             }
       }
@@ -345,7 +396,7 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
     aload(0, Ae);
     aload(1, Ao);
     wload(0);
-    if constexpr (FMT == FMT_Q4) {
+    if constexpr (FMT == FMT_Q4 && !DQ) {
         // The q4 bias term sum_g b_g X_g of every output, on the matrix cores before the loop:
         // per 32 groups, A = the token block's group sums X (scaled by 2^-8 into fp16 range,
         // hi + lo parts) and B = the rows' fp16 biases, exact.  The loop's group epilogue is then
@@ -427,8 +478,9 @@ __global__ __launch_bounds__(512) void pf_gemm_kernel(PfGemmArgs a) {
                         *xo = v;
                     }
                 } else {  // EPI_SWIGLU: block RB tn + rb = gate units 8 (RB tn + rb) + 0..7, then their up rows
-                    const float up = __shfl_xor(y, 8);
-                    if (t < a.M && r16 < 8) a.h[(size_t)t * FF + (tn * PG_RB + rb) * 8 + r16] = (y / (1.f + expf(-y))) * up;
+                    const float up = dpp<0x128>(y);  // lane r16 ^ 8 of the row of 16 (a rotation by 8)
+                    const float hv = y * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-y * 1.4426950408889634f)) * up;
+                    if (t < a.M && r16 < 8) a.h[(size_t)t * FF + (tn * PG_RB + rb) * 8 + r16] = hv;
                 }
             }
         }
