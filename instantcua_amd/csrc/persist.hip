@@ -264,7 +264,8 @@ struct Shared {
     // hi 2g + 1, lo 2g, lo 2g + 1): the A operand rows of the score tiles
     alignas(16) uint16_t qf[8][HD];
     alignas(16) float pw[MW][2][2][4][12];  // probabilities of a math wave's slots, [row][head][lane / 16][i]
-    float ktail[2][HD], vtail[2][HD];      // the pass's new K / V rows (fp16 values)
+    alignas(16) uint16_t ktail[2][HD];     // the pass's new K / V rows (fp16), in the cache
+    alignas(16) uint16_t vtail[2][HD];     // layout: one 16-byte read is an operand's 8 dims
     float sc[2][ATT_PAD];
     float ored[MW][4][HD];    // per math wave: o of (row, head)
     float nw[H];              // RMSNorm weights of the current stage
@@ -648,6 +649,27 @@ __device__ __forceinline__ void norm_rope(float& a, float& b, float w0, float w1
     b = b2;
 }
 
+// Wave 0 of a workgroup waits until the (l, m) packets of all 32 attention splits of its KV group
+// carry tag tg (lane s < 32 polls split s's packet at base + s * stride), then stores go in S.go.
+// A wait that fails or runs past SPIN_LIMIT sets S.fail first (the next barrier returns).  Lanes
+// leave the loop together (a ballot), so S.go is always stored.
+__device__ __forceinline__ void watch_partials(Shared& S, const uint64_t* base, size_t stride, unsigned tg, int go,
+                                               unsigned* err, int lane) {
+    const bool mine = lane < ATT_SPLITS;
+    const uint64_t* q = base + (size_t)(mine ? lane : 0) * stride;
+    for (int it = 0;; ++it) {
+        const bool waiting = mine && tag_of(ld64(q)) != tg;
+        if (__builtin_amdgcn_ballot_w64(waiting) == 0) break;
+        if (it >= SPIN_LIMIT) raise_err(err);
+        if (it >= SPIN_LIMIT || ((it & 63) == 63 && load_err(err))) {
+            if (lane == 0) S.fail = 1;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) __hip_atomic_store(&S.go, go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Math threads: the cache rows of one attention block (block slots 0 .. ATT_BLOCK - 1 at split
 // row j0 + b0) that this lane holds; only rows < nprior come from the cache, zeros elsewhere.
 //   K, for the score tiles: tile T of math wave mw has 16 columns; column c = lane % 16 is block
@@ -682,13 +704,6 @@ __device__ __forceinline__ void load_kv_block(uint4 (&kt)[ATT_NT][4], uint4 (&vr
 }
 
 __device__ __forceinline__ h8 as_h8(uint4 v) { return __builtin_bit_cast(h8, u32x4{v.x, v.y, v.z, v.w}); }
-// Eight fp32 values that are exact in fp16, packed as fp16.
-__device__ __forceinline__ uint4 pack8_f16(const float* f) {
-    uint32_t w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = (uint32_t)f2h(f[2 * j]) | ((uint32_t)f2h(f[2 * j + 1]) << 16);
-    return make_uint4(w[0], w[1], w[2], w[3]);
-}
 
 // Max over the 16 lanes of each row of 16 (every lane gets its row's maximum).
 __device__ __forceinline__ float max16(float v) {
@@ -1053,10 +1068,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 } else if (wave == 2 && tail) {
                     float k0 = S.vec[2 * HD + lane], k1 = S.vec[2 * HD + lane + 64];
                     norm_rope(k0, k1, kn0, kn1, rc, rs);
-                    S.ktail[0][lane] = h2f(f2h(k0));
-                    S.ktail[0][lane + 64] = h2f(f2h(k1));
-                    S.vtail[0][lane] = h2f(f2h(S.vec[3 * HD + lane]));
-                    S.vtail[0][lane + 64] = h2f(f2h(S.vec[3 * HD + lane + 64]));
+                    S.ktail[0][lane] = f2h(k0);
+                    S.ktail[0][lane + 64] = f2h(k1);
+                    S.vtail[0][lane] = f2h(S.vec[3 * HD + lane]);
+                    S.vtail[0][lane + 64] = f2h(S.vec[3 * HD + lane + 64]);
                 }
             }
             __syncthreads();
@@ -1064,10 +1079,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 // The new cache row (fp16), device-scope stores by exchange threads, acknowledged
                 // before this workgroup publishes its partials.
                 const int c = tid - MT;
-                const float* src = c < 64 ? S.ktail[0] : S.vtail[0];
+                const uint16_t* src = c < 64 ? S.ktail[0] : S.vtail[0];
                 uint16_t* dst = (uint16_t*)(c < 64 ? kb : vb) + (size_t)pos * HD;
                 const int d = 2 * (c % 64);
-                const uint32_t v = (uint32_t)f2h(src[d]) | ((uint32_t)f2h(src[d + 1]) << 16);
+                const uint32_t v = (uint32_t)src[d] | ((uint32_t)src[d + 1] << 16);
                 __hip_atomic_store((uint32_t*)(dst + d), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __builtin_amdgcn_s_waitcnt(0);
             }
@@ -1102,11 +1117,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                             for (int T = 0; T < ATT_NT; ++T)
                                 if (4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) == pnew) {
 #pragma unroll
-                                    for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail[0] + 32 * j + 8 * kq);
+                                    for (int j = 0; j < 4; ++j) kt[T][j] = *(const uint4*)(S.ktail[0] + 32 * j + 8 * kq);
                                 }
 #pragma unroll
                             for (int i = 0; i < ATT_SPQ; ++i)
-                                if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail[0] + 8 * ql);
+                                if (quad + ATT_QW * i == pnew) vr[i] = *(const uint4*)(S.vtail[0] + 8 * ql);
                         }
                         // D[variant][slot]: lane l holds rows 4 (l / 16) + r, i.e. variant r.
                         float sc[2][ATT_NT];
@@ -1289,26 +1304,14 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // Workgroups 128..223 (no O, no merge) request their next stages' weights only once
             // their KV group's split partials are all out: issued as their attention ends, these
             // ~10 MB would queue at the memory controllers ahead of the mergers' polls of those
-            // partials.  The last split to publish is the one holding the new cache row (it
-            // waits for that row's acknowledgement first); their math waves watch its (l, m)
-            // packet, and nothing else of theirs is in flight then.
+            // partials.  Which split publishes last varies (the one holding the new cache row
+            // also waits for that row's acknowledgement): their math waves' wave 0 watches the
+            // (l, m) packets of all 32, and nothing else of theirs is in flight then.
             if (!F16 && math && w >= NWG / 2 && w < MERGER0) {
-                // One lane watches; the other math waves wait for it in LDS.
-                if (wave == 0 && lane == 0) {
-                    const int s_tail = min(pos / chunk, ATT_SPLITS - 1);
-                    const uint64_t* q = ll + PARTP + (size_t)(g * ATT_SPLITS + s_tail) * 2 * PART2 + HD / 2;
-                    const unsigned tg = tag4(r + 1);
-                    for (int it = 0;; ++it) {
-                        if (tag_of(ld64(q)) == tg) break;
-                        if (it >= SPIN_LIMIT) raise_err(err);
-                        if (it >= SPIN_LIMIT || ((it & 63) == 63 && load_err(err))) {
-                            S.fail = 1;  // the next barrier returns
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(1);
-                    }
-                    __hip_atomic_store(&S.go, (int)r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
+                // Wave 0 watches; the other math waves wait for it in LDS.
+                if (wave == 0)
+                    watch_partials(S, ll + PARTP + (size_t)g * ATT_SPLITS * 2 * PART2 + HD / 2, 2 * PART2, tag4(r + 1),
+                                   (int)r + 1, err, lane);
                 while (__hip_atomic_load(&S.go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (int)r + 1)
                     __builtin_amdgcn_s_sleep(1);
             }
@@ -1823,10 +1826,10 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
                     const int t = wave - kw;
                     float k0 = S.vec[512 * t + 2 * HD + lane], k1 = S.vec[512 * t + 2 * HD + lane + 64];
                     norm_rope(k0, k1, kn0, kn1, rc[t], rs[t]);
-                    S.ktail[t][lane] = h2f(f2h(k0));
-                    S.ktail[t][lane + 64] = h2f(f2h(k1));
-                    S.vtail[t][lane] = h2f(f2h(S.vec[512 * t + 3 * HD + lane]));
-                    S.vtail[t][lane + 64] = h2f(f2h(S.vec[512 * t + 3 * HD + lane + 64]));
+                    S.ktail[t][lane] = f2h(k0);
+                    S.ktail[t][lane + 64] = f2h(k1);
+                    S.vtail[t][lane] = f2h(S.vec[512 * t + 3 * HD + lane]);
+                    S.vtail[t][lane + 64] = f2h(S.vec[512 * t + 3 * HD + lane + 64]);
                 }
             }
             __syncthreads();
@@ -1837,10 +1840,10 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
 #pragma unroll
                 for (int t = 0; t < NR; ++t) {
                     if (!tl(t)) continue;
-                    const float* src = c < 64 ? S.ktail[t] : S.vtail[t];
+                    const uint16_t* src = c < 64 ? S.ktail[t] : S.vtail[t];
                     uint16_t* dst = (uint16_t*)(c < 64 ? kb : vb) + (size_t)(pos + t) * HD;
                     const int d = 2 * (c % 64);
-                    const uint32_t v = (uint32_t)f2h(src[d]) | ((uint32_t)f2h(src[d + 1]) << 16);
+                    const uint32_t v = (uint32_t)src[d] | ((uint32_t)src[d + 1] << 16);
                     __hip_atomic_store((uint32_t*)(dst + d), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
                 __builtin_amdgcn_s_waitcnt(0);
@@ -1885,11 +1888,11 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
                                 for (int T = 0; T < ATT_NT; ++T)
                                     if (4 * T + (c >> 2) < ATT_SPQ && att_slot(T, c, mw) == pnew) {
 #pragma unroll
-                                        for (int j = 0; j < 4; ++j) kt[T][j] = pack8_f16(S.ktail[t] + 32 * j + 8 * kq);
+                                        for (int j = 0; j < 4; ++j) kt[T][j] = *(const uint4*)(S.ktail[t] + 32 * j + 8 * kq);
                                     }
 #pragma unroll
                                 for (int i = 0; i < ATT_SPQ; ++i)
-                                    if (quad + ATT_QW * i == pnew) vr[i] = pack8_f16(S.vtail[t] + 8 * ql);
+                                    if (quad + ATT_QW * i == pnew) vr[i] = *(const uint4*)(S.vtail[t] + 8 * ql);
                             }
                         }
                         // D[variant][slot]: lane l holds rows 4 (l / 16) + r, i.e. variant
@@ -2089,27 +2092,14 @@ __device__ __forceinline__ void decode_pass_loop(const PersistArgs& a, Shared& S
             // Workgroups 128..223 (no O, no merge) request their next stages' weights only once
             // their KV group's split partials are all out: issued as their attention ends, these
             // ~10 MB would queue at the memory controllers ahead of the mergers' polls of those
-            // partials.  The last split to publish is the one holding the newest cache row (it
-            // waits for that row's acknowledgement first); their math waves watch one of its
-            // (l, m) packets, and nothing else of theirs is in flight then.
+            // partials.  Which split publishes last varies (those holding new cache rows also
+            // wait for the rows' acknowledgement): their math waves' wave 0 watches an (l, m)
+            // packet of each of the 32, and nothing else of theirs is in flight then.
             if (math && w >= NWG / 2 && w < MERGER0) {
-                // One lane watches; the other math waves wait for it in LDS.
-                if (wave == 0 && lane == 0) {
-                    const int s_tail = min((pos + NR - 1) / chunk, ATT_SPLITS - 1);
-                    const uint64_t* q = ll + PK::PARTP + (size_t)(g * ATT_SPLITS + s_tail) * NR * 2 * PART2 +
-                                        (NR - 1) * 2 * PART2 + HD / 2;
-                    const unsigned tg = tag4(r + 1);
-                    for (int it = 0;; ++it) {
-                        if (tag_of(ld64(q)) == tg) break;
-                        if (it >= SPIN_LIMIT) raise_err(err);
-                        if (it >= SPIN_LIMIT || ((it & 63) == 63 && load_err(err))) {
-                            S.fail = 1;  // the next barrier returns
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(1);
-                    }
-                    __hip_atomic_store(&S.go, (int)r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
+                // Wave 0 watches; the other math waves wait for it in LDS.
+                if (wave == 0)
+                    watch_partials(S, ll + PK::PARTP + (size_t)g * ATT_SPLITS * NR * 2 * PART2 + (NR - 1) * 2 * PART2 + HD / 2,
+                                   (size_t)NR * 2 * PART2, tag4(r + 1), (int)r + 1, err, lane);
                 while (__hip_atomic_load(&S.go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (int)r + 1)
                     __builtin_amdgcn_s_sleep(1);
             }

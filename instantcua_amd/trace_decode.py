@@ -145,12 +145,38 @@ def table(t, layer_ids, points, title, x_pollers=slice(128, 256)):
     return "\n".join(rows)
 
 
+WG_CLASSES = [("0..127", slice(0, 128)), ("128..223", slice(128, 224)), ("224..255", slice(224, 256))]
+
+
+def class_table(t, layer_ids, points, title):
+    """Median and latest stamp of each workgroup class (0..127: O and the lower down halves;
+    128..255: QKV; 224..255 also merge), median over the layers; "-" where a class never stamps."""
+    head = " | ".join(f"{n} median | {n} latest" for n, _ in WG_CLASSES)
+    rows = [f"| {title} | {head} |", "|---|" + "---:|" * (2 * len(WG_CLASSES))]
+    for ev, _, what in points:
+        cells = []
+        for _, sl in WG_CLASSES:
+            med, hi = [], []
+            for l in layer_ids:
+                start = np.min(t[:, l, 0][t[:, l, 0] > 0])
+                v = t[sl, l, ev]
+                v = v[v > 0] - start
+                if v.size:
+                    med.append(np.median(v))
+                    hi.append(v.max())
+            cells += [f"{np.median(med):.2f}", f"{np.median(hi):.2f}"] if med else ["-", "-"]
+        rows.append(f"| {what} | " + " | ".join(cells) + " |")
+    return "\n".join(rows)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--pos", type=int, default=4096)
     ap.add_argument("--steps", type=int, default=16)
     ap.add_argument("--f16", action="store_true", help="the 28-layer f16 decoder instead of q4")
+    ap.add_argument("--classes", action="store_true", help="also tabulate each workgroup class's median and latest stamps")
+    ap.add_argument("--save", default=None, help="write the raw stamp array [workgroup][layer][event] (us) to this .npy file")
     ap.add_argument("--pairs", action="store_true",
                     help="tabulate a one-row pass and a grammar-pair pass of the pair-forcing model instead")
     a = ap.parse_args()
@@ -177,6 +203,11 @@ def main():
                 slice(0, 256) if a.f16 else slice(128, 256)))
     print()
     print(table(t, [L], HEAD_POINTS, "lm_head / commit point"))
+    if a.classes:
+        print()
+        print(class_table(t, mid, LAYER_POINTS, "layer point, by workgroup class"))
+    if a.save:
+        np.save(a.save, t)
 
 
 if __name__ == "__main__":
