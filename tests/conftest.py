@@ -1,3 +1,4 @@
+import ctypes
 import os
 import sys
 
@@ -7,6 +8,22 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+
+def _keep_freed_memory() -> None:
+    """The tests build many synthetic model images of 100-300 MB.  Serving large allocations
+    from the heap and never trimming it lets each image reuse the pages of the previous one
+    instead of mapping and first-touching fresh ones, which on some hosts costs more than the
+    test's own work (mallopt M_MMAP_THRESHOLD = 1 GiB, M_TRIM_THRESHOLD = 2 GiB - 1)."""
+    try:
+        libc = ctypes.CDLL("libc.so.6")
+        libc.mallopt(-3, 1 << 30)
+        libc.mallopt(-1, 2**31 - 1)
+    except OSError:
+        pass
+
+
+_keep_freed_memory()
 
 
 def pytest_configure(config):
