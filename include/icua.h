@@ -35,7 +35,7 @@ enum {
     ICUA_FLAG_PASS_PREFILL = 8,  /* prefill q4 prompts in passes of 8 rows instead of the matrix-core GEMMs */
     ICUA_FLAG_VISION_DELTA_CACHE = 16, /* icua_generate_vision skips the encoder on an identical frame (Engine.swift:707-716) */
     ICUA_FLAG_FIRST_LOGITS = 32, /* icua_generate(_vision) keep the first token's logits for icua_logits (writeFirstLogits, Engine.swift:697) */
-    ICUA_FLAG_PREFILL_FP16 = 64, /* matrix-core prefill on fp16 operands alone (the reference engine's precision, Shaders.swift:976-992) instead of fp16 hi + lo parts */
+    ICUA_FLAG_PREFILL_FP16 = 64, /* matrix-core prefill on fp16 operands alone: activations, queries and probabilities in fp16, weights dequantised to fp16 (the reference engine's precision, Shaders.swift:976-992), instead of fp16 hi + lo activations against exact codes */
 };
 
 /* Decode control block, first twelve fields as `State` (Shaders.swift:41-54). */
