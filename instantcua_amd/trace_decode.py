@@ -119,7 +119,7 @@ def read_pair_traces(layers: int):
                 got = (grab(), e.last_timing["decode_ms"])
                 if was_pair:
                     pair = got
-                else:
+                elif not e.state()["done"]:  # a stopping pass leaves before the commit's last stamp
                     single = got
     if pair is None:
         raise SystemExit("no grammar pair was forced")
