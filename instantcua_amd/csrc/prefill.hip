@@ -14,12 +14,16 @@
 // accumulator chain; the group epilogue is acc += s C_g (q4 and q8: the q4 bias term
 // sum_g b_g X_g, X_g = sum_k x''_k, runs on the matrix cores once per tile before the loop),
 // f16 weights accumulate directly, and the row scale 2^(E_t - 14) is applied once at the end.
+// With fp16 operands alone (ICUA_FLAG_PREFILL_FP16, the reference engine's precision) there is
+// no lo part, and the B operands are the weights dequantised to fp16 (q4 fp16(s q + b), q8
+// fp16(s q)), so the products accumulate straight into the outputs with no group epilogue.
 //
 // Attention.  Causal GQA flash attention on v_mfma_f32_16x16x32_f16: scores are computed
 // transposed (S^T = K Q^T) so that the probabilities come out of the accumulator already in
 // the B-operand layout of the P.V product (O^T = V^T P^T); V is transposed through LDS.  The
 // fp32 queries and probabilities are split into fp16 hi + lo parts (two products each), which
-// keeps them at ~22 bits against the fp16 cache.
+// keeps them at ~22 bits against the fp16 cache (one part with fp16 operands alone).  Each wave
+// holds 32 queries, so every K and V operand it reads from LDS feeds two products.
 #include "icua_device.h"
 #include "icua_kernels.h"
 
