@@ -259,7 +259,7 @@ struct Shared {
     float xhi[2][16];         // the upper-half down sums of those rows from the previous layer
     float aml[MW][8];         // per math wave and row: (m head 0, m head 1, l head 0, l head 1)
     float fx[192 * 2];        // per-group (2^(e-21), sum X * 2^(e-21))
-    float red[6 * MW * 64];   // math-wave partial sums (up to 6 blocks: 3 blocks x 2 rows)
+    alignas(16) float red[6 * MW * 64];  // partial sums of the waves (up to 6 blocks: 3 blocks x 2 rows)
     // attention: the two query heads of each pass row t as fp16 hi and lo parts, rows 4 t + (hi 2g,
     // hi 2g + 1, lo 2g, lo 2g + 1): the A operand rows of the score tiles
     alignas(16) uint16_t qf[8][HD];
@@ -841,24 +841,38 @@ __device__ __forceinline__ void mac_f16(const Shared& S, const WF<NB, CPW>& wf, 
     }
 }
 
-// The partials of N <= 3 blocks from the NWV waves that computed them (lanes 0-15 of waves
-// w0 .. w0 + NWV - 1) into S.red; one barrier.  red_sum then adds them in a fixed order.
+// The partials of N <= 3 blocks from the NWV waves that computed them (lanes 0-15 of the waves in
+// slots 0 .. NWV - 1) into S.red as [block][row][slot], one barrier.  red_sum16 then reads a
+// row's NWV partials with one or two 16-byte LDS reads (not NWV dependent ones) and adds them in
+// slot order.
 template <int N>
 __device__ __forceinline__ void red_store16(Shared& S, const float (&acc)[N], int slot) {
     static_assert(N * WAVES * 16 <= 6 * MW * 64, "S.red holds the partials");
     const int lane = my_tid() % 64;
     if (slot >= 0 && lane < 16) {
 #pragma unroll
-        for (int b = 0; b < N; ++b) S.red[(b * WAVES + slot) * 16 + lane] = acc[b];
+        for (int b = 0; b < N; ++b) S.red[(b * 16 + lane) * WAVES + slot] = acc[b];
     }
     lds_barrier();
 }
 template <int NWV>
 __device__ __forceinline__ float red_sum16(const Shared& S, int b) {
-    const float* r = S.red + b * WAVES * 16 + my_tid() % 16;
-    float t = r[0];
+    static_assert(NWV % 4 == 0 && NWV <= WAVES && WAVES % 4 == 0, "whole 16-byte reads of a row");
+    const float4* r = (const float4*)(S.red + (b * 16 + (unsigned)my_tid() % 16u) * WAVES);
+    float4 v[NWV / 4];
 #pragma unroll
-    for (int i = 1; i < NWV; ++i) t += r[16 * i];
+    for (int i = 0; i < NWV / 4; ++i) v[i] = r[i];
+    float t = v[0].x;
+    t += v[0].y;
+    t += v[0].z;
+    t += v[0].w;
+#pragma unroll
+    for (int i = 1; i < NWV / 4; ++i) {
+        t += v[i].x;
+        t += v[i].y;
+        t += v[i].z;
+        t += v[i].w;
+    }
     return t;
 }
 
@@ -907,12 +921,12 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // Math waves: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127) of
     // the current layer.
     WB<FMT, CW2> wx[2];
-    // f16: each wave's K-slices of its QKV block, gate|up blocks and down half-block.  The math
-    // waves request theirs a stage ahead (QKV after the previous down publish, gate|up after the
-    // attention partial or the merge, down after the SwiGLU publish); the exchange waves once
-    // their stage input is in.
+    // f16: each wave's K-slices of its QKV block, gate|up blocks and down half-block, requested a
+    // stage ahead where its registers are free: QKV after the previous down publish (math waves;
+    // the exchange waves after the x poll); gate|up by the O workgroups' exchange waves two
+    // blocks at the attention-output poll and one after their O products, by every other wave
+    // after its attention partial, merge or O stage; down after the SwiGLU publish.
     constexpr int F16_CPW = H / F16_CHK / WAVES, F16_CPWD = FFH / F16_CHK / WAVES;
-    constexpr int F16_GU_EARLY = 1;  // gate|up blocks whose math-wave slices are requested early
     WF<1, F16_CPW> wqf;
     WF<3, F16_CPW> wgf;
     WF<1, F16_CPWD> wdf;
@@ -1229,11 +1243,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             WF<1, H / F16_CHK / XW> wof;
             if constexpr (F16) {
                 if (!math && w < H / 16) wof.load(P.wo, {w}, H / F16_CHK, (wave - MW) * (H / F16_CHK / XW), lane);
-                // The math waves' gate|up slices (the mergers' after the merge: in flight during
-                // their partials poll, they would delay it).
-                if (math && w < MERGER0) wgf.load<0, F16_GU_EARLY>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
                 // Workgroups 128..223 (no O, no merge) idle until the x' poll: their exchange waves
-                // request all of their slices now.
+                // request all of their gate|up slices now (the mergers' after the merge: in flight
+                // during their partials poll, they would delay it).
                 if (!math && w >= H / 16 && w < MERGER0) wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
             }
 
@@ -1290,8 +1302,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE(l, 17);
                 __syncthreads();  // the partials in S.A are read before the next staging
                 if constexpr (F16) {
-                    if (math) wgf.load<0, F16_GU_EARLY>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
-                    else wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                    if (!math) wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
                 }
                 PK_TRACE(l, 6);
             }
@@ -1334,9 +1345,14 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE_X(l, 7);
                 float y = 0.f;
                 if constexpr (F16) {
+                    // Two gate|up blocks go out beside the O block's registers, the third once the O
+                    // products are done (all three before them: 860 against 834 us per token at 4k
+                    // context, one before them: 836).
+                    if (!math) wgf.load<0, 2>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
                     stage_f16<H>(S, S.vec, false);
                     float acc1[1] = {0.f};
                     if (!math) mac_f16(S, wof, (wave - MW) * (H / F16_CHK / XW), lane, acc1);
+                    if (!math) wgf.load<2, 3>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
                     red_store16<1>(S, acc1, math ? -1 : wave - MW);
                     y = red_sum16<XW>(S, 0);
                 } else {
@@ -1358,6 +1374,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // Workgroups 128..255 request the upper down half-block and the next layer's QKV
             // blocks here, where they wait for no stage input (workgroups 0..127 run O): loads
             // issued later would queue ahead of their x' and h polls.
+            // f16: the math waves' gate|up slices (after the O publish on workgroups 0..127).  One
+            // block requested earlier, at the attention partial, measured slower (868 against 855 us
+            // per token at 4k context), and so did one at the start of the O stage (864 against 857).
+            if (F16 && math) wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
             if (!F16 && math && qkv_wg) {
                 wd_request<FMT>(wdb, P.wd, P.wd_sb, w - NWG / 2, 1, mw, lane);
                 wx[0].forget();
@@ -1383,13 +1403,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE_X(l, 9);
                 float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
                 if constexpr (F16) {
-                    // Blocks 3w .. 3w + 2 (192 KiB): the math waves' remaining K-slices now, and the
-                    // O workgroups' exchange waves' (the others' are in flight since their attention
-                    // partial or merge).
-                    if (math)
-                        wgf.load<F16_GU_EARLY, 3>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
-                    else if (w < H / 16)  // the O workgroups' exchange waves (their O publish went first)
-                        wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                    // Blocks 3w .. 3w + 2 (192 KiB), every wave's slices in flight since its O work
+                    // or attention ended.
                     stage_f16<H>(S, S.vec, true);
                     PK_TRACE(l, 13);
                     mac_f16(S, wgf, wave * F16_CPW, lane, acc);
@@ -1418,10 +1433,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     }
                 }
                 PK_TRACE(l, 10);
-                if constexpr (F16) {  // the math waves' down slices
-                    if (math)
-                        wdf.load(P.wd, {w % (NWG / 2)}, FF / F16_CHK, (w / (NWG / 2)) * (FFH / F16_CHK) + wave * F16_CPWD, lane);
-                }
+                if constexpr (F16)  // every wave's down slices (the gate|up slices are spent)
+                    wdf.load(P.wd, {w % (NWG / 2)}, FF / F16_CHK, (w / (NWG / 2)) * (FFH / F16_CHK) + wave * F16_CPWD, lane);
             }
 
             // ---------------- down: K half w / 128 of row block w % 128 --------------------
@@ -1438,7 +1451,6 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 float y = 0.f;
                 if constexpr (F16) {
                     // K half `half` of row block rb (96 KiB): chunks half * 96 .. of the block.
-                    if (!math) wdf.load(P.wd, {rb}, FF / F16_CHK, half * (FFH / F16_CHK) + wave * F16_CPWD, lane);
                     stage_f16<FFH>(S, S.vec, false);
                     PK_TRACE(l, 18);
                     float acc1[1] = {0.f};
