@@ -253,11 +253,15 @@ def run_q8_prefill(img):
             "prefill_mfma_frac": round(PREFILL_FLOPS / (ms * 1e-3) / MFMA_F16_PEAK, 4)}
 
 
-def run_f16_decode(steps=32, warmup=4):
-    """The 4k-context vision workload on a 28-layer f16 decoder: f16 weights decode on the
-    per-stage kernels (one step per HIP-graph replay); tok/s and the fraction of the HBM roofline
-    (2-byte weights plus K/V per token).  The weights are random f16 bit patterns (a timing run)."""
-    img = synth.build_model_image(WeightFormat.F16, n_layers=LAYERS, tag="bench-f16", f16_bits=True)
+def run_fmt_decode(fmt, steps=32, warmup=4, img=None):
+    """The 4k-context vision workload on a 28-layer f16 or q8 g32 decoder, decoded by the
+    persistent kernel's slice-streaming form: tok/s and the fraction of the HBM roofline (the
+    format's weight bytes plus K/V per token).  The f16 weights are random f16 bit patterns (a
+    timing run); the q8 model is the synthetic q8 decoder of the q8 prefill and verify lines."""
+    name = "f16" if fmt == WeightFormat.F16 else "q8 g32"
+    if img is None:
+        img = (synth.build_model_image(WeightFormat.F16, n_layers=LAYERS, tag="bench-f16", f16_bits=True)
+               if fmt == WeightFormat.F16 else synth.build_model_image(fmt, n_layers=LAYERS, tag="bench-q8"))
     vp = synth.visual_prompt(PREFILL, VIS_OFFSET, LLM_H, LLM_W, tag="bench-vis")
     e = eng.Engine(image=img, max_context=PREFILL + warmup + steps + 8, max_steps=warmup + steps + 2)
     e.eos = (-1, -1)
@@ -270,15 +274,14 @@ def run_f16_decode(steps=32, warmup=4):
     persistent = e.last_decode_persistent
     e.close()
     del img
-    nbytes = sum(weight_bytes_per_token(WeightFormat.F16) + kv_bytes_per_token(PREFILL + warmup + i + 1)
-                 for i in range(steps))
-    out = {"workload": "28-layer f16 decoder, the same 4096-token vision-context prefill, greedy decode",
+    nbytes = sum(weight_bytes_per_token(fmt) + kv_bytes_per_token(PREFILL + warmup + i + 1) for i in range(steps))
+    out = {"workload": f"28-layer {name} decoder, the same 4096-token vision-context prefill, greedy decode",
            "steps": steps, "decode_tok_s": round(steps / (dec_ms / 1e3), 1),
            "decode_us_per_token": round(dec_ms * 1e3 / steps, 1),
            "bytes_per_token": int(nbytes / steps), "GB_s": round(nbytes / (dec_ms * 1e-3) / 1e9, 1),
            "roofline_frac": round(nbytes / (dec_ms * 1e-3) / HBM_PEAK, 4),
            "path": "persistent kernel" if persistent else "per-stage kernels, HIP graph per step"}
-    log(f"f16 decode: {out['decode_us_per_token']} us/token, {out['roofline_frac']:.3f} of roofline ({out['path']})")
+    log(f"{name} decode: {out['decode_us_per_token']} us/token, {out['roofline_frac']:.3f} of roofline ({out['path']})")
     return out
 
 
@@ -609,12 +612,12 @@ def main():
                     help="profiling runs: start decoding at the same 4096-slot context without the prefill "
                          "(cache rows stay zero; same bytes per step), so a profile holds only the decode launch")
     ap.add_argument("--workload", choices=["decode", "verify", "gemv", "quant", "vision", "prefill",
-                                           "prefill-fp16", "f16-decode"], default="decode",
+                                           "prefill-fp16", "f16-decode", "q8-decode"], default="decode",
                     help="decode: the 4k-context q4 decode (default); verify: 8-draft q8 verify over 8192 rows; "
                          "gemv: isolated q4 GEMV sweep; quant: converter quantisers over the backbone shapes; "
                          "vision: the vision tower on a 640x384 frame; prefill / prefill-fp16: the decode "
-                         "workload's 4096-row q4 prefill alone (fp16 hi + lo or fp16 operands); f16-decode: "
-                         "the same decode on a 28-layer f16 decoder")
+                         "workload's 4096-row q4 prefill alone (fp16 hi + lo or fp16 operands); f16-decode / "
+                         "q8-decode: the same decode on a 28-layer f16 / q8 decoder")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU decode is a design note only",
@@ -641,8 +644,9 @@ def main():
         print(json.dumps(run_prefill(img, args.workload == "prefill-fp16")))
         dump_maps()
         return
-    if args.workload == "f16-decode":
-        print(json.dumps(run_f16_decode(args.steps, args.warmup)))
+    if args.workload in ("f16-decode", "q8-decode"):
+        fmt = WeightFormat.F16 if args.workload == "f16-decode" else WeightFormat.Q8
+        print(json.dumps(run_fmt_decode(fmt, args.steps, args.warmup)))
         dump_maps()
         return
 
@@ -712,11 +716,12 @@ def main():
         rows["oracle_decode_4k"] = cpu_oracle_decode(img, PREFILL)
         rows["text_context_1024_fp32_port"] = cpu_text_context(img)
     del img
-    q8 = ver = f16 = None
+    q8 = q8d = ver = f16 = None
     if not args.no_prefill:
-        f16 = run_f16_decode()
+        f16 = run_fmt_decode(WeightFormat.F16)
         img8 = synth.build_model_image(WeightFormat.Q8, n_layers=LAYERS, tag="bench-q8")
         q8 = run_q8_prefill(img8)
+        q8d = run_fmt_decode(WeightFormat.Q8, img=img8)
         v = run_verify(10, 2, img8)  # the verify workload (--workload verify), a short run
         ver = {"workload": v["config"]["workload"], "ms_per_pass": v["ms_per_step"], "passes_s": v["value"],
                "roofline_frac": v["roofline"]["frac"], "GB_s": v["roofline"]["achieved"]}
@@ -767,6 +772,7 @@ def main():
         "prefill_q8_4096": q8,
         "verify_q8_8192": ver,
         "decode_f16_4k": f16,
+        "decode_q8_4k": q8d,
     }
     print(json.dumps(out))
     dump_maps()

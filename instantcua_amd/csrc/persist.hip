@@ -274,6 +274,17 @@ struct Shared {
     float emb[2 * H];         // embeddings of the pass's tokens (row t at t H)
 };
 
+// Workgroup barrier for data exchanged through LDS only: waits for this wave's LDS accesses, not
+// for its vector-memory loads (__syncthreads would drain the weight slices in flight, so a stage
+// could not stage its input while its tiles land).  The empty asm statements keep the compiler
+// from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // vmcnt 63, expcnt 7, lgkmcnt 0
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Workgroup barrier that also tells every thread whether any thread's wait failed.  The flag is
 // written only on failure, so the common path is one barrier and one LDS read (the library's
 // __syncthreads_or costs three barriers and three LDS operations).
@@ -299,7 +310,7 @@ __device__ __forceinline__ bool sync_failed(Shared& S, bool failed) {
 // K / 4 is not a multiple of THREADS the last unit row is held by the first waves only (whole
 // waves, so whole groups).  NRS rows (src + t K) are staged with one barrier: row t's groups
 // follow row t - 1's (group offset t K / G) and its sum of squares goes to S.misc[40 + 8 t + wave].
-template <int FMT, int K, int NRS = 1, class SH>
+template <int FMT, int K, int NRS = 1, class SH, bool LDS_ONLY = false>
 __device__ __forceinline__ void stage_c(SH& S, const float* src, bool normed) {
     constexpr int G = (FMT == FMT_Q4) ? 64 : 32;
     constexpr int TILE = (FMT == FMT_Q4) ? 192 : 96;
@@ -375,7 +386,10 @@ __device__ __forceinline__ void stage_c(SH& S, const float* src, bool normed) {
             if (lane == 0) S.misc[40 + 8 * rw + wave] = ss;
         }
     }
-    __syncthreads();
+    if constexpr (LDS_ONLY)
+        lds_barrier();  // the slice-streaming form: the weight slices in flight stay in flight
+    else
+        __syncthreads();
 }
 
 // RMS factor of the last normed staging of a K-vector: 1/sqrt(mean(v^2) + eps) from the eight
@@ -732,17 +746,6 @@ __device__ __forceinline__ void load_norm8(float (&n)[8], const float* p) {
 
 constexpr int F16_CHK = 32;  // K per 1 KiB f16 chunk
 
-// Workgroup barrier for data exchanged through LDS only: waits for this wave's LDS accesses, not
-// for its vector-memory loads (__syncthreads would drain the weight slices in flight, so a stage
-// could not stage its input while its tiles land).  The empty asm statements keep the compiler
-// from moving memory accesses across it.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // vmcnt 63, expcnt 7, lgkmcnt 0
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
 // The K values of src (fp32, times S.nw when normed) -> S.A, chunk c at c * 128 bytes: 32 fp16 hi
 // parts, then 32 lo parts, of v * 2^(14 - e_c); S.fx[c] = 2^(e_c - 14); each wave's sum of squares
 // to S.misc[40 + wave] (normed), as stage_c leaves them for norm_scale.  Whole workgroup, one
@@ -841,6 +844,52 @@ __device__ __forceinline__ void mac_f16(const Shared& S, const WF<NB, CPW>& wf, 
     }
 }
 
+// Slice tiles, for the forms whose stages stream their weight tiles on all eight waves (f16 and
+// q8 blocks): a wave's slice of NB 16-row blocks is CPW 1 KiB chunks, chunks slice * CPW .. of each
+// block (with their group scales for q8).  mac(S, slice, ...) multiplies them with the staged
+// chunks slice * CPW .. (the slice's chunks within the staged vector) and leaves this wave's sum
+// of block b in lanes 0-15 of acc[b].
+template <int FMT, int NB, int CPW>
+struct SliceTiles;
+template <int NB, int CPW>
+struct SliceTiles<FMT_F16, NB, CPW> {
+    WF<NB, CPW> t;
+    template <int B0 = 0, int B1 = NB>
+    __device__ __forceinline__ void load(const uint8_t* w, const uint8_t*, const int (&rb)[NB], int K, int slice, int lane) {
+        t.template load<B0, B1>(w, rb, K / F16_CHK, slice * CPW, lane);
+    }
+    __device__ __forceinline__ void forget() { t.forget(); }
+    __device__ __forceinline__ void mac(const Shared& S, int slice, int lane, float (&acc)[NB]) const {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+        mac_f16(S, t, slice * CPW, lane, acc);
+    }
+};
+template <int NB, int CPW>
+struct SliceTiles<FMT_Q8, NB, CPW> {
+    WB<FMT_Q8, CPW> t[NB];
+    template <int B0 = 0, int B1 = NB>
+    __device__ __forceinline__ void load(const uint8_t* w, const uint8_t* sb, const int (&rb)[NB], int K, int slice, int lane) {
+#pragma unroll
+        for (int b = B0; b < B1; ++b) t[b].load(w, sb, rb[b], K, slice, lane);
+    }
+    __device__ __forceinline__ void forget() {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) t[b].forget();
+    }
+    __device__ __forceinline__ void mac(const Shared& S, int slice, int lane, float (&acc)[NB]) const {
+        mac_blocks<FMT_Q8, CPW, NB>(S, t, slice, lane, acc);
+    }
+};
+// The staging of the slice-streaming forms (an LDS-only closing barrier).
+template <int FMT, int K>
+__device__ __forceinline__ void stage_slices(Shared& S, const float* src, bool normed) {
+    if constexpr (FMT == FMT_F16)
+        stage_f16<K>(S, src, normed);
+    else
+        stage_c<FMT, K, 1, Shared, true>(S, src, normed);
+}
+
 // The partials of N <= 3 blocks from the NWV waves that computed them (lanes 0-15 of the waves in
 // slots 0 .. NWV - 1) into S.red as [block][row][slot], one barrier.  red_sum16 then reads a
 // row's NWV partials with one or two 16-byte LDS reads (not NWV dependent ones) and adds them in
@@ -903,6 +952,11 @@ __device__ uint64_t g_trace[NWG][MAX_LAYERS + 1][32];
 template <int FMT, bool MATH>
 __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uint8_t* wdb, int w, int pos, int stp) {
     constexpr bool F16 = FMT == FMT_F16;  // f16 tiles stream through their stages (stage_f16 above)
+    // The slice-streaming form (f16 and q8 weights): every wave takes a K-slice of each stage's
+    // blocks; q4 blocks are held whole by the math waves.
+    constexpr bool SL = F16 || FMT == FMT_Q8;
+    constexpr int SF = SL ? FMT : FMT_Q8;               // slice tile format (unused by q4)
+    constexpr int SCHK = F16 ? F16_CHK : 64;            // K per 1 KiB chunk of a slice
     constexpr int XW = WAVES - MW;        // exchange waves
     constexpr int CHK = (FMT == FMT_Q4) ? 128 : 64;
     constexpr int CW2 = H / CHK / MW;   // chunks per math wave, K = 2048
@@ -921,27 +975,27 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // Math waves: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127) of
     // the current layer.
     WB<FMT, CW2> wx[2];
-    // f16: each wave's K-slices of its QKV block, gate|up blocks and down half-block, requested a
+    // f16 / q8: each wave's K-slices of its QKV block, gate|up blocks and down half-block, requested a
     // stage ahead where its registers are free: QKV after the previous down publish (math waves;
     // the exchange waves after the x poll); gate|up by the O workgroups' exchange waves two
     // blocks at the attention-output poll and one after their O products, by every other wave
     // after its attention partial, merge or O stage; down after the SwiGLU publish.
-    constexpr int F16_CPW = H / F16_CHK / WAVES, F16_CPWD = FFH / F16_CHK / WAVES;
-    WF<1, F16_CPW> wqf;
-    WF<3, F16_CPW> wgf;
-    WF<1, F16_CPWD> wdf;
+    constexpr int S_CPW = H / SCHK / WAVES, S_CPWD = FFH / SCHK / WAVES, S_CPWO = H / SCHK / XW;
+    SliceTiles<SF, 1, S_CPW> wqf;
+    SliceTiles<SF, 3, S_CPW> wgf;
+    SliceTiles<SF, 1, S_CPWD> wdf;
     __syncthreads();
 
     for (int step = 0; step < a.nsteps; ++step) {
         if (pos + 1 > maxctx) break;  // the commit stops earlier; guards the cache row
-        if (!F16 && MATH) {
+        if (!SL && MATH) {
             wx[0].forget();
             wx[1].forget();
         }
-        if constexpr (F16) {
-            if (MATH) wqf.load(a.layers[0].wqkv, {w}, H / F16_CHK, wave_id() * F16_CPW, my_tid() % 64);
+        if constexpr (SL) {
+            if (MATH) wqf.load(a.layers[0].wqkv, a.layers[0].wqkv_sb, {w}, H, wave_id(), my_tid() % 64);
         }
-        if (!F16 && MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
+        if (!SL && MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
             wx[0].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w - NWG / 2, H, wave_id(), my_tid() % 64);
             wx[1].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w, H, wave_id(), my_tid() % 64);
         }
@@ -969,7 +1023,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // Math-wave register tiles: each is requested while the exchange waves wait for the
             // input of its stage or of an earlier one.  The down half-block streams into LDS.
             WB<FMT, CW2> wgu[3];
-            if constexpr (F16) {  // slices loaded under role conditions: last layer's values are dead
+            if constexpr (SL) {  // slices loaded under role conditions: last layer's values are dead
                 wgf.forget();
                 wdf.forget();
                 if (!math) wqf.forget();
@@ -980,7 +1034,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // workgroups 128..255 would queue ahead of it on their CU: their QKV blocks are
             // requested during the previous layer's down stage (layer 0's at the start of the
             // step) and their K/V rows after the QKV publish.
-            const bool qkv_wg = F16 || w >= NWG / 2;  // f16: one block per workgroup
+            const bool qkv_wg = SL || w >= NWG / 2;  // f16 / q8: one block per workgroup
             PK_TRACE(l, 0);
             uint4 kt[ATT_NT][4], vr[ATT_SPQ];
             float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rs = 0.f;
@@ -995,7 +1049,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 // the O block and the mlp norm.
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.nw[tid * 8 + i] = nreg[i];
-                if (!F16 && !qkv_wg) {
+                if (!SL && !qkv_wg) {
                     wx[0].load(P.wo, P.wo_sb, w, H, mw, lane);
                     load_kv_block(kt, vr, kb, vb, j0, 0, nprior, tid);
                     // The lower down half-block of row block w into LDS: it lands long before the
@@ -1013,13 +1067,13 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             }
             if (sync_failed(S, !ok_in)) return;
             PK_TRACE_X(l, 1);
-            if constexpr (F16) {
+            if constexpr (SL) {
                 // Row block w: the exchange waves request their 8-chunk K-slices now (the math
                 // waves' are in flight since the previous layer), then the staging.
-                if (!math) wqf.load(P.wqkv, {w}, H / F16_CHK, wave * F16_CPW, lane);
-                stage_f16<H>(S, l == 0 ? S.emb : S.vec, true);
+                if (!math) wqf.load(P.wqkv, P.wqkv_sb, {w}, H, wave, lane);
+                stage_slices<FMT, H>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[1] = {0.f};
-                mac_f16(S, wqf, wave * F16_CPW, lane, acc);
+                wqf.mac(S, wave, lane, acc);
                 PK_TRACE(l, 28);
                 red_store16<1>(S, acc, wave);
                 if (wave == 0) {  // rows 2i, 2i + 1 of the block in packet i (even lanes)
@@ -1240,13 +1294,13 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             PK_TRACE(l, 4);
             // f16: the exchange waves of workgroups 0..127 request their O block (64 KiB) now; it
             // lands during the merge and is multiplied by them after the attention-output poll.
-            WF<1, H / F16_CHK / XW> wof;
-            if constexpr (F16) {
-                if (!math && w < H / 16) wof.load(P.wo, {w}, H / F16_CHK, (wave - MW) * (H / F16_CHK / XW), lane);
+            SliceTiles<SF, 1, S_CPWO> wof;
+            if constexpr (SL) {
+                if (!math && w < H / 16) wof.load(P.wo, P.wo_sb, {w}, H, wave - MW, lane);
                 // Workgroups 128..223 (no O, no merge) idle until the x' poll: their exchange waves
                 // request all of their gate|up slices now (the mergers' after the merge: in flight
                 // during their partials poll, they would delay it).
-                if (!math && w >= H / 16 && w < MERGER0) wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                if (!math && w >= H / 16 && w < MERGER0) wgf.load(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
             }
 
             // ---------------- merge of group g: workgroups 224..255 ------------------------
@@ -1301,8 +1355,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 }
                 PK_TRACE(l, 17);
                 __syncthreads();  // the partials in S.A are read before the next staging
-                if constexpr (F16) {
-                    if (!math) wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                if constexpr (SL) {
+                    if (!math) wgf.load(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
                 }
                 PK_TRACE(l, 6);
             }
@@ -1318,7 +1372,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // partials.  Which split publishes last varies (the one holding the new cache row
             // also waits for that row's acknowledgement): their math waves' wave 0 watches the
             // (l, m) packets of all 32, and nothing else of theirs is in flight then.
-            if (!F16 && math && w >= NWG / 2 && w < MERGER0) {
+            if (!SL && math && w >= NWG / 2 && w < MERGER0) {
                 // Wave 0 watches; the other math waves wait for it in LDS.
                 if (wave == 0)
                     watch_partials(S, ll + PARTP + (size_t)g * ATT_SPLITS * 2 * PART2 + HD / 2, 2 * PART2, tag4(r + 1),
@@ -1335,7 +1389,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                         S.xhi[0][tid - MT] = 0.f;
                     ok = ok && poll_vec<H / 2 / CT>(ll + ATTNP, H / 2, r + 1, S.vec, err);
                 }
-                if (!F16 && math) {
+                if (!SL && math) {
 #pragma unroll
                     for (int j = 0; j < 3; ++j) wgu[j].load(P.wgu, P.wgu_sb, 3 * w + j, H, mw, lane);
                 }
@@ -1344,15 +1398,15 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             if (w < H / 16) {
                 PK_TRACE_X(l, 7);
                 float y = 0.f;
-                if constexpr (F16) {
+                if constexpr (SL) {
                     // Two gate|up blocks go out beside the O block's registers, the third once the O
                     // products are done (all three before them: 860 against 834 us per token at 4k
                     // context, one before them: 836).
-                    if (!math) wgf.load<0, 2>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
-                    stage_f16<H>(S, S.vec, false);
+                    if (!math) wgf.template load<0, 2>(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
+                    stage_slices<FMT, H>(S, S.vec, false);
                     float acc1[1] = {0.f};
-                    if (!math) mac_f16(S, wof, (wave - MW) * (H / F16_CHK / XW), lane, acc1);
-                    if (!math) wgf.load<2, 3>(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
+                    if (!math) wof.mac(S, wave - MW, lane, acc1);
+                    if (!math) wgf.template load<2, 3>(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
                     red_store16<1>(S, acc1, math ? -1 : wave - MW);
                     y = red_sum16<XW>(S, 0);
                 } else {
@@ -1377,8 +1431,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // f16: the math waves' gate|up slices (after the O publish on workgroups 0..127).  One
             // block requested earlier, at the attention partial, measured slower (868 against 855 us
             // per token at 4k context), and so did one at the start of the O stage (864 against 857).
-            if (F16 && math) wgf.load(P.wgu, {3 * w, 3 * w + 1, 3 * w + 2}, H / F16_CHK, wave * F16_CPW, lane);
-            if (!F16 && math && qkv_wg) {
+            if (SL && math) wgf.load(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
+            if (!SL && math && qkv_wg) {
                 wd_request<FMT>(wdb, P.wd, P.wd_sb, w - NWG / 2, 1, mw, lane);
                 wx[0].forget();
                 wx[1].forget();
@@ -1402,12 +1456,12 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 if (sync_failed(S, !ok)) return;
                 PK_TRACE_X(l, 9);
                 float acc[3] = {0.f, 0.f, 0.f}, y[3] = {0.f, 0.f, 0.f};
-                if constexpr (F16) {
+                if constexpr (SL) {
                     // Blocks 3w .. 3w + 2 (192 KiB), every wave's slices in flight since its O work
                     // or attention ended.
-                    stage_f16<H>(S, S.vec, true);
+                    stage_slices<FMT, H>(S, S.vec, true);
                     PK_TRACE(l, 13);
-                    mac_f16(S, wgf, wave * F16_CPW, lane, acc);
+                    wgf.mac(S, wave, lane, acc);
                     PK_TRACE(l, 26);
                     red_store16<3>(S, acc, wave);
                     if (wave == 0) {
@@ -1433,8 +1487,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     }
                 }
                 PK_TRACE(l, 10);
-                if constexpr (F16)  // every wave's down slices (the gate|up slices are spent)
-                    wdf.load(P.wd, {w % (NWG / 2)}, FF / F16_CHK, (w / (NWG / 2)) * (FFH / F16_CHK) + wave * F16_CPWD, lane);
+                if constexpr (SL)  // every wave's down slices (the gate|up slices are spent)
+                    wdf.load(P.wd, P.wd_sb, {w % (NWG / 2)}, FF, (w / (NWG / 2)) * WAVES + wave, lane);
             }
 
             // ---------------- down: K half w / 128 of row block w % 128 --------------------
@@ -1442,19 +1496,19 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 const int rb = w % (NWG / 2), half = w / (NWG / 2);
                 bool ok = true;
                 if (!math) ok = poll_vec<FFH / 2 / CT>(ll + HP + half * (FFH / 2), FFH / 2, r + 1, S.vec, err);
-                if (!F16 && math && !qkv_wg) {
+                if (!SL && math && !qkv_wg) {
                     wx[0].forget();
                     wx[1].forget();
                 }
                 if (sync_failed(S, !ok)) return;
                 PK_TRACE_X(l, 11);
                 float y = 0.f;
-                if constexpr (F16) {
+                if constexpr (SL) {
                     // K half `half` of row block rb (96 KiB): chunks half * 96 .. of the block.
-                    stage_f16<FFH>(S, S.vec, false);
+                    stage_slices<FMT, FFH>(S, S.vec, false);
                     PK_TRACE(l, 18);
                     float acc1[1] = {0.f};
-                    mac_f16(S, wdf, wave * F16_CPWD, lane, acc1);
+                    wdf.mac(S, wave, lane, acc1);
                     PK_TRACE(l, 24);
                     red_store16<1>(S, acc1, wave);
                     y = red_sum16<WAVES>(S, 0);
@@ -1483,8 +1537,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     }
                 }
                 PK_TRACE(l, 12);
-                if constexpr (F16) {  // the math waves' QKV slices of the next layer
-                    if (math && l + 1 < L) wqf.load(a.layers[l + 1].wqkv, {w}, H / F16_CHK, wave * F16_CPW, lane);
+                if constexpr (SL) {  // the math waves' QKV slices of the next layer
+                    if (math && l + 1 < L) wqf.load(a.layers[l + 1].wqkv, a.layers[l + 1].wqkv_sb, {w}, H, wave, lane);
                 }
             }
         }

@@ -6,7 +6,7 @@ prints a markdown table: for each point, when it is reached after the layer star
 workgroup's QKV start), as the median over layers 4..23 of the median, earliest and latest
 workgroup; then the same for the final norm, lm_head and the greedy commit.
 
-Usage (on a GPU):  python -m instantcua_amd.trace_decode [--layers 28] [--pos 4096] [--steps 16] [--f16]
+Usage (on a GPU):  python -m instantcua_amd.trace_decode [--layers 28] [--pos 4096] [--steps 16] [--f16 | --q8]
                    python -m instantcua_amd.trace_decode --pairs   (a one-row and a grammar-pair pass)
 The model is the 28-layer q4 group-64 decoder of the decode benchmark; the cache rows before
 --pos are left zero (the bytes moved per step do not depend on their values).
@@ -32,7 +32,7 @@ from instantcua_amd.modelfile import WeightFormat  # noqa: E402
 # (math thread 0 or exchange thread 0), what has just happened).
 LAYER_POINTS = [
     (0, "math", "layer start (QKV stage entered)"),
-    (1, "exch", "x polled (QKV workgroups: 128..255; f16 all)"),
+    (1, "exch", "x polled (QKV workgroups: 128..255; f16 / q8 all)"),
     (28, "math", "QKV matrix-core sums (before the reduction)"),
     (30, "math", "q|k|v published"),
     (2, "math", "K/V rows requested"),
@@ -75,6 +75,8 @@ def read_trace(layers: int, pos: int, steps: int, fmt: int = WeightFormat.Q4):
         raise SystemExit(f"{TRACE_LIB} is missing: build it with python -m instantcua_amd.build --trace")
     if fmt == WeightFormat.F16:  # the f16 decode benchmark's model (random f16 bit patterns)
         img = synth.build_model_image(WeightFormat.F16, n_layers=layers, tag="bench-f16", f16_bits=True)
+    elif fmt == WeightFormat.Q8:  # the q8 decode benchmark's model
+        img = synth.build_model_image(WeightFormat.Q8, n_layers=layers, tag="bench-q8")
     else:
         img = synth.build_model_image(WeightFormat.Q4, n_layers=layers, tag="bench-q4")
     with eng.Engine(flags=0, image=img, max_context=pos + steps + 16, max_steps=steps + 8) as e:
@@ -128,7 +130,7 @@ def read_pair_traces(layers: int):
 
 def table(t, layer_ids, points, title, x_pollers=slice(128, 256)):
     """x_pollers: the workgroups whose stamp 1 of a layer is the x poll (the others stamp their
-    first barrier there): 128..255 in the q4 / q8 form, all 256 in the f16 form."""
+    first barrier there): 128..255 in the q4 form, all 256 in the f16 / q8 form."""
     rows = [f"| {title} | stamped by | median WG (us) | earliest WG | latest WG |", "|---|---|---|---|---|"]
     for ev, who, what in points:
         med, lo, hi = [], [], []
@@ -175,6 +177,7 @@ def main():
     ap.add_argument("--pos", type=int, default=4096)
     ap.add_argument("--steps", type=int, default=16)
     ap.add_argument("--f16", action="store_true", help="the 28-layer f16 decoder instead of q4")
+    ap.add_argument("--q8", action="store_true", help="the 28-layer q8 g32 decoder instead of q4")
     ap.add_argument("--classes", action="store_true", help="also tabulate each workgroup class's median and latest stamps")
     ap.add_argument("--save", default=None, help="write the raw stamp array [workgroup][layer][event] (us) to this .npy file")
     ap.add_argument("--pairs", action="store_true",
@@ -189,18 +192,20 @@ def main():
             print(table(t, list(range(4, 24)), LAYER_POINTS, "layer point"))
             print()
         return
-    t, us_tok = read_trace(a.layers, a.pos, a.steps, WeightFormat.F16 if a.f16 else WeightFormat.Q4)
+    fmt = WeightFormat.F16 if a.f16 else WeightFormat.Q8 if a.q8 else WeightFormat.Q4
+    name = "f16" if a.f16 else "q8" if a.q8 else "q4"
+    t, us_tok = read_trace(a.layers, a.pos, a.steps, fmt)
     L = a.layers
     starts = [np.min(t[:, l, 0][t[:, l, 0] > 0]) for l in range(L + 1)]
     period = np.diff(starts[:L])
     mid = list(range(min(4, L - 1), max(min(24, L - 1), 5)))
-    print(f"Persistent decode, {L}-layer {'f16' if a.f16 else 'q4'} decoder, context {a.pos}, {a.steps} steps in one launch: "
+    print(f"Persistent decode, {L}-layer {name} decoder, context {a.pos}, {a.steps} steps in one launch: "
           f"{us_tok:.1f} us/token with the trace stores (the last step is traced).\n")
     print(f"Layer period (layer start to the next layer's start): median {np.median(period[mid[0]:mid[-1]]):.2f} us, "
           f"min {period.min():.2f}, max {period.max():.2f}; final norm + lm_head + commit "
           f"{np.max(t[:, L, 4]) - starts[L]:.2f} us.\n")
     print(table(t, mid, LAYER_POINTS, f"layer point (median of layers {mid[0]}..{mid[-1]})",
-                slice(0, 256) if a.f16 else slice(128, 256)))
+                slice(0, 256) if fmt != WeightFormat.Q4 else slice(128, 256)))
     print()
     print(table(t, [L], HEAD_POINTS, "lm_head / commit point"))
     if a.classes:
