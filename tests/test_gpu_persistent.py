@@ -65,7 +65,7 @@ def test_persistent_path_is_available(images, fmt_name):
         assert e.last_decode_persistent
 
 
-@pytest.mark.parametrize("fmt_name,pos", [("q4", 4095), ("q8", 1000), ("q4", 9000), ("f16", 4095), ("f16", 300)])
+@pytest.mark.parametrize("fmt_name,pos", [("q4", 4095), ("q8", 1000), ("q8", 4095), ("q4", 9000), ("f16", 4095), ("f16", 300)])
 def test_long_context_decode(oracle_mod, images, fmt_name, pos):
     """Decode from a prefilled random cache: 4095 slots (uneven splits), 9000 (several 256-slot
     blocks per split)."""
