@@ -981,6 +981,9 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // blocks at the attention-output poll and one after their O products, by every other wave
     // after its attention partial, merge or O stage; down after the SwiGLU publish.
     constexpr int S_CPW = H / SCHK / WAVES, S_CPWD = FFH / SCHK / WAVES, S_CPWO = H / SCHK / XW;
+    // q8: the exchange waves also request their QKV slices of the next layer at the down publish
+    // (648 against 662 us per token at 4k context); the f16 slices, twice the size, spill there.
+    constexpr bool QKV_AHEAD_ALL = FMT == FMT_Q8;
     SliceTiles<SF, 1, S_CPW> wqf;
     SliceTiles<SF, 3, S_CPW> wgf;
     SliceTiles<SF, 1, S_CPWD> wdf;
@@ -993,7 +996,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             wx[1].forget();
         }
         if constexpr (SL) {
-            if (MATH) wqf.load(a.layers[0].wqkv, a.layers[0].wqkv_sb, {w}, H, wave_id(), my_tid() % 64);
+            if (MATH || QKV_AHEAD_ALL) wqf.load(a.layers[0].wqkv, a.layers[0].wqkv_sb, {w}, H, wave_id(), my_tid() % 64);
         }
         if (!SL && MATH && w >= NWG / 2) {  // layer 0's QKV blocks (no x poll follows at layer 0)
             wx[0].load(a.layers[0].wqkv, a.layers[0].wqkv_sb, w - NWG / 2, H, wave_id(), my_tid() % 64);
@@ -1026,7 +1029,7 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             if constexpr (SL) {  // slices loaded under role conditions: last layer's values are dead
                 wgf.forget();
                 wdf.forget();
-                if (!math) wqf.forget();
+                if (!math && !QKV_AHEAD_ALL) wqf.forget();
             }
 
             // ---------------- QKV: row blocks w - 128 and w (workgroups 128..255) ------------
@@ -1068,9 +1071,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             if (sync_failed(S, !ok_in)) return;
             PK_TRACE_X(l, 1);
             if constexpr (SL) {
-                // Row block w: the exchange waves request their 8-chunk K-slices now (the math
-                // waves' are in flight since the previous layer), then the staging.
-                if (!math) wqf.load(P.wqkv, P.wqkv_sb, {w}, H, wave, lane);
+                // Row block w: the f16 exchange waves request their K-slices now (the math waves',
+                // and the q8 exchange waves', are in flight since the previous layer), then the
+                // staging.
+                if (!math && !QKV_AHEAD_ALL) wqf.load(P.wqkv, P.wqkv_sb, {w}, H, wave, lane);
                 stage_slices<FMT, H>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[1] = {0.f};
                 wqf.mac(S, wave, lane, acc);
@@ -1537,8 +1541,8 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     }
                 }
                 PK_TRACE(l, 12);
-                if constexpr (SL) {  // the math waves' QKV slices of the next layer
-                    if (math && l + 1 < L) wqf.load(a.layers[l + 1].wqkv, a.layers[l + 1].wqkv_sb, {w}, H, wave, lane);
+                if constexpr (SL) {  // the math waves' (q8: every wave's) QKV slices of the next layer
+                    if ((math || QKV_AHEAD_ALL) && l + 1 < L) wqf.load(a.layers[l + 1].wqkv, a.layers[l + 1].wqkv_sb, {w}, H, wave, lane);
                 }
             }
         }
