@@ -35,9 +35,9 @@ VIS_OFFSET, LLM_H, LLM_W = 16, 32, 32
 PREFILL = 4096
 # HBM bytes the persistent decode launch moves per algorithmic byte, from rocprofv3 FETCH_SIZE
 # (scaled by 1.964, the factor that makes it read a GEMV of known footprint correctly) plus
-# WRITE_SIZE over a 16-step launch at this context: 1.4766 GB per step against 1.4391 GB of
+# WRITE_SIZE over a 16-step launch at this context: 1.4769 GB per step against 1.4391 GB of
 # weights and K/V (profiles/decode_q4_4k_persistent_counters.md).
-DECODE_TRAFFIC_RATIO = 1.4766 / 1.4391
+DECODE_TRAFFIC_RATIO = 1.4769 / 1.4391
 
 
 def weight_bytes_per_token(fmt=WeightFormat.Q4) -> int:
