@@ -984,6 +984,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // q8: the exchange waves also request their QKV slices of the next layer at the down publish
     // (648 against 662 us per token at 4k context); the f16 slices, twice the size, spill there.
     constexpr bool QKV_AHEAD_ALL = FMT == FMT_Q8;
+    // q8: workgroups 128..223 hold their gate|up requests until their KV group's last split
+    // partial is out, as the q4 form holds its bulk requests there (642 against 646 us per token;
+    // the f16 form measured 832 against 824 with the hold).
+    constexpr bool GU_HOLD = FMT == FMT_Q8;
     SliceTiles<SF, 1, S_CPW> wqf;
     SliceTiles<SF, 3, S_CPW> wgf;
     SliceTiles<SF, 1, S_CPWD> wdf;
@@ -1302,9 +1306,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             if constexpr (SL) {
                 if (!math && w < H / 16) wof.load(P.wo, P.wo_sb, {w}, H, wave - MW, lane);
                 // Workgroups 128..223 (no O, no merge) idle until the x' poll: their exchange waves
-                // request all of their gate|up slices now (the mergers' after the merge: in flight
-                // during their partials poll, they would delay it).
-                if (!math && w >= H / 16 && w < MERGER0) wgf.load(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
+                // request all of their gate|up slices now (q8: once their KV group's partials are
+                // out, below; the mergers' after the merge: in flight during their partials poll,
+                // they would delay it).
+                if (!GU_HOLD && !math && w >= H / 16 && w < MERGER0) wgf.load(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
             }
 
             // ---------------- merge of group g: workgroups 224..255 ------------------------
@@ -1376,13 +1381,16 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             // partials.  Which split publishes last varies (the one holding the new cache row
             // also waits for that row's acknowledgement): their math waves' wave 0 watches the
             // (l, m) packets of all 32, and nothing else of theirs is in flight then.
-            if (!SL && math && w >= NWG / 2 && w < MERGER0) {
-                // Wave 0 watches; the other math waves wait for it in LDS.
+            if (((!SL && math) || GU_HOLD) && w >= NWG / 2 && w < MERGER0) {
+                // Wave 0 watches; the other waves taking part wait for it in LDS.
                 if (wave == 0)
                     watch_partials(S, ll + PARTP + (size_t)g * ATT_SPLITS * 2 * PART2 + HD / 2, 2 * PART2, tag4(r + 1),
                                    (int)r + 1, err, lane);
                 while (__hip_atomic_load(&S.go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (int)r + 1)
                     __builtin_amdgcn_s_sleep(1);
+                if constexpr (GU_HOLD) {
+                    if (!math) wgf.load(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
+                }
             }
             {
                 bool ok = true;
