@@ -982,13 +982,15 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // after its attention partial, merge or O stage; down after the SwiGLU publish.
     constexpr int S_CPW = H / SCHK / WAVES, S_CPWD = FFH / SCHK / WAVES, S_CPWO = H / SCHK / XW;
     // q8: the exchange waves also request their QKV slices of the next layer at the down publish
-    // (648 against 662 us per token at 4k context); the f16 slices, twice the size, spill there.
+    // (648 against 662 us per token at 4k context), so every wave multiplies a slice; f16 exchange
+    // wave slices spill there, and the f16 math waves hold the whole block instead.
     constexpr bool QKV_AHEAD_ALL = FMT == FMT_Q8;
     // q8: workgroups 128..223 hold their gate|up requests until their KV group's last split
     // partial is out, as the q4 form holds its bulk requests there (642 against 646 us per token;
     // the f16 form measured 832 against 824 with the hold).
     constexpr bool GU_HOLD = FMT == FMT_Q8;
-    SliceTiles<SF, 1, S_CPW> wqf;
+    // f16: the math waves hold the whole QKV block (16 chunks each); q8: every wave a slice.
+    SliceTiles<SF, 1, (F16 ? 2 * S_CPW : S_CPW)> wqf;
     SliceTiles<SF, 3, S_CPW> wgf;
     SliceTiles<SF, 1, S_CPWD> wdf;
     __syncthreads();
@@ -1075,17 +1077,16 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
             if (sync_failed(S, !ok_in)) return;
             PK_TRACE_X(l, 1);
             if constexpr (SL) {
-                // Row block w: the f16 exchange waves request their K-slices now (the math waves',
-                // and the q8 exchange waves', are in flight since the previous layer), then the
-                // staging.
-                if (!math && !QKV_AHEAD_ALL) wqf.load(P.wqkv, P.wqkv_sb, {w}, H, wave, lane);
+                // Row block w, in flight since the previous layer's down publish: held whole by the
+                // f16 math waves (the exchange waves' slices, requested after the x poll, landed
+                // last: 822 against 818 us per token at 4k context), as slices by every q8 wave.
                 stage_slices<FMT, H>(S, l == 0 ? S.emb : S.vec, true);
                 float acc[1] = {0.f};
-                wqf.mac(S, wave, lane, acc);
+                if (!F16 || math) wqf.mac(S, wave, lane, acc);
                 PK_TRACE(l, 28);
-                red_store16<1>(S, acc, wave);
+                red_store16<1>(S, acc, F16 && !math ? -1 : wave);
                 if (wave == 0) {  // rows 2i, 2i + 1 of the block in packet i (even lanes)
-                    const float y0 = red_sum16<WAVES>(S, 0) * norm_scale<H>(S);
+                    const float y0 = (F16 ? red_sum16<MW>(S, 0) : red_sum16<WAVES>(S, 0)) * norm_scale<H>(S);
                     const float n0 = xor1(y0);
                     if (lane < 16 && !(lane & 1)) st64(ll + QKVP + w * 8 + lane / 2, pack2(y0, n0, r + 1));
                 }
