@@ -975,11 +975,11 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // Math waves: the two QKV blocks (workgroups 128..255) or the O block (workgroups 0..127) of
     // the current layer.
     WB<FMT, CW2> wx[2];
-    // f16 / q8: each wave's K-slices of its QKV block, gate|up blocks and down half-block, requested a
-    // stage ahead where its registers are free: QKV after the previous down publish (math waves;
-    // the exchange waves after the x poll); gate|up by the O workgroups' exchange waves two
-    // blocks at the attention-output poll and one after their O products, by every other wave
-    // after its attention partial, merge or O stage; down after the SwiGLU publish.
+    // f16 / q8: the tiles of the QKV block, gate|up blocks and down half-block, requested a stage
+    // ahead where the registers are free: the QKV block after the previous down publish; gate|up
+    // by the O workgroups' exchange waves two blocks at the attention-output poll and one after
+    // their O products, by every other wave after its attention partial, merge or O stage; the
+    // down half-block's slices after the SwiGLU publish.
     constexpr int S_CPW = H / SCHK / WAVES, S_CPWD = FFH / SCHK / WAVES, S_CPWO = H / SCHK / XW;
     // q8: the exchange waves also request their QKV slices of the next layer at the down publish
     // (648 against 662 us per token at 4k context), so every wave multiplies a slice; f16 exchange
