@@ -989,6 +989,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
     // partial is out, as the q4 form holds its bulk requests there (642 against 646 us per token;
     // the f16 form measured 832 against 824 with the hold).
     constexpr bool GU_HOLD = FMT == FMT_Q8;
+    // q8: the O block is multiplied by all eight waves (the math waves' slices requested after
+    // their attention partial; 639 against 642 us per token); the f16 math waves' share spills,
+    // so there the four exchange waves take it.
+    constexpr bool O_ALL = FMT == FMT_Q8;
     // f16: the math waves hold the whole QKV block (16 chunks each); q8: every wave a slice.
     SliceTiles<SF, 1, (F16 ? 2 * S_CPW : S_CPW)> wqf;
     SliceTiles<SF, 3, S_CPW> wgf;
@@ -1301,11 +1305,12 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                 PK_TRACE(l, 20);
             }
             PK_TRACE(l, 4);
-            // f16: the exchange waves of workgroups 0..127 request their O block (64 KiB) now; it
-            // lands during the merge and is multiplied by them after the attention-output poll.
-            SliceTiles<SF, 1, S_CPWO> wof;
+            // f16 / q8: workgroups 0..127 request their O block now (f16: the exchange waves, 64 KiB;
+            // q8: every wave its slice); it lands during the merge and is multiplied after the
+            // attention-output poll.
+            SliceTiles<SF, 1, (O_ALL ? S_CPW : S_CPWO)> wof;
             if constexpr (SL) {
-                if (!math && w < H / 16) wof.load(P.wo, P.wo_sb, {w}, H, wave - MW, lane);
+                if ((O_ALL || !math) && w < H / 16) wof.load(P.wo, P.wo_sb, {w}, H, O_ALL ? wave : wave - MW, lane);
                 // Workgroups 128..223 (no O, no merge) idle until the x' poll: their exchange waves
                 // request all of their gate|up slices now (q8: once their KV group's partials are
                 // out, below; the mergers' after the merge: in flight during their partials poll,
@@ -1418,10 +1423,10 @@ __device__ __forceinline__ void decode_loop(const PersistArgs& a, Shared& S, uin
                     if (!math) wgf.template load<0, 2>(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
                     stage_slices<FMT, H>(S, S.vec, false);
                     float acc1[1] = {0.f};
-                    if (!math) wof.mac(S, wave - MW, lane, acc1);
+                    if (O_ALL || !math) wof.mac(S, O_ALL ? wave : wave - MW, lane, acc1);
                     if (!math) wgf.template load<2, 3>(P.wgu, P.wgu_sb, {3 * w, 3 * w + 1, 3 * w + 2}, H, wave, lane);
-                    red_store16<1>(S, acc1, math ? -1 : wave - MW);
-                    y = red_sum16<XW>(S, 0);
+                    red_store16<1>(S, acc1, O_ALL ? wave : math ? -1 : wave - MW);
+                    y = O_ALL ? red_sum16<WAVES>(S, 0) : red_sum16<XW>(S, 0);
                 } else {
                     stage_c<FMT, H>(S, S.vec, false);
                     float acc1[1] = {0.f};
