@@ -78,6 +78,35 @@ def test_grammar_pairs_f16_match_the_oracle(oracle_mod, scales, seed):
     assert list(got_split) == ref, (list(got_split), ref)
 
 
+@pytest.mark.parametrize("scales,seed,n_pairs", [({11: 16, 3678: 16, 8: 4}, 4, 2), ({11: 24, 3678: 24, 8: 6}, 4, 1)])
+def test_grammar_pairs_q8_match_the_oracle(oracle_mod, scales, seed, n_pairs):
+    """q8 weights: single-row passes on the persistent kernel's slice-streaming form, each forced
+    pair as a two-row pass of its register-tile form (the state handed between the two forms by
+    the control block and the residual rows); the first sequence forces the step-1 action pair
+    and an 11 pair, the second the action pair and then stops on ")"."""
+    img = scale_embedding_rows(synth.build_model_image(WeightFormat.Q8, n_layers=2, tag="q8-grammar"), scales)
+    toks = synth.random_tokens(9, "gram", seed)
+    steps = 20
+    om = oracle_mod.OracleModel(img, 128)
+    ref = [int(t) for t in om.generate_commit(toks, steps, grammar=True)]
+    assert ref[:2] == [3678, 7] and ref.count(220) + 1 == n_pairs, ref
+    with Engine(flags=0, image=img, max_context=128, max_steps=steps) as e:
+        e.eos = (-1, -1)
+        e.grammar_pairs = True
+        p0 = e.pair_passes
+        got = e.generate(toks, max_new_tokens=steps)
+        assert e.last_decode_persistent
+        assert e.pair_passes - p0 == n_pairs  # each pair as one two-row persistent pass
+        e.prefill(toks, max_new=steps)
+        for _ in range(steps):  # one pass per call: pairs pending between calls
+            if e.state()["done"]:
+                break
+            e.decode_steps(1)
+        got_split = e.tokens(e.state()["step"])
+    assert got == ref, (got, ref)
+    assert list(got_split) == ref, (list(got_split), ref)
+
+
 @pytest.mark.parametrize("split", [1, 2, 3])
 def test_grammar_pairs_across_decode_calls(oracle_mod, grammar_base, split):
     """A forced pair left pending at the end of a decode call (state n = 2) continues in the next
